@@ -1,0 +1,168 @@
+/*
+ * rpfq.h -- C ABI of the MI355X (gfx950) packed complex-phase linear kernels.
+ *
+ * Contract shared by every entry point:
+ *   - all array arguments are caller-owned DEVICE pointers (HIP memory);
+ *     nothing is allocated on the hot path;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t passed as
+ *     void*; NULL = the default stream) and the call returns without waiting;
+ *   - the return value is RPFQ_OK or a positive RPFQ_ERR_* status; the entry
+ *     points never abort or throw.  rpfq_last_error() returns a thread-local
+ *     message for the last failing call on the calling thread;
+ *   - argument validation happens on the host before any HIP call, so every
+ *     shape / null / alignment / enum error is reported without a GPU;
+ *   - the library holds no mutable global state: calls are reentrant and
+ *     may be issued from several threads on different streams.
+ *
+ * Feature layout: a "wide" (widely-linear) layer maps x = [x_re | x_im]
+ * ([M, 2K'] row-major) to y = [y_re | y_im] ([M, 2N']) with
+ * y = U x + W conj(x) + bias, where U and W are complex [N', K'] matrices held
+ * as phase codes times scales.  This is the reference layer
+ * QATLinearComplexPhase (RPFQ-ViT-main/quant_models/quant_i.py:475-554).
+ */
+#ifndef RPFQ_H_
+#define RPFQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RPFQ_ABI_VERSION 1
+
+/* status codes */
+#define RPFQ_OK 0
+#define RPFQ_ERR_NULL 1      /* a required pointer is NULL */
+#define RPFQ_ERR_SHAPE 2     /* non-positive, odd or inconsistent dimensions */
+#define RPFQ_ERR_ALIGN 3     /* dimension or pointer not aligned as required */
+#define RPFQ_ERR_BITS 4      /* unsupported code width / codebook / planes */
+#define RPFQ_ERR_DTYPE 5     /* unsupported element type */
+#define RPFQ_ERR_VALUE 6     /* invalid value (e.g. block not a multiple of 32) */
+#define RPFQ_ERR_HIP 7       /* the HIP runtime reported an error */
+
+/* element types of activations / outputs */
+#define RPFQ_F32 0
+#define RPFQ_F16 1
+#define RPFQ_BF16 2
+
+/* codebooks of the packed planes */
+#define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages
+                            (quant_i.py:36-118, export_rpfq_vit_to_mlx.py:189-224) */
+#define RPFQ_CB_SIGN 1   /* 2-bit quadrant-sign codes (quant_i.py:84-91):
+                            bit0 = (re >= 0), bit1 = (im >= 0) */
+#define RPFQ_CB_PSK16 2  /* 4-bit code c -> exp(i 2 pi c / 16); build-defined,
+                            no counterpart in the reference */
+
+/* Descriptor of one packed widely-linear layer. */
+typedef struct rpfq_wide_desc {
+    int64_t n_complex; /* N' = out_features / 2 */
+    int64_t k_complex; /* K' = in_features / 2 (multiple of 8) */
+    int64_t block;     /* scale block along K' in complex columns: 0 = one
+                          scale per row, else a multiple of 32 */
+    int32_t codebook;  /* RPFQ_CB_* */
+    int32_t stages;    /* residual stages per U/W: 1 or 2 (AXIS/SIGN); 1 (PSK16) */
+    int32_t rotate;    /* 1: de-rotate the quantized U/W by (cos,sin) below,
+                          quant_i.py:425-435 */
+    float rot_u[2];    /* cos(theta_u), sin(theta_u) as float32 */
+    float rot_w[2];    /* cos(theta_w), sin(theta_w) as float32 */
+} rpfq_wide_desc;
+
+/* Library identity. */
+int rpfq_abi_version(void);
+const char* rpfq_last_error(void);
+
+/*
+ * Decode one packed plane to float32 real/imag planes.
+ * Replaces the unpack + dequantize of
+ *   RPFQ-ViTApple/scripts/export_rpfq_vit_to_mlx.py:227-254 (dequantize_axis)
+ *   RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:15-19, :143-154
+ * bits = 2: codes [rows, k/4] uint8 (4 codes per byte, low bits first),
+ *           code -> {-1, +1, -i, +i};
+ * bits = 4: codes [rows, k/2] uint8 (low nibble first), 16-PSK codebook.
+ * gamma_re / gamma_im: fp16 bit patterns [rows, ceil(k/block)]; the value is
+ * codebook / gamma (as the exporter).  Both NULL: unit codebook values.
+ * Bit-exact with the reference.
+ */
+int rpfq_unpack(const uint8_t* codes, int bits, int64_t rows, int64_t k,
+                const uint16_t* gamma_re, const uint16_t* gamma_im, int64_t block,
+                float* re, float* im, void* stream);
+
+/*
+ * Single packed plane complex linear, the reference primitive
+ *   RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:119-164
+ *   (phaseLinearReference; also RPFQViTMetalKernels.swift:91-174 prefill):
+ *   conj_x = 1:  y = W conj(x):  Re = sum wRe xr + wIm xi, Im = sum wIm xr - wRe xi
+ *   conj_x = 0:  y = W x (the U-branch feed (xr, -xi), phase_linear.cpp:189-192)
+ * xr, xi: [M, K] planes; codes [N, K/4] uint8; gamma_re/gamma_im fp16 bits
+ * [N, ceil(K/block)] (block multiple of 32, or 0 = one per row); yr, yi:
+ * [M, N].  K must be a multiple of 32.  Codes are contracted exactly
+ * (ternary MFMA operands) and the scales are applied in the epilogue;
+ * float32 x is split into two fp16 terms (relative error ~2^-22).
+ */
+int rpfq_phase_linear(const void* xr, const void* xi, int x_dtype, int conj_x,
+                      int64_t M, int64_t K, const uint8_t* codes,
+                      const uint16_t* gamma_re, const uint16_t* gamma_im, int64_t block,
+                      int64_t N, void* yr, void* yi, int y_dtype, void* stream);
+
+/* Bytes of the device blob that rpfq_wide_pack writes for `desc`. */
+size_t rpfq_wide_packed_bytes(const rpfq_wide_desc* desc);
+
+/*
+ * Repack a layer's code planes into the MI355X tiled layout.
+ * Replaces the loader step of
+ *   RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:90-117 (loadWideParams)
+ *   and the fused cache of kernels/phase_linear_cache.cpp:84-131.
+ * planes (AXIS/SIGN): 2*stages code planes ordered u_s0[, u_s1], w_s0[, w_s1],
+ *   each [N', K'/4] uint8 in the exporter's packing (export…py:148-159);
+ * planes (PSK16): u, w, each [N', K'/2] uint8 (low nibble first).
+ * scale_re[p] / scale_im[p]: float32 [N', nblk] multipliers of plane p
+ *   (the training scale, or 1/gamma of the exporter); PSK16 uses scale_re
+ *   only (magnitude).  nblk = 1 if desc->block == 0 else ceil(K'/block).
+ * packed: device buffer of rpfq_wide_packed_bytes(desc) bytes.
+ */
+int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int nplanes,
+                   const float* const* scale_re, const float* const* scale_im,
+                   void* packed, size_t packed_bytes, void* stream);
+
+/*
+ * Widely-linear layer y = U x + W conj(x) + bias on [re | im] features.
+ * Replaces the contraction F.linear(x, A_q, bias) of quant_i.py:554 and
+ *   RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:166-256
+ *   (wideLinearReference / wideLinear; Metal widePrefill
+ *   RPFQViTMetalKernels.swift:176-268).
+ * x: [M, 2K'] of x_dtype (rows 16-byte aligned); bias: float32 [2N'] or NULL;
+ * y: [M, 2N'] of y_dtype.  The fused coefficients A = W + U (etc.) are formed
+ * in float32 exactly as the reference does, rounded once to fp16 for the
+ * MFMA, and accumulated in float32.  flags: 0 (reserved).
+ */
+int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
+                     const void* x, int x_dtype, int64_t M, const float* bias,
+                     void* y, int y_dtype, int flags, void* stream);
+
+/*
+ * Activation fake quantization of a [M, in_features] feature block laid out
+ * [re | im]: per row and per half, scale = qmax / max(max|x|, 1e-5),
+ * y = clamp(round_half_even(x * scale), -2^(bits-1), 2^(bits-1)-1) / scale,
+ * in float32 (bit-exact for float32 in/out).
+ * Replaces ActivationQuantSTE / ComplexActivationQuantizer
+ *   RPFQ-ViT-main/quant_models/quant_i.py:438-472, applied at :546-551.
+ */
+int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, int bits,
+                   void* y, int y_dtype, void* stream);
+
+/*
+ * Write the fused float32 weight A_q [2N', 2K'] that the packed layer
+ * represents (quant_i.py:534-544 layout), decoded by the same device code the
+ * GEMM uses.  round_fp16 = 1 writes the fp16-rounded values the MFMA consumes.
+ * Replaces export_rpfq_vit_to_mlx.py:336-375 (quantized_forward_weight).
+ */
+int rpfq_wide_decode(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
+                     float* a, int round_fp16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RPFQ_H_ */

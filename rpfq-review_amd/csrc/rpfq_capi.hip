@@ -1,0 +1,174 @@
+// C ABI entry points (include/rpfq.h): argument validation on the host, then
+// dispatch to the launchers.  Every check runs before the first HIP call so
+// the error paths are testable without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "rpfq_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = 0;
+    return RPFQ_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(RPFQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool dtype_ok(int dt) { return dt == RPFQ_F32 || dt == RPFQ_F16 || dt == RPFQ_BF16; }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_desc(const rpfq_wide_desc* d) {
+    if (!d) return fail(RPFQ_ERR_NULL, "desc is NULL");
+    if (d->n_complex <= 0 || d->k_complex <= 0)
+        return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld must be positive",
+                    (long long)d->n_complex, (long long)d->k_complex);
+    if (d->k_complex % 8 != 0)
+        return fail(RPFQ_ERR_ALIGN, "k_complex=%lld must be a multiple of 8", (long long)d->k_complex);
+    if (d->block < 0 || (d->block > 0 && d->block % 32 != 0))
+        return fail(RPFQ_ERR_VALUE, "block=%lld must be 0 or a multiple of 32", (long long)d->block);
+    if (d->codebook != RPFQ_CB_AXIS && d->codebook != RPFQ_CB_SIGN && d->codebook != RPFQ_CB_PSK16)
+        return fail(RPFQ_ERR_BITS, "unknown codebook %d", d->codebook);
+    if (d->codebook == RPFQ_CB_PSK16 && d->stages != 1)
+        return fail(RPFQ_ERR_BITS, "PSK16 layers have one stage, got %d", d->stages);
+    if (d->stages != 1 && d->stages != 2)
+        return fail(RPFQ_ERR_BITS, "stages=%d unsupported (1 or 2)", d->stages);
+    if (d->rotate != 0 && d->rotate != 1) return fail(RPFQ_ERR_VALUE, "rotate must be 0 or 1");
+    return RPFQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rpfq_abi_version(void) { return RPFQ_ABI_VERSION; }
+
+const char* rpfq_last_error(void) { return g_err; }
+
+int rpfq_unpack(const uint8_t* codes, int bits, int64_t rows, int64_t k, const uint16_t* gamma_re,
+                const uint16_t* gamma_im, int64_t block, float* re, float* im, void* stream) {
+    if (!codes || !re || !im) return fail(RPFQ_ERR_NULL, "codes/re/im must not be NULL");
+    if ((gamma_re == nullptr) != (gamma_im == nullptr))
+        return fail(RPFQ_ERR_NULL, "gamma_re and gamma_im must both be set or both NULL");
+    if (bits != 2 && bits != 4) return fail(RPFQ_ERR_BITS, "bits=%d unsupported (2 or 4)", bits);
+    if (rows <= 0 || k <= 0) return fail(RPFQ_ERR_SHAPE, "rows=%lld k=%lld must be positive", (long long)rows, (long long)k);
+    if (k % (8 / bits) != 0) return fail(RPFQ_ERR_ALIGN, "k=%lld must fill whole bytes", (long long)k);
+    if (block < 0) return fail(RPFQ_ERR_VALUE, "block must be >= 0");
+    int64_t nblk = block > 0 ? (k + block - 1) / block : 1;
+    return hip_status(rpfq::launch_unpack(codes, bits, rows, k, gamma_re, gamma_im, nblk, block, re, im,
+                                          reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_unpack");
+}
+
+int rpfq_phase_linear(const void* xr, const void* xi, int x_dtype, int conj_x, int64_t M, int64_t K,
+                      const uint8_t* codes, const uint16_t* gamma_re, const uint16_t* gamma_im, int64_t block,
+                      int64_t N, void* yr, void* yi, int y_dtype, void* stream) {
+    if (!xr || !xi || !codes || !gamma_re || !gamma_im || !yr || !yi)
+        return fail(RPFQ_ERR_NULL, "rpfq_phase_linear: NULL pointer argument");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0 || K <= 0 || N <= 0)
+        return fail(RPFQ_ERR_SHAPE, "M=%lld K=%lld N=%lld must be positive", (long long)M, (long long)K, (long long)N);
+    if (K % 32 != 0) return fail(RPFQ_ERR_ALIGN, "K=%lld must be a multiple of 32", (long long)K);
+    if (block < 0 || (block > 0 && block % 32 != 0))
+        return fail(RPFQ_ERR_VALUE, "block=%lld must be 0 or a multiple of 32", (long long)block);
+    if (!aligned(xr, 16) || !aligned(xi, 16) || !aligned(codes, 8))
+        return fail(RPFQ_ERR_ALIGN, "x planes must be 16-byte and codes 8-byte aligned");
+    int64_t nblk = block > 0 ? (K + block - 1) / block : 1;
+    int64_t block_ks = block > 0 ? block / 32 : K / 32;
+    return hip_status(rpfq::launch_phase_linear(xr, xi, x_dtype, conj_x, M, K, codes, gamma_re, gamma_im, nblk,
+                                                block_ks, N, yr, yi, y_dtype, reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_phase_linear");
+}
+
+size_t rpfq_wide_packed_bytes(const rpfq_wide_desc* desc) {
+    if (check_desc(desc) != RPFQ_OK) return 0;
+    return rpfq::wide_geom(*desc).total_bytes;
+}
+
+int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int nplanes,
+                   const float* const* scale_re, const float* const* scale_im, void* packed, size_t packed_bytes,
+                   void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!planes || !scale_re || !packed) return fail(RPFQ_ERR_NULL, "planes/scale_re/packed must not be NULL");
+    int want = desc->codebook == RPFQ_CB_PSK16 ? 2 : 2 * desc->stages;
+    if (nplanes != want) return fail(RPFQ_ERR_BITS, "expected %d planes, got %d", want, nplanes);
+    if (desc->codebook != RPFQ_CB_PSK16 && !scale_im) return fail(RPFQ_ERR_NULL, "scale_im must not be NULL");
+    for (int p = 0; p < nplanes; ++p) {
+        if (!planes[p] || !scale_re[p] || (desc->codebook != RPFQ_CB_PSK16 && !scale_im[p]))
+            return fail(RPFQ_ERR_NULL, "plane %d has a NULL pointer", p);
+    }
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256)) return fail(RPFQ_ERR_ALIGN, "packed buffer must be 256-byte aligned");
+    return hip_status(rpfq::launch_wide_pack(*desc, g, planes, nplanes, scale_re, scale_im, packed,
+                                             reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_pack");
+}
+
+int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                     int x_dtype, int64_t M, const float* bias, void* y, int y_dtype, int flags, void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!packed || !x || !y) return fail(RPFQ_ERR_NULL, "packed/x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
+    if (flags != 0) return fail(RPFQ_ERR_VALUE, "flags=%d: no flags are defined", flags);
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256) || !aligned(x, 16))
+        return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte and x 16-byte aligned");
+    if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, y, y_dtype, flags,
+                                               reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_linear");
+}
+
+int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, int bits, void* y, int y_dtype,
+                   void* stream) {
+    if (!x || !y) return fail(RPFQ_ERR_NULL, "x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0 || in_features <= 0 || in_features % 2 != 0)
+        return fail(RPFQ_ERR_SHAPE, "M=%lld in_features=%lld: need M > 0 and even in_features > 0",
+                    (long long)M, (long long)in_features);
+    if (bits < 2 || bits > 16) return fail(RPFQ_ERR_BITS, "bits=%d unsupported (2..16)", bits);
+    if (M > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    return hip_status(rpfq::launch_act_quant(x, x_dtype, M, in_features / 2, bits, y, y_dtype,
+                                             reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_act_quant");
+}
+
+int rpfq_wide_decode(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, float* a, int round_fp16,
+                     void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!packed || !a) return fail(RPFQ_ERR_NULL, "packed/a must not be NULL");
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256)) return fail(RPFQ_ERR_ALIGN, "packed buffer must be 256-byte aligned");
+    return hip_status(rpfq::launch_wide_decode(*desc, g, packed, a, round_fp16 ? 1 : 0,
+                                               reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_decode");
+}
+
+}  // extern "C"

@@ -1,0 +1,906 @@
+// HIP kernels for gfx950 (MI355X): packed complex-phase linear layers.
+//
+//   unpack_kernel        bit-exact decode of one packed plane
+//   phase_linear_kernel  single plane, ternary MFMA operands, scales in epilogue
+//   wide_pack_kernel     reference planes -> native tiled blob
+//   wide_linear_kernel   widely-linear layer: per-row LUT decode in LDS ->
+//                        fp16 fused coefficients -> 32x32x16 f16 MFMA
+//   wide_decode_kernel   fused float32 weight, same decode as the GEMM
+//
+// Arithmetic order of the decoded coefficients follows the reference exactly
+// (RPFQ-ViT-main/quant_models/quant_i.py:111-118 stage sums, :534-544
+// recombination) so the float32 coefficient is bit-identical to A_q; it is
+// rounded once to fp16 for the MFMA.
+#include <mutex>
+
+#include "rpfq_internal.h"
+
+namespace rpfq {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// codebooks
+// ---------------------------------------------------------------------------
+// 16-PSK: exact octant symmetry from three float32 constants
+// (cos pi/8, sin pi/8, sqrt(2)/2 rounded to nearest float32).
+#define PSK_C1 0x1.d906bcp-1f  /* float32(cos pi/8) */
+#define PSK_S1 0x1.87de2ap-2f  /* float32(sin pi/8) */
+#define PSK_R2 0x1.6a09e6p-1f  /* float32(sqrt(2)/2) */
+__constant__ float kPskCos[16] = {1.0f,    PSK_C1,  PSK_R2,  PSK_S1,  0.0f,    -PSK_S1, -PSK_R2, -PSK_C1,
+                                  -1.0f,   -PSK_C1, -PSK_R2, -PSK_S1, 0.0f,    PSK_S1,  PSK_R2,  PSK_C1};
+__constant__ float kPskSin[16] = {0.0f,    PSK_S1,  PSK_R2,  PSK_C1,  1.0f,    PSK_C1,  PSK_R2,  PSK_S1,
+                                  0.0f,    -PSK_S1, -PSK_R2, -PSK_C1, -1.0f,   -PSK_C1, -PSK_R2, -PSK_S1};
+
+// 2-bit axis code -> value, codes 00=-1, 01=+1, 10=-i, 11=+i
+// (export_rpfq_vit_to_mlx.py:598-603; phase_linear.cpp:143-154).
+__device__ __forceinline__ float2 axis_val(uint32_t c, float sr, float si) {
+    float2 v;
+    v.x = (c & 2u) ? 0.0f : ((c & 1u) ? sr : -sr);
+    v.y = (c & 2u) ? ((c & 1u) ? si : -si) : 0.0f;
+    return v;
+}
+
+// 2-bit quadrant-sign code: bit0 = re >= 0, bit1 = im >= 0 (quant_i.py:84-91).
+__device__ __forceinline__ float2 sign_val(uint32_t c, float sr, float si) {
+    float2 v;
+    v.x = (c & 1u) ? sr : -sr;
+    v.y = (c & 2u) ? si : -si;
+    return v;
+}
+
+// Quantized complex value of one U (or W) index under the per-row
+// parameters p = (s0 re, s0 im, s1 re, s1 im).  Stages are summed in the
+// reference's order q = step0 + step1 (quant_i.py:111-118).
+template <int CB>
+__device__ __forceinline__ float2 lut_entry(uint32_t idx, float4 p) {
+    if (CB == RPFQ_CB_PSK16) {
+        return make_float2(p.x * kPskCos[idx], p.x * kPskSin[idx]);
+    }
+    float2 v0, v1;
+    if (CB == RPFQ_CB_SIGN) {
+        v0 = sign_val(idx & 3u, p.x, p.y);
+        v1 = sign_val(idx >> 2, p.z, p.w);
+    } else {
+        v0 = axis_val(idx & 3u, p.x, p.y);
+        v1 = axis_val(idx >> 2, p.z, p.w);
+    }
+    return make_float2(v0.x + v1.x, v0.y + v1.y);
+}
+
+// De-rotation after quantization (quant_i.py:433-434); built without
+// contraction (-ffp-contract=off) so each product rounds as in torch.
+__device__ __forceinline__ float2 derotate(float2 q, float c, float s) {
+    float a = q.x * c;
+    float b = q.y * s;
+    float d = q.y * c;
+    float e = q.x * s;
+    return make_float2(a - b, d + e);
+}
+
+// ---------------------------------------------------------------------------
+// element I/O
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// 8 consecutive elements at element offset `off` -> 8 fp16 in a uint4.
+template <int XDT>
+__device__ __forceinline__ uint4 load8_f16(const void* base, int64_t off) {
+    if (XDT == RPFQ_F16) {
+        return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    } else if (XDT == RPFQ_BF16) {
+        uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        uint4 o;
+        o.x = pack_h2(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16));
+        o.y = pack_h2(bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16));
+        o.z = pack_h2(bf16_to_f32(v.z & 0xffffu), bf16_to_f32(v.z >> 16));
+        o.w = pack_h2(bf16_to_f32(v.w & 0xffffu), bf16_to_f32(v.w >> 16));
+        return o;
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+        float4 a = p[0], b = p[1];
+        uint4 o;
+        o.x = pack_h2(a.x, a.y);
+        o.y = pack_h2(a.z, a.w);
+        o.z = pack_h2(b.x, b.y);
+        o.w = pack_h2(b.z, b.w);
+        return o;
+    }
+}
+
+// float32 -> (hi, lo) fp16 pair with x ~= hi + lo (relative error ~2^-22).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    _Float16 la = (_Float16)(a - (float)ha), lb = (_Float16)(b - (float)hb);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+}
+
+template <int YDT>
+__device__ __forceinline__ void store1(void* base, int64_t off, float v) {
+    if (YDT == RPFQ_F32) {
+        reinterpret_cast<float*>(base)[off] = v;
+    } else if (YDT == RPFQ_F16) {
+        reinterpret_cast<_Float16*>(base)[off] = (_Float16)v;
+    } else {
+        reinterpret_cast<uint16_t*>(base)[off] = f32_to_bf16(v);
+    }
+}
+
+__device__ __forceinline__ half8 as_half8(uint4 v) { return __builtin_bit_cast(half8, v); }
+
+__device__ __forceinline__ half8 to_half8(const float* v) {
+    uint4 u;
+    u.x = pack_h2(v[0], v[1]);
+    u.y = pack_h2(v[2], v[3]);
+    u.z = pack_h2(v[4], v[5]);
+    u.w = pack_h2(v[6], v[7]);
+    return as_half8(u);
+}
+
+// Workgroup id -> tile id so that each XCD (ids are dealt round-robin over 8
+// XCDs) owns one contiguous run of tiles; consecutive tiles share an M-tile
+// and hit the same L2.
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+    int xcd = bid & 7, local = bid >> 3;
+    int q = total >> 3, r = total & 7;
+    return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+// Row i of the 32x32 MFMA accumulator element v held by lane group g (lane/32).
+__device__ __forceinline__ int acc_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }
+
+// ---------------------------------------------------------------------------
+// unpack / dequantize one plane (export_rpfq_vit_to_mlx.py:227-254)
+// ---------------------------------------------------------------------------
+__global__ void unpack_kernel(const uint8_t* __restrict__ codes, int bits, int64_t rows, int64_t k,
+                              const uint16_t* __restrict__ gre, const uint16_t* __restrict__ gim,
+                              int64_t nblk, int64_t block, float* __restrict__ re,
+                              float* __restrict__ im) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * k) return;
+    int64_t row = i / k, col = i - row * k;
+    float vr, vi;
+    if (bits == 2) {
+        uint32_t byte = codes[row * (k >> 2) + (col >> 2)];
+        uint32_t c = (byte >> (2 * (col & 3))) & 3u;
+        float2 v = axis_val(c, 1.0f, 1.0f);
+        vr = v.x;
+        vi = v.y;
+    } else {
+        uint32_t byte = codes[row * (k >> 1) + (col >> 1)];
+        uint32_t c = (byte >> (4 * (col & 1))) & 15u;
+        vr = kPskCos[c];
+        vi = kPskSin[c];
+    }
+    if (gre != nullptr) {
+        int64_t b = block > 0 ? col / block : 0;
+        float g_re = (float)__builtin_bit_cast(_Float16, gre[row * nblk + b]);
+        float g_im = (float)__builtin_bit_cast(_Float16, gim[row * nblk + b]);
+        vr = vr / g_re;
+        vi = vi / g_im;
+    }
+    re[i] = vr;
+    im[i] = vi;
+}
+
+// ---------------------------------------------------------------------------
+// single-plane phase linear (phase_linear.cpp:119-164 semantics)
+// ---------------------------------------------------------------------------
+struct PhaseArgs {
+    const void* xr;
+    const void* xi;
+    int64_t M, K, N;
+    const uint8_t* codes;   // [N, K/4]
+    const uint16_t* gre;    // [N, nblk] fp16 bits
+    const uint16_t* gim;
+    int64_t nblk, block_ks;
+    float xsign;            // +1: W conj(x), -1: W x
+    void* yr;
+    void* yi;
+    int tiles_m, tiles_n;
+};
+
+// Ternary operand table: nibble (c0 | c1 << 2) -> fp16 pairs (tr0, tr1), (ti0, ti1)
+// with tr = Re(code), ti = Im(code) in {-1, 0, +1}.
+__device__ __forceinline__ uint2 tern_entry(uint32_t nib) {
+    const uint16_t h[4][2] = {{0xBC00u, 0x0000u}, {0x3C00u, 0x0000u}, {0x0000u, 0xBC00u}, {0x0000u, 0x3C00u}};
+    uint32_t c0 = nib & 3u, c1 = nib >> 2;
+    uint2 e;
+    e.x = (uint32_t)h[c0][0] | ((uint32_t)h[c1][0] << 16);
+    e.y = (uint32_t)h[c0][1] | ((uint32_t)h[c1][1] << 16);
+    return e;
+}
+
+template <int BM, int XDT, int YDT, bool PERBLOCK>
+__global__ void __launch_bounds__(256) phase_linear_kernel(PhaseArgs a) {
+    constexpr bool SPLIT = (XDT == RPFQ_F32);
+    constexpr int MB = BM / 32;
+    constexpr int XROW = SPLIT ? 272 : 144;  // bytes per LDS row (+16 pad)
+    constexpr int XSTAGE = BM * XROW;
+    constexpr int CPT = BM / 32;             // 16-byte chunks per thread per plane pair
+    __shared__ __align__(16) char smem[2 * XSTAGE];
+    __shared__ uint2 tern[16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 31, g = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
+    const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
+    const int64_t m0 = (int64_t)mt * BM;
+    const int64_t n = (int64_t)ntl * 128 + wave * 32 + r;
+    const bool n_ok = n < a.N;
+    const int64_t KS = a.K / 32;
+    const int64_t kb = a.K / 4;
+
+    if (tid < 16) tern[tid] = tern_entry(tid);
+
+    uint4 xh[CPT], xl[CPT];
+    uint2 creg = make_uint2(0, 0);
+
+    auto load_x = [&](int64_t ks) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            int c = tid + 256 * j;
+            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
+            int64_t m = m0 + row;
+            const void* plane = part ? a.xi : a.xr;
+            int64_t off = m * a.K + ks * 32 + sub * 8;
+            if (m < a.M) {
+                if (SPLIT) {
+                    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(plane) + off);
+                    float4 u = p[0], v = p[1];
+                    split2(u.x, u.y, xh[j].x, xl[j].x);
+                    split2(u.z, u.w, xh[j].y, xl[j].y);
+                    split2(v.x, v.y, xh[j].z, xl[j].z);
+                    split2(v.z, v.w, xh[j].w, xl[j].w);
+                } else {
+                    xh[j] = load8_f16<XDT>(plane, off);
+                }
+            } else {
+                xh[j] = make_uint4(0, 0, 0, 0);
+                xl[j] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto store_x = [&](int stage) {
+        char* xs = smem + stage * XSTAGE;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            int c = tid + 256 * j;
+            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
+            *reinterpret_cast<uint4*>(xs + row * XROW + part * 64 + sub * 16) = xh[j];
+            if (SPLIT) *reinterpret_cast<uint4*>(xs + row * XROW + 128 + part * 64 + sub * 16) = xl[j];
+        }
+    };
+    auto load_codes = [&](int64_t ks) {
+        creg = n_ok ? *reinterpret_cast<const uint2*>(a.codes + n * kb + ks * 8) : make_uint2(0, 0);
+    };
+
+    floatx16 c1[MB], c2[MB], c3[MB], c4[MB], tre[MB], tim[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        c1[i] = c2[i] = c3[i] = c4[i] = floatx16{0};
+        tre[i] = tim[i] = floatx16{0};
+    }
+
+    auto flush = [&](int64_t blk) {
+        float sr = 0.0f, si = 0.0f;
+        if (n_ok) {
+            sr = 1.0f / (float)__builtin_bit_cast(_Float16, a.gre[n * a.nblk + blk]);
+            si = 1.0f / (float)__builtin_bit_cast(_Float16, a.gim[n * a.nblk + blk]);
+        }
+        const float xs = a.xsign;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                tre[i][v] += sr * c1[i][v] + xs * (si * c2[i][v]);
+                tim[i][v] += si * c3[i][v] - xs * (sr * c4[i][v]);
+            }
+            c1[i] = c2[i] = c3[i] = c4[i] = floatx16{0};
+        }
+    };
+
+    load_x(0);
+    load_codes(0);
+    store_x(0);
+    __syncthreads();
+
+    for (int64_t ks = 0; ks < KS; ++ks) {
+        const uint2 cw = creg;
+        const bool more = ks + 1 < KS;
+        if (more) {
+            load_x(ks + 1);
+            load_codes(ks + 1);
+        }
+        const char* xs = smem + (ks & 1) * XSTAGE;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            uint32_t c16 = ((s ? cw.y : cw.x) >> (16 * g)) & 0xffffu;
+            uint2 t0 = tern[c16 & 15u], t1 = tern[(c16 >> 4) & 15u];
+            uint2 t2 = tern[(c16 >> 8) & 15u], t3 = tern[c16 >> 12];
+            half8 btr = as_half8(make_uint4(t0.x, t1.x, t2.x, t3.x));
+            half8 bti = as_half8(make_uint4(t0.y, t1.y, t2.y, t3.y));
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const char* rp = xs + (i * 32 + r) * XROW + (16 * s + 8 * g) * 2;
+                half8 axr = *reinterpret_cast<const half8*>(rp);
+                half8 axi = *reinterpret_cast<const half8*>(rp + 64);
+                c1[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, btr, c1[i], 0, 0, 0);
+                c2[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, bti, c2[i], 0, 0, 0);
+                c3[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, bti, c3[i], 0, 0, 0);
+                c4[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, btr, c4[i], 0, 0, 0);
+                if (SPLIT) {
+                    half8 lxr = *reinterpret_cast<const half8*>(rp + 128);
+                    half8 lxi = *reinterpret_cast<const half8*>(rp + 192);
+                    c1[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxr, btr, c1[i], 0, 0, 0);
+                    c2[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxi, bti, c2[i], 0, 0, 0);
+                    c3[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxr, bti, c3[i], 0, 0, 0);
+                    c4[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxi, btr, c4[i], 0, 0, 0);
+                }
+            }
+        }
+        if (PERBLOCK && (ks + 1) % a.block_ks == 0) flush(ks / a.block_ks);
+        if (more) store_x((ks + 1) & 1);
+        __syncthreads();
+    }
+    if (!PERBLOCK) flush(0);
+    else if (KS % a.block_ks != 0) flush(KS / a.block_ks);
+
+    if (!n_ok) return;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            int64_t m = m0 + i * 32 + acc_row(v, g);
+            if (m < a.M) {
+                store1<YDT>(a.yr, m * a.N + n, tre[i][v]);
+                store1<YDT>(a.yi, m * a.N + n, tim[i][v]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// native packing (loadWideParams analogue, phase_linear.cpp:90-117)
+// ---------------------------------------------------------------------------
+struct PackArgs {
+    const uint8_t* planes[4];
+    const float* sre[4];
+    const float* sim[4];
+    int nplanes, stages, codebook;
+    int64_t N, K, NT, KS, nblk;
+    uint8_t* codes;
+    float* params;
+};
+
+__global__ void wide_pack_codes_kernel(PackArgs a) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t total = a.NT * a.KS * 1024;
+    if (idx >= total) return;
+    int b = (int)(idx & 31), rr = (int)((idx >> 5) & 31);
+    int64_t t = idx >> 10;
+    int64_t ks = t % a.KS, nt = t / a.KS;
+    int64_t n = nt * 32 + rr;
+    int gg = b >> 4, s = (b >> 3) & 1, e = b & 7;
+    int64_t k = ks * 32 + 16 * s + 8 * gg + e;
+    uint32_t out = 0;
+    if (n < a.N && k < a.K) {
+        if (a.codebook == RPFQ_CB_PSK16) {
+            int64_t kb = a.K >> 1;
+            uint32_t cu = (a.planes[0][n * kb + (k >> 1)] >> (4 * (k & 1))) & 15u;
+            uint32_t cw = (a.planes[1][n * kb + (k >> 1)] >> (4 * (k & 1))) & 15u;
+            out = cu | (cw << 4);
+        } else {
+            int64_t kb = a.K >> 2;
+            int sh = 2 * (int)(k & 3);
+            uint32_t c[4] = {0, 0, 0, 0};
+            for (int p = 0; p < a.nplanes; ++p) c[p] = (a.planes[p][n * kb + (k >> 2)] >> sh) & 3u;
+            uint32_t iu, iw;
+            if (a.stages == 2) {
+                iu = c[0] | (c[1] << 2);
+                iw = c[2] | (c[3] << 2);
+            } else {
+                iu = c[0];
+                iw = c[1];
+            }
+            out = iu | (iw << 4);
+        }
+    }
+    a.codes[idx] = (uint8_t)out;
+}
+
+__global__ void wide_pack_params_kernel(PackArgs a) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t total = a.NT * 32 * a.nblk;
+    if (idx >= total) return;
+    int64_t n = idx / a.nblk;
+    float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (n < a.N) {
+        if (a.codebook == RPFQ_CB_PSK16) {
+            p[0] = a.sre[0][idx];
+            p[4] = a.sre[1][idx];
+        } else if (a.stages == 2) {
+            for (int q = 0; q < 4; ++q) {
+                p[2 * q] = a.sre[q][idx];
+                p[2 * q + 1] = a.sim[q][idx];
+            }
+        } else {
+            p[0] = a.sre[0][idx];
+            p[1] = a.sim[0][idx];
+            p[4] = a.sre[1][idx];
+            p[5] = a.sim[1][idx];
+        }
+    }
+    float4* dst = reinterpret_cast<float4*>(a.params + idx * 8);
+    dst[0] = make_float4(p[0], p[1], p[2], p[3]);
+    dst[1] = make_float4(p[4], p[5], p[6], p[7]);
+}
+
+// ---------------------------------------------------------------------------
+// widely-linear GEMM
+// ---------------------------------------------------------------------------
+struct WideArgs {
+    const void* x;
+    int64_t M, K, N, NT, KS, nblk, block_ks;
+    const uint4* codes;
+    const float4* params;
+    RotParams rot;
+    const float* bias;
+    void* y;
+    int tiles_m, tiles_n;
+};
+
+constexpr int kXRow = 144;              // LDS bytes per activation row (+16 pad)
+constexpr int kLutWave = 32 * 32 * 8;   // 32 entries x 32 rows x float2
+
+template <int BM>
+constexpr int wide_lds_bytes() {
+    return 2 * BM * kXRow + 4 * kLutWave;
+}
+
+// Builds the wave's LUT for scale block `blk`: entries 0..15 hold U(idx),
+// 16..31 hold W(idx), each for the wave's 32 rows; layout [entry][row].
+template <int CB>
+__device__ __forceinline__ void build_lut(float2* lut, const float4* params, int64_t n, bool active,
+                                          int64_t nblk, int64_t blk, const RotParams& rot, int r, int g) {
+    float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
+    if (active) {
+        const float4* p = params + (n * nblk + blk) * 2;
+        pu = p[0];
+        pw = p[1];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t idx = (uint32_t)(g + 2 * j);
+        float2 u = lut_entry<CB>(idx, pu);
+        float2 w = lut_entry<CB>(idx, pw);
+        if (rot.rotate) {
+            u = derotate(u, rot.cu, rot.su);
+            w = derotate(w, rot.cw, rot.sw);
+        }
+        lut[idx * 32 + r] = u;
+        lut[(16 + idx) * 32 + r] = w;
+    }
+}
+
+template <int BM, int XDT, int YDT, int CB>
+__global__ void __launch_bounds__(256) wide_linear_kernel(WideArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int MB = BM / 32;
+    constexpr int XSTAGE = BM * kXRow;
+    constexpr int CPT = BM / 32;  // 16-byte activation chunks per thread
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 31, g = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
+    const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
+    const int64_t m0 = (int64_t)mt * BM;
+    const int64_t ntw = (int64_t)ntl * 4 + wave;  // this wave's 32-row tile
+    const bool active = ntw < a.NT;
+    const int64_t n = ntw * 32 + r;
+    float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
+    const int64_t ldx = 2 * a.K;
+
+    uint4 xreg[CPT];
+    uint4 creg = make_uint4(0, 0, 0, 0);
+
+    auto load_x = [&](int64_t ks) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            int c = tid + 256 * j;
+            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
+            int64_t m = m0 + row;
+            int64_t kk = ks * 32 + sub * 8;
+            if (m < a.M && kk < a.K)
+                xreg[j] = load8_f16<XDT>(a.x, m * ldx + part * a.K + kk);
+            else
+                xreg[j] = make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_x = [&](int stage) {
+        char* xs = smem + stage * XSTAGE;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            int c = tid + 256 * j;
+            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
+            *reinterpret_cast<uint4*>(xs + row * kXRow + part * 64 + sub * 16) = xreg[j];
+        }
+    };
+    auto load_codes = [&](int64_t ks) {
+        if (active) creg = a.codes[((ntw * a.KS + ks) * 32 + r) * 2 + g];
+    };
+
+    floatx16 acc_re[MB], acc_im[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
+
+    int64_t cur_blk = 0;
+    build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
+    load_x(0);
+    load_codes(0);
+    store_x(0);
+    __syncthreads();
+
+    for (int64_t ks = 0; ks < a.KS; ++ks) {
+        const uint4 cw = creg;
+        const bool more = ks + 1 < a.KS;
+        if (more) {
+            load_x(ks + 1);
+            load_codes(ks + 1);
+        }
+        const char* xs = smem + (ks & 1) * XSTAGE;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const uint32_t w0 = s ? cw.z : cw.x;
+            const uint32_t w1 = s ? cw.w : cw.y;
+            float a11[8], a12[8], a21[8], a22[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint32_t byte = ((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 0xffu;
+                float2 U = lut[(byte & 15u) * 32 + r];
+                float2 W = lut[(16u + (byte >> 4)) * 32 + r];
+                // quant_i.py:534-537
+                a11[e] = W.x + U.x;
+                a12[e] = W.y - U.y;
+                a21[e] = W.y + U.y;
+                a22[e] = -W.x + U.x;
+            }
+            const half8 b11 = to_half8(a11), b12 = to_half8(a12);
+            const half8 b21 = to_half8(a21), b22 = to_half8(a22);
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const char* rp = xs + (i * 32 + r) * kXRow + (16 * s + 8 * g) * 2;
+                const half8 axr = *reinterpret_cast<const half8*>(rp);
+                const half8 axi = *reinterpret_cast<const half8*>(rp + 64);
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, b11, acc_re[i], 0, 0, 0);
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, b12, acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, b21, acc_im[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, b22, acc_im[i], 0, 0, 0);
+            }
+        }
+        if (more) {
+            store_x((ks + 1) & 1);
+            const int64_t nb = (ks + 1) / a.block_ks;
+            if (nb != cur_blk) {
+                __syncthreads();
+                build_lut<CB>(lut, a.params, n, active, a.nblk, nb, a.rot, r, g);
+                cur_blk = nb;
+            }
+        }
+        __syncthreads();
+    }
+
+    if (!active || n >= a.N) return;
+    const float br = a.bias ? a.bias[n] : 0.0f;
+    const float bi = a.bias ? a.bias[a.N + n] : 0.0f;
+    const int64_t ldy = 2 * a.N;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            int64_t m = m0 + i * 32 + acc_row(v, g);
+            if (m < a.M) {
+                store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
+                store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+            }
+        }
+    }
+}
+
+// Fused weight A_q [2N, 2K] from the native blob (same decode as the GEMM).
+template <int CB>
+__global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const float4* __restrict__ params,
+                                   int64_t N, int64_t K, int64_t KS, int64_t nblk, int64_t block_ks,
+                                   RotParams rot, float* __restrict__ out, int round_fp16) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * K) return;
+    int64_t n = i / K, k = i - n * K;
+    int64_t nt = n >> 5, rr = n & 31, ks = k >> 5, kk = k & 31;
+    int s = (int)(kk >> 4), gg = (int)((kk >> 3) & 1), e = (int)(kk & 7);
+    int b = gg * 16 + s * 8 + e;
+    uint32_t byte = codes[((nt * KS + ks) * 32 + rr) * 32 + b];
+    int64_t blk = ks / block_ks;
+    const float4* p = params + (n * nblk + blk) * 2;
+    float2 U = lut_entry<CB>(byte & 15u, p[0]);
+    float2 W = lut_entry<CB>(byte >> 4, p[1]);
+    if (rot.rotate) {
+        U = derotate(U, rot.cu, rot.su);
+        W = derotate(W, rot.cw, rot.sw);
+    }
+    float a11 = W.x + U.x, a12 = W.y - U.y, a21 = W.y + U.y, a22 = -W.x + U.x;
+    if (round_fp16) {
+        a11 = (float)(_Float16)a11;
+        a12 = (float)(_Float16)a12;
+        a21 = (float)(_Float16)a21;
+        a22 = (float)(_Float16)a22;
+    }
+    int64_t ld = 2 * K;
+    out[n * ld + k] = a11;
+    out[n * ld + K + k] = a12;
+    out[(N + n) * ld + k] = a21;
+    out[(N + n) * ld + K + k] = a22;
+}
+
+// ---------------------------------------------------------------------------
+// activation fake quantization (quant_i.py:438-455, applied at :546-551)
+// ---------------------------------------------------------------------------
+template <int XDT>
+__device__ __forceinline__ float load1(const void* base, int64_t off) {
+    if (XDT == RPFQ_F32) return reinterpret_cast<const float*>(base)[off];
+    if (XDT == RPFQ_F16) return (float)reinterpret_cast<const _Float16*>(base)[off];
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+}
+
+// One 256-thread workgroup per row; each half [0, K) and [K, 2K) gets its own
+// scale = qmax * (1 / max(max|x|, 1e-5)) and x_hat = clamp(rint(x scale)) / scale,
+// all in float32 (rint = round half to even, as torch.round).
+template <int XDT, int YDT>
+__global__ void __launch_bounds__(256) act_quant_kernel(const void* __restrict__ x, int64_t K, int bits,
+                                                        void* __restrict__ y) {
+    __shared__ float red[2][4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t base = row * 2 * K;
+    float mx[2] = {0.0f, 0.0f};
+    for (int h = 0; h < 2; ++h)
+        for (int64_t k = tid; k < K; k += 256) mx[h] = fmaxf(mx[h], fabsf(load1<XDT>(x, base + h * K + k)));
+    for (int h = 0; h < 2; ++h) {
+        float v = mx[h];
+        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+        if (lane == 0) red[h][wave] = v;
+    }
+    __syncthreads();
+    const float qmax = (float)((1 << (bits - 1)) - 1);
+    const float qmin = -(float)(1 << (bits - 1));
+    for (int h = 0; h < 2; ++h) {
+        float amax = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+        // torch evaluates `float(qmax) / tensor` as reciprocal(tensor) * qmax
+        float scale = (1.0f / fmaxf(amax, 1e-5f)) * qmax;
+        for (int64_t k = tid; k < K; k += 256) {
+            float q = rintf(load1<XDT>(x, base + h * K + k) * scale);
+            q = fminf(fmaxf(q, qmin), qmax);
+            store1<YDT>(y, base + h * K + k, q / scale);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline unsigned grid1d(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+hipError_t launch_unpack(const uint8_t* codes, int bits, int64_t rows, int64_t k, const uint16_t* gre,
+                         const uint16_t* gim, int64_t nblk, int64_t block, float* re, float* im,
+                         hipStream_t s) {
+    int64_t total = rows * k;
+    hipLaunchKernelGGL(unpack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, s, codes, bits, rows, k, gre,
+                       gim, nblk, block, re, im);
+    return hipGetLastError();
+}
+
+template <int BM, int XDT, int YDT, bool PB>
+static hipError_t phase_go(PhaseArgs& a, hipStream_t s) {
+    a.tiles_m = (int)((a.M + BM - 1) / BM);
+    a.tiles_n = (int)((a.N + 127) / 128);
+    hipLaunchKernelGGL((phase_linear_kernel<BM, XDT, YDT, PB>), dim3(a.tiles_m * a.tiles_n), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int XDT, int YDT>
+static hipError_t phase_pb(PhaseArgs& a, hipStream_t s) {
+    if (a.nblk > 1) return phase_go<64, XDT, YDT, true>(a, s);
+    return phase_go<64, XDT, YDT, false>(a, s);
+}
+
+template <int XDT>
+static hipError_t phase_y(PhaseArgs& a, int ydt, hipStream_t s) {
+    switch (ydt) {
+        case RPFQ_F32: return phase_pb<XDT, RPFQ_F32>(a, s);
+        case RPFQ_F16: return phase_pb<XDT, RPFQ_F16>(a, s);
+        default: return phase_pb<XDT, RPFQ_BF16>(a, s);
+    }
+}
+
+hipError_t launch_phase_linear(const void* xr, const void* xi, int xdt, int conj_x, int64_t M, int64_t K,
+                               const uint8_t* codes, const uint16_t* gre, const uint16_t* gim, int64_t nblk,
+                               int64_t block_ks, int64_t N, void* yr, void* yi, int ydt, hipStream_t s) {
+    PhaseArgs a;
+    a.xr = xr;
+    a.xi = xi;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.codes = codes;
+    a.gre = gre;
+    a.gim = gim;
+    a.nblk = nblk;
+    a.block_ks = block_ks;
+    a.xsign = conj_x ? 1.0f : -1.0f;
+    a.yr = yr;
+    a.yi = yi;
+    switch (xdt) {
+        case RPFQ_F32: return phase_y<RPFQ_F32>(a, ydt, s);
+        case RPFQ_F16: return phase_y<RPFQ_F16>(a, ydt, s);
+        default: return phase_y<RPFQ_BF16>(a, ydt, s);
+    }
+}
+
+hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const uint8_t* const* planes, int nplanes,
+                            const float* const* sre, const float* const* sim, void* packed, hipStream_t s) {
+    PackArgs a;
+    for (int p = 0; p < 4; ++p) {
+        a.planes[p] = p < nplanes ? planes[p] : nullptr;
+        a.sre[p] = p < nplanes ? sre[p] : nullptr;
+        a.sim[p] = (p < nplanes && sim) ? sim[p] : nullptr;
+    }
+    a.nplanes = nplanes;
+    a.stages = d.stages;
+    a.codebook = d.codebook;
+    a.N = g.N;
+    a.K = g.K;
+    a.NT = g.NT;
+    a.KS = g.KS;
+    a.nblk = g.nblk;
+    a.codes = reinterpret_cast<uint8_t*>(packed);
+    a.params = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) + g.codes_bytes);
+    int64_t nc = g.NT * g.KS * 1024;
+    hipLaunchKernelGGL(wide_pack_codes_kernel, dim3(grid1d(nc, 256)), dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    int64_t np = g.NT * 32 * g.nblk;
+    hipLaunchKernelGGL(wide_pack_params_kernel, dim3(grid1d(np, 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+static RotParams rot_of(const rpfq_wide_desc& d) {
+    RotParams r;
+    r.rotate = d.rotate;
+    r.cu = d.rot_u[0];
+    r.su = d.rot_u[1];
+    r.cw = d.rot_w[0];
+    r.sw = d.rot_w[1];
+    return r;
+}
+
+template <int BM, int XDT, int YDT, int CB>
+static hipError_t wide_go(WideArgs& a, hipStream_t s) {
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    constexpr int lds = wide_lds_bytes<BM>();
+    std::call_once(once, [] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_kernel<BM, XDT, YDT, CB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    a.tiles_m = (int)((a.M + BM - 1) / BM);
+    a.tiles_n = (int)((a.NT + 3) / 4);
+    hipLaunchKernelGGL((wide_linear_kernel<BM, XDT, YDT, CB>), dim3(a.tiles_m * a.tiles_n), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int XDT, int YDT, int CB>
+static hipError_t wide_bm(WideArgs& a, hipStream_t s) {
+    if (a.M <= 32) return wide_go<32, XDT, YDT, CB>(a, s);
+    if (a.M <= 64) return wide_go<64, XDT, YDT, CB>(a, s);
+    return wide_go<128, XDT, YDT, CB>(a, s);
+}
+
+template <int XDT, int CB>
+static hipError_t wide_y(WideArgs& a, int ydt, hipStream_t s) {
+    switch (ydt) {
+        case RPFQ_F32: return wide_bm<XDT, RPFQ_F32, CB>(a, s);
+        case RPFQ_F16: return wide_bm<XDT, RPFQ_F16, CB>(a, s);
+        default: return wide_bm<XDT, RPFQ_BF16, CB>(a, s);
+    }
+}
+
+template <int CB>
+static hipError_t wide_x(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return wide_y<RPFQ_F32, CB>(a, ydt, s);
+        case RPFQ_F16: return wide_y<RPFQ_F16, CB>(a, ydt, s);
+        default: return wide_y<RPFQ_BF16, CB>(a, ydt, s);
+    }
+}
+
+hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
+                              int xdt, int64_t M, const float* bias, void* y, int ydt, int flags, hipStream_t s) {
+    (void)flags;
+    WideArgs a;
+    a.x = x;
+    a.M = M;
+    a.K = g.K;
+    a.N = g.N;
+    a.NT = g.NT;
+    a.KS = g.KS;
+    a.nblk = g.nblk;
+    a.block_ks = g.block_ks;
+    a.codes = reinterpret_cast<const uint4*>(packed);
+    a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
+    a.rot = rot_of(d);
+    a.bias = bias;
+    a.y = y;
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, s);
+        case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, s);
+        default: return wide_x<RPFQ_CB_AXIS>(a, xdt, ydt, s);
+    }
+}
+
+template <int XDT>
+static hipError_t act_y(const void* x, int64_t M, int64_t K, int bits, void* y, int ydt, hipStream_t s) {
+    switch (ydt) {
+        case RPFQ_F32: hipLaunchKernelGGL((act_quant_kernel<XDT, RPFQ_F32>), dim3(M), dim3(256), 0, s, x, K, bits, y); break;
+        case RPFQ_F16: hipLaunchKernelGGL((act_quant_kernel<XDT, RPFQ_F16>), dim3(M), dim3(256), 0, s, x, K, bits, y); break;
+        default: hipLaunchKernelGGL((act_quant_kernel<XDT, RPFQ_BF16>), dim3(M), dim3(256), 0, s, x, K, bits, y); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return act_y<RPFQ_F32>(x, M, K, bits, y, ydt, s);
+        case RPFQ_F16: return act_y<RPFQ_F16>(x, M, K, bits, y, ydt, s);
+        default: return act_y<RPFQ_BF16>(x, M, K, bits, y, ydt, s);
+    }
+}
+
+hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, float* out,
+                              int round_fp16, hipStream_t s) {
+    const uint8_t* codes = reinterpret_cast<const uint8_t*>(packed);
+    const float4* params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
+    int64_t total = g.N * g.K;
+    RotParams rot = rot_of(d);
+    dim3 grid(grid1d(total, 256));
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN:
+            hipLaunchKernelGGL(wide_decode_kernel<RPFQ_CB_SIGN>, grid, dim3(256), 0, s, codes, params, g.N, g.K,
+                               g.KS, g.nblk, g.block_ks, rot, out, round_fp16);
+            break;
+        case RPFQ_CB_PSK16:
+            hipLaunchKernelGGL(wide_decode_kernel<RPFQ_CB_PSK16>, grid, dim3(256), 0, s, codes, params, g.N, g.K,
+                               g.KS, g.nblk, g.block_ks, rot, out, round_fp16);
+            break;
+        default:
+            hipLaunchKernelGGL(wide_decode_kernel<RPFQ_CB_AXIS>, grid, dim3(256), 0, s, codes, params, g.N, g.K,
+                               g.KS, g.nblk, g.block_ks, rot, out, round_fp16);
+            break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rpfq

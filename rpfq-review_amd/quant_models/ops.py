@@ -1,0 +1,200 @@
+"""Tensor-level entry points over the C ABI (include/rpfq.h).
+
+Every function here runs the HIP kernels of librpfq.so on device tensors and
+raises if the library is unavailable or a tensor is on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _native as N
+
+
+def unpack(codes: torch.Tensor, bits: int, k: int, gamma_re: torch.Tensor | None = None,
+           gamma_im: torch.Tensor | None = None, block: int = 0):
+    """Decode a packed plane [rows, k*bits/8] -> float32 (re, im) [rows, k].
+
+    With fp16 gammas the values are codebook / gamma, as
+    export_rpfq_vit_to_mlx.py:227-254 computes them (bit-exact)."""
+    N.require_device(codes, gamma_re, gamma_im)
+    if codes.dtype != torch.uint8 or not codes.is_contiguous():
+        raise TypeError("codes must be a contiguous uint8 tensor")
+    for g in (gamma_re, gamma_im):
+        if g is not None and (g.dtype != torch.float16 or not g.is_contiguous()):
+            raise TypeError("gammas must be contiguous float16 tensors")
+    rows = codes.shape[0]
+    re = torch.empty(rows, k, dtype=torch.float32, device=codes.device)
+    im = torch.empty_like(re)
+    lib = N.load()
+    N.check("rpfq_unpack", lib.rpfq_unpack(N.ptr(codes), bits, rows, k, N.ptr(gamma_re), N.ptr(gamma_im),
+                                          block, N.ptr(re), N.ptr(im), N.stream_of(codes)))
+    return re, im
+
+
+def phase_linear(xr: torch.Tensor, xi: torch.Tensor, codes: torch.Tensor, gamma_re: torch.Tensor,
+                 gamma_im: torch.Tensor, block: int = 0, conj_x: bool = True,
+                 out_dtype: torch.dtype = torch.float32):
+    """One packed plane, phaseLinearReference semantics
+    (RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:119-164).
+    conj_x=True computes W conj(x); False computes W x."""
+    N.require_device(xr, xi, codes, gamma_re, gamma_im)
+    if xr.shape != xi.shape or xr.dim() != 2:
+        raise ValueError("xr and xi must be equal 2-D planes")
+    if xr.dtype != xi.dtype:
+        raise TypeError("xr and xi must share a dtype")
+    xr, xi = xr.contiguous(), xi.contiguous()
+    m, k = xr.shape
+    n = codes.shape[0]
+    yr = torch.empty(m, n, dtype=out_dtype, device=xr.device)
+    yi = torch.empty_like(yr)
+    lib = N.load()
+    N.check("rpfq_phase_linear", lib.rpfq_phase_linear(
+        N.ptr(xr), N.ptr(xi), N.dtype_code(xr.dtype), int(bool(conj_x)), m, k, N.ptr(codes.contiguous()),
+        N.ptr(gamma_re.contiguous()), N.ptr(gamma_im.contiguous()), block, n, N.ptr(yr), N.ptr(yi),
+        N.dtype_code(out_dtype), N.stream_of(xr)))
+    return yr, yi
+
+
+def act_quant(x: torch.Tensor, num_bits: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Per-row, per-half symmetric fake quantization of [..., 2K'] features
+    (quant_i.py:438-455 applied at :546-551) on the device."""
+    N.require_device(x)
+    lead, f = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, f).contiguous()
+    y = torch.empty(x2.shape, dtype=out_dtype or x.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return y.reshape(*lead, f)
+    lib = N.load()
+    N.check("rpfq_act_quant", lib.rpfq_act_quant(
+        x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], f, int(num_bits), y.data_ptr(),
+        N.dtype_code(y.dtype), N.stream_of(x2)))
+    return y.reshape(*lead, f)
+
+
+@dataclass
+class PackedWide:
+    """One widely-linear layer in the MI355X tiled layout (a device blob).
+
+    n_complex / k_complex: N' = out/2, K' = in/2; codebook: _native.CB_*;
+    stages: residual stages per U/W; rotation: ((cos_u, sin_u), (cos_w, sin_w))
+    float32 values or None."""
+
+    n_complex: int
+    k_complex: int
+    codebook: int
+    stages: int
+    block: int
+    blob: torch.Tensor
+    rotation: tuple | None = None
+    desc: N.WideDesc = field(init=False, repr=False)
+
+    def __post_init__(self):
+        self.desc = make_desc(self.n_complex, self.k_complex, self.codebook, self.stages, self.block,
+                              self.rotation)
+
+    @property
+    def in_features(self) -> int:
+        return 2 * self.k_complex
+
+    @property
+    def out_features(self) -> int:
+        return 2 * self.n_complex
+
+    @classmethod
+    def from_planes(cls, planes, scale_re, scale_im, n_complex: int, k_complex: int, codebook: int = N.CB_AXIS,
+                    stages: int = 2, block: int = 0, rotation=None) -> "PackedWide":
+        """planes: packed code planes (u_s0[, u_s1], w_s0[, w_s1] or u, w for
+        PSK16) as uint8 device tensors; scale_re/scale_im: float32 [N', nblk]
+        multipliers per plane."""
+        dev = planes[0].device
+        N.require_device(*planes)
+        desc = make_desc(n_complex, k_complex, codebook, stages, block, rotation)
+        lib = N.load()
+        nbytes = lib.rpfq_wide_packed_bytes(ctypes.byref(desc))
+        if nbytes == 0:
+            N.check("rpfq_wide_packed_bytes", 2)
+        blob = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        planes = [p.contiguous() for p in planes]
+        sre = [s.contiguous().float() for s in scale_re]
+        sim = [s.contiguous().float() for s in (scale_im if scale_im is not None else scale_re)]
+        arr = ctypes.c_void_p * len(planes)
+        N.check("rpfq_wide_pack", lib.rpfq_wide_pack(
+            ctypes.byref(desc), arr(*[p.data_ptr() for p in planes]), len(planes),
+            arr(*[s.data_ptr() for s in sre]), arr(*[s.data_ptr() for s in sim]),
+            blob.data_ptr(), nbytes, N.stream_of(blob)))
+        # keep the sources alive until the pack kernels have consumed them
+        torch.cuda.current_stream(dev).synchronize()
+        return cls(n_complex, k_complex, codebook, stages, block, blob, rotation)
+
+    def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N']."""
+        N.require_device(x, bias)
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
+        if m == 0:
+            return y.reshape(*lead, self.out_features)
+        if bias is not None:
+            bias = bias.contiguous().float()
+        lib = N.load()
+        N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
+            N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), 0,
+            N.stream_of(x2)))
+        return y.reshape(*lead, self.out_features)
+
+    def decode(self, round_fp16: bool = False) -> torch.Tensor:
+        """Fused float32 weight A_q [2N', 2K'] (quant_i.py:534-544 layout)."""
+        a = torch.empty(self.out_features, self.in_features, dtype=torch.float32, device=self.blob.device)
+        lib = N.load()
+        N.check("rpfq_wide_decode", lib.rpfq_wide_decode(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), a.data_ptr(),
+            int(bool(round_fp16)), N.stream_of(self.blob)))
+        return a
+
+    @property
+    def code_bytes(self) -> int:
+        """Algorithmic bytes of the packed codes: 2*stages planes of 2 bits
+        (AXIS/SIGN) or 2 planes of 4 bits (PSK16) per complex element."""
+        bits = 8 if self.codebook == N.CB_PSK16 else 4 * self.stages
+        return self.n_complex * self.k_complex * bits // 8
+
+
+def make_desc(n_complex, k_complex, codebook, stages, block, rotation) -> N.WideDesc:
+    d = N.WideDesc()
+    d.n_complex = int(n_complex)
+    d.k_complex = int(k_complex)
+    d.block = int(block)
+    d.codebook = int(codebook)
+    d.stages = int(stages)
+    if rotation is not None:
+        (cu, su), (cw, sw) = rotation
+        d.rotate = 1
+        d.rot_u[0], d.rot_u[1] = float(cu), float(su)
+        d.rot_w[0], d.rot_w[1] = float(cw), float(sw)
+    else:
+        d.rotate = 0
+    return d
+
+
+def wide_flops(m: int, n_complex: int, k_complex: int) -> int:
+    """Algorithmic FLOPs of one widely-linear layer (one real GEMM)."""
+    return 2 * m * (2 * k_complex) * (2 * n_complex)
+
+
+def wide_bytes(m: int, n_complex: int, k_complex: int, act_bytes: int = 2, out_bytes: int = 2,
+               code_bits: int = 8, nscale: int = 8) -> int:
+    """Algorithmic HBM bytes: activations in/out, codes, per-row scales, bias."""
+    return (m * 2 * k_complex * act_bytes + m * 2 * n_complex * out_bytes
+            + math.ceil(n_complex * k_complex * code_bits / 8) + 4 * nscale * n_complex + 4 * 2 * n_complex)

@@ -1,0 +1,341 @@
+"""Complex phase-quantized linear layer, MI355X edition.
+
+Keeps the module API of RPFQ-ViT-main/quant_models/quant_i.py (class names,
+constructor signatures, attributes, state-dict keys and errors) so models and
+checkpoints written against the reference load unchanged:
+
+* ``QATLinearComplexPhase(quant_method_u, quant_method_w, enable_act_quant,
+  act_num_bits, enable_rotation, quant_group_size, *args, **kwargs)``
+  (quant_i.py:475-511), ``forward(x[..., in]) -> y[..., out]``;
+* ``ComplexWeightQuantizer`` / ``ComplexActivationQuantizer`` and the STE
+  autograd functions (quant_i.py:121-191, :374-472);
+* ``SUPPORTED_QUANT_METHODS`` (quant_i.py:355-362).
+
+Execution:
+* eval mode, device tensors -> the packed HIP path: the layer is packed once
+  (codes + scales, re-packed when the weight changes) and every call runs the
+  gfx950 kernels of librpfq.so through the C ABI.  There is no host fallback:
+  if the library is missing the call raises.
+* training mode (any device) or host tensors -> quantization-aware forward in
+  torch with straight-through gradients, the reference's training semantics.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import packing as P
+
+TensorPair = Tuple[torch.Tensor, torch.Tensor]
+EPS = 1e-6
+
+
+# ---------------------------------------------------------------------------
+# straight-through quantizers (training semantics)
+# ---------------------------------------------------------------------------
+def _axis_value(re, im):
+    st = P.axis_stage(re, im, P.TRAIN_MIN_SCALE)
+    return st.value_re, st.value_im
+
+
+def _sign_value(re, im):
+    st = P.sign_stage(re, im)
+    return st.value_re, st.value_im
+
+
+def _residual(re, im, steps, stage_fn):
+    q_re, q_im = torch.zeros_like(re), torch.zeros_like(im)
+    for _ in range(steps):
+        s_re, s_im = stage_fn(re, im)
+        q_re, q_im = q_re + s_re, q_im + s_im
+        re, im = re - s_re, im - s_im
+    return q_re, q_im
+
+
+def _ste(name: str, steps: int, stage_fn, doc: str):
+    """Autograd function: forward = quantizer, backward = identity."""
+
+    def forward(ctx, w_real, w_imag):
+        return _residual(w_real, w_imag, steps, stage_fn)
+
+    def backward(ctx, grad_real, grad_imag):
+        return grad_real, grad_imag
+
+    return type(name, (torch.autograd.Function,), {
+        "__doc__": doc, "forward": staticmethod(forward), "backward": staticmethod(backward)})
+
+
+PhaseQuantSTE = _ste("PhaseQuantSTE", 1, _axis_value, "2-bit axis quantization (quant_i.py:121-130).")
+PhaseQuantSTE_V2 = _ste("PhaseQuantSTE_V2", 2, _axis_value, "Two residual axis stages (quant_i.py:133-142).")
+PhaseQuantSTE_V3 = _ste("PhaseQuantSTE_V3", 3, _axis_value, "Three residual axis stages (quant_i.py:145-154).")
+PhaseQuantSTE_V4 = _ste("PhaseQuantSTE_V4", 4, _axis_value, "Four residual axis stages (quant_i.py:157-166).")
+NewPhaseQuantSTE = _ste("NewPhaseQuantSTE", 1, _sign_value, "Quadrant-sign quantization (quant_i.py:169-178).")
+NewPhaseQuantSTE_V2 = _ste("NewPhaseQuantSTE_V2", 2, _sign_value,
+                           "Two residual quadrant-sign stages (quant_i.py:181-190).")
+
+
+class LearnableGroupedPhaseQuant(nn.Module):
+    """Learnable grouped phase quantizer (quant_i.py:193-351): per group of
+    rows an optional rotation, nearest codeword of a learnable 4-phase
+    codebook by cosine similarity, a least-squares group magnitude, and one
+    residual quadrant-sign step; straight-through gradient for the weight."""
+
+    def __init__(self, n_rows: int, group_size: int = 32, n_codewords: int = 4, enable_rotation: bool = True,
+                 use_residual: bool = True, init_mode: str = "quadrant"):
+        super().__init__()
+        self.n_rows = n_rows
+        self.group_size = group_size
+        self.n_codewords = n_codewords
+        self.enable_rotation = enable_rotation
+        self.use_residual = use_residual
+        self.num_groups = math.ceil(n_rows / group_size)
+        if init_mode == "quadrant":
+            phases = [math.pi / 4, 3 * math.pi / 4, -3 * math.pi / 4, -math.pi / 4]
+        elif init_mode == "axis":
+            phases = [0.0, math.pi / 2, math.pi, -math.pi / 2]
+        else:
+            raise ValueError(f"Unsupported init_mode: {init_mode}")
+        init = torch.tensor(phases, dtype=torch.float32)
+        if n_codewords != 4:
+            init = torch.linspace(-math.pi, math.pi, steps=n_codewords + 1)[:-1]
+        self.phase_angles = nn.Parameter(init)
+        if enable_rotation:
+            self.rotation_angles = nn.Parameter(torch.zeros(self.num_groups, 1, 1))
+        else:
+            self.register_parameter("rotation_angles", None)
+
+    def forward(self, w_real: torch.Tensor, w_imag: torch.Tensor) -> TensorPair:
+        if w_real.shape != w_imag.shape:
+            raise ValueError("w_real and w_imag must have the same shape.")
+        rows, cols = w_real.shape
+        gs = self.group_size
+        pad = (gs - rows % gs) % gs
+        valid = w_real.new_ones(rows, 1)
+        wr, wi = w_real, w_imag
+        if pad:
+            wr, wi, valid = F.pad(wr, (0, 0, 0, pad)), F.pad(wi, (0, 0, 0, pad)), F.pad(valid, (0, 0, 0, pad))
+        groups = wr.shape[0] // gs
+        wr = wr.reshape(groups, gs, cols)
+        wi = wi.reshape(groups, gs, cols)
+        valid = valid.reshape(groups, gs, 1)
+        if self.enable_rotation:
+            c, s = torch.cos(self.rotation_angles), torch.sin(self.rotation_angles)
+            rr, ri = wr * c + wi * s, wi * c - wr * s
+        else:
+            rr, ri = wr, wi
+        inv = torch.rsqrt((rr.square() + ri.square()).clamp_min(EPS))
+        book = torch.stack((torch.cos(self.phase_angles), torch.sin(self.phase_angles)), dim=-1)
+        sim = (rr * inv).unsqueeze(-1) * book[:, 0].view(1, 1, 1, -1) + \
+              (ri * inv).unsqueeze(-1) * book[:, 1].view(1, 1, 1, -1)
+        chosen = book[sim.argmax(dim=-1)]
+        d_re, d_im = chosen[..., 0], chosen[..., 1]
+        num = ((rr * d_re + ri * d_im) * valid).sum(dim=(1, 2), keepdim=True)
+        den = (((d_re.square() + d_im.square()) * valid).sum(dim=(1, 2), keepdim=True)).clamp_min(EPS)
+        alpha = num / den
+        q_re, q_im = alpha * d_re, alpha * d_im
+        if self.use_residual:
+            e_re, e_im = rr - q_re, ri - q_im
+            count = (valid.sum(dim=(1, 2), keepdim=True) * e_re.shape[-1]).clamp_min(1.0)
+            b_re = (e_re.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
+            b_im = (e_im.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
+            q_re = q_re + b_re * torch.where(e_re >= 0, 1.0, -1.0).to(e_re.dtype)
+            q_im = q_im + b_im * torch.where(e_im >= 0, 1.0, -1.0).to(e_im.dtype)
+        if self.enable_rotation:
+            q_re, q_im = q_re * c - q_im * s, q_im * c + q_re * s
+        q_re = q_re.reshape(-1, cols)[:rows]
+        q_im = q_im.reshape(-1, cols)[:rows]
+        return q_re + (w_real - w_real.detach()), q_im + (w_imag - w_imag.detach())
+
+
+SUPPORTED_QUANT_METHODS = (
+    "complex_phase_v1",
+    "complex_phase_v2",
+    "complex_phase_v3",
+    "complex_phase_v4",
+    "complex_phase_new_v2",
+    "complex_phase_next_v1",
+)
+
+_FUNCTION_QUANTIZERS: Dict[str, type] = {
+    "complex_phase_v1": PhaseQuantSTE,
+    "complex_phase_v2": PhaseQuantSTE_V2,
+    "complex_phase_v3": PhaseQuantSTE_V3,
+    "complex_phase_v4": PhaseQuantSTE_V4,
+    "complex_phase_new_v2": NewPhaseQuantSTE_V2,
+}
+
+
+class ComplexWeightQuantizer(nn.Module):
+    """Quantizer of one complex plane (quant_i.py:374-435)."""
+
+    def __init__(self, quant_method: str = "complex_phase_v1", enable_rotation: bool = False,
+                 n_rows: int | None = None, group_size: int = 32):
+        super().__init__()
+        self.quant_method = quant_method
+        self.enable_rotation = enable_rotation
+        self.is_module_quantizer = quant_method == "complex_phase_next_v1"
+        if quant_method not in SUPPORTED_QUANT_METHODS:
+            raise ValueError(f"Unsupported quantization method: {quant_method}")
+        if self.is_module_quantizer:
+            if n_rows is None:
+                raise ValueError("complex_phase_next_v1 requires n_rows.")
+            self.quant_fn = LearnableGroupedPhaseQuant(n_rows=n_rows, group_size=group_size, n_codewords=4,
+                                                       enable_rotation=enable_rotation, use_residual=True,
+                                                       init_mode="quadrant")
+            self.register_parameter("rotation_angle", None)
+            return
+        self.quant_fn = _FUNCTION_QUANTIZERS[quant_method]
+        if enable_rotation:
+            self.rotation_angle = nn.Parameter(torch.zeros(1))
+        else:
+            self.register_parameter("rotation_angle", None)
+
+    def rotation_cos_sin(self):
+        """float32 (cos, sin) of the learned global rotation, or None."""
+        if self.is_module_quantizer or not self.enable_rotation:
+            return None
+        return torch.cos(self.rotation_angle).detach(), torch.sin(self.rotation_angle).detach()
+
+    def forward(self, w_real: torch.Tensor, w_imag: torch.Tensor) -> TensorPair:
+        if self.is_module_quantizer:
+            return self.quant_fn(w_real, w_imag)
+        if not self.enable_rotation:
+            return self.quant_fn.apply(w_real, w_imag)
+        c, s = torch.cos(self.rotation_angle), torch.sin(self.rotation_angle)
+        r_re, r_im = P.rotate_for_quant(w_real, w_imag, c, s)
+        q_re, q_im = self.quant_fn.apply(r_re, r_im)
+        return P.rotate_back(q_re, q_im, c, s)
+
+
+class ActivationQuantSTE(torch.autograd.Function):
+    """Per-row symmetric fake quantization of each half (quant_i.py:438-460):
+    scale = qmax / max(|x|, 1e-5), x_hat = clamp(round(x scale)) / scale,
+    round half to even."""
+
+    @staticmethod
+    def forward(ctx, x_real, x_imag, num_bits: int):
+        qmax = (1 << (num_bits - 1)) - 1
+        qmin = -(1 << (num_bits - 1))
+        out = []
+        for x in (x_real, x_imag):
+            scale = float(qmax) / x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-5)
+            out.append((x * scale).round().clamp(qmin, qmax) / scale)
+        return out[0], out[1]
+
+    @staticmethod
+    def backward(ctx, grad_real, grad_imag):
+        return grad_real, grad_imag, None
+
+
+class ComplexActivationQuantizer(nn.Module):
+    """Activation quantizer wrapper (quant_i.py:463-472)."""
+
+    def __init__(self, num_bits: int):
+        super().__init__()
+        self.num_bits = num_bits
+
+    def forward(self, x_real: torch.Tensor, x_imag: torch.Tensor) -> TensorPair:
+        return ActivationQuantSTE.apply(x_real, x_imag, self.num_bits)
+
+
+class QATLinearComplexPhase(nn.Linear):
+    """Complex-structured quantized linear layer (quant_i.py:475-554).
+
+    The weight [out, in] acts on features laid out [real half | imag half] as
+    the widely-linear map y = U x + W conj(x) + b with U and W quantized to
+    phase codes.  Eval-mode device tensors run the packed HIP kernels."""
+
+    def __init__(self, quant_method_u: str = "complex_phase_v1", quant_method_w: str = "complex_phase_v1",
+                 enable_act_quant: bool = True, act_num_bits: int = 4, enable_rotation: bool = False,
+                 quant_group_size: int = 32, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        if self.in_features % 2 != 0 or self.out_features % 2 != 0:
+            raise ValueError("Complex-phase QAT requires even in/out features.")
+        self.enable_act_quant = enable_act_quant
+        rows = self.out_features // 2
+        self.quantizer_u = ComplexWeightQuantizer(quant_method=quant_method_u, enable_rotation=enable_rotation,
+                                                  n_rows=rows, group_size=quant_group_size)
+        self.quantizer_w = ComplexWeightQuantizer(quant_method=quant_method_w, enable_rotation=enable_rotation,
+                                                  n_rows=rows, group_size=quant_group_size)
+        self.act_quantizer = ComplexActivationQuantizer(num_bits=act_num_bits) if enable_act_quant else None
+        # packed HIP state (not part of the state dict)
+        self.use_packed = True
+        self._packed = None
+        self._packed_key = None
+        self._override = None
+
+    # -- training-semantics forward (reference arithmetic, autograd STE) ----
+    def quantized_weight(self) -> torch.Tensor:
+        """A_q [out, in] as the reference forms it (quant_i.py:514-544)."""
+        u_re, u_im, w_re, w_im = P.split_blocks(self.weight)
+        uq_re, uq_im = self.quantizer_u(u_re, u_im)
+        wq_re, wq_im = self.quantizer_w(w_re, w_im)
+        return P.join_blocks(uq_re, uq_im, wq_re, wq_im)
+
+    def _qat_forward(self, x: torch.Tensor) -> torch.Tensor:
+        q_weight = self.quantized_weight()
+        if self.act_quantizer is not None:
+            h = self.in_features // 2
+            qr, qi = self.act_quantizer(x[..., :h], x[..., h:])
+            x = torch.cat((qr, qi), dim=-1)
+        return F.linear(x, q_weight, self.bias)
+
+    # -- packed HIP path ------------------------------------------------------
+    def load_packed(self, codes: "P.LayerCodes") -> None:
+        """Run this layer from externally supplied code planes and scales
+        (e.g. an exported bundle or the benchmark's synthetic codes) instead
+        of packing its own float32 weight."""
+        if codes.n_complex * 2 != self.out_features or codes.k_complex * 2 != self.in_features:
+            raise ValueError("packed codes do not match the layer shape")
+        self._override = codes
+        self._packed = None
+        self._packed_key = None
+
+    def packed(self, device: torch.device):
+        """The layer's PackedWide on `device`, packing on first use and again
+        whenever the float32 weight changed."""
+        from .ops import PackedWide
+
+        key = ("override", id(self._override)) if self._override is not None else \
+            (self.weight.data_ptr(), self.weight._version, self._rotation_version())
+        if self._packed is not None and self._packed_key == key and self._packed.blob.device == device:
+            return self._packed
+        if self._override is not None:
+            lc = self._override
+        else:
+            rot_u = self.quantizer_u.rotation_cos_sin()
+            rot_w = self.quantizer_w.rotation_cos_sin()
+            lc = P.quantize_layer(self.weight.detach().to(device), self.quantizer_u.quant_method,
+                                  self.quantizer_w.quant_method, rot_u, rot_w)
+        self._packed = PackedWide.from_planes([p.to(device) for p in lc.planes],
+                                              [s.to(device) for s in lc.scale_re],
+                                              [s.to(device) for s in lc.scale_im],
+                                              lc.n_complex, lc.k_complex, lc.codebook, lc.stages, lc.block,
+                                              lc.rotation)
+        self._packed_key = key
+        return self._packed
+
+    def _rotation_version(self):
+        vs = []
+        for q in (self.quantizer_u, self.quantizer_w):
+            if q.rotation_angle is not None:
+                vs.append((q.rotation_angle.data_ptr(), q.rotation_angle._version))
+        return tuple(vs)
+
+    def _packed_forward(self, x: torch.Tensor) -> torch.Tensor:
+        from . import ops
+
+        pw = self.packed(x.device)
+        if self.act_quantizer is not None:
+            x = ops.act_quant(x, self.act_quantizer.num_bits)
+        bias = None if self.bias is None else self.bias.detach()
+        return pw.linear(x, bias, out_dtype=x.dtype if x.dtype != torch.float32 else torch.float32)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda and not self.training and self.use_packed:
+            return self._packed_forward(x)
+        return self._qat_forward(x)

@@ -1,0 +1,282 @@
+"""GPU parity of the HIP kernels against the CPU oracle (through the C ABI).
+
+Bars: code unpacking, fused-weight decode and activation fake-quant are
+bit-exact; contractions are checked (a) tightly against the float64 oracle fed
+the very operands the MFMA consumes (fp16 inputs / fp16-rounded coefficients),
+and (b) against the exact reference weight within the rigorous fp16-rounding
+bound  |dy| <= 2^-11 * sum_k |x_k| |A_k| + 1e-5  written in each test.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import rpfq_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def qm():
+    from quant_models import _native, ops
+    return ops, _native
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def rand_gamma(r, rows, nblk, lo=0.01, hi=0.1):
+    """fp16 gammas = fp16(1/s), s ~ U(lo, hi) per (row, block)."""
+    s = r.uniform(lo, hi, size=(rows, nblk))
+    return (1.0 / s).astype(np.float16)
+
+
+def tdev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+# ---------------------------------------------------------------------------
+# unpack (export_rpfq_vit_to_mlx.py:227-254) -- bit-exact
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,k,block", [(7, 64, 32), (64, 768, 256), (3, 40, 0)])
+def test_unpack_axis_bit_exact(rows, k, block):
+    ops, _ = qm()
+    r = rng(1)
+    codes = r.integers(0, 4, size=(rows, k), dtype=np.uint8)
+    packed = O.pack_codes(codes)
+    nblk = 1 if block == 0 else -(-k // block)
+    g_re, g_im = rand_gamma(r, rows, nblk), rand_gamma(r, rows, nblk)
+    re, im = ops.unpack(tdev(packed), 2, k, tdev(g_re.view(np.float16)), tdev(g_im), block)
+    ref_re, ref_im = O.dequantize_axis(packed, g_re, g_im, rows, k, block if block else k)
+    assert np.array_equal(re.cpu().numpy(), ref_re)
+    assert np.array_equal(im.cpu().numpy(), ref_im)
+    # unit codebook
+    ure, uim = ops.unpack(tdev(packed), 2, k)
+    cb = O.AXIS_CODEBOOK[codes]
+    assert np.array_equal(ure.cpu().numpy(), cb[..., 0]) and np.array_equal(uim.cpu().numpy(), cb[..., 1])
+
+
+def test_unpack_all_byte_values():
+    """Every byte value 0..255 decodes to its four codes (brute force)."""
+    ops, _ = qm()
+    packed = np.arange(256, dtype=np.uint8).reshape(256, 1)
+    re, im = ops.unpack(tdev(packed), 2, 4)
+    codes = O.unpack_codes(packed)
+    cb = O.AXIS_CODEBOOK[codes]
+    assert np.array_equal(re.cpu().numpy(), cb[..., 0]) and np.array_equal(im.cpu().numpy(), cb[..., 1])
+
+
+def test_unpack_psk16_bit_exact():
+    ops, _ = qm()
+    r = rng(2)
+    codes = r.integers(0, 16, size=(9, 32), dtype=np.uint8)
+    packed = O.pack_codes4(codes)
+    re, im = ops.unpack(tdev(packed), 4, 32)
+    cb = O.psk16_codebook()[codes]
+    assert np.array_equal(re.cpu().numpy(), cb[..., 0]) and np.array_equal(im.cpu().numpy(), cb[..., 1])
+
+
+# ---------------------------------------------------------------------------
+# activation fake-quant (quant_i.py:438-455) -- bit-exact in float32
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_act_quant_bit_exact(bits, golden):
+    ops, _ = qm()
+    x = np.concatenate([golden["act_xr"], golden["act_xi"]], axis=1)
+    y = ops.act_quant(tdev(x), bits).cpu().numpy()
+    assert np.array_equal(y[:, :8], golden[f"act{bits}_re"])
+    assert np.array_equal(y[:, 8:], golden[f"act{bits}_im"])
+    r = rng(3)
+    xs = (r.standard_normal((37, 2 * 300)) * 3).astype(np.float32)
+    ys = ops.act_quant(tdev(xs), bits).cpu().numpy()
+    qr, qi = O.act_quant(xs[:, :300], xs[:, 300:], bits)
+    assert np.array_equal(ys, np.concatenate([qr, qi], axis=1))
+
+
+# ---------------------------------------------------------------------------
+# single plane phase linear (phase_linear.cpp:119-164)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,k,n,block,conj", [(1576, 768, 3072, 0, False), (33, 64, 200, 32, True),
+                                              (130, 256, 129, 64, False), (1, 512, 128, 256, True)])
+def test_phase_linear_f32_split(m, k, n, block, conj):
+    ops, _ = qm()
+    r = rng(10 + m)
+    xr = r.standard_normal((m, k)).astype(np.float32)
+    xi = r.standard_normal((m, k)).astype(np.float32)
+    codes = r.integers(0, 4, size=(n, k), dtype=np.uint8)
+    nblk = 1 if block == 0 else -(-k // block)
+    g_re, g_im = rand_gamma(r, n, nblk), rand_gamma(r, n, nblk)
+    yr, yi = ops.phase_linear(tdev(xr), tdev(xi), tdev(O.pack_codes(codes)), tdev(g_re), tdev(g_im),
+                              block, conj_x=conj)
+    bs = block if block else k
+    inv_re = np.repeat(O.inv_gamma(g_re), bs, axis=1)[:, :k]
+    inv_im = np.repeat(O.inv_gamma(g_im), bs, axis=1)[:, :k]
+    ref_re, ref_im = O.phase_linear(xr, xi, codes, inv_re, inv_im, conj_input=conj)
+    scale = max(np.abs(ref_re).max(), np.abs(ref_im).max())
+    # fp32 x split into two fp16 terms: relative error ~2^-22 per term
+    assert np.abs(yr.cpu().numpy() - ref_re).max() <= 2e-6 * scale + 1e-6
+    assert np.abs(yi.cpu().numpy() - ref_im).max() <= 2e-6 * scale + 1e-6
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_phase_linear_half_inputs(dt):
+    ops, _ = qm()
+    r = rng(20)
+    m, k, n = 70, 96, 160
+    xr = torch.from_numpy(r.standard_normal((m, k)).astype(np.float32)).to(dt)
+    xi = torch.from_numpy(r.standard_normal((m, k)).astype(np.float32)).to(dt)
+    codes = r.integers(0, 4, size=(n, k), dtype=np.uint8)
+    g_re, g_im = rand_gamma(r, n, 1), rand_gamma(r, n, 1)
+    yr, yi = ops.phase_linear(xr.to(DEV), xi.to(DEV), tdev(O.pack_codes(codes)), tdev(g_re), tdev(g_im), 0)
+    ref_re, ref_im = O.phase_linear(xr.float().numpy(), xi.float().numpy(), codes, O.inv_gamma(g_re)[:, 0],
+                                    O.inv_gamma(g_im)[:, 0], conj_input=True)
+    scale = max(np.abs(ref_re).max(), np.abs(ref_im).max())
+    assert np.abs(yr.cpu().numpy() - ref_re).max() <= 2e-6 * scale + 1e-6
+    assert np.abs(yi.cpu().numpy() - ref_im).max() <= 2e-6 * scale + 1e-6
+
+
+# ---------------------------------------------------------------------------
+# widely-linear layer: pack -> decode (bit-exact) -> GEMM
+# ---------------------------------------------------------------------------
+def make_wide(r, n_c, k_c, codebook="axis", stages=2, per_row=True, block=0):
+    """Random planes + per-(plane,row[,block]) scales in the oracle format."""
+    _, N = qm()
+    nplanes = 2 if codebook == "psk16" else 2 * stages
+    nblk = 1 if block == 0 else -(-k_c // block)
+    planes_np, sre, sim, packed = [], [], [], []
+    for p in range(nplanes):
+        if codebook == "psk16":
+            c = r.integers(0, 16, size=(n_c, k_c), dtype=np.uint8)
+            packed.append(O.pack_codes4(c))
+        else:
+            c = r.integers(0, 4, size=(n_c, k_c), dtype=np.uint8)
+            packed.append(O.pack_codes(c))
+        s1 = r.uniform(0.01, 0.1, size=(n_c, nblk)).astype(np.float32)
+        s2 = r.uniform(0.01, 0.1, size=(n_c, nblk)).astype(np.float32)
+        if not per_row:
+            s1[:] = s1[0, 0]
+            s2[:] = s2[0, 0]
+        planes_np.append(c)
+        sre.append(s1)
+        sim.append(s2)
+    kinds = (["u"] * (nplanes // 2)) + (["w"] * (nplanes // 2))
+    cb = {"axis": N.CB_AXIS, "sign": N.CB_SIGN, "psk16": N.CB_PSK16}[codebook]
+    return planes_np, packed, sre, sim, kinds, cb, nblk
+
+
+def oracle_planes(planes_np, sre, sim, kinds, k_c, block):
+    """Expand per-block scales to per-element for the oracle."""
+    out = []
+    bs = block if block else k_c
+    for c, a, b, kind in zip(planes_np, sre, sim, kinds):
+        out.append((c, np.repeat(a, bs, axis=1)[:, :k_c], np.repeat(b, bs, axis=1)[:, :k_c], kind))
+    return out
+
+
+def expand_scales(planes):
+    """oracle.wide_weight takes per-row or per-element scales."""
+    return planes
+
+
+CASES = [
+    # n_c, k_c, codebook, stages, block, rotation
+    (96, 64, "axis", 2, 0, None),
+    (1536, 384, "axis", 2, 0, None),
+    (50, 48, "axis", 2, 0, None),          # N' and K' not multiples of 32
+    (64, 96, "axis", 1, 0, None),          # v1
+    (130, 512, "axis", 2, 256, None),      # per-(row, block) scales
+    (64, 64, "sign", 2, 0, None),          # new_v2
+    (96, 128, "psk16", 1, 0, None),        # 16-PSK
+    (128, 96, "axis", 2, 0, ((0.95533645, 0.29552022), (0.98006660, -0.19866933))),  # rotation
+]
+
+
+def build_packed(r, case):
+    ops, N = qm()
+    n_c, k_c, codebook, stages, block, rot = case
+    planes_np, packed, sre, sim, kinds, cb, nblk = make_wide(r, n_c, k_c, codebook, stages, True, block)
+    pw = ops.PackedWide.from_planes([tdev(p) for p in packed], [tdev(s) for s in sre], [tdev(s) for s in sim],
+                                    n_c, k_c, cb, stages, block, rot)
+    rotation = None
+    if rot is not None:
+        rotation = tuple((np.float32(c), np.float32(s)) for c, s in rot)
+    oplanes = oracle_planes(planes_np, sre, sim, kinds, k_c, block)
+    a_ref = O.wide_weight(oplanes, codebook, rotation)
+    return pw, oplanes, a_ref, codebook, rotation
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
+                                             for c in CASES])
+def test_wide_decode_bit_exact(case):
+    r = rng(100)
+    pw, _, a_ref, _, _ = build_packed(r, case)
+    a = pw.decode().cpu().numpy()
+    assert a.shape == a_ref.shape
+    assert np.array_equal(a, a_ref)
+    a16 = pw.decode(round_fp16=True).cpu().numpy()
+    assert np.array_equal(a16, a_ref.astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("m", [1, 5, 31, 64, 65, 300])
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
+                                             for c in CASES])
+def test_wide_linear(case, m):
+    r = rng(200 + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    k_in = 2 * case[1]
+    x = torch.from_numpy(r.standard_normal((m, k_in)).astype(np.float32)).to(torch.float16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    # (a) tight: the exact product of the operands the MFMA sees
+    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T + bias
+    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T + np.abs(bias)
+    assert np.all(np.abs(y - y16) <= 1e-5 * scale + 1e-5)
+    # (b) against the exact reference weight: fp16 coefficient rounding bound
+    yex = xf @ a_ref.astype(np.float64).T + bias
+    assert np.all(np.abs(y - yex) <= 2.0 ** -11 * scale + 1e-5)
+
+
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
+def test_wide_linear_dtypes(xdt, ydt):
+    r = rng(300)
+    case = (160, 128, "axis", 2, 0, None)
+    pw, oplanes, a_ref, _, _ = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((77, 256)).astype(np.float32)).to(xdt)
+    y = pw.linear(x.to(DEV), None, out_dtype=ydt).float().cpu().numpy()
+    # the kernel converts x to fp16 on load: reference on the same operands
+    xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
+    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T
+    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T
+    out_ulp = {torch.float32: 1e-6, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
+    assert np.all(np.abs(y - y16) <= 1e-5 * scale + out_ulp * np.abs(y16) + 1e-5)
+
+
+def test_wide_linear_matches_reference_android_runtime():
+    """Same packed planes through the compiled reference (oracle/_ref,
+    wideLinearReference) and through the HIP kernel."""
+    ref = pytest.importorskip("oracle.ref_lib")
+    lib = ref.load()
+    if lib is None:
+        pytest.skip("oracle/_ref not built")
+    r = rng(400)
+    n_c, k_c = 64, 256
+    planes = [r.integers(0, 4, size=(n_c, k_c), dtype=np.uint8) for _ in range(4)]
+    g_re = [rand_gamma(r, n_c, 1) for _ in range(4)]
+    g_im = [rand_gamma(r, n_c, 1) for _ in range(4)]
+    bias = r.standard_normal(2 * n_c).astype(np.float32)
+    x = torch.from_numpy(r.standard_normal((9, 2 * k_c)).astype(np.float32)).to(torch.float16)
+    xf = x.float().numpy()
+    y_ref = ref.wide_linear(xf, planes, g_re, g_im, bias, block=k_c, mode=0)
+    ops, N = qm()
+    inv_re = [tdev(O.inv_gamma(g)) for g in g_re]
+    inv_im = [tdev(O.inv_gamma(g)) for g in g_im]
+    pw = ops.PackedWide.from_planes([tdev(O.pack_codes(p)) for p in planes], inv_re, inv_im, n_c, k_c,
+                                    N.CB_AXIS, 2, 0, None)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
+    a = O.wide_weight([(p, O.inv_gamma(gr)[:, 0], O.inv_gamma(gi)[:, 0], kd) for p, gr, gi, kd in
+                       zip(planes, g_re, g_im, "uuww")])
+    scale = np.abs(xf.astype(np.float64)) @ np.abs(a.astype(np.float64)).T + np.abs(bias)
+    assert np.all(np.abs(y - y_ref) <= 2.0 ** -11 * scale + 1e-4)
