@@ -395,8 +395,8 @@ __global__ void wide_pack_codes_kernel(PackArgs a) {
     int64_t t = idx >> 10;
     int64_t ks = t % a.KS, nt = t / a.KS;
     int64_t n = nt * 32 + rr;
-    int gg = b >> 4, s = (b >> 3) & 1, e = b & 7;
-    int64_t k = ks * 32 + 16 * s + 8 * gg + e;
+    int gg = b >> 4, s = (b >> 2) & 3, e = b & 3;
+    int64_t k = ks * 32 + 8 * s + 4 * gg + e;
     uint32_t out = 0;
     if (n < a.N && k < a.K) {
         if (a.codebook == RPFQ_CB_PSK16) {
@@ -455,28 +455,36 @@ __global__ void wide_pack_params_kernel(PackArgs a) {
 // ---------------------------------------------------------------------------
 struct WideArgs {
     const void* x;
-    int64_t M, K, N, NT, KS, nblk, block_ks;
+    int64_t M;
+    int K, N, NT, KS, nblk, block_ks;
     const uint4* codes;
     const float4* params;
     RotParams rot;
     const float* bias;
     void* y;
     int tiles_m, tiles_n;
+    int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
 };
 
-constexpr int kXRow = 144;              // LDS bytes per activation row (+16 pad)
-constexpr int kLutWave = 32 * 32 * 8;   // 32 entries x 32 rows x float2
+// LDS activation row: 32 complex columns as (re, im) fp16 pairs = 128 B,
+// padded to 144 B so the 8 lanes of a 128-bit read hit distinct banks.
+constexpr int kXRow = 144;
+constexpr int kLutWave = 32 * 32 * 8;  // 32 entries x 32 rows x float2
+
+constexpr int kTRow = 64 * 2 + 16;     // epilogue tile row: 64 fp16 outputs (+16 pad)
 
 template <int BM>
 constexpr int wide_lds_bytes() {
-    return 2 * BM * kXRow + 4 * kLutWave;
+    return (2 * BM * kXRow + 4 * kLutWave) > (4 * BM * kTRow) ? (2 * BM * kXRow + 4 * kLutWave)
+                                                               : (4 * BM * kTRow);
 }
 
 // Builds the wave's LUT for scale block `blk`: entries 0..15 hold U(idx),
-// 16..31 hold W(idx), each for the wave's 32 rows; layout [entry][row].
+// 16..31 hold W(idx), each for the wave's 32 rows; layout [entry][row] so the
+// 32 lanes of a lookup touch 32 consecutive float2 (no bank conflicts).
 template <int CB>
-__device__ __forceinline__ void build_lut(float2* lut, const float4* params, int64_t n, bool active,
-                                          int64_t nblk, int64_t blk, const RotParams& rot, int r, int g) {
+__device__ __forceinline__ void build_lut(float2* lut, const float4* params, int64_t n, bool active, int nblk,
+                                          int blk, const RotParams& rot, int r, int g) {
     float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
     if (active) {
         const float4* p = params + (n * nblk + blk) * 2;
@@ -497,65 +505,130 @@ __device__ __forceinline__ void build_lut(float2* lut, const float4* params, int
     }
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed fp16 pair (one v_cvt_pk_f16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+    half2v h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// 8 consecutive activations -> 8 floats (bf16 / f32 sources).
+template <int XDT>
+__device__ __forceinline__ void load8_f32(const void* base, int64_t off, float* v) {
+    if (XDT == RPFQ_BF16) {
+        uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+            v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        }
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+}
+
+// Widely-linear GEMM.  Workgroup = 4 waves; tile = BM rows of x times 128
+// complex output rows (wave w owns complex rows 32w..32w+31 and produces both
+// their real and imaginary outputs).  Per k-step of 32 complex columns:
+//   * activations: BM x 32 (re, im) pairs staged to LDS (double buffered);
+//   * codes: one 128-bit load per lane (16 elements, one byte each);
+//   * decode: byte -> U, W from the wave's LUT (fp32), fused coefficients
+//     (A11,A12) and (A21,A22) formed in fp32 as the reference does and packed
+//     to fp16 pairs that are directly the MFMA B operands (k order re, im);
+//   * 2 x MB v_mfma_f32_32x32x16_f16 per 8 complex columns.
 template <int BM, int XDT, int YDT, int CB>
-__global__ void __launch_bounds__(256) wide_linear_kernel(WideArgs a) {
+__global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int MB = BM / 32;
     constexpr int XSTAGE = BM * kXRow;
-    constexpr int CPT = BM / 32;  // 16-byte activation chunks per thread
+    constexpr int CPT = BM >= 64 ? BM / 64 : 1;  // (row, 8-column) chunks per thread per k-step
+    constexpr int NCHUNK = BM * 4;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 31, g = lane >> 5;
     const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
     const int64_t m0 = (int64_t)mt * BM;
-    const int64_t ntw = (int64_t)ntl * 4 + wave;  // this wave's 32-row tile
+    const int ntw = ntl * 4 + wave;  // this wave's 32-row tile
     const bool active = ntw < a.NT;
-    const int64_t n = ntw * 32 + r;
+    const int64_t n = (int64_t)ntw * 32 + r;
     float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
-    const int64_t ldx = 2 * a.K;
+    const int64_t ldx = 2 * (int64_t)a.K;
 
-    uint4 xreg[CPT];
+    uint4 xreg[CPT][2];
     uint4 creg = make_uint4(0, 0, 0, 0);
 
-    auto load_x = [&](int64_t ks) {
+    // chunk c = tid + 256 j: row c >> 2, columns 8 (c & 3) .. +7 of the k-step
+    auto load_x = [&](int ks) {
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            int c = tid + 256 * j;
-            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
-            int64_t m = m0 + row;
-            int64_t kk = ks * 32 + sub * 8;
-            if (m < a.M && kk < a.K)
-                xreg[j] = load8_f16<XDT>(a.x, m * ldx + part * a.K + kk);
-            else
-                xreg[j] = make_uint4(0, 0, 0, 0);
+            const int c = tid + 256 * j;
+            const int row = c >> 2, sub = c & 3;
+            const int64_t m = m0 + row;
+            const int kk = ks * 32 + sub * 8;
+            uint4 o0 = make_uint4(0, 0, 0, 0), o1 = make_uint4(0, 0, 0, 0);
+            if (c < NCHUNK && m < a.M && kk < a.K) {
+                const int64_t off = m * ldx + kk;
+                if (XDT == RPFQ_F16) {
+                    const uint4 vr = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off);
+                    const uint4 vi =
+                        *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off + a.K);
+                    // interleave (re, im) halves: perm selects bytes of (vi, vr)
+                    o0.x = __builtin_amdgcn_perm(vi.x, vr.x, 0x05040100u);
+                    o0.y = __builtin_amdgcn_perm(vi.x, vr.x, 0x07060302u);
+                    o0.z = __builtin_amdgcn_perm(vi.y, vr.y, 0x05040100u);
+                    o0.w = __builtin_amdgcn_perm(vi.y, vr.y, 0x07060302u);
+                    o1.x = __builtin_amdgcn_perm(vi.z, vr.z, 0x05040100u);
+                    o1.y = __builtin_amdgcn_perm(vi.z, vr.z, 0x07060302u);
+                    o1.z = __builtin_amdgcn_perm(vi.w, vr.w, 0x05040100u);
+                    o1.w = __builtin_amdgcn_perm(vi.w, vr.w, 0x07060302u);
+                } else {
+                    float fr[8], fi[8];
+                    load8_f32<XDT>(a.x, off, fr);
+                    load8_f32<XDT>(a.x, off + a.K, fi);
+                    o0 = make_uint4(cvt_pk(fr[0], fi[0]), cvt_pk(fr[1], fi[1]), cvt_pk(fr[2], fi[2]),
+                                    cvt_pk(fr[3], fi[3]));
+                    o1 = make_uint4(cvt_pk(fr[4], fi[4]), cvt_pk(fr[5], fi[5]), cvt_pk(fr[6], fi[6]),
+                                    cvt_pk(fr[7], fi[7]));
+                }
+            }
+            xreg[j][0] = o0;
+            xreg[j][1] = o1;
         }
     };
     auto store_x = [&](int stage) {
         char* xs = smem + stage * XSTAGE;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            int c = tid + 256 * j;
-            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
-            *reinterpret_cast<uint4*>(xs + row * kXRow + part * 64 + sub * 16) = xreg[j];
+            const int c = tid + 256 * j;
+            if (c >= NCHUNK) break;
+            const int row = c >> 2, sub = c & 3;
+            uint4* dst = reinterpret_cast<uint4*>(xs + row * kXRow + sub * 32);
+            dst[0] = xreg[j][0];
+            dst[1] = xreg[j][1];
         }
     };
-    auto load_codes = [&](int64_t ks) {
-        if (active) creg = a.codes[((ntw * a.KS + ks) * 32 + r) * 2 + g];
+    auto load_codes = [&](int ks) {
+        if (active) creg = a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g];
     };
 
     floatx16 acc_re[MB], acc_im[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
-    int64_t cur_blk = 0;
+    int cur_blk = 0;
     build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
     load_x(0);
     load_codes(0);
     store_x(0);
     __syncthreads();
 
-    for (int64_t ks = 0; ks < a.KS; ++ks) {
+    for (int ks = 0; ks < a.KS; ++ks) {
         const uint4 cw = creg;
         const bool more = ks + 1 < a.KS;
         if (more) {
@@ -564,37 +637,30 @@ __global__ void __launch_bounds__(256) wide_linear_kernel(WideArgs a) {
         }
         const char* xs = smem + (ks & 1) * XSTAGE;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const uint32_t w0 = s ? cw.z : cw.x;
-            const uint32_t w1 = s ? cw.w : cw.y;
-            float a11[8], a12[8], a21[8], a22[8];
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t word = s == 0 ? cw.x : s == 1 ? cw.y : s == 2 ? cw.z : cw.w;
+            uint32_t bre[4], bim[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint32_t byte = ((e < 4 ? w0 : w1) >> (8 * (e & 3))) & 0xffu;
-                float2 U = lut[(byte & 15u) * 32 + r];
-                float2 W = lut[(16u + (byte >> 4)) * 32 + r];
-                // quant_i.py:534-537
-                a11[e] = W.x + U.x;
-                a12[e] = W.y - U.y;
-                a21[e] = W.y + U.y;
-                a22[e] = -W.x + U.x;
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t byte = (word >> (8 * e)) & 0xffu;
+                const float2 U = lut[(byte & 15u) * 32 + r];
+                const float2 W = lut[(16u + (byte >> 4)) * 32 + r];
+                // fused coefficients in the reference's order (quant_i.py:534-537)
+                bre[e] = cvt_pk(W.x + U.x, W.y - U.y);   // (A11, A12)
+                bim[e] = cvt_pk(W.y + U.y, -W.x + U.x);  // (A21, A22)
             }
-            const half8 b11 = to_half8(a11), b12 = to_half8(a12);
-            const half8 b21 = to_half8(a21), b22 = to_half8(a22);
+            const half8 b_re = as_half8(make_uint4(bre[0], bre[1], bre[2], bre[3]));
+            const half8 b_im = as_half8(make_uint4(bim[0], bim[1], bim[2], bim[3]));
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
-                const char* rp = xs + (i * 32 + r) * kXRow + (16 * s + 8 * g) * 2;
-                const half8 axr = *reinterpret_cast<const half8*>(rp);
-                const half8 axi = *reinterpret_cast<const half8*>(rp + 64);
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, b11, acc_re[i], 0, 0, 0);
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, b12, acc_re[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, b21, acc_im[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, b22, acc_im[i], 0, 0, 0);
+                const half8 ax = *reinterpret_cast<const half8*>(xs + (i * 32 + r) * kXRow + (8 * s + 4 * g) * 4);
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, b_re, acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, b_im, acc_im[i], 0, 0, 0);
             }
         }
         if (more) {
             store_x((ks + 1) & 1);
-            const int64_t nb = (ks + 1) / a.block_ks;
+            const int nb = (ks + 1) / a.block_ks;
             if (nb != cur_blk) {
                 __syncthreads();
                 build_lut<CB>(lut, a.params, n, active, a.nblk, nb, a.rot, r, g);
@@ -604,19 +670,66 @@ __global__ void __launch_bounds__(256) wide_linear_kernel(WideArgs a) {
         __syncthreads();
     }
 
-    if (!active || n >= a.N) return;
-    const float br = a.bias ? a.bias[n] : 0.0f;
-    const float bi = a.bias ? a.bias[a.N + n] : 0.0f;
-    const int64_t ldy = 2 * a.N;
+    const bool n_ok = active && n < a.N;
+    const float br = (a.bias && n_ok) ? a.bias[n] : 0.0f;
+    const float bi = (a.bias && n_ok) ? a.bias[a.N + n] : 0.0f;
+    const int64_t ldy = 2 * (int64_t)a.N;
+    if (YDT == RPFQ_F32) {
+        if (!n_ok) return;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t m = m0 + i * 32 + acc_row(v, g);
+                if (m < a.M) {
+                    store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
+                    store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+                }
+            }
+        }
+        return;
+    }
+    // 16-bit outputs: transpose the wave's [BM x 64] tile through LDS (the
+    // staging buffers are free after the final barrier) and write 16-byte
+    // chunks: per row, 32 real then 32 imaginary outputs of this wave.
+    constexpr int TROW = kTRow;
+    uint16_t* tt = reinterpret_cast<uint16_t*>(smem + wave * (BM * TROW));
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            int64_t m = m0 + i * 32 + acc_row(v, g);
-            if (m < a.M) {
-                store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
-                store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+            const int row = i * 32 + acc_row(v, g);
+            uint16_t hr, hi;
+            if (YDT == RPFQ_F16) {
+                hr = __builtin_bit_cast(uint16_t, (_Float16)(acc_re[i][v] + br));
+                hi = __builtin_bit_cast(uint16_t, (_Float16)(acc_im[i][v] + bi));
+            } else {
+                hr = f32_to_bf16(acc_re[i][v] + br);
+                hi = f32_to_bf16(acc_im[i][v] + bi);
             }
+            tt[row * (TROW / 2) + r] = hr;
+            tt[row * (TROW / 2) + 32 + r] = hi;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_wave_barrier();
+    if (!active) return;
+    const int64_t nbase = (int64_t)ntw * 32;
+    // lane -> (row offset lane >> 3, 16-byte chunk q = lane & 7): chunks 0-3 real, 4-7 imaginary
+    const int q = lane & 7;
+    const int64_t col0 = (q < 4 ? 0 : a.N) + nbase + 8 * (q & 3);
+    const int64_t nfirst = nbase + 8 * (q & 3);
+#pragma unroll 4
+    for (int row = lane >> 3; row < BM; row += 8) {
+        const int64_t m = m0 + row;
+        if (m >= a.M) break;
+        const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tt) + row * TROW + q * 16);
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
+        if (a.vec_store && nfirst + 8 <= a.N) {
+            *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+            for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = h[t];
         }
     }
 }
@@ -630,8 +743,8 @@ __global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const floa
     if (i >= N * K) return;
     int64_t n = i / K, k = i - n * K;
     int64_t nt = n >> 5, rr = n & 31, ks = k >> 5, kk = k & 31;
-    int s = (int)(kk >> 4), gg = (int)((kk >> 3) & 1), e = (int)(kk & 7);
-    int b = gg * 16 + s * 8 + e;
+    int s = (int)(kk >> 3), gg = (int)((kk >> 2) & 1), e = (int)(kk & 3);
+    int b = gg * 16 + s * 4 + e;
     uint32_t byte = codes[((nt * KS + ks) * 32 + rr) * 32 + b];
     int64_t blk = ks / block_ks;
     const float4* p = params + (n * nblk + blk) * 2;
@@ -843,17 +956,18 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     WideArgs a;
     a.x = x;
     a.M = M;
-    a.K = g.K;
-    a.N = g.N;
-    a.NT = g.NT;
-    a.KS = g.KS;
-    a.nblk = g.nblk;
-    a.block_ks = g.block_ks;
+    a.K = (int)g.K;
+    a.N = (int)g.N;
+    a.NT = (int)g.NT;
+    a.KS = (int)g.KS;
+    a.nblk = (int)g.nblk;
+    a.block_ks = (int)g.block_ks;
     a.codes = reinterpret_cast<const uint4*>(packed);
     a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
     a.rot = rot_of(d);
     a.bias = bias;
     a.y = y;
+    a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
     switch (d.codebook) {
         case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, s);
         case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, s);

@@ -13,6 +13,16 @@ import torch
 
 from . import _native as N
 
+# Optional per-launch timing hook: when set, PackedWide.linear records HIP
+# events around each wide-linear launch on the launch stream and hands
+# (start_event, end_event, flops, algorithmic_bytes, shape) to the recorder.
+_launch_recorder = None
+
+
+def set_launch_recorder(recorder) -> None:
+    global _launch_recorder
+    _launch_recorder = recorder
+
 
 def unpack(codes: torch.Tensor, bits: int, k: int, gamma_re: torch.Tensor | None = None,
            gamma_im: torch.Tensor | None = None, block: int = 0):
@@ -148,10 +158,21 @@ class PackedWide:
         if bias is not None:
             bias = bias.contiguous().float()
         lib = N.load()
+        rec = _launch_recorder
+        if rec is not None:
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
         N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
             ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
             N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), 0,
             N.stream_of(x2)))
+        if rec is not None:
+            ev1.record()
+            rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex),
+                wide_bytes(m, self.n_complex, self.k_complex, x2.element_size(), y.element_size(),
+                           self.code_bytes * 8 // max(1, self.n_complex * self.k_complex)),
+                (m, self.n_complex, self.k_complex))
         return y.reshape(*lead, self.out_features)
 
     def decode(self, round_fp16: bool = False) -> torch.Tensor:

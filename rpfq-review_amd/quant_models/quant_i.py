@@ -333,7 +333,7 @@ class QATLinearComplexPhase(nn.Linear):
         if self.act_quantizer is not None:
             x = ops.act_quant(x, self.act_quantizer.num_bits)
         bias = None if self.bias is None else self.bias.detach()
-        return pw.linear(x, bias, out_dtype=x.dtype if x.dtype != torch.float32 else torch.float32)
+        return pw.linear(x, bias, out_dtype=x.dtype)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda and not self.training and self.use_packed:

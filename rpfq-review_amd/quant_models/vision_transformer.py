@@ -1,0 +1,200 @@
+"""ViT and distilled-DeiT backbones with timm's module layout.
+
+The reference builds on timm's VisionTransformer / VisionTransformerDistilled
+(RPFQ-ViT-main/quant_models/quant_rpfq_vit.py:8, quant_rpfq_deit.py:8).  timm
+is unavailable offline, so these backbones are written here with the same
+submodule names (patch_embed.proj, cls_token, pos_embed, blocks.i.norm1,
+attn.qkv, attn.proj, norm2, mlp.fc1, mlp.fc2, norm, head[, dist_token,
+head_dist]) so the reference's checkpoints load by state-dict key, and with
+the forward semantics the reference's parity audit spells out
+(RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:518-558):
+norm1 -> qkv -> SDPA -> proj -> +res -> norm2 -> fc1 -> GELU(erf) -> fc2 -> +res.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+def _trunc_normal_(t: torch.Tensor, std: float = 0.02) -> torch.Tensor:
+    with torch.no_grad():
+        return nn.init.trunc_normal_(t, std=std, a=-2 * std, b=2 * std)
+
+
+class PatchEmbed(nn.Module):
+    def __init__(self, img_size=224, patch_size=16, in_chans=3, embed_dim=768, norm_layer=None, flatten=True):
+        super().__init__()
+        self.img_size = (img_size, img_size)
+        self.patch_size = (patch_size, patch_size)
+        self.grid_size = (img_size // patch_size, img_size // patch_size)
+        self.num_patches = self.grid_size[0] * self.grid_size[1]
+        self.flatten = flatten
+        self.proj = nn.Conv2d(in_chans, embed_dim, kernel_size=patch_size, stride=patch_size)
+        self.norm = norm_layer(embed_dim) if norm_layer else nn.Identity()
+
+    def forward(self, x):
+        x = self.proj(x)
+        if self.flatten:
+            x = x.flatten(2).transpose(1, 2)  # B, N, C
+        else:
+            x = x.permute(0, 2, 3, 1)  # B, H, W, C
+        return self.norm(x)
+
+
+class Mlp(nn.Module):
+    def __init__(self, in_features, hidden_features, act_layer=nn.GELU, drop=0.0):
+        super().__init__()
+        self.fc1 = nn.Linear(in_features, hidden_features)
+        self.act = act_layer()
+        self.drop1 = nn.Dropout(drop)
+        self.norm = nn.Identity()
+        self.fc2 = nn.Linear(hidden_features, in_features)
+        self.drop2 = nn.Dropout(drop)
+
+    def forward(self, x):
+        return self.drop2(self.fc2(self.norm(self.drop1(self.act(self.fc1(x))))))
+
+
+class Attention(nn.Module):
+    def __init__(self, dim, num_heads=8, qkv_bias=False, attn_drop=0.0, proj_drop=0.0):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.qkv = nn.Linear(dim, dim * 3, bias=qkv_bias)
+        self.q_norm = nn.Identity()
+        self.k_norm = nn.Identity()
+        self.attn_drop = nn.Dropout(attn_drop)
+        self.proj = nn.Linear(dim, dim)
+        self.proj_drop = nn.Dropout(proj_drop)
+
+    def forward(self, x):
+        b, n, c = x.shape
+        qkv = self.qkv(x).reshape(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv.unbind(0)
+        x = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
+        x = x.transpose(1, 2).reshape(b, n, c)
+        return self.proj_drop(self.proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, dim, num_heads, mlp_ratio=4.0, qkv_bias=False, norm_layer=nn.LayerNorm, drop=0.0,
+                 attn_drop=0.0):
+        super().__init__()
+        self.norm1 = norm_layer(dim)
+        self.attn = Attention(dim, num_heads=num_heads, qkv_bias=qkv_bias, attn_drop=attn_drop, proj_drop=drop)
+        self.ls1 = nn.Identity()
+        self.norm2 = norm_layer(dim)
+        self.mlp = Mlp(dim, int(dim * mlp_ratio), drop=drop)
+        self.ls2 = nn.Identity()
+
+    def forward(self, x):
+        x = x + self.ls1(self.attn(self.norm1(x)))
+        x = x + self.ls2(self.mlp(self.norm2(x)))
+        return x
+
+
+class VisionTransformer(nn.Module):
+    """Class-token ViT (timm VisionTransformer, global_pool='token')."""
+
+    num_prefix_tokens = 1
+
+    def __init__(self, img_size=224, patch_size=16, in_chans=3, num_classes=1000, embed_dim=768, depth=12,
+                 num_heads=12, mlp_ratio=4.0, qkv_bias=True, norm_layer=None, drop_rate=0.0,
+                 attn_drop_rate=0.0, drop_path_rate=0.0, **kwargs):
+        super().__init__()
+        norm_layer = norm_layer or (lambda d: nn.LayerNorm(d, eps=1e-6))
+        self.num_classes = num_classes
+        self.num_features = self.embed_dim = embed_dim
+        self.patch_embed = PatchEmbed(img_size, patch_size, in_chans, embed_dim)
+        num_patches = self.patch_embed.num_patches
+        self.cls_token = nn.Parameter(torch.zeros(1, 1, embed_dim))
+        self._init_extra_tokens(embed_dim)
+        self.pos_embed = nn.Parameter(torch.zeros(1, num_patches + self.num_prefix_tokens, embed_dim))
+        self.pos_drop = nn.Dropout(drop_rate)
+        self.norm_pre = nn.Identity()
+        self.blocks = nn.Sequential(*[
+            Block(embed_dim, num_heads, mlp_ratio, qkv_bias, norm_layer, drop_rate, attn_drop_rate)
+            for _ in range(depth)])
+        self.norm = norm_layer(embed_dim)
+        self.fc_norm = nn.Identity()
+        self.head_drop = nn.Dropout(drop_rate)
+        self.head = nn.Linear(embed_dim, num_classes) if num_classes > 0 else nn.Identity()
+        self._init_extra_heads(embed_dim, num_classes)
+        self._init_weights()
+
+    def _init_extra_tokens(self, embed_dim):
+        pass
+
+    def _init_extra_heads(self, embed_dim, num_classes):
+        pass
+
+    def _init_weights(self):
+        _trunc_normal_(self.pos_embed, 0.02)
+        nn.init.normal_(self.cls_token, std=1e-6)
+        for m in self.modules():
+            if isinstance(m, nn.Linear):
+                _trunc_normal_(m.weight, 0.02)
+                if m.bias is not None:
+                    nn.init.zeros_(m.bias)
+            elif isinstance(m, nn.LayerNorm):
+                nn.init.ones_(m.weight)
+                nn.init.zeros_(m.bias)
+
+    def _prefix_tokens(self, x):
+        return self.cls_token.expand(x.shape[0], -1, -1).to(x.dtype)
+
+    def forward_features(self, x):
+        x = self.patch_embed(x)
+        x = torch.cat((self._prefix_tokens(x), x), dim=1) + self.pos_embed.to(x.dtype)
+        x = self.norm_pre(self.pos_drop(x))
+        x = self.blocks(x)
+        return self.norm(x)
+
+    def forward_head(self, x, pre_logits: bool = False):
+        x = self.head_drop(self.fc_norm(x[:, 0]))
+        return x if pre_logits else self.head(x)
+
+    def forward(self, x):
+        return self.forward_head(self.forward_features(x))
+
+
+class VisionTransformerDistilled(VisionTransformer):
+    """DeiT with class and distillation tokens and two heads (timm
+    VisionTransformerDistilled): eval output is the mean of both heads."""
+
+    num_prefix_tokens = 2
+
+    def _init_extra_tokens(self, embed_dim):
+        self.dist_token = nn.Parameter(torch.zeros(1, 1, embed_dim))
+        self.distilled_training = False
+
+    def _init_extra_heads(self, embed_dim, num_classes):
+        self.head_dist = nn.Linear(embed_dim, num_classes) if num_classes > 0 else nn.Identity()
+
+    def _init_weights(self):
+        super()._init_weights()
+        _trunc_normal_(self.dist_token, 0.02)
+
+    def _prefix_tokens(self, x):
+        b = x.shape[0]
+        return torch.cat((self.cls_token.expand(b, -1, -1), self.dist_token.expand(b, -1, -1)), dim=1).to(x.dtype)
+
+    def forward_head(self, x, pre_logits: bool = False):
+        x, x_dist = x[:, 0], x[:, 1]
+        if pre_logits:
+            return (x + x_dist) / 2
+        x = self.head(x)
+        x_dist = self.head_dist(x_dist)
+        if self.distilled_training and self.training:
+            return x, x_dist
+        return (x + x_dist) / 2
+
+
+def num_tokens(img_size: int, patch_size: int, prefix: int) -> int:
+    return (img_size // patch_size) ** 2 + prefix
+
+
+__all__ = ["VisionTransformer", "VisionTransformerDistilled", "PatchEmbed", "Attention", "Block", "Mlp",
+           "num_tokens"]
