@@ -195,10 +195,12 @@ class ComplexWeightQuantizer(nn.Module):
             self.register_parameter("rotation_angle", None)
 
     def rotation_cos_sin(self):
-        """float32 (cos, sin) of the learned global rotation, or None."""
+        """float32 (cos, sin) of the learned global rotation, evaluated on the
+        host (as the reference's CPU quantization does), or None."""
         if self.is_module_quantizer or not self.enable_rotation:
             return None
-        return torch.cos(self.rotation_angle).detach(), torch.sin(self.rotation_angle).detach()
+        theta = self.rotation_angle.detach().cpu()
+        return torch.cos(theta), torch.sin(theta)
 
     def forward(self, w_real: torch.Tensor, w_imag: torch.Tensor) -> TensorPair:
         if self.is_module_quantizer:
@@ -307,9 +309,12 @@ class QATLinearComplexPhase(nn.Linear):
         if self._override is not None:
             lc = self._override
         else:
+            # offline step, on the host in float32 like the reference's
+            # exporter, so codes and scales are bit-identical to the
+            # reference's CPU quantization (device sums reorder float32 adds)
             rot_u = self.quantizer_u.rotation_cos_sin()
             rot_w = self.quantizer_w.rotation_cos_sin()
-            lc = P.quantize_layer(self.weight.detach().to(device), self.quantizer_u.quant_method,
+            lc = P.quantize_layer(self.weight.detach().cpu(), self.quantizer_u.quant_method,
                                   self.quantizer_w.quant_method, rot_u, rot_w)
         self._packed = PackedWide.from_planes([p.to(device) for p in lc.planes],
                                               [s.to(device) for s in lc.scale_re],

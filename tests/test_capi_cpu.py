@@ -1,0 +1,103 @@
+"""The C-ABI library loads, exports every symbol include/rpfq.h declares, and
+rejects bad arguments with status codes -- all without a GPU (validation
+runs before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rpfq.h")
+
+
+def lib():
+    from quant_models import _native
+    if not os.path.exists(_native.library_path()):
+        pytest.skip("librpfq.so not built")
+    return _native.load(), _native
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(rpfq_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_binding_list():
+    _, N = lib()
+    assert declared() == sorted(N.EXPORTED)
+
+
+def test_every_declared_symbol_exported():
+    L, _ = lib()
+    for name in declared():
+        assert hasattr(L, name), name
+    assert L.rpfq_abi_version() == 1
+
+
+def _desc(N, n=64, k=64, block=0, cb=0, stages=2):
+    d = N.WideDesc()
+    d.n_complex, d.k_complex, d.block, d.codebook, d.stages, d.rotate = n, k, block, cb, stages, 0
+    return d
+
+
+def test_wide_packed_bytes_geometry():
+    L, N = lib()
+    d = _desc(N, n=50, k=48, block=0)
+    nt, ks = 2, 2  # ceil(50/32), ceil(48/32)
+    codes = nt * ks * 1024
+    assert L.rpfq_wide_packed_bytes(ctypes.byref(d)) == ((codes + 255) // 256) * 256 + nt * 32 * 1 * 32
+    d2 = _desc(N, n=64, k=512, block=256)
+    assert L.rpfq_wide_packed_bytes(ctypes.byref(d2)) == 2 * 16 * 1024 + 2 * 32 * 2 * 32
+    assert L.rpfq_wide_packed_bytes(ctypes.byref(_desc(N, k=12))) == 0  # invalid -> 0
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("k_complex", 12, 3), ("n_complex", 0, 2), ("block", 48, 6), ("codebook", 9, 4), ("stages", 3, 4)])
+def test_wide_linear_rejects_bad_desc(field, value, code):
+    L, N = lib()
+    d = _desc(N)
+    setattr(d, field, value)
+    buf = ctypes.create_string_buffer(64)
+    rc = L.rpfq_wide_linear(ctypes.byref(d), buf, 1 << 20, buf, 1, 4, None, buf, 1, 0, None)
+    assert rc == code
+    assert L.rpfq_last_error().decode()
+
+
+def test_wide_linear_argument_errors():
+    L, N = lib()
+    d = _desc(N)
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    assert L.rpfq_wide_linear(None, p, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
+    assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 3, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 16, p, 1, 4, None, p, 1, 0, None) == 2
+    assert L.rpfq_wide_linear(ctypes.byref(d), ctypes.c_void_p(258), 1 << 20, p, 1, 4, None, p, 1, 0, None) == 3
+    assert "aligned" in L.rpfq_last_error().decode()
+
+
+def test_unpack_phase_act_argument_errors():
+    L, _ = lib()
+    p = ctypes.c_void_p(256)
+    assert L.rpfq_unpack(None, 2, 4, 8, None, None, 0, p, p, None) == 1
+    assert L.rpfq_unpack(p, 3, 4, 8, None, None, 0, p, p, None) == 4
+    assert L.rpfq_unpack(p, 2, 4, 6, None, None, 0, p, p, None) == 3
+    assert L.rpfq_unpack(p, 2, 4, 8, p, None, 0, p, p, None) == 1
+    assert L.rpfq_phase_linear(p, p, 0, 1, 4, 40, p, p, p, 0, 8, p, p, 0, None) == 3   # K % 32
+    assert L.rpfq_phase_linear(p, p, 0, 1, 4, 64, p, p, p, 40, 8, p, p, 0, None) == 6  # block
+    assert L.rpfq_phase_linear(p, p, 4, 1, 4, 64, p, p, p, 0, 8, p, p, 0, None) == 5   # dtype
+    assert L.rpfq_act_quant(p, 0, 4, 7, 4, p, 0, None) == 2
+    assert L.rpfq_act_quant(p, 0, 4, 8, 1, p, 0, None) == 4
+    assert L.rpfq_act_quant(None, 0, 4, 8, 4, p, 0, None) == 1
+
+
+def test_wide_pack_plane_count():
+    L, N = lib()
+    d = _desc(N)
+    arr = (ctypes.c_void_p * 4)(256, 256, 256, 256)
+    p = ctypes.c_void_p(256)
+    assert L.rpfq_wide_pack(ctypes.byref(d), arr, 3, arr, arr, p, 1 << 20, None) == 4
+    d.codebook, d.stages = 2, 1
+    assert L.rpfq_wide_pack(ctypes.byref(d), arr, 4, arr, arr, p, 1 << 20, None) == 4

@@ -1,0 +1,134 @@
+"""GPU parity of the drop-in layer and models against the reference path.
+
+* Layer: QATLinearComplexPhase in eval mode on the GPU (packed HIP path) vs
+  the outputs the reference's own quant_i.QATLinearComplexPhase wrote
+  (tests/golden), for the methods the packed path covers, with rotation and
+  activation quantization on and off.  Bound: the kernel rounds the
+  activations and the float32 fused coefficients to fp16 once each, so
+  |dy| <= 2^-10 * sum_k |x_k| |A_k| + 1e-5 (two half-ulp roundings).
+* Model: a DeiT-Tiny / ViT-Tiny forward in fp16 on the GPU vs the same model
+  in float32 on the CPU with every quantized layer evaluated as
+  x @ A_q.T + b on the oracle's decoded weight.  Stated tolerance: logits
+  max-abs <= 2e-2 * max|logit| + 2e-3; top-1 agreement 100% on samples whose
+  reference margin exceeds 4x the observed max logit error (margin-aware),
+  raw top-1 agreement reported and required >= 99% over 64 images.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import rpfq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _layer(method, act, rot, golden):
+    from quant_models.quant_i import QATLinearComplexPhase
+
+    layer = QATLinearComplexPhase(quant_method_u=method, quant_method_w=method, enable_act_quant=bool(act),
+                                  act_num_bits=4, enable_rotation=bool(rot), in_features=96, out_features=64)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(golden["w_weight"]))
+        layer.bias.copy_(torch.from_numpy(golden["fwd_bias"]))
+        if rot:
+            layer.quantizer_u.rotation_angle.fill_(0.3)
+            layer.quantizer_w.rotation_angle.fill_(-0.2)
+    return layer
+
+
+@pytest.mark.parametrize("method", ["complex_phase_v1", "complex_phase_v2", "complex_phase_new_v2"])
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("rot", [0, 1])
+def test_packed_layer_vs_reference_outputs(golden, method, act, rot):
+    layer = _layer(method, act, rot, golden).to(DEV).eval()
+    x = torch.from_numpy(golden["fwd_x"])
+    with torch.no_grad():
+        y = layer(x.to(DEV)).cpu().numpy()
+    tag = f"{method}_a{act}_r{rot}"
+    y_ref = golden[f"fwd_y_{tag}"].astype(np.float64)
+    a_ref = golden[f"fwd_aq_{tag}"].astype(np.float64)
+    xs = golden["fwd_x"]
+    if act:
+        h = xs.shape[1] // 2
+        xs = np.concatenate(O.act_quant(xs[:, :h], xs[:, h:], 4), axis=1)
+    bound = 2.0 ** -10 * (np.abs(xs.astype(np.float64)) @ np.abs(a_ref).T) + 1e-5
+    assert np.all(np.abs(y - y_ref) <= bound), np.abs(y - y_ref).max()
+    # the decoded float32 weight is the reference's A_q exactly
+    assert np.array_equal(layer.packed(torch.device(DEV)).decode().cpu().numpy(), golden[f"fwd_aq_{tag}"])
+
+
+def test_packed_path_refuses_unsupported_method(golden):
+    layer = _layer("complex_phase_v3", 0, 0, golden).to(DEV).eval()
+    with pytest.raises(NotImplementedError):
+        with torch.no_grad():
+            layer(torch.randn(2, 96, device=DEV))
+
+
+def test_packed_layer_repacks_after_weight_update(golden):
+    layer = _layer("complex_phase_v2", 0, 0, golden).to(DEV).eval()
+    x = torch.randn(3, 96, device=DEV)
+    with torch.no_grad():
+        y0 = layer(x)
+        layer.weight.mul_(2.0)
+        y1 = layer(x)
+        ref = F.linear(x.cpu(), layer.cpu().quantized_weight(), layer.bias)
+    assert not torch.allclose(y0.cpu(), y1.cpu())
+    assert torch.allclose(y1.cpu(), ref, rtol=0, atol=2e-3)
+
+
+def _reference_forward_cpu(model_gpu, name, x_cpu, state):
+    """float32 CPU copy of the model whose quantized layers run x @ A_q.T + b
+    on the oracle's decoding of exactly the codes the GPU model uses."""
+    import copy
+
+    import quant_models as qm
+    from quant_models.inference import quant_layers
+
+    ref = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                          quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    ref.load_state_dict({k: v.float().cpu() for k, v in state.items()})
+    ref.eval()
+    for (n_g, l_g), (n_c, l_c) in zip(quant_layers(model_gpu), quant_layers(ref)):
+        lc = l_g._override
+        planes = [(O.unpack_codes(p.cpu().numpy()), a.cpu().numpy()[:, 0], b.cpu().numpy()[:, 0], k)
+                  for p, a, b, k in zip(lc.planes, lc.scale_re, lc.scale_im, "uuww")]
+        a_q = torch.from_numpy(O.wide_weight(planes))
+        bias = None if l_c.bias is None else l_c.bias.detach().float()
+        l_c.forward = (lambda xx, a_q=a_q, bias=bias: F.linear(xx, a_q, bias))
+    with torch.no_grad():
+        return ref(x_cpu)
+
+
+@pytest.mark.parametrize("name", ["rpfq_deit_tiny_patch16_224_q", "rpfq_vit_tiny_patch16_224_q"])
+def test_end_to_end_logits(name):
+    import quant_models as qm
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(1)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    load_synthetic_codes(model, 1)
+    # LayerNorm affine / embeddings get non-trivial values so logits spread
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, torch.nn.LayerNorm):
+                m.weight.normal_(1.0, 0.1)
+                m.bias.normal_(0.0, 0.1)
+    ref_state = {k: v.clone() for k, v in model.state_dict().items()}
+    prepare_inference(model, DEV, torch.float16)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(64, 3, 224, 224, generator=g)
+    with torch.no_grad():
+        y = model(x.to(DEV, torch.float16)).float().cpu()
+    # reference in float32 on the host with the same parameters and codes
+    y_ref = _reference_forward_cpu(model, name, x, ref_state)
+    err = (y - y_ref).abs()
+    assert err.max() <= 2e-2 * y_ref.abs().max() + 2e-3, (err.max(), y_ref.abs().max())
+    top = y_ref.topk(2, dim=1).values
+    margin = top[:, 0] - top[:, 1]
+    agree = (y.argmax(1) == y_ref.argmax(1)).float()
+    confident = margin > 4 * err.max()
+    assert bool(agree[confident].all())
+    assert agree.mean() >= 0.99, f"top-1 agreement {agree.mean():.4f}"
