@@ -132,7 +132,19 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--layer-report", default=None, help="write per-shape kernel timings (JSON) here")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a device copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_probe_mib:
+        import torch
+        src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": src.numel(), "copy_probe_bytes_written": dst.numel(),
+                          "launches": args.steps}))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is a design "
               "note in DESIGN.md, not a benchmark of this build", file=sys.stderr)

@@ -34,11 +34,18 @@ class PatchEmbed(nn.Module):
         self.norm = norm_layer(embed_dim) if norm_layer else nn.Identity()
 
     def forward(self, x):
-        x = self.proj(x)
-        if self.flatten:
-            x = x.flatten(2).transpose(1, 2)  # B, N, C
-        else:
-            x = x.permute(0, 2, 3, 1)  # B, H, W, C
+        # stride == kernel: patchify is an exact reshape, then one GEMM with
+        # the conv weight viewed as [C_out, C_in*p*p] (same result as the
+        # Conv2d, without depending on the convolution library's kernel pick)
+        b, c, h, w = x.shape
+        p = self.patch_size[0]
+        gh, gw = h // p, w // p
+        patches = x.reshape(b, c, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh * gw, c * p * p)
+        weight = self.proj.weight.reshape(self.proj.out_channels, -1)
+        x = F.linear(patches, weight.to(patches.dtype),
+                     None if self.proj.bias is None else self.proj.bias.to(patches.dtype))
+        if not self.flatten:
+            x = x.reshape(b, gh, gw, -1)  # B, H, W, C
         return self.norm(x)
 
 
