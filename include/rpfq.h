@@ -47,6 +47,10 @@ extern "C" {
 #define RPFQ_F16 1
 #define RPFQ_BF16 2
 
+/* rpfq_wide_linear flags: tile-height hints (default: chosen from M) */
+#define RPFQ_FLAG_TILE_M128 1
+#define RPFQ_FLAG_TILE_M256 2
+
 /* codebooks of the packed planes */
 #define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages
                             (quant_i.py:36-118, export_rpfq_vit_to_mlx.py:189-224) */
@@ -135,7 +139,8 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  * x: [M, 2K'] of x_dtype (rows 16-byte aligned); bias: float32 [2N'] or NULL;
  * y: [M, 2N'] of y_dtype.  The fused coefficients A = W + U (etc.) are formed
  * in float32 exactly as the reference does, rounded once to fp16 for the
- * MFMA, and accumulated in float32.  flags: 0 (reserved).
+ * MFMA, and accumulated in float32.  flags: 0 (tile chosen from M) or one
+ * RPFQ_FLAG_TILE_* hint.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                      const void* x, int x_dtype, int64_t M, const float* bias,
@@ -143,7 +148,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
 
 /*
  * Activation fake quantization of a [M, in_features] feature block laid out
- * [re | im]: per row and per half, scale = qmax / max(max|x|, 1e-5),
+ * [re | im]: per row and per half, scale = qmax * (1 / max(max|x|, 1e-5)),
  * y = clamp(round_half_even(x * scale), -2^(bits-1), 2^(bits-1)-1) / scale,
  * in float32 (bit-exact for float32 in/out).
  * Replaces ActivationQuantSTE / ComplexActivationQuantizer

@@ -560,24 +560,53 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
     const int64_t ldx = 2 * (int64_t)a.K;
 
-    uint4 xreg[CPT][2];
-    uint4 creg = make_uint4(0, 0, 0, 0);
+    // Raw activation prefetch: the loads for k-step ks+1 are issued before
+    // the MFMAs of k-step ks and converted/interleaved only when stored to
+    // LDS afterwards, so their latency overlaps the math.  Out-of-range
+    // chunks load a valid address and are zeroed at store time.
+    constexpr int RAW = (XDT == RPFQ_F32) ? 4 : 2;  // uint4 per (re|im) chunk pair
+    // Two raw buffers: the data of k-step ks+1 waits in one while the loads
+    // of k-step ks+2 land in the other (prefetch distance 2 k-steps).
+    uint4 xbufA[CPT][RAW], xbufB[CPT][RAW];
+    uint32_t okA = 0, okB = 0;
+    uint4 cA = make_uint4(0, 0, 0, 0), cB = make_uint4(0, 0, 0, 0);
 
     // chunk c = tid + 256 j: row c >> 2, columns 8 (c & 3) .. +7 of the k-step
-    auto load_x = [&](int ks) {
+    auto load_x = [&](int ks, uint4 (&xraw)[CPT][RAW], uint32_t& xok) {
+        xok = 0;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int c = tid + 256 * j;
             const int row = c >> 2, sub = c & 3;
             const int64_t m = m0 + row;
             const int kk = ks * 32 + sub * 8;
+            const bool ok = c < NCHUNK && m < a.M && kk < a.K;
+            xok |= (ok ? 1u : 0u) << j;
+            const int64_t off = ok ? m * ldx + kk : 0;
+            if (XDT == RPFQ_F32) {
+                const uint4* pr = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off);
+                const uint4* pi = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off + a.K);
+                xraw[j][0] = pr[0];
+                xraw[j][1] = pr[1];
+                xraw[j][RAW - 2] = pi[0];
+                xraw[j][RAW - 1] = pi[1];
+            } else {
+                xraw[j][0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off);
+                xraw[j][1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off + a.K);
+            }
+        }
+    };
+    auto store_x = [&](int stage, const uint4 (&xraw)[CPT][RAW], uint32_t xok) {
+        char* xs = smem + stage * XSTAGE;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tid + 256 * j;
+            if (c >= NCHUNK) break;
+            const int row = c >> 2, sub = c & 3;
             uint4 o0 = make_uint4(0, 0, 0, 0), o1 = make_uint4(0, 0, 0, 0);
-            if (c < NCHUNK && m < a.M && kk < a.K) {
-                const int64_t off = m * ldx + kk;
+            if ((xok >> j) & 1u) {
                 if (XDT == RPFQ_F16) {
-                    const uint4 vr = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off);
-                    const uint4 vi =
-                        *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off + a.K);
+                    const uint4 vr = xraw[j][0], vi = xraw[j][1];
                     // interleave (re, im) halves: perm selects bytes of (vi, vr)
                     o0.x = __builtin_amdgcn_perm(vi.x, vr.x, 0x05040100u);
                     o0.y = __builtin_amdgcn_perm(vi.x, vr.x, 0x07060302u);
@@ -589,32 +618,38 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
                     o1.w = __builtin_amdgcn_perm(vi.w, vr.w, 0x07060302u);
                 } else {
                     float fr[8], fi[8];
-                    load8_f32<XDT>(a.x, off, fr);
-                    load8_f32<XDT>(a.x, off + a.K, fi);
+                    if (XDT == RPFQ_BF16) {
+                        const uint32_t wr[4] = {xraw[j][0].x, xraw[j][0].y, xraw[j][0].z, xraw[j][0].w};
+                        const uint32_t wi[4] = {xraw[j][1].x, xraw[j][1].y, xraw[j][1].z, xraw[j][1].w};
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            fr[2 * t] = bf16_to_f32(wr[t] & 0xffffu);
+                            fr[2 * t + 1] = bf16_to_f32(wr[t] >> 16);
+                            fi[2 * t] = bf16_to_f32(wi[t] & 0xffffu);
+                            fi[2 * t + 1] = bf16_to_f32(wi[t] >> 16);
+                        }
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const float4 r4 = __builtin_bit_cast(float4, xraw[j][t]);
+                            const float4 i4 = __builtin_bit_cast(float4, xraw[j][RAW - 2 + t]);
+                            fr[4 * t] = r4.x; fr[4 * t + 1] = r4.y; fr[4 * t + 2] = r4.z; fr[4 * t + 3] = r4.w;
+                            fi[4 * t] = i4.x; fi[4 * t + 1] = i4.y; fi[4 * t + 2] = i4.z; fi[4 * t + 3] = i4.w;
+                        }
+                    }
                     o0 = make_uint4(cvt_pk(fr[0], fi[0]), cvt_pk(fr[1], fi[1]), cvt_pk(fr[2], fi[2]),
                                     cvt_pk(fr[3], fi[3]));
                     o1 = make_uint4(cvt_pk(fr[4], fi[4]), cvt_pk(fr[5], fi[5]), cvt_pk(fr[6], fi[6]),
                                     cvt_pk(fr[7], fi[7]));
                 }
             }
-            xreg[j][0] = o0;
-            xreg[j][1] = o1;
-        }
-    };
-    auto store_x = [&](int stage) {
-        char* xs = smem + stage * XSTAGE;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = tid + 256 * j;
-            if (c >= NCHUNK) break;
-            const int row = c >> 2, sub = c & 3;
             uint4* dst = reinterpret_cast<uint4*>(xs + row * kXRow + sub * 32);
-            dst[0] = xreg[j][0];
-            dst[1] = xreg[j][1];
+            dst[0] = o0;
+            dst[1] = o1;
         }
     };
-    auto load_codes = [&](int ks) {
-        if (active) creg = a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g];
+    auto load_codes = [&](int ks) -> uint4 {
+        return active ? a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g] : make_uint4(0, 0, 0, 0);
     };
 
     floatx16 acc_re[MB], acc_im[MB];
@@ -623,43 +658,56 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
 
     int cur_blk = 0;
     build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
-    load_x(0);
-    load_codes(0);
-    store_x(0);
+    load_x(0, xbufA, okA);
+    cA = load_codes(0);
+    store_x(0, xbufA, okA);
+    if (a.KS > 1) {
+        load_x(1, xbufB, okB);
+        cB = load_codes(1);
+    }
     __syncthreads();
 
-    for (int ks = 0; ks < a.KS; ++ks) {
-        const uint4 cw = creg;
-        const bool more = ks + 1 < a.KS;
-        if (more) {
-            load_x(ks + 1);
-            load_codes(ks + 1);
+    // One k-step: prefetch k-step ks+2 into `fill`, run the MFMAs of ks, stage
+    // k-step ks+1 (waiting in `next`) into the other LDS buffer.
+    auto kstep = [&](int ks, const uint4 cw, uint4 (&next)[CPT][RAW], uint32_t next_ok, uint4 (&fill)[CPT][RAW],
+                     uint32_t& fill_ok, uint4& fill_codes) {
+        if (ks + 2 < a.KS) {
+            load_x(ks + 2, fill, fill_ok);
+            fill_codes = load_codes(ks + 2);
         }
         const char* xs = smem + (ks & 1) * XSTAGE;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const uint32_t word = s == 0 ? cw.x : s == 1 ? cw.y : s == 2 ? cw.z : cw.w;
-            uint32_t bre[4], bim[4];
+            // issue every LDS read of the substep first: 8 LUT entries, MB operands
+            float2 U[4], W[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t byte = (word >> (8 * e)) & 0xffu;
-                const float2 U = lut[(byte & 15u) * 32 + r];
-                const float2 W = lut[(16u + (byte >> 4)) * 32 + r];
+                U[e] = lut[(byte & 15u) * 32 + r];
+                W[e] = lut[(16u + (byte >> 4)) * 32 + r];
+            }
+            half8 ax[MB];
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                ax[i] = *reinterpret_cast<const half8*>(xs + (i * 32 + r) * kXRow + (8 * s + 4 * g) * 4);
+            uint32_t bre[4], bim[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
                 // fused coefficients in the reference's order (quant_i.py:534-537)
-                bre[e] = cvt_pk(W.x + U.x, W.y - U.y);   // (A11, A12)
-                bim[e] = cvt_pk(W.y + U.y, -W.x + U.x);  // (A21, A22)
+                bre[e] = cvt_pk(W[e].x + U[e].x, W[e].y - U[e].y);   // (A11, A12)
+                bim[e] = cvt_pk(W[e].y + U[e].y, -W[e].x + U[e].x);  // (A21, A22)
             }
             const half8 b_re = as_half8(make_uint4(bre[0], bre[1], bre[2], bre[3]));
             const half8 b_im = as_half8(make_uint4(bim[0], bim[1], bim[2], bim[3]));
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
-                const half8 ax = *reinterpret_cast<const half8*>(xs + (i * 32 + r) * kXRow + (8 * s + 4 * g) * 4);
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, b_re, acc_re[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax, b_im, acc_im[i], 0, 0, 0);
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[i], b_re, acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax[i], b_im, acc_im[i], 0, 0, 0);
             }
         }
-        if (more) {
-            store_x((ks + 1) & 1);
+        if (ks + 1 < a.KS) {
+            store_x((ks + 1) & 1, next, next_ok);
             const int nb = (ks + 1) / a.block_ks;
             if (nb != cur_blk) {
                 __syncthreads();
@@ -668,6 +716,14 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
             }
         }
         __syncthreads();
+    };
+    for (int ks = 0; ks < a.KS; ks += 2) {
+        const uint4 c0 = cA;
+        kstep(ks, c0, xbufB, okB, xbufA, okA, cA);
+        if (ks + 1 < a.KS) {
+            const uint4 c1 = cB;
+            kstep(ks + 1, c1, xbufA, okA, xbufB, okB, cB);
+        }
     }
 
     const bool n_ok = active && n < a.N;
@@ -730,6 +786,248 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
         } else {
             const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
             for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = h[t];
+        }
+    }
+}
+
+// Large-M widely-linear GEMM.  Workgroup = 4 waves, one per SIMD; tile =
+// 256 rows of x times 128 complex output rows; wave w owns complex rows
+// 32w..32w+31 for all 256 rows.  Compared with wide_linear_kernel every
+// decoded coefficient feeds twice as many MFMAs (LUT bytes per MFMA halve),
+// the accumulators (256 fp32) live in AGPRs, and the work of a substep is
+// software pipelined: the LUT and activation reads of substep s+1 are issued
+// before the MFMAs of substep s.  The MFMA computes the transposed product
+// (decoded weights as the A operand), so each lane ends with 4 consecutive
+// outputs of one row and the epilogue stores straight from registers.
+constexpr int kBigBM = 256;
+
+constexpr int wide_big_lds_bytes() { return 2 * kBigBM * kXRow + 4 * kLutWave; }
+
+template <int XDT, int YDT, int CB>
+__global__ void __launch_bounds__(256, 1) wide_linear_big_kernel(WideArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    constexpr int BM = kBigBM;
+    constexpr int MB = BM / 32;
+    constexpr int XSTAGE = BM * kXRow;
+    constexpr int CPT = BM / 64;
+    constexpr int RAW = (XDT == RPFQ_F32) ? 4 : 2;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 31, g = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
+    const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
+    const int64_t m0 = (int64_t)mt * BM;
+    const int ntw = ntl * 4 + wave;
+    const bool active = ntw < a.NT;
+    const int64_t n = (int64_t)ntw * 32 + r;
+    float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
+    const int64_t ldx = 2 * (int64_t)a.K;
+
+    uint4 xraw[CPT][RAW];
+    uint32_t xok = 0;
+    uint4 creg = make_uint4(0, 0, 0, 0);
+
+    auto load_x = [&](int ks) {
+        xok = 0;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tid + 256 * j;
+            const int row = c >> 2, sub = c & 3;
+            const int64_t m = m0 + row;
+            const int kk = ks * 32 + sub * 8;
+            const bool ok = m < a.M && kk < a.K;
+            xok |= (ok ? 1u : 0u) << j;
+            const int64_t off = ok ? m * ldx + kk : 0;
+            if (XDT == RPFQ_F32) {
+                const uint4* pr = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off);
+                const uint4* pi = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off + a.K);
+                xraw[j][0] = pr[0];
+                xraw[j][1] = pr[1];
+                xraw[j][RAW - 2] = pi[0];
+                xraw[j][RAW - 1] = pi[1];
+            } else {
+                xraw[j][0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off);
+                xraw[j][1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off + a.K);
+            }
+        }
+    };
+    auto store_x = [&](int stage) {
+        char* xs = smem + stage * XSTAGE;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int c = tid + 256 * j;
+            const int row = c >> 2, sub = c & 3;
+            uint4 o0 = make_uint4(0, 0, 0, 0), o1 = make_uint4(0, 0, 0, 0);
+            if ((xok >> j) & 1u) {
+                if (XDT == RPFQ_F16) {
+                    const uint4 vr = xraw[j][0], vi = xraw[j][1];
+                    o0.x = __builtin_amdgcn_perm(vi.x, vr.x, 0x05040100u);
+                    o0.y = __builtin_amdgcn_perm(vi.x, vr.x, 0x07060302u);
+                    o0.z = __builtin_amdgcn_perm(vi.y, vr.y, 0x05040100u);
+                    o0.w = __builtin_amdgcn_perm(vi.y, vr.y, 0x07060302u);
+                    o1.x = __builtin_amdgcn_perm(vi.z, vr.z, 0x05040100u);
+                    o1.y = __builtin_amdgcn_perm(vi.z, vr.z, 0x07060302u);
+                    o1.z = __builtin_amdgcn_perm(vi.w, vr.w, 0x05040100u);
+                    o1.w = __builtin_amdgcn_perm(vi.w, vr.w, 0x07060302u);
+                } else {
+                    float fr[8], fi[8];
+                    if (XDT == RPFQ_BF16) {
+                        const uint32_t wr[4] = {xraw[j][0].x, xraw[j][0].y, xraw[j][0].z, xraw[j][0].w};
+                        const uint32_t wi[4] = {xraw[j][1].x, xraw[j][1].y, xraw[j][1].z, xraw[j][1].w};
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            fr[2 * t] = bf16_to_f32(wr[t] & 0xffffu);
+                            fr[2 * t + 1] = bf16_to_f32(wr[t] >> 16);
+                            fi[2 * t] = bf16_to_f32(wi[t] & 0xffffu);
+                            fi[2 * t + 1] = bf16_to_f32(wi[t] >> 16);
+                        }
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const float4 r4 = __builtin_bit_cast(float4, xraw[j][t]);
+                            const float4 i4 = __builtin_bit_cast(float4, xraw[j][RAW - 2 + t]);
+                            fr[4 * t] = r4.x; fr[4 * t + 1] = r4.y; fr[4 * t + 2] = r4.z; fr[4 * t + 3] = r4.w;
+                            fi[4 * t] = i4.x; fi[4 * t + 1] = i4.y; fi[4 * t + 2] = i4.z; fi[4 * t + 3] = i4.w;
+                        }
+                    }
+                    o0 = make_uint4(cvt_pk(fr[0], fi[0]), cvt_pk(fr[1], fi[1]), cvt_pk(fr[2], fi[2]),
+                                    cvt_pk(fr[3], fi[3]));
+                    o1 = make_uint4(cvt_pk(fr[4], fi[4]), cvt_pk(fr[5], fi[5]), cvt_pk(fr[6], fi[6]),
+                                    cvt_pk(fr[7], fi[7]));
+                }
+            }
+            uint4* dst = reinterpret_cast<uint4*>(xs + row * kXRow + sub * 32);
+            dst[0] = o0;
+            dst[1] = o1;
+        }
+    };
+    auto load_codes = [&](int ks) {
+        if (active) creg = a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g];
+    };
+    auto lut_read = [&](uint32_t word, float2* U, float2* W) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t byte = (word >> (8 * e)) & 0xffu;
+            U[e] = lut[(byte & 15u) * 32 + r];
+            W[e] = lut[(16u + (byte >> 4)) * 32 + r];
+        }
+    };
+
+    floatx16 acc_re[MB], acc_im[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
+
+    int cur_blk = 0;
+    build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
+    load_x(0);
+    load_codes(0);
+    store_x(0);
+    __syncthreads();
+
+    for (int ks = 0; ks < a.KS; ++ks) {
+        const uint4 cw = creg;
+        const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
+        const bool more = ks + 1 < a.KS;
+        const char* xs = smem + (ks & 1) * XSTAGE;
+        const char* arow = xs + r * kXRow + 16 * g;  // (8 s + 4 g) * 4 bytes into the row
+        float2 Un[4], Wn[4];
+        half8 an[MB];
+        lut_read(words[0], Un, Wn);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) an[i] = *reinterpret_cast<const half8*>(arow + i * 32 * kXRow);
+        if (more) {
+            load_x(ks + 1);
+            load_codes(ks + 1);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            float2 U[4], W[4];
+            half8 ac[MB];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                U[e] = Un[e];
+                W[e] = Wn[e];
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) ac[i] = an[i];
+            if (s < 3) {  // issue the next substep's LDS reads before this substep's MFMAs
+                lut_read(words[s + 1], Un, Wn);
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    an[i] = *reinterpret_cast<const half8*>(arow + i * 32 * kXRow + 32 * (s + 1));
+            }
+            uint32_t bre[4], bim[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // fused coefficients in the reference's order (quant_i.py:534-537)
+                bre[e] = cvt_pk(W[e].x + U[e].x, W[e].y - U[e].y);   // (A11, A12)
+                bim[e] = cvt_pk(W[e].y + U[e].y, -W[e].x + U[e].x);  // (A21, A22)
+            }
+            const half8 b_re = as_half8(make_uint4(bre[0], bre[1], bre[2], bre[3]));
+            const half8 b_im = as_half8(make_uint4(bim[0], bim[1], bim[2], bim[3]));
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_re, ac[i], acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_im, ac[i], acc_im[i], 0, 0, 0);
+            }
+        }
+        if (more) {
+            store_x((ks + 1) & 1);
+            const int nb = (ks + 1) / a.block_ks;
+            if (nb != cur_blk) {
+                __syncthreads();
+                build_lut<CB>(lut, a.params, n, active, a.nblk, nb, a.rot, r, g);
+                cur_blk = nb;
+            }
+        }
+        __syncthreads();
+    }
+
+    if (!active) return;
+    // epilogue: lane holds C^T[n][m] for m = m0 + 32 i + r and
+    // n = 32 ntw + 8 j + 4 g + t (t = 0..3) in acc[i][4 j + t]
+    const int64_t ldy = 2 * (int64_t)a.N;
+    float4 bias[2][4];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n0 = (int64_t)ntw * 32 + 8 * j + 4 * g;
+            float b4[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) b4[t] = (a.bias && n0 + t < a.N) ? a.bias[p * a.N + n0 + t] : 0.0f;
+            bias[p][j] = make_float4(b4[0], b4[1], b4[2], b4[3]);
+        }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int64_t m = m0 + i * 32 + r;
+        if (m >= a.M) break;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const floatx16& acc = p ? acc_im[i] : acc_re[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t n0 = (int64_t)ntw * 32 + 8 * j + 4 * g;
+                const float v0 = acc[4 * j] + bias[p][j].x, v1 = acc[4 * j + 1] + bias[p][j].y;
+                const float v2 = acc[4 * j + 2] + bias[p][j].z, v3 = acc[4 * j + 3] + bias[p][j].w;
+                const int64_t off = m * ldy + p * a.N + n0;
+                if (a.vec_store && n0 + 4 <= a.N) {
+                    if (YDT == RPFQ_F32) {
+                        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.y) + off) = make_float4(v0, v1, v2, v3);
+                    } else if (YDT == RPFQ_F16) {
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + off) =
+                            make_uint2(cvt_pk(v0, v1), cvt_pk(v2, v3));
+                    } else {
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + off) =
+                            make_uint2((uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16),
+                                       (uint32_t)f32_to_bf16(v2) | ((uint32_t)f32_to_bf16(v3) << 16));
+                    }
+                } else {
+                    const float vv[4] = {v0, v1, v2, v3};
+                    for (int t = 0; t < 4; ++t)
+                        if (n0 + t < a.N) store1<YDT>(a.y, off + t, vv[t]);
+                }
+            }
         }
     }
 }
@@ -926,33 +1224,50 @@ static hipError_t wide_go(WideArgs& a, hipStream_t s) {
 }
 
 template <int XDT, int YDT, int CB>
-static hipError_t wide_bm(WideArgs& a, hipStream_t s) {
+static hipError_t wide_big_go(WideArgs& a, hipStream_t s) {
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    constexpr int lds = wide_big_lds_bytes();
+    std::call_once(once, [] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_big_kernel<XDT, YDT, CB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    a.tiles_m = (int)((a.M + kBigBM - 1) / kBigBM);
+    a.tiles_n = (int)((a.NT + 3) / 4);
+    hipLaunchKernelGGL((wide_linear_big_kernel<XDT, YDT, CB>), dim3(a.tiles_m * a.tiles_n), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int XDT, int YDT, int CB>
+static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
+    if (flags & RPFQ_FLAG_TILE_M256) return wide_big_go<XDT, YDT, CB>(a, s);
+    if (flags & RPFQ_FLAG_TILE_M128) return wide_go<128, XDT, YDT, CB>(a, s);
     if (a.M <= 32) return wide_go<32, XDT, YDT, CB>(a, s);
     if (a.M <= 64) return wide_go<64, XDT, YDT, CB>(a, s);
     return wide_go<128, XDT, YDT, CB>(a, s);
 }
 
 template <int XDT, int CB>
-static hipError_t wide_y(WideArgs& a, int ydt, hipStream_t s) {
+static hipError_t wide_y(WideArgs& a, int ydt, int flags, hipStream_t s) {
     switch (ydt) {
-        case RPFQ_F32: return wide_bm<XDT, RPFQ_F32, CB>(a, s);
-        case RPFQ_F16: return wide_bm<XDT, RPFQ_F16, CB>(a, s);
-        default: return wide_bm<XDT, RPFQ_BF16, CB>(a, s);
+        case RPFQ_F32: return wide_bm<XDT, RPFQ_F32, CB>(a, flags, s);
+        case RPFQ_F16: return wide_bm<XDT, RPFQ_F16, CB>(a, flags, s);
+        default: return wide_bm<XDT, RPFQ_BF16, CB>(a, flags, s);
     }
 }
 
 template <int CB>
-static hipError_t wide_x(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+static hipError_t wide_x(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s) {
     switch (xdt) {
-        case RPFQ_F32: return wide_y<RPFQ_F32, CB>(a, ydt, s);
-        case RPFQ_F16: return wide_y<RPFQ_F16, CB>(a, ydt, s);
-        default: return wide_y<RPFQ_BF16, CB>(a, ydt, s);
+        case RPFQ_F32: return wide_y<RPFQ_F32, CB>(a, ydt, flags, s);
+        case RPFQ_F16: return wide_y<RPFQ_F16, CB>(a, ydt, flags, s);
+        default: return wide_y<RPFQ_BF16, CB>(a, ydt, flags, s);
     }
 }
 
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
                               int xdt, int64_t M, const float* bias, void* y, int ydt, int flags, hipStream_t s) {
-    (void)flags;
     WideArgs a;
     a.x = x;
     a.M = M;
@@ -967,11 +1282,11 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     a.rot = rot_of(d);
     a.bias = bias;
     a.y = y;
-    a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);  // also covers 4-wide stores
     switch (d.codebook) {
-        case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, s);
-        case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, s);
-        default: return wide_x<RPFQ_CB_AXIS>(a, xdt, ydt, s);
+        case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
+        default: return wide_x<RPFQ_CB_AXIS>(a, xdt, ydt, flags, s);
     }
 }
 

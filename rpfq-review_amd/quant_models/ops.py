@@ -141,8 +141,9 @@ class PackedWide:
         return cls(n_complex, k_complex, codebook, stages, block, blob, rotation)
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
-               out_dtype: torch.dtype | None = None) -> torch.Tensor:
-        """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N']."""
+               out_dtype: torch.dtype | None = None, flags: int = 0) -> torch.Tensor:
+        """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
+        flags: 0 or a tile-height hint (_native.FLAG_TILE_M128 / _M256)."""
         N.require_device(x, bias)
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
@@ -165,7 +166,7 @@ class PackedWide:
             ev0.record()
         N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
             ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
-            N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), 0,
+            N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), int(flags),
             N.stream_of(x2)))
         if rec is not None:
             ev1.record()

@@ -280,3 +280,20 @@ def test_wide_linear_matches_reference_android_runtime():
                        zip(planes, g_re, g_im, "uuww")])
     scale = np.abs(xf.astype(np.float64)) @ np.abs(a.astype(np.float64)).T + np.abs(bias)
     assert np.all(np.abs(y - y_ref) <= 2.0 ** -11 * scale + 1e-4)
+
+
+@pytest.mark.parametrize("flags", [1, 2])
+@pytest.mark.parametrize("m", [33, 300, 513])
+@pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[4], CASES[7]],
+                         ids=["1536x384", "50x48", "130x512-b256", "rot"])
+def test_wide_linear_tile_hints(case, m, flags):
+    """Both tile heights (RPFQ_FLAG_TILE_M128 / _M256) give the same bound."""
+    r = rng(500 + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16, flags=flags).float().cpu().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T + bias
+    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T + np.abs(bias)
+    assert np.all(np.abs(y - y16) <= 1e-5 * scale + 2.0 ** -11 * np.abs(y16) + 1e-5)
