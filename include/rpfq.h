@@ -47,9 +47,12 @@ extern "C" {
 #define RPFQ_F16 1
 #define RPFQ_BF16 2
 
-/* rpfq_wide_linear flags: tile-height hints (default: chosen from M) */
+/* rpfq_wide_linear flags.  Default (0): the kernel is chosen from the shape
+ * (fp16 x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA; other
+ * cases stage them through registers with a 32/64/128-row tile).
+ * RPFQ_FLAG_TILE_M128 forces the register-staged 128-row kernel; every
+ * kernel feeds the MFMA the same fp16 coefficients. */
 #define RPFQ_FLAG_TILE_M128 1
-#define RPFQ_FLAG_TILE_M256 2
 
 /* codebooks of the packed planes */
 #define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages
@@ -137,10 +140,11 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  *   (wideLinearReference / wideLinear; Metal widePrefill
  *   RPFQViTMetalKernels.swift:176-268).
  * x: [M, 2K'] of x_dtype (rows 16-byte aligned); bias: float32 [2N'] or NULL;
- * y: [M, 2N'] of y_dtype.  The fused coefficients A = W + U (etc.) are formed
- * in float32 exactly as the reference does, rounded once to fp16 for the
- * MFMA, and accumulated in float32.  flags: 0 (tile chosen from M) or one
- * RPFQ_FLAG_TILE_* hint.
+ * y: [M, 2N'] of y_dtype.  U and W are formed in float32 exactly as the
+ * reference does (stage sums, de-rotation) and rounded to fp16; each fused
+ * coefficient (A11 = Wre + Ure, A12 = Wim - Uim, A21 = Wim + Uim,
+ * A22 = -Wre + Ure) is one correctly rounded fp16 add of those; the MFMA
+ * accumulates in float32.  flags: 0 or RPFQ_FLAG_TILE_M128.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                      const void* x, int x_dtype, int64_t M, const float* bias,
@@ -160,7 +164,8 @@ int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, i
 /*
  * Write the fused float32 weight A_q [2N', 2K'] that the packed layer
  * represents (quant_i.py:534-544 layout), decoded by the same device code the
- * GEMM uses.  round_fp16 = 1 writes the fp16-rounded values the MFMA consumes.
+ * GEMM uses (bit-identical to the reference's float32 A_q).  round_fp16 = 1
+ * writes the fp16 coefficients the MFMA consumes (see rpfq_wide_linear).
  * Replaces export_rpfq_vit_to_mlx.py:336-375 (quantized_forward_weight).
  */
 int rpfq_wide_decode(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,

@@ -25,6 +25,12 @@ Parity status per function (how each one is pinned; see tests/test_oracle.py):
 * ``phase_linear``          -- compiled reference (oracle/_ref) and brute force.
 * ``wide_linear``           -- compiled reference (oracle/_ref); equals
                                ``x @ A_q.T + b`` in float64 (golden A_q).
+* ``fp16_add`` / ``recompose_fp16`` -- build-defined fp16 operand (no
+                               reference counterpart): fp16_add pinned by exact
+                               rational arithmetic (fractions) on every fp16
+                               pair class incl. ties and subnormals;
+                               recompose_fp16 by its error bound against the
+                               reference A_q and by sign/permutation identities.
 * ``linear_forward``        -- golden outputs of the reference layer.
 * ``psk16_*``               -- PARITY UNPINNED by the reference (the 16-PSK
                                codebook does not exist there); pinned only by
@@ -349,15 +355,14 @@ def derotate(re, im, c, s):
     return (re * c - im * s).astype(F32), (im * c + re * s).astype(F32)
 
 
-def wide_weight(planes, codebook: str = "axis", rotation=None):
-    """Fused real [2N, 2K] weight of the widely-linear layer.
+def wide_parts(planes, codebook: str = "axis", rotation=None):
+    """Quantized U and W of the widely-linear layer as float32 (re, im) planes.
 
     planes: list of (codes [N,K] unpacked, s_re [N], s_im [N], kind) with kind
     'u' or 'w', stage order preserved; the per-stage float32 values are summed
     as the reference does (quant_i.py:111-118: q = 0 + step0 + step1), then
-    optionally de-rotated (quant_i.py:433-434) and recombined
-    (quant_i.py:534-544).  codebook 'axis' | 'sign' | 'psk16' (for 'psk16'
-    s_re is the magnitude and s_im is ignored)."""
+    optionally de-rotated (quant_i.py:433-434).  codebook 'axis' | 'sign' |
+    'psk16' (for 'psk16' s_re is the magnitude and s_im is ignored)."""
     acc = {}
     for codes, s_re, s_im, kind in planes:
         if codebook == "psk16":
@@ -378,17 +383,57 @@ def wide_weight(planes, codebook: str = "axis", rotation=None):
         (cu, su), (cw, sw) = rotation
         u_re, u_im = derotate(u_re, u_im, cu, su)
         w_re, w_im = derotate(w_re, w_im, cw, sw)
-    return recompose(u_re, u_im, w_re, w_im)
+    return u_re, u_im, w_re, w_im
+
+
+def fp16_add(a, b):
+    """Correctly rounded fp16 sum of two fp16 arrays.  The exact sum of two
+    fp16 numbers spans at most 40 bits, so it is exact in float64 and the one
+    float64 -> fp16 conversion (round to nearest even) is the only rounding."""
+    a = np.asarray(a, np.float16).astype(np.float64)
+    b = np.asarray(b, np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):  # sums beyond 65504 round to +-inf, as in IEEE fp16
+        return (a + b).astype(np.float16)
+
+
+def recompose_fp16(u_re, u_im, w_re, w_im):
+    """Fused weight as the MFMA operand of the HIP kernels: U and W rounded to
+    fp16, then each coefficient one correctly rounded fp16 add in the
+    reference's recombination order (quant_i.py:534-537).  Build-defined (the
+    reference has no fp16 operand); returned as float32 holding fp16 values."""
+    ur, ui, wr, wi = (np.asarray(v, F32).astype(np.float16) for v in (u_re, u_im, w_re, w_im))
+    a11 = fp16_add(wr, ur)
+    a12 = fp16_add(wi, -ui)
+    a21 = fp16_add(wi, ui)
+    a22 = fp16_add(-wr, ur)
+    return np.concatenate(
+        [np.concatenate([a11, a12], axis=1), np.concatenate([a21, a22], axis=1)], axis=0
+    ).astype(F32)
+
+
+def wide_weight(planes, codebook: str = "axis", rotation=None, fp16: bool = False):
+    """Fused real [2N, 2K] weight of the widely-linear layer: the reference's
+    float32 A_q (quant_i.py:534-544), or with fp16=True the fp16 operand the
+    MFMA sees (recompose_fp16)."""
+    parts = wide_parts(planes, codebook, rotation)
+    return recompose_fp16(*parts) if fp16 else recompose(*parts)
+
+
+def wide_magnitude(planes, codebook: str = "axis", rotation=None):
+    """|W part| + |U part| of every fused coefficient, [2N, 2K] float64: the
+    scale of the fp16 fusing error, |recompose_fp16 - recompose| <=
+    (2u + u^2) * magnitude with u = 2^-11 (normal fp16 range)."""
+    u_re, u_im, w_re, w_im = (np.abs(np.asarray(v, np.float64)) for v in wide_parts(planes, codebook, rotation))
+    m_re, m_im = w_re + u_re, w_im + u_im
+    return np.concatenate(
+        [np.concatenate([m_re, m_im], axis=1), np.concatenate([m_im, m_re], axis=1)], axis=0)
 
 
 def wide_linear(x, planes, bias=None, codebook: str = "axis", rotation=None, fp16_weight: bool = False):
     """Widely-linear layer y = U x + W conj(x) on [re | im] features
     (phase_linear.cpp:166-207), evaluated as x @ A_q.T + b in float64.
-    fp16_weight=True rounds A_q to fp16 first (the operand the MFMA sees)."""
-    a = wide_weight(planes, codebook, rotation)
-    if fp16_weight:
-        a = a.astype(np.float16)
-    a = a.astype(np.float64)
+    fp16_weight=True uses the fp16 operand the MFMA sees (recompose_fp16)."""
+    a = wide_weight(planes, codebook, rotation, fp16=fp16_weight).astype(np.float64)
     y = np.asarray(x, np.float64) @ a.T
     if bias is not None:
         y = y + np.asarray(bias, np.float64)

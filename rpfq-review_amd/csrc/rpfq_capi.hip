@@ -130,10 +130,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
-    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_TILE_M256))
-        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
-    if ((flags & RPFQ_FLAG_TILE_M128) && (flags & RPFQ_FLAG_TILE_M256))
-        return fail(RPFQ_ERR_VALUE, "flags=%d: choose one tile height", flags);
+    if (flags & ~RPFQ_FLAG_TILE_M128) return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);

@@ -469,7 +469,7 @@ struct WideArgs {
 // LDS activation row: 32 complex columns as (re, im) fp16 pairs = 128 B,
 // padded to 144 B so the 8 lanes of a 128-bit read hit distinct banks.
 constexpr int kXRow = 144;
-constexpr int kLutWave = 32 * 32 * 8;  // 32 entries x 32 rows x float2
+constexpr int kLutWave = 32 * 32 * 4;  // 32 entries x 32 rows x fp16 pair
 
 constexpr int kTRow = 64 * 2 + 16;     // epilogue tile row: 64 fp16 outputs (+16 pad)
 
@@ -479,11 +479,31 @@ constexpr int wide_lds_bytes() {
                                                                : (4 * BM * kTRow);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed fp16 pair (one v_cvt_pk_f16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+    half2v h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Fused fp16 coefficient pairs of one code byte from its U and W entries
+// (fp16 (re, im) pairs): p1 = (A11, A12) = (Wre + Ure, Wim - Uim),
+// p2 = (A21, A22) = (Wim + Uim, -Wre + Ure), each one correctly rounded fp16
+// add in the reference's recombination order (quant_i.py:534-537); one
+// v_pk_add_f16 per pair.
+__device__ __forceinline__ void fuse_h(uint32_t U, uint32_t W, uint32_t& p1, uint32_t& p2) {
+    const half2v u = __builtin_bit_cast(half2v, U), w = __builtin_bit_cast(half2v, W);
+    p1 = __builtin_bit_cast(uint32_t, w + (half2v){u.x, -u.y});
+    p2 = __builtin_bit_cast(uint32_t, (half2v){w.y, -w.x} + (half2v){u.y, u.x});
+}
+
 // Builds the wave's LUT for scale block `blk`: entries 0..15 hold U(idx),
-// 16..31 hold W(idx), each for the wave's 32 rows; layout [entry][row] so the
-// 32 lanes of a lookup touch 32 consecutive float2 (no bank conflicts).
+// 16..31 hold W(idx) as fp16 (re, im) pairs, each for the wave's 32 rows;
+// layout [entry][row] so the 32 lanes of a lookup touch 32 consecutive
+// dwords (no bank conflicts).
 template <int CB>
-__device__ __forceinline__ void build_lut(float2* lut, const float4* params, int64_t n, bool active, int nblk,
+__device__ __forceinline__ void build_lut(uint32_t* lut, const float4* params, int64_t n, bool active, int nblk,
                                           int blk, const RotParams& rot, int r, int g) {
     float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
     if (active) {
@@ -500,17 +520,9 @@ __device__ __forceinline__ void build_lut(float2* lut, const float4* params, int
             u = derotate(u, rot.cu, rot.su);
             w = derotate(w, rot.cw, rot.sw);
         }
-        lut[idx * 32 + r] = u;
-        lut[(16 + idx) * 32 + r] = w;
+        lut[idx * 32 + r] = cvt_pk(u.x, u.y);
+        lut[(16 + idx) * 32 + r] = cvt_pk(w.x, w.y);
     }
-}
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-// Two floats -> packed fp16 pair (one v_cvt_pk_f16_f32, round to nearest even).
-__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
-    half2v h = {(_Float16)lo, (_Float16)hi};
-    return __builtin_bit_cast(uint32_t, h);
 }
 
 // 8 consecutive activations -> 8 floats (bf16 / f32 sources).
@@ -557,7 +569,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     const int ntw = ntl * 4 + wave;  // this wave's 32-row tile
     const bool active = ntw < a.NT;
     const int64_t n = (int64_t)ntw * 32 + r;
-    float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
+    uint32_t* lut = reinterpret_cast<uint32_t*>(smem + 2 * XSTAGE) + wave * 1024;
     const int64_t ldx = 2 * (int64_t)a.K;
 
     // Raw activation prefetch: the loads for k-step ks+1 are issued before
@@ -601,10 +613,10 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int c = tid + 256 * j;
-            if (c >= NCHUNK) break;
+            if (NCHUNK < 256 && c >= NCHUNK) break;
             const int row = c >> 2, sub = c & 3;
-            uint4 o0 = make_uint4(0, 0, 0, 0), o1 = make_uint4(0, 0, 0, 0);
-            if ((xok >> j) & 1u) {
+            uint4 o0, o1;
+            {
                 if (XDT == RPFQ_F16) {
                     const uint4 vr = xraw[j][0], vi = xraw[j][1];
                     // interleave (re, im) halves: perm selects bytes of (vi, vr)
@@ -643,13 +655,21 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
                                     cvt_pk(fr[7], fi[7]));
                 }
             }
+            // branch-free zero fill of out-of-range chunks: the waitcnt pass
+            // then sees straight-line code and keeps the prefetch in flight
+            const uint32_t keep = 0u - ((xok >> j) & 1u);
+            o0 = make_uint4(o0.x & keep, o0.y & keep, o0.z & keep, o0.w & keep);
+            o1 = make_uint4(o1.x & keep, o1.y & keep, o1.z & keep, o1.w & keep);
             uint4* dst = reinterpret_cast<uint4*>(xs + row * kXRow + sub * 32);
             dst[0] = o0;
             dst[1] = o1;
         }
     };
+    // Inactive waves (past the last 32-row tile) read tile NT-1 and never
+    // store: loads stay unconditional so the wait counts stay exact.
+    const int ntw_ld = active ? ntw : a.NT - 1;
     auto load_codes = [&](int ks) -> uint4 {
-        return active ? a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g] : make_uint4(0, 0, 0, 0);
+        return a.codes[(((int64_t)ntw_ld * a.KS + ks) * 32 + r) * 2 + g];
     };
 
     floatx16 acc_re[MB], acc_im[MB];
@@ -660,27 +680,29 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
     load_x(0, xbufA, okA);
     cA = load_codes(0);
-    store_x(0, xbufA, okA);
-    if (a.KS > 1) {
-        load_x(1, xbufB, okB);
-        cB = load_codes(1);
+    {
+        const int k1 = a.KS > 1 ? 1 : 0;
+        load_x(k1, xbufB, okB);
+        cB = load_codes(k1);
     }
+    store_x(0, xbufA, okA);
     __syncthreads();
 
     // One k-step: prefetch k-step ks+2 into `fill`, run the MFMAs of ks, stage
     // k-step ks+1 (waiting in `next`) into the other LDS buffer.
     auto kstep = [&](int ks, const uint4 cw, uint4 (&next)[CPT][RAW], uint32_t next_ok, uint4 (&fill)[CPT][RAW],
                      uint32_t& fill_ok, uint4& fill_codes) {
-        if (ks + 2 < a.KS) {
-            load_x(ks + 2, fill, fill_ok);
-            fill_codes = load_codes(ks + 2);
+        {   // unconditional: past the end the last k-step is reloaded, unused
+            const int kp = ks + 2 < a.KS ? ks + 2 : a.KS - 1;
+            load_x(kp, fill, fill_ok);
+            fill_codes = load_codes(kp);
         }
         const char* xs = smem + (ks & 1) * XSTAGE;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const uint32_t word = s == 0 ? cw.x : s == 1 ? cw.y : s == 2 ? cw.z : cw.w;
             // issue every LDS read of the substep first: 8 LUT entries, MB operands
-            float2 U[4], W[4];
+            uint32_t U[4], W[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t byte = (word >> (8 * e)) & 0xffu;
@@ -693,11 +715,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
                 ax[i] = *reinterpret_cast<const half8*>(xs + (i * 32 + r) * kXRow + (8 * s + 4 * g) * 4);
             uint32_t bre[4], bim[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // fused coefficients in the reference's order (quant_i.py:534-537)
-                bre[e] = cvt_pk(W[e].x + U[e].x, W[e].y - U[e].y);   // (A11, A12)
-                bim[e] = cvt_pk(W[e].y + U[e].y, -W[e].x + U[e].x);  // (A21, A22)
-            }
+            for (int e = 0; e < 4; ++e) fuse_h(U[e], W[e], bre[e], bim[e]);  // (A11, A12), (A21, A22)
             const half8 b_re = as_half8(make_uint4(bre[0], bre[1], bre[2], bre[3]));
             const half8 b_im = as_half8(make_uint4(bim[0], bim[1], bim[2], bim[3]));
 #pragma unroll
@@ -790,245 +808,294 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     }
 }
 
-// Large-M widely-linear GEMM.  Workgroup = 4 waves, one per SIMD; tile =
-// 256 rows of x times 128 complex output rows; wave w owns complex rows
-// 32w..32w+31 for all 256 rows.  Compared with wide_linear_kernel every
-// decoded coefficient feeds twice as many MFMAs (LUT bytes per MFMA halve),
-// the accumulators (256 fp32) live in AGPRs, and the work of a substep is
-// software pipelined: the LUT and activation reads of substep s+1 are issued
-// before the MFMAs of substep s.  The MFMA computes the transposed product
-// (decoded weights as the A operand), so each lane ends with 4 consecutive
-// outputs of one row and the epilogue stores straight from registers.
-constexpr int kBigBM = 256;
+// ---------------------------------------------------------------------------
+// widely-linear GEMM, fp16 activations staged by LDS DMA (large M)
+// ---------------------------------------------------------------------------
+// Workgroup = 4 waves, tile = 128 rows of x times 128 complex output rows;
+// wave w owns complex rows 32w..32w+31 (both their real and imaginary
+// outputs) for all 128 rows, as in wide_linear_kernel.  Differences:
+//   * activations and codes go global -> LDS by DMA (global_load_lds_dwordx4):
+//     no registers hold in-flight loads and no VALU work converts them; a
+//     3-stage activation ring keeps two k-steps of loads in flight;
+//   * an LDS activation row is the k-step's 8 chunks of 16 B (re cols 0-7,
+//     8-15, 16-23, 24-31, then im), chunk c stored at slot c ^ ((row>>1)&7)
+//     so the MFMA operand reads hit distinct banks;
+//   * MFMA k order: substep s covers complex columns c0 = 8s .. 8s+7; lanes
+//     0-31 hold re c0..c0+7 and lanes 32-63 im c0..c0+7 (one 16-B read each);
+//     the matching B operand is A11 (or A21) of the 8 columns on lanes 0-31
+//     and A12 (or A22) on lanes 32-63.  Each lane still decodes the 4 columns
+//     c0 + 4g + e of its code word; v_perm_b32 groups the coefficients by kind
+//     and v_permlane32_swap_b32 trades the half the other lane group needs;
+//   * the LUT is [entry][row] fp16 (re, im) pairs (conflict-free lookups);
+//   * per substep the 12 LDS reads of substep s+1 are issued before the MFMAs
+//     of substep s and its decode runs beside the last 4 of them (fenced with
+//     sched_barrier); one raw barrier per k-step with explicit wait counts
+//     keeps the DMA prefetch in flight (a __syncthreads fence would drain it).
+// Requires K' % 32 == 0 and M >= 128; the last row tile starts at M - 128 so
+// every DMA row is inside x (rows shared with the previous tile are written
+// twice with the same values).
+constexpr int kDmaBM = 128;
+constexpr int kDmaStage = kDmaBM * 128;                           // 16384 B
+constexpr int kDmaStages = 3;
+constexpr int kDmaLutWave = 32 * 32 * 4;                          // [entry][row] fp16 pairs
+constexpr int kDmaEpiRows = 64;                                   // epilogue half tile
+constexpr int kDmaCodes = 4 * 1024;                               // codes of one k-step, 4 waves
+constexpr int kDmaLds = kDmaStages * kDmaStage + 2 * kDmaCodes + 4 * kDmaLutWave;  // 73728 B
+static_assert(4 * kDmaEpiRows * kTRow <= kDmaStages * kDmaStage, "epilogue tile fits the stages");
 
-constexpr int wide_big_lds_bytes() { return 2 * kBigBM * kXRow + 4 * kLutWave; }
+typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
+typedef __attribute__((address_space(3))) const half8* lds_h8_t;
 
-template <int XDT, int YDT, int CB>
-__global__ void __launch_bounds__(256, 1) wide_linear_big_kernel(WideArgs a) {
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
+}
+
+// LDS DMA: lane l copies 16 B from gbase + voff[l] to LDS address lds + 16 l.
+// Written as asm so that the compiler's wait-count pass does not see the LDS
+// write (it would otherwise wait for every outstanding DMA before each LDS
+// read); every consumer waits explicitly (s_waitcnt vmcnt + s_barrier)
+// before reading the destination.
+__device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
+}
+
+template <int YDT, int CB>
+__global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
-    constexpr int BM = kBigBM;
-    constexpr int MB = BM / 32;
-    constexpr int XSTAGE = BM * kXRow;
-    constexpr int CPT = BM / 64;
-    constexpr int RAW = (XDT == RPFQ_F32) ? 4 : 2;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int MB = kDmaBM / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31, g = lane >> 5;
     const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
-    const int64_t m0 = (int64_t)mt * BM;
+    const int64_t m0 = min((int64_t)mt * kDmaBM, a.M - kDmaBM);
     const int ntw = ntl * 4 + wave;
     const bool active = ntw < a.NT;
+    const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
     const int64_t n = (int64_t)ntw * 32 + r;
-    float2* lut = reinterpret_cast<float2*>(smem + 2 * XSTAGE) + wave * 1024;
-    const int64_t ldx = 2 * (int64_t)a.K;
 
-    uint4 xraw[CPT][RAW];
-    uint32_t xok = 0;
-    uint4 creg = make_uint4(0, 0, 0, 0);
+    char* stages = smem;
+    char* cbufs = smem + kDmaStages * kDmaStage;  // two k-steps of codes
+    uint32_t* lut = reinterpret_cast<uint32_t*>(cbufs + 2 * kDmaCodes) + wave * (32 * 32);
+    const uint32_t lut_r = lds_addr(lut + r);  // LDS byte address of entry 0 of this lane's row
+    uint32_t entry_bytes;  // 128 (one LUT entry = 32 rows x 4 B), opaque so that
+    asm("s_mov_b32 %0, 128" : "=s"(entry_bytes));  // the address stays v_bfe + v_mad
 
-    auto load_x = [&](int ks) {
-        xok = 0;
+    // Activation DMA: wave w fills rows 32w .. 32w+31 of a stage with 4
+    // 1-KB loads of 8 rows; lane l writes row l >> 3, slot l & 7, which holds
+    // chunk (l & 7) ^ ((row >> 1) & 7).  The swizzle depends on the load's
+    // parity (row >> 1 = 16w + 4j + (l >> 4)), hence two lane offsets.
+    const int64_t ldx = 2 * (int64_t)a.K;  // fp16 elements per x row
+    uint32_t voff[2];
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = tid + 256 * j;
-            const int row = c >> 2, sub = c & 3;
-            const int64_t m = m0 + row;
-            const int kk = ks * 32 + sub * 8;
-            const bool ok = m < a.M && kk < a.K;
-            xok |= (ok ? 1u : 0u) << j;
-            const int64_t off = ok ? m * ldx + kk : 0;
-            if (XDT == RPFQ_F32) {
-                const uint4* pr = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off);
-                const uint4* pi = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(a.x) + off + a.K);
-                xraw[j][0] = pr[0];
-                xraw[j][1] = pr[1];
-                xraw[j][RAW - 2] = pi[0];
-                xraw[j][RAW - 1] = pi[1];
-            } else {
-                xraw[j][0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off);
-                xraw[j][1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + off + a.K);
-            }
-        }
+    for (int jp = 0; jp < 2; ++jp) {
+        const int chunk = (lane & 7) ^ ((4 * jp + (lane >> 4)) & 7);
+        voff[jp] = (uint32_t)((lane >> 3) * ldx * 2 + (chunk >> 2) * (int64_t)a.K * 2 + (chunk & 3) * 16);
+    }
+    const char* xw = reinterpret_cast<const char*>(a.x) + (m0 + 32 * wave) * ldx * 2;
+    const uint32_t lds_stages = lds_addr(stages) + 32 * wave * 128;
+    auto issue_x = [&](int ks, int stage) {
+        const char* src = xw + ks * 64;
+        const uint32_t dst = lds_stages + stage * kDmaStage;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma_dwordx4(src + 8 * j * ldx * 2, voff[j & 1], dst + j * 1024);
     };
-    auto store_x = [&](int stage) {
-        char* xs = smem + stage * XSTAGE;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int c = tid + 256 * j;
-            const int row = c >> 2, sub = c & 3;
-            uint4 o0 = make_uint4(0, 0, 0, 0), o1 = make_uint4(0, 0, 0, 0);
-            if ((xok >> j) & 1u) {
-                if (XDT == RPFQ_F16) {
-                    const uint4 vr = xraw[j][0], vi = xraw[j][1];
-                    o0.x = __builtin_amdgcn_perm(vi.x, vr.x, 0x05040100u);
-                    o0.y = __builtin_amdgcn_perm(vi.x, vr.x, 0x07060302u);
-                    o0.z = __builtin_amdgcn_perm(vi.y, vr.y, 0x05040100u);
-                    o0.w = __builtin_amdgcn_perm(vi.y, vr.y, 0x07060302u);
-                    o1.x = __builtin_amdgcn_perm(vi.z, vr.z, 0x05040100u);
-                    o1.y = __builtin_amdgcn_perm(vi.z, vr.z, 0x07060302u);
-                    o1.z = __builtin_amdgcn_perm(vi.w, vr.w, 0x05040100u);
-                    o1.w = __builtin_amdgcn_perm(vi.w, vr.w, 0x07060302u);
-                } else {
-                    float fr[8], fi[8];
-                    if (XDT == RPFQ_BF16) {
-                        const uint32_t wr[4] = {xraw[j][0].x, xraw[j][0].y, xraw[j][0].z, xraw[j][0].w};
-                        const uint32_t wi[4] = {xraw[j][1].x, xraw[j][1].y, xraw[j][1].z, xraw[j][1].w};
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            fr[2 * t] = bf16_to_f32(wr[t] & 0xffffu);
-                            fr[2 * t + 1] = bf16_to_f32(wr[t] >> 16);
-                            fi[2 * t] = bf16_to_f32(wi[t] & 0xffffu);
-                            fi[2 * t + 1] = bf16_to_f32(wi[t] >> 16);
-                        }
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < 2; ++t) {
-                            const float4 r4 = __builtin_bit_cast(float4, xraw[j][t]);
-                            const float4 i4 = __builtin_bit_cast(float4, xraw[j][RAW - 2 + t]);
-                            fr[4 * t] = r4.x; fr[4 * t + 1] = r4.y; fr[4 * t + 2] = r4.z; fr[4 * t + 3] = r4.w;
-                            fi[4 * t] = i4.x; fi[4 * t + 1] = i4.y; fi[4 * t + 2] = i4.z; fi[4 * t + 3] = i4.w;
-                        }
-                    }
-                    o0 = make_uint4(cvt_pk(fr[0], fi[0]), cvt_pk(fr[1], fi[1]), cvt_pk(fr[2], fi[2]),
-                                    cvt_pk(fr[3], fi[3]));
-                    o1 = make_uint4(cvt_pk(fr[4], fi[4]), cvt_pk(fr[5], fi[5]), cvt_pk(fr[6], fi[6]),
-                                    cvt_pk(fr[7], fi[7]));
-                }
-            }
-            uint4* dst = reinterpret_cast<uint4*>(xs + row * kXRow + sub * 32);
-            dst[0] = o0;
-            dst[1] = o1;
-        }
+    // Codes: one 1-KB block per wave and k-step; lane l fetches the uint4 of
+    // MFMA lane l (row l & 31, half l >> 5) so the reads are consecutive.
+    const char* cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)ntw_ld * a.KS * 64);
+    const uint32_t cw_voff = (uint32_t)((2 * (lane & 31) + (lane >> 5)) * 16);
+    const uint32_t lds_codes = lds_addr(cbufs) + wave * 1024;
+    auto issue_codes = [&](int ks, int buf) {
+        dma_dwordx4(cw_src + (int64_t)ks * 1024, cw_voff, lds_codes + buf * kDmaCodes);
     };
-    auto load_codes = [&](int ks) {
-        if (active) creg = a.codes[(((int64_t)ntw * a.KS + ks) * 32 + r) * 2 + g];
+    auto read_codes = [&](int buf) -> uint4 {
+        return *reinterpret_cast<const uint4*>(cbufs + buf * kDmaCodes + wave * 1024 + lane * 16);
     };
-    auto lut_read = [&](uint32_t word, float2* U, float2* W) {
+    // MFMA operand of row R = 32 i + r, substep s: chunk 4 g + s of row R, at
+    // slot (4 g + s) ^ ((r >> 1) & 7); the stage and i parts are immediates
+    uint32_t aoff[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t byte = (word >> (8 * e)) & 0xffu;
-            U[e] = lut[(byte & 15u) * 32 + r];
-            W[e] = lut[(16u + (byte >> 4)) * 32 + r];
-        }
-    };
+    for (int s = 0; s < 4; ++s) aoff[s] = lds_addr(stages) + r * 128 + (((4 * g + s) ^ ((r >> 1) & 7)) * 16);
 
     floatx16 acc_re[MB], acc_im[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
     int cur_blk = 0;
-    build_lut<CB>(lut, a.params, n, active, a.nblk, 0, a.rot, r, g);
-    load_x(0);
-    load_codes(0);
-    store_x(0);
-    __syncthreads();
+    build_lut<CB>(lut, a.params, (int64_t)ntw_ld * 32 + r, true, a.nblk, 0, a.rot, r, g);
+    issue_codes(0, 0);
+    issue_x(0, 0);
+    issue_x(a.KS > 1 ? 1 : 0, 1);
+    // codes and stage 0 landed (at most the 4 newest loads in flight), LUT written
+    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
-    for (int ks = 0; ks < a.KS; ++ks) {
-        const uint4 cw = creg;
+    // One k-step on stage `st`: first the codes of k-step ks + 1 and the
+    // activations of ks + 2 (into the buffers read at ks - 1, free since the
+    // last barrier; past the end the last k-step is reloaded, unused), then
+    // the math.  The loop below is unrolled by 3 so stage offsets are static.
+    auto kstep = [&](int ks, int st) {
+        issue_codes(ks + 1 < a.KS ? ks + 1 : a.KS - 1, (ks + 1) & 1);
+        issue_x(ks + 2 < a.KS ? ks + 2 : a.KS - 1, st == 0 ? 2 : st - 1);
+        const uint4 cw = read_codes(ks & 1);
         const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
-        const bool more = ks + 1 < a.KS;
-        const char* xs = smem + (ks & 1) * XSTAGE;
-        const char* arow = xs + r * kXRow + 16 * g;  // (8 s + 4 g) * 4 bytes into the row
-        float2 Un[4], Wn[4];
-        half8 an[MB];
-        lut_read(words[0], Un, Wn);
+        auto read_sub = [&](int s, uint32_t (&U)[4], uint32_t (&W)[4], half8 (&ax)[MB]) {
+            const uint32_t word = words[s];
 #pragma unroll
-        for (int i = 0; i < MB; ++i) an[i] = *reinterpret_cast<const half8*>(arow + i * 32 * kXRow);
-        if (more) {
-            load_x(ks + 1);
-            load_codes(ks + 1);
-        }
+            for (int e = 0; e < 4; ++e) {  // [entry][row] LUT (128-B entries): 32 lanes hit 32 banks
+                const uint32_t au = __umul24(__builtin_amdgcn_ubfe(word, 8 * e, 4), entry_bytes) + lut_r;
+                const uint32_t aw = __umul24(__builtin_amdgcn_ubfe(word, 8 * e + 4, 4), entry_bytes) + lut_r;
+                U[e] = *((lds_u32_t)au);
+                W[e] = *((lds_u32_t)aw + 16 * 32);
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) ax[i] = *((lds_h8_t)aoff[s] + (st * kDmaStage + i * 4096) / 16);
+        };
+        auto decode = [&](const uint32_t (&U)[4], const uint32_t (&W)[4], half8& b_re, half8& b_im) {
+            uint32_t p1[4], p2[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) fuse_h(U[e], W[e], p1[e], p2[e]);
+            // group by kind: x = (A11 | A21) pairs, y = (A12 | A22) pairs of
+            // this lane's 4 columns, then trade x of lanes 32-63 for y of
+            // lanes 0-31 so lanes 0-31 hold the re-column coefficients of all
+            // 8 columns and lanes 32-63 the im-column ones
+            uint32_t xr0 = __builtin_amdgcn_perm(p1[1], p1[0], 0x05040100u);
+            uint32_t xr1 = __builtin_amdgcn_perm(p1[3], p1[2], 0x05040100u);
+            uint32_t yr0 = __builtin_amdgcn_perm(p1[1], p1[0], 0x07060302u);
+            uint32_t yr1 = __builtin_amdgcn_perm(p1[3], p1[2], 0x07060302u);
+            uint32_t xi0 = __builtin_amdgcn_perm(p2[1], p2[0], 0x05040100u);
+            uint32_t xi1 = __builtin_amdgcn_perm(p2[3], p2[2], 0x05040100u);
+            uint32_t yi0 = __builtin_amdgcn_perm(p2[1], p2[0], 0x07060302u);
+            uint32_t yi1 = __builtin_amdgcn_perm(p2[3], p2[2], 0x07060302u);
+            const auto sr0 = __builtin_amdgcn_permlane32_swap(xr0, yr0, false, false);
+            const auto sr1 = __builtin_amdgcn_permlane32_swap(xr1, yr1, false, false);
+            const auto si0 = __builtin_amdgcn_permlane32_swap(xi0, yi0, false, false);
+            const auto si1 = __builtin_amdgcn_permlane32_swap(xi1, yi1, false, false);
+            b_re = as_half8(make_uint4(sr0[0], sr1[0], sr0[1], sr1[1]));
+            b_im = as_half8(make_uint4(si0[0], si1[0], si0[1], si1[1]));
+        };
+        uint32_t U[4], W[4];
+        half8 ax_c[MB], b_re, b_im;
+        read_sub(0, U, W, ax_c);
+        decode(U, W, b_re, b_im);
+        // Substep pipeline, fenced so the scheduler keeps it: (1) LUT
+        // addresses and the 12 LDS reads of substep s+1; (2) 4 MFMAs of
+        // substep s, covering the LDS latency; (3) the decode of s+1 next to
+        // the other 4 MFMAs of s.
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float2 U[4], W[4];
-            half8 ac[MB];
+            half8 ax_n[MB];
+            if (s < 3) read_sub(s + 1, U, W, ax_n);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                U[e] = Un[e];
-                W[e] = Wn[e];
+            for (int i = 0; i < MB / 2; ++i) {
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_re, acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_im, acc_im[i], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < MB; ++i) ac[i] = an[i];
-            if (s < 3) {  // issue the next substep's LDS reads before this substep's MFMAs
-                lut_read(words[s + 1], Un, Wn);
-#pragma unroll
-                for (int i = 0; i < MB; ++i)
-                    an[i] = *reinterpret_cast<const half8*>(arow + i * 32 * kXRow + 32 * (s + 1));
+            for (int i = MB / 2; i < MB; ++i) {
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_re, acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_im, acc_im[i], 0, 0, 0);
             }
-            uint32_t bre[4], bim[4];
+            if (s < 3) {
+                decode(U, W, b_re, b_im);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // fused coefficients in the reference's order (quant_i.py:534-537)
-                bre[e] = cvt_pk(W[e].x + U[e].x, W[e].y - U[e].y);   // (A11, A12)
-                bim[e] = cvt_pk(W[e].y + U[e].y, -W[e].x + U[e].x);  // (A21, A22)
+                for (int i = 0; i < MB; ++i) ax_c[i] = ax_n[i];
             }
-            const half8 b_re = as_half8(make_uint4(bre[0], bre[1], bre[2], bre[3]));
-            const half8 b_im = as_half8(make_uint4(bim[0], bim[1], bim[2], bim[3]));
-#pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_re, ac[i], acc_re[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_im, ac[i], acc_im[i], 0, 0, 0);
-            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (more) {
-            store_x((ks + 1) & 1);
+        if (ks + 1 < a.KS) {
             const int nb = (ks + 1) / a.block_ks;
-            if (nb != cur_blk) {
-                __syncthreads();
-                build_lut<CB>(lut, a.params, n, active, a.nblk, nb, a.rot, r, g);
+            if (nb != cur_blk) {  // new scale block: this wave's LUT rows only
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                build_lut<CB>(lut, a.params, (int64_t)ntw_ld * 32 + r, true, a.nblk, nb, a.rot, r, g);
                 cur_blk = nb;
             }
         }
-        __syncthreads();
+        // codes ks + 1 and stage ks + 1 landed: only the 4 newest loads
+        // (activations of ks + 2) may still be in flight; every LDS read of
+        // this k-step is complete
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    int ks = 0;
+    for (; ks + 3 <= a.KS; ks += 3) {
+        kstep(ks, 0);
+        kstep(ks + 1, 1);
+        kstep(ks + 2, 2);
     }
+    if (ks < a.KS) kstep(ks, 0);
+    if (ks + 1 < a.KS) kstep(ks + 1, 1);
+    // the clamped tail loads may still target the stages: drain before reuse
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
-    if (!active) return;
-    // epilogue: lane holds C^T[n][m] for m = m0 + 32 i + r and
-    // n = 32 ntw + 8 j + 4 g + t (t = 0..3) in acc[i][4 j + t]
+    const bool n_ok = active && n < a.N;
+    const float br = (a.bias && n_ok) ? a.bias[n] : 0.0f;
+    const float bi = (a.bias && n_ok) ? a.bias[a.N + n] : 0.0f;
     const int64_t ldy = 2 * (int64_t)a.N;
-    float4 bias[2][4];
+    if (YDT == RPFQ_F32) {
+        if (!n_ok) return;
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+        for (int i = 0; i < MB; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t n0 = (int64_t)ntw * 32 + 8 * j + 4 * g;
-            float b4[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) b4[t] = (a.bias && n0 + t < a.N) ? a.bias[p * a.N + n0 + t] : 0.0f;
-            bias[p][j] = make_float4(b4[0], b4[1], b4[2], b4[3]);
+            for (int v = 0; v < 16; ++v) {
+                const int64_t m = m0 + i * 32 + acc_row(v, g);
+                store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
+                store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+            }
         }
+        return;
+    }
+    // 16-bit outputs: transpose through LDS in two 64-row halves, then write
+    // 16-byte chunks (per row: 32 real then 32 imaginary outputs of the wave)
+    uint16_t* tt = reinterpret_cast<uint16_t*>(smem + wave * (kDmaEpiRows * kTRow));
+    const int64_t nbase = (int64_t)ntw * 32;
+    const int q = lane & 7;
+    const int64_t col0 = (q < 4 ? 0 : a.N) + nbase + 8 * (q & 3);
+    const int64_t nfirst = nbase + 8 * (q & 3);
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int64_t m = m0 + i * 32 + r;
-        if (m >= a.M) break;
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const floatx16& acc = p ? acc_im[i] : acc_re[i];
+        for (int ii = 0; ii < MB / 2; ++ii) {
+            const int i = h * (MB / 2) + ii;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int64_t n0 = (int64_t)ntw * 32 + 8 * j + 4 * g;
-                const float v0 = acc[4 * j] + bias[p][j].x, v1 = acc[4 * j + 1] + bias[p][j].y;
-                const float v2 = acc[4 * j + 2] + bias[p][j].z, v3 = acc[4 * j + 3] + bias[p][j].w;
-                const int64_t off = m * ldy + p * a.N + n0;
-                if (a.vec_store && n0 + 4 <= a.N) {
-                    if (YDT == RPFQ_F32) {
-                        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.y) + off) = make_float4(v0, v1, v2, v3);
-                    } else if (YDT == RPFQ_F16) {
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + off) =
-                            make_uint2(cvt_pk(v0, v1), cvt_pk(v2, v3));
-                    } else {
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + off) =
-                            make_uint2((uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16),
-                                       (uint32_t)f32_to_bf16(v2) | ((uint32_t)f32_to_bf16(v3) << 16));
-                    }
+            for (int v = 0; v < 16; ++v) {
+                const int row = ii * 32 + acc_row(v, g);
+                uint16_t hr, hi;
+                if (YDT == RPFQ_F16) {
+                    hr = __builtin_bit_cast(uint16_t, (_Float16)(acc_re[i][v] + br));
+                    hi = __builtin_bit_cast(uint16_t, (_Float16)(acc_im[i][v] + bi));
                 } else {
-                    const float vv[4] = {v0, v1, v2, v3};
-                    for (int t = 0; t < 4; ++t)
-                        if (n0 + t < a.N) store1<YDT>(a.y, off + t, vv[t]);
+                    hr = f32_to_bf16(acc_re[i][v] + br);
+                    hi = f32_to_bf16(acc_im[i][v] + bi);
+                }
+                tt[row * (kTRow / 2) + r] = hr;
+                tt[row * (kTRow / 2) + 32 + r] = hi;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        if (active) {
+#pragma unroll
+            for (int row = lane >> 3; row < kDmaEpiRows; row += 8) {
+                const int64_t m = m0 + h * kDmaEpiRows + row;
+                const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tt) + row * kTRow + q * 16);
+                uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
+                if (a.vec_store && nfirst + 8 <= a.N) {
+                    *reinterpret_cast<uint4*>(dst) = v;
+                } else {
+                    const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
+                    for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = hv[t];
                 }
             }
         }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads of this half done before the next overwrite
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1053,11 +1120,14 @@ __global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const floa
         W = derotate(W, rot.cw, rot.sw);
     }
     float a11 = W.x + U.x, a12 = W.y - U.y, a21 = W.y + U.y, a22 = -W.x + U.x;
-    if (round_fp16) {
-        a11 = (float)(_Float16)a11;
-        a12 = (float)(_Float16)a12;
-        a21 = (float)(_Float16)a21;
-        a22 = (float)(_Float16)a22;
+    if (round_fp16) {  // the MFMA operand: fp16 U, W and one fp16 add each (fuse_h)
+        uint32_t p1, p2;
+        fuse_h(cvt_pk(U.x, U.y), cvt_pk(W.x, W.y), p1, p2);
+        const half2v h1 = __builtin_bit_cast(half2v, p1), h2 = __builtin_bit_cast(half2v, p2);
+        a11 = (float)h1.x;
+        a12 = (float)h1.y;
+        a21 = (float)h2.x;
+        a22 = (float)h2.y;
     }
     int64_t ld = 2 * K;
     out[n * ld + k] = a11;
@@ -1223,25 +1293,24 @@ static hipError_t wide_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int XDT, int YDT, int CB>
-static hipError_t wide_big_go(WideArgs& a, hipStream_t s) {
+template <int YDT, int CB>
+static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
-    constexpr int lds = wide_big_lds_bytes();
     std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_big_kernel<XDT, YDT, CB>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_dma_kernel<YDT, CB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
     });
     if (attr_err != hipSuccess) return attr_err;
-    a.tiles_m = (int)((a.M + kBigBM - 1) / kBigBM);
+    a.tiles_m = (int)((a.M + kDmaBM - 1) / kDmaBM);
     a.tiles_n = (int)((a.NT + 3) / 4);
-    hipLaunchKernelGGL((wide_linear_big_kernel<XDT, YDT, CB>), dim3(a.tiles_m * a.tiles_n), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((wide_linear_dma_kernel<YDT, CB>), dim3(a.tiles_m * a.tiles_n), dim3(256), kDmaLds, s, a);
     return hipGetLastError();
 }
 
 template <int XDT, int YDT, int CB>
 static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
-    if (flags & RPFQ_FLAG_TILE_M256) return wide_big_go<XDT, YDT, CB>(a, s);
+    if (XDT == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= kDmaBM) return wide_dma_go<YDT, CB>(a, s);
     if (flags & RPFQ_FLAG_TILE_M128) return wide_go<128, XDT, YDT, CB>(a, s);
     if (a.M <= 32) return wide_go<32, XDT, YDT, CB>(a, s);
     if (a.M <= 64) return wide_go<64, XDT, YDT, CB>(a, s);

@@ -143,7 +143,7 @@ class PackedWide:
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, flags: int = 0) -> torch.Tensor:
         """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
-        flags: 0 or a tile-height hint (_native.FLAG_TILE_M128 / _M256)."""
+        flags: 0 (kernel chosen from the shape) or _native.FLAG_TILE_M128."""
         N.require_device(x, bias)
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")

@@ -72,7 +72,7 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 3, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 2, None) == 6
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 8, None) == 6
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 16, p, 1, 4, None, p, 1, 0, None) == 2
     assert L.rpfq_wide_linear(ctypes.byref(d), ctypes.c_void_p(258), 1 << 20, p, 1, 4, None, p, 1, 0, None) == 3

@@ -203,7 +203,28 @@ def build_packed(r, case):
         rotation = tuple((np.float32(c), np.float32(s)) for c, s in rot)
     oplanes = oracle_planes(planes_np, sre, sim, kinds, k_c, block)
     a_ref = O.wide_weight(oplanes, codebook, rotation)
+    build_packed.last_oplanes, build_packed.last_rotation = oplanes, rotation
     return pw, oplanes, a_ref, codebook, rotation
+
+
+def check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp=0.0):
+    """y from the HIP kernel vs the oracle on the same operands.
+    (a) tight: the exact product with the fp16 coefficients the MFMA sees
+        (oracle.recompose_fp16), float32 accumulation error only;
+    (b) against the reference's float32 A_q: the fp16 fusing bound
+        |A16 - A_q| <= (2u + u^2) (|W| + |U|), u = 2^-11, per coefficient."""
+    bias = np.zeros(0) if bias is None else bias
+    b = bias if bias.size else 0.0
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    a = O.wide_weight(oplanes, codebook, rotation).astype(np.float64)
+    mag = O.wide_magnitude(oplanes, codebook, rotation)
+    ax = np.abs(xf)
+    y16 = xf @ a16.T + b
+    scale = ax @ np.abs(a16).T + np.abs(b)
+    assert np.all(np.abs(y - y16) <= 1e-5 * scale + out_ulp * np.abs(y16) + 1e-5)
+    yex = xf @ a.T + b
+    u = 2.0 ** -11
+    assert np.all(np.abs(y - yex) <= (2 * u + u * u) * (ax @ mag.T) + 1e-5 * scale + out_ulp * np.abs(y16) + 1e-5)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
@@ -215,10 +236,10 @@ def test_wide_decode_bit_exact(case):
     assert a.shape == a_ref.shape
     assert np.array_equal(a, a_ref)
     a16 = pw.decode(round_fp16=True).cpu().numpy()
-    assert np.array_equal(a16, a_ref.astype(np.float16).astype(np.float32))
+    assert np.array_equal(a16, O.wide_weight(build_packed.last_oplanes, case[2], build_packed.last_rotation, fp16=True))
 
 
-@pytest.mark.parametrize("m", [1, 5, 31, 64, 65, 300])
+@pytest.mark.parametrize("m", [1, 5, 31, 64, 65, 128, 129, 300])
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
                                              for c in CASES])
 def test_wide_linear(case, m):
@@ -229,29 +250,23 @@ def test_wide_linear(case, m):
     bias = r.standard_normal(2 * case[0]).astype(np.float32)
     y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
     xf = x.float().numpy().astype(np.float64)
-    # (a) tight: the exact product of the operands the MFMA sees
-    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T + bias
-    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T + np.abs(bias)
-    assert np.all(np.abs(y - y16) <= 1e-5 * scale + 1e-5)
-    # (b) against the exact reference weight: fp16 coefficient rounding bound
-    yex = xf @ a_ref.astype(np.float64).T + bias
-    assert np.all(np.abs(y - yex) <= 2.0 ** -11 * scale + 1e-5)
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
 
 
+@pytest.mark.parametrize("m", [77, 300])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
-                                     (torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
-def test_wide_linear_dtypes(xdt, ydt):
+                                     (torch.float16, torch.float16), (torch.bfloat16, torch.float32),
+                                     (torch.float16, torch.bfloat16)])
+def test_wide_linear_dtypes(xdt, ydt, m):
     r = rng(300)
     case = (160, 128, "axis", 2, 0, None)
-    pw, oplanes, a_ref, _, _ = build_packed(r, case)
-    x = torch.from_numpy(r.standard_normal((77, 256)).astype(np.float32)).to(xdt)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 256)).astype(np.float32)).to(xdt)
     y = pw.linear(x.to(DEV), None, out_dtype=ydt).float().cpu().numpy()
     # the kernel converts x to fp16 on load: reference on the same operands
     xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
-    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T
-    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T
     out_ulp = {torch.float32: 1e-6, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
-    assert np.all(np.abs(y - y16) <= 1e-5 * scale + out_ulp * np.abs(y16) + 1e-5)
+    check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
 
 
 def test_wide_linear_matches_reference_android_runtime():
@@ -276,24 +291,40 @@ def test_wide_linear_matches_reference_android_runtime():
     pw = ops.PackedWide.from_planes([tdev(O.pack_codes(p)) for p in planes], inv_re, inv_im, n_c, k_c,
                                     N.CB_AXIS, 2, 0, None)
     y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
-    a = O.wide_weight([(p, O.inv_gamma(gr)[:, 0], O.inv_gamma(gi)[:, 0], kd) for p, gr, gi, kd in
-                       zip(planes, g_re, g_im, "uuww")])
-    scale = np.abs(xf.astype(np.float64)) @ np.abs(a.astype(np.float64)).T + np.abs(bias)
-    assert np.all(np.abs(y - y_ref) <= 2.0 ** -11 * scale + 1e-4)
+    op = [(p, O.inv_gamma(gr)[:, 0], O.inv_gamma(gi)[:, 0], kd) for p, gr, gi, kd in zip(planes, g_re, g_im, "uuww")]
+    a = O.wide_weight(op)
+    mag = O.wide_magnitude(op)
+    ax = np.abs(xf.astype(np.float64))
+    scale = ax @ np.abs(a.astype(np.float64)).T + np.abs(bias)
+    u = 2.0 ** -11
+    assert np.all(np.abs(y - y_ref) <= (2 * u + u * u) * (ax @ mag.T) + 1e-5 * scale + 1e-4)
 
 
-@pytest.mark.parametrize("flags", [1, 2])
-@pytest.mark.parametrize("m", [33, 300, 513])
+@pytest.mark.parametrize("flags", [0, 1])
+@pytest.mark.parametrize("m", [33, 128, 300, 513])
 @pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[4], CASES[7]],
                          ids=["1536x384", "50x48", "130x512-b256", "rot"])
-def test_wide_linear_tile_hints(case, m, flags):
-    """Both tile heights (RPFQ_FLAG_TILE_M128 / _M256) give the same bound."""
+def test_wide_linear_kernels_agree(case, m, flags):
+    """The LDS-DMA kernel (flags 0, fp16 x, K' % 32 == 0, M >= 128) and the
+    register-staged kernel (RPFQ_FLAG_TILE_M128) meet the same bound, with
+    fp16 outputs through the LDS-transposed epilogue."""
     r = rng(500 + m)
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
     x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
     bias = r.standard_normal(2 * case[0]).astype(np.float32)
     y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16, flags=flags).float().cpu().numpy()
     xf = x.float().numpy().astype(np.float64)
-    y16 = xf @ a_ref.astype(np.float16).astype(np.float64).T + bias
-    scale = np.abs(xf) @ np.abs(a_ref.astype(np.float64)).T + np.abs(bias)
-    assert np.all(np.abs(y - y16) <= 1e-5 * scale + 2.0 ** -11 * np.abs(y16) + 1e-5)
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+
+
+def test_wide_linear_kernels_consistent():
+    """Both kernels contract the same fp16 operands (they differ only in the
+    k order inside each MFMA), so float32 outputs agree to accumulation order."""
+    r = rng(600)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, CASES[1])
+    x = torch.from_numpy(r.standard_normal((1000, 768)).astype(np.float32)).to(torch.float16).to(DEV)
+    y0 = pw.linear(x, None, out_dtype=torch.float32, flags=0).cpu().numpy().astype(np.float64)
+    y1 = pw.linear(x, None, out_dtype=torch.float32, flags=1).cpu().numpy().astype(np.float64)
+    scale = np.abs(x.float().cpu().numpy().astype(np.float64)) @ np.abs(
+        O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)).T
+    assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)

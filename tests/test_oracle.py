@@ -259,3 +259,82 @@ def test_oracle_wide_linear_vs_compiled_reference(mode):
     scale = np.abs(x.astype(np.float64)) @ np.abs(a.astype(np.float64)).T + np.abs(bias)
     tol = (2.0 ** -10 if mode == 1 else 1e-6) * scale + 1e-5
     assert np.all(np.abs(y - yo) <= tol)
+
+
+# --------------------------------------------------------------------------
+# fp16 operand of the HIP kernels (build-defined: pinned by exact arithmetic)
+# --------------------------------------------------------------------------
+def _fp16_round_exact(q):
+    """Round a Fraction to the nearest fp16 (ties to even) by exhaustive
+    neighbour search on the fp16 grid -- independent of numpy's rounding."""
+    from fractions import Fraction
+    if q == 0:
+        return np.float16(0.0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = max(math.floor(math.log2(a)) if a > 0 else -24, -14)
+    step = Fraction(2) ** (e - 10)  # fp16 spacing at this binade (subnormals: 2^-24)
+    lo = (a // step) * step
+    hi = lo + step
+    if a - lo < hi - a:
+        v = lo
+    elif hi - a < a - lo:
+        v = hi
+    else:  # tie: even significand
+        v = lo if (lo / step) % 2 == 0 else hi
+    if v > Fraction(65504):
+        return np.float16(sign * np.inf)
+    return np.float16(sign * float(v))
+
+
+def test_fp16_add_exact_rounding():
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 0x7c00, size=(4000, 2), dtype=np.uint32).astype(np.uint16)  # finite magnitudes
+    signs = rng.integers(0, 2, size=(4000, 2), dtype=np.uint16) << 15
+    h = (bits | signs).view(np.float16)
+    # add classes the random draw rarely hits: exact ties, cancellation, subnormals
+    extra = np.array([[1.0, 2.0 ** -11], [1.0, 3 * 2.0 ** -12], [2.0 ** -24, 2.0 ** -24], [-6.1e-5, 6.1e-5],
+                      [65504.0, 16.0], [0.1, -0.1], [1.0009765625, 2.0 ** -11]], np.float64).astype(np.float16)
+    h = np.concatenate([h, extra])
+    got = O.fp16_add(h[:, 0], h[:, 1])
+    for (a, b), g in zip(h, got):
+        want = _fp16_round_exact(Fraction(float(a)) + Fraction(float(b)))
+        assert g.view(np.uint16) == want.view(np.uint16) or (g == 0 and want == 0), (a, b, g, want)
+
+
+def _wide_case(seed, n=24, k=40, codebook="axis", rot=None):
+    rng = np.random.default_rng(seed)
+    ncode = 16 if codebook == "psk16" else 4
+    planes = []
+    for kind in "uuww" if codebook != "psk16" else "uw":
+        planes.append((rng.integers(0, ncode, size=(n, k), dtype=np.uint8),
+                       rng.uniform(0.01, 0.1, n).astype(F32), rng.uniform(0.01, 0.1, n).astype(F32), kind))
+    return planes
+
+
+@pytest.mark.parametrize("codebook,rot", [("axis", None), ("sign", None), ("psk16", None),
+                                          ("axis", ((0.95533645, 0.29552022), (0.98006660, -0.19866933)))])
+def test_recompose_fp16_bound_and_identities(codebook, rot):
+    rotation = None if rot is None else tuple((F32(c), F32(s)) for c, s in rot)
+    planes = _wide_case(12, codebook=codebook)
+    a = O.wide_weight(planes, codebook, rotation).astype(np.float64)
+    a16 = O.wide_weight(planes, codebook, rotation, fp16=True).astype(np.float64)
+    mag = O.wide_magnitude(planes, codebook, rotation)
+    u = 2.0 ** -11
+    assert np.all(np.abs(a16 - a) <= (2 * u + u * u) * mag + 2.0 ** -25)
+    # every value is an fp16 number
+    assert np.array_equal(a16.astype(np.float16).astype(np.float64), a16)
+    # block identities of the fused layout: A22 = -(W_re) + U_re and A11 = W_re + U_re
+    # swap roles under W <-> conj-free negation: with U = 0, A11 = W_re = -A22
+    u_re, u_im, w_re, w_im = O.wide_parts(planes, codebook, rotation)
+    z = np.zeros_like(u_re)
+    only_w = O.recompose_fp16(z, z, w_re, w_im).astype(np.float64)
+    n, k = u_re.shape
+    assert np.array_equal(only_w[:n, :k], -only_w[n:, k:])
+    assert np.array_equal(only_w[:n, k:], only_w[n:, :k])
+    only_u = O.recompose_fp16(u_re, u_im, z, z).astype(np.float64)
+    assert np.array_equal(only_u[:n, :k], only_u[n:, k:])
+    assert np.array_equal(only_u[:n, k:], -only_u[n:, :k])
+    # exact where fp16 represents both terms and their sum (W = 0: coefficient = fp16(U))
+    assert np.array_equal(only_u[:n, :k], u_re.astype(np.float16).astype(np.float64))
