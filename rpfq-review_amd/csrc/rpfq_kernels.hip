@@ -827,6 +827,9 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
 //     c0 + 4g + e of its code word; v_perm_b32 groups the coefficients by kind
 //     and v_permlane32_swap_b32 trades the half the other lane group needs;
 //   * the LUT is [entry][row] fp16 (re, im) pairs (conflict-free lookups);
+//   * outputs leave through an LDS transpose as 16-B non-temporal stores, so
+//     the output stream does not evict the activation tiles the other
+//     workgroups of the same row tile are about to read from L2;
 //   * per substep the 12 LDS reads of substep s+1 are issued before the MFMAs
 //     of substep s and its decode runs beside the last 4 of them (fenced with
 //     sched_barrier); one raw barrier per k-step with explicit wait counts
@@ -838,12 +841,15 @@ constexpr int kDmaBM = 128;
 constexpr int kDmaStage = kDmaBM * 128;                           // 16384 B
 constexpr int kDmaStages = 3;
 constexpr int kDmaLutWave = 32 * 32 * 4;                          // [entry][row] fp16 pairs
-constexpr int kDmaEpiRows = 64;                                   // epilogue half tile
 constexpr int kDmaCodes = 4 * 1024;                               // codes of one k-step, 4 waves
-constexpr int kDmaLds = kDmaStages * kDmaStage + 2 * kDmaCodes + 4 * kDmaLutWave;  // 73728 B
+constexpr int kDmaBias = 4 * 64 * 4;                              // bias of the tile's 128 rows, re | im
+constexpr int kDmaEpiRows = 64;                                   // epilogue transposes half a tile
+constexpr int kDmaLds = kDmaStages * kDmaStage + 2 * kDmaCodes + 4 * kDmaLutWave + kDmaBias;  // 74752 B
 static_assert(4 * kDmaEpiRows * kTRow <= kDmaStages * kDmaStage, "epilogue tile fits the stages");
 
 typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) const half8* lds_h8_t;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -866,17 +872,11 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31, g = lane >> 5;
-    const int tile = xcd_tile(blockIdx.x, a.tiles_m * a.tiles_n);
-    const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
-    const int64_t m0 = min((int64_t)mt * kDmaBM, a.M - kDmaBM);
-    const int ntw = ntl * 4 + wave;
-    const bool active = ntw < a.NT;
-    const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
-    const int64_t n = (int64_t)ntw * 32 + r;
 
     char* stages = smem;
     char* cbufs = smem + kDmaStages * kDmaStage;  // two k-steps of codes
     uint32_t* lut = reinterpret_cast<uint32_t*>(cbufs + 2 * kDmaCodes) + wave * (32 * 32);
+    float* bias_s = reinterpret_cast<float*>(cbufs + 2 * kDmaCodes + 4 * kDmaLutWave);  // [wave][re 32 | im 32]
     const uint32_t lut_r = lds_addr(lut + r);  // LDS byte address of entry 0 of this lane's row
     uint32_t entry_bytes;  // 128 (one LUT entry = 32 rows x 4 B), opaque so that
     asm("s_mov_b32 %0, 128" : "=s"(entry_bytes));  // the address stays v_bfe + v_mad
@@ -892,8 +892,9 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         const int chunk = (lane & 7) ^ ((4 * jp + (lane >> 4)) & 7);
         voff[jp] = (uint32_t)((lane >> 3) * ldx * 2 + (chunk >> 2) * (int64_t)a.K * 2 + (chunk & 3) * 16);
     }
-    const char* xw = reinterpret_cast<const char*>(a.x) + (m0 + 32 * wave) * ldx * 2;
     const uint32_t lds_stages = lds_addr(stages) + 32 * wave * 128;
+    const char* xw = nullptr;      // this wave's first x row of the current tile
+    const char* cw_src = nullptr;  // codes of the current tile's 32-row block
     auto issue_x = [&](int ks, int stage) {
         const char* src = xw + ks * 64;
         const uint32_t dst = lds_stages + stage * kDmaStage;
@@ -902,7 +903,6 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     };
     // Codes: one 1-KB block per wave and k-step; lane l fetches the uint4 of
     // MFMA lane l (row l & 31, half l >> 5) so the reads are consecutive.
-    const char* cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)ntw_ld * a.KS * 64);
     const uint32_t cw_voff = (uint32_t)((2 * (lane & 31) + (lane >> 5)) * 16);
     const uint32_t lds_codes = lds_addr(cbufs) + wave * 1024;
     auto issue_codes = [&](int ks, int buf) {
@@ -917,12 +917,31 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) aoff[s] = lds_addr(stages) + r * 128 + (((4 * g + s) ^ ((r >> 1) & 7)) * 16);
 
+    // Persistent: the grid holds two workgroups per CU and walks the tiles in
+    // the same XCD-local order as a one-tile-per-workgroup launch (the grid
+    // size is a multiple of 8, so vb & 7 stays this workgroup's XCD).
+    const int total = a.tiles_m * a.tiles_n;
+    for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
+    const int tile = xcd_tile(vb, total);
+    const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
+    const int64_t m0 = min((int64_t)mt * kDmaBM, a.M - kDmaBM);
+    const int ntw = ntl * 4 + wave;
+    const bool active = ntw < a.NT;
+    const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
+    xw = reinterpret_cast<const char*>(a.x) + (m0 + 32 * wave) * ldx * 2;
+    cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)ntw_ld * a.KS * 64);
+
     floatx16 acc_re[MB], acc_im[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
     int cur_blk = 0;
     build_lut<CB>(lut, a.params, (int64_t)ntw_ld * 32 + r, true, a.nblk, 0, a.rot, r, g);
+    {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue
+        const int64_t nn = (int64_t)ntw * 32 + r;
+        const bool ok = a.bias && active && nn < a.N;
+        bias_s[wave * 64 + g * 32 + r] = ok ? a.bias[g * (int64_t)a.N + nn] : 0.0f;
+    }
     issue_codes(0, 0);
     issue_x(0, 0);
     issue_x(a.KS > 1 ? 1 : 0, 1);
@@ -933,11 +952,11 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
 
     // One k-step on stage `st`: first the codes of k-step ks + 1 and the
     // activations of ks + 2 (into the buffers read at ks - 1, free since the
-    // last barrier; past the end the last k-step is reloaded, unused), then
-    // the math.  The loop below is unrolled by 3 so stage offsets are static.
+    // last barrier), then the math.  The loop below is unrolled by 3 so stage
+    // offsets are static.
     auto kstep = [&](int ks, int st) {
-        issue_codes(ks + 1 < a.KS ? ks + 1 : a.KS - 1, (ks + 1) & 1);
-        issue_x(ks + 2 < a.KS ? ks + 2 : a.KS - 1, st == 0 ? 2 : st - 1);
+        if (ks + 1 < a.KS) issue_codes(ks + 1, (ks + 1) & 1);
+        if (ks + 2 < a.KS) issue_x(ks + 2, st == 0 ? 2 : st - 1);
         const uint4 cw = read_codes(ks & 1);
         const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
         auto read_sub = [&](int s, uint32_t (&U)[4], uint32_t (&W)[4], half8 (&ax)[MB]) {
@@ -989,15 +1008,15 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
             if (s < 3) read_sub(s + 1, U, W, ax_n);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < MB / 2; ++i) {
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_re, acc_re[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_im, acc_im[i], 0, 0, 0);
+            for (int i = 0; i < MB / 2; ++i) {  // transposed product: weights are the A operand
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_re, ax_c[i], acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_im, ax_c[i], acc_im[i], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = MB / 2; i < MB; ++i) {
-                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_re, acc_re[i], 0, 0, 0);
-                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ax_c[i], b_im, acc_im[i], 0, 0, 0);
+                acc_re[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_re, ax_c[i], acc_re[i], 0, 0, 0);
+                acc_im[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b_im, ax_c[i], acc_im[i], 0, 0, 0);
             }
             if (s < 3) {
                 decode(U, W, b_re, b_im);
@@ -1016,8 +1035,12 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         }
         // codes ks + 1 and stage ks + 1 landed: only the 4 newest loads
         // (activations of ks + 2) may still be in flight; every LDS read of
-        // this k-step is complete
-        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+        // this k-step is complete.  Near the end nothing is prefetched, so
+        // everything must land.
+        if (ks + 2 < a.KS)
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -1029,53 +1052,85 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     }
     if (ks < a.KS) kstep(ks, 0);
     if (ks + 1 < a.KS) kstep(ks + 1, 1);
-    // the clamped tail loads may still target the stages: drain before reuse
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-
-    const bool n_ok = active && n < a.N;
-    const float br = (a.bias && n_ok) ? a.bias[n] : 0.0f;
-    const float bi = (a.bias && n_ok) ? a.bias[a.N + n] : 0.0f;
+    // Epilogue.  The accumulators hold the transposed tile: lane (r, g) of
+    // subtile i has, for x row 32 i + r, outputs n = 32 ntw + 8 q + 4 g + t at
+    // element 4 q + t.  Each 4 consecutive outputs go to LDS as one 8-B write
+    // ([row][re 32 | im 32] fp16 per wave, half a tile at a time); rows are
+    // then read back as 16-B chunks, 8 lanes per row, for coalesced stores.
+    // The stages are free: the last k-step drained every DMA and LDS read.
     const int64_t ldy = 2 * (int64_t)a.N;
-    if (YDT == RPFQ_F32) {
-        if (!n_ok) return;
+    float bre[16], bim[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 b0 = *reinterpret_cast<const float4*>(bias_s + wave * 64 + 8 * q + 4 * g);
+        const float4 b1 = *reinterpret_cast<const float4*>(bias_s + wave * 64 + 32 + 8 * q + 4 * g);
+        bre[4 * q] = b0.x; bre[4 * q + 1] = b0.y; bre[4 * q + 2] = b0.z; bre[4 * q + 3] = b0.w;
+        bim[4 * q] = b1.x; bim[4 * q + 1] = b1.y; bim[4 * q + 2] = b1.z; bim[4 * q + 3] = b1.w;
+    }
+    if (YDT == RPFQ_F32) {  // float32 outputs: 4 consecutive outputs = one 16-B store
+      if (active) {
+        const int64_t nb0 = (int64_t)ntw * 32 + 4 * g;
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
+            const int64_t m = m0 + 32 * i + r;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t m = m0 + i * 32 + acc_row(v, g);
-                store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
-                store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+            for (int q = 0; q < 4; ++q) {
+                const int64_t n0 = nb0 + 8 * q;
+                float vr[4], vi[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    vr[t] = acc_re[i][4 * q + t] + bre[4 * q + t];
+                    vi[t] = acc_im[i][4 * q + t] + bim[4 * q + t];
+                }
+                float* yr = reinterpret_cast<float*>(a.y) + m * ldy + n0;
+                float* yi = reinterpret_cast<float*>(a.y) + m * ldy + a.N + n0;
+                if (a.vec_store && n0 + 4 <= a.N) {
+                    __builtin_nontemporal_store((f32x4){vr[0], vr[1], vr[2], vr[3]}, reinterpret_cast<f32x4*>(yr));
+                    __builtin_nontemporal_store((f32x4){vi[0], vi[1], vi[2], vi[3]}, reinterpret_cast<f32x4*>(yi));
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        if (n0 + t < a.N) {
+                            yr[t] = vr[t];
+                            yi[t] = vi[t];
+                        }
+                    }
+                }
             }
         }
-        return;
-    }
-    // 16-bit outputs: transpose through LDS in two 64-row halves, then write
-    // 16-byte chunks (per row: 32 real then 32 imaginary outputs of the wave)
-    uint16_t* tt = reinterpret_cast<uint16_t*>(smem + wave * (kDmaEpiRows * kTRow));
+      }
+    } else {
+    char* tt = smem + wave * (kDmaEpiRows * kTRow);
     const int64_t nbase = (int64_t)ntw * 32;
-    const int q = lane & 7;
-    const int64_t col0 = (q < 4 ? 0 : a.N) + nbase + 8 * (q & 3);
-    const int64_t nfirst = nbase + 8 * (q & 3);
+    const int cq = lane & 7;  // 16-B chunk of a row: 0-3 real, 4-7 imaginary
+    const int64_t col0 = (cq < 4 ? 0 : a.N) + nbase + 8 * (cq & 3);
+    const int64_t nfirst = nbase + 8 * (cq & 3);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int ii = 0; ii < MB / 2; ++ii) {
             const int i = h * (MB / 2) + ii;
+            char* trow = tt + (32 * ii + r) * kTRow;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = ii * 32 + acc_row(v, g);
-                uint16_t hr, hi;
+            for (int q = 0; q < 4; ++q) {
+                uint2 pr, pi;
                 if (YDT == RPFQ_F16) {
-                    hr = __builtin_bit_cast(uint16_t, (_Float16)(acc_re[i][v] + br));
-                    hi = __builtin_bit_cast(uint16_t, (_Float16)(acc_im[i][v] + bi));
+                    pr = make_uint2(cvt_pk(acc_re[i][4 * q] + bre[4 * q], acc_re[i][4 * q + 1] + bre[4 * q + 1]),
+                                    cvt_pk(acc_re[i][4 * q + 2] + bre[4 * q + 2], acc_re[i][4 * q + 3] + bre[4 * q + 3]));
+                    pi = make_uint2(cvt_pk(acc_im[i][4 * q] + bim[4 * q], acc_im[i][4 * q + 1] + bim[4 * q + 1]),
+                                    cvt_pk(acc_im[i][4 * q + 2] + bim[4 * q + 2], acc_im[i][4 * q + 3] + bim[4 * q + 3]));
                 } else {
-                    hr = f32_to_bf16(acc_re[i][v] + br);
-                    hi = f32_to_bf16(acc_im[i][v] + bi);
+                    pr = make_uint2(f32_to_bf16(acc_re[i][4 * q] + bre[4 * q]) |
+                                        ((uint32_t)f32_to_bf16(acc_re[i][4 * q + 1] + bre[4 * q + 1]) << 16),
+                                    f32_to_bf16(acc_re[i][4 * q + 2] + bre[4 * q + 2]) |
+                                        ((uint32_t)f32_to_bf16(acc_re[i][4 * q + 3] + bre[4 * q + 3]) << 16));
+                    pi = make_uint2(f32_to_bf16(acc_im[i][4 * q] + bim[4 * q]) |
+                                        ((uint32_t)f32_to_bf16(acc_im[i][4 * q + 1] + bim[4 * q + 1]) << 16),
+                                    f32_to_bf16(acc_im[i][4 * q + 2] + bim[4 * q + 2]) |
+                                        ((uint32_t)f32_to_bf16(acc_im[i][4 * q + 3] + bim[4 * q + 3]) << 16));
                 }
-                tt[row * (kTRow / 2) + r] = hr;
-                tt[row * (kTRow / 2) + 32 + r] = hi;
+                *reinterpret_cast<uint2*>(trow + (8 * q + 4 * g) * 2) = pr;
+                *reinterpret_cast<uint2*>(trow + 64 + (8 * q + 4 * g) * 2) = pi;
             }
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
@@ -1084,10 +1139,10 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
 #pragma unroll
             for (int row = lane >> 3; row < kDmaEpiRows; row += 8) {
                 const int64_t m = m0 + h * kDmaEpiRows + row;
-                const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tt) + row * kTRow + q * 16);
+                const uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
                 uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
                 if (a.vec_store && nfirst + 8 <= a.N) {
-                    *reinterpret_cast<uint4*>(dst) = v;
+                    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
                 } else {
                     const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
                     for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = hv[t];
@@ -1097,7 +1152,15 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         __builtin_amdgcn_s_waitcnt(0xc07f);  // reads of this half done before the next overwrite
         __builtin_amdgcn_wave_barrier();
     }
+    }
+    // every wave is done with this tile's LDS before the next tile refills it
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    }
 }
+
+
 
 // Fused weight A_q [2N, 2K] from the native blob (same decode as the GEMM).
 template <int CB>
@@ -1277,6 +1340,19 @@ static RotParams rot_of(const rpfq_wide_desc& d) {
     return r;
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev] & ~3;  // keep the grid a multiple of 8 (XCD-local tile order)
+}
+
 template <int BM, int XDT, int YDT, int CB>
 static hipError_t wide_go(WideArgs& a, hipStream_t s) {
     static std::once_flag once;
@@ -1304,7 +1380,10 @@ static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     if (attr_err != hipSuccess) return attr_err;
     a.tiles_m = (int)((a.M + kDmaBM - 1) / kDmaBM);
     a.tiles_n = (int)((a.NT + 3) / 4);
-    hipLaunchKernelGGL((wide_linear_dma_kernel<YDT, CB>), dim3(a.tiles_m * a.tiles_n), dim3(256), kDmaLds, s, a);
+    const int total = a.tiles_m * a.tiles_n;
+    const int slots = 2 * device_cus();  // two 74-KB workgroups per CU
+    const int grid = total < slots ? total : slots;
+    hipLaunchKernelGGL((wide_linear_dma_kernel<YDT, CB>), dim3(grid), dim3(256), kDmaLds, s, a);
     return hipGetLastError();
 }
 
