@@ -216,7 +216,8 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved_tflops / PEAK_F16_TFLOPS, 4),
             "traffic": None,
-            "kernel": "rpfq::wide_linear_kernel (all packed-layer launches in the timed region)",
+            "kernel": "rpfq::wide_linear_dma_kernel (fp16 x, K' % 32 == 0, M >= 128; else "
+                      "rpfq::wide_linear_kernel): all packed-layer launches in the timed region",
             "launches": len(launches),
             "avg_launch_us": round(1e3 * kt / max(1, len(launches)), 2),
             "algorithmic_gbs": round(kb / (kt / 1e3) / 1e9, 1),
