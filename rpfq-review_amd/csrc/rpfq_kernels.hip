@@ -837,15 +837,25 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
 // Requires K' % 32 == 0 and M >= 128; the last row tile starts at M - 128 so
 // every DMA row is inside x (rows shared with the previous tile are written
 // twice with the same values).
-constexpr int kDmaBM = 128;
-constexpr int kDmaStage = kDmaBM * 128;                           // 16384 B
+// Row tile BM = 128 (two workgroups per CU) or 256 (one per CU, accumulators
+// in AGPRs, each decoded coefficient feeds twice the MFMAs).
 constexpr int kDmaStages = 3;
 constexpr int kDmaLutWave = 32 * 32 * 4;                          // [entry][row] fp16 pairs
 constexpr int kDmaCodes = 4 * 1024;                               // codes of one k-step, 4 waves
-constexpr int kDmaBias = 4 * 64 * 4;                              // bias of the tile's 128 rows, re | im
-constexpr int kDmaEpiRows = 64;                                   // epilogue transposes half a tile
-constexpr int kDmaLds = kDmaStages * kDmaStage + 2 * kDmaCodes + 4 * kDmaLutWave + kDmaBias;  // 74752 B
-static_assert(4 * kDmaEpiRows * kTRow <= kDmaStages * kDmaStage, "epilogue tile fits the stages");
+constexpr int kDmaBias = 4 * 64 * 4;                              // bias of the tile's 128 outputs, re | im
+template <int BM> constexpr int dma_stage() { return BM * 128; }  // 16/32 KB
+// LDS map: LUT of waves 0-1 at [0, 8K), stages, codes, LUT of waves 2-3 at
+// [64K, 72K), bias.  The LUT bases are multiples of 64 KB so an entry address
+// is base | (index << 8) | (row slot << 2): one v_perm_b32 forms it.
+constexpr int kDmaLutPair = 2 * kDmaLutWave;                      // 8 KB: 32 entries x 64 rows
+template <int BM> constexpr int dma_stages_at() { return kDmaLutPair; }
+template <int BM> constexpr int dma_codes_at() { return kDmaLutPair + kDmaStages * dma_stage<BM>(); }
+template <int BM> constexpr int dma_lut1_at() { return dma_codes_at<BM>() + 2 * kDmaCodes <= 65536 ? 65536 : 131072; }
+template <int BM> constexpr int dma_bias_at() { return dma_lut1_at<BM>() + kDmaLutPair; }
+template <int BM> constexpr int dma_lds() { return dma_bias_at<BM>() + kDmaBias; }  // 74752 B (BM = 128)
+static_assert(dma_lds<128>() == 74752, "two workgroups per CU");
+static_assert(4 * 64 * kTRow <= kDmaStages * dma_stage<128>(), "epilogue half tile fits the stages");
+static_assert(4 * 128 * kTRow <= kDmaStages * dma_stage<256>(), "epilogue half tile fits the stages");
 
 typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -865,26 +875,54 @@ __device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, ui
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
 }
 
-template <int YDT, int CB>
-__global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
+// LUT of one output row in the wave-pair layout: entry e (0..15 U, 16..31 W)
+// of row slot `slot` at lut_pair[64 e + slot]; lane group g writes the even
+// or odd indices.  Same values as build_lut.
+template <int CB>
+__device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, const float4* params, int64_t n,
+                                               int nblk, int blk, const RotParams& rot, int g) {
+    const float4* p = params + (n * nblk + blk) * 2;
+    const float4 pu = p[0], pw = p[1];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t idx = (uint32_t)(g + 2 * j);
+        float2 u = lut_entry<CB>(idx, pu);
+        float2 w = lut_entry<CB>(idx, pw);
+        if (rot.rotate) {
+            u = derotate(u, rot.cu, rot.su);
+            w = derotate(w, rot.cw, rot.sw);
+        }
+        lut_pair[idx * 64 + slot] = cvt_pk(u.x, u.y);
+        lut_pair[(16 + idx) * 64 + slot] = cvt_pk(w.x, w.y);
+    }
+}
+
+template <int BM, int YDT, int CB>
+__global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
-    constexpr int MB = kDmaBM / 32;
+    constexpr int MB = BM / 32;
+    constexpr int kDmaStage = dma_stage<BM>();
+    constexpr int RPW = BM / 4;          // activation rows each wave loads per k-step
+    constexpr int EPI = BM / 2;          // epilogue transposes half a tile
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31, g = lane >> 5;
 
-    char* stages = smem;
-    char* cbufs = smem + kDmaStages * kDmaStage;  // two k-steps of codes
-    uint32_t* lut = reinterpret_cast<uint32_t*>(cbufs + 2 * kDmaCodes) + wave * (32 * 32);
-    float* bias_s = reinterpret_cast<float*>(cbufs + 2 * kDmaCodes + 4 * kDmaLutWave);  // [wave][re 32 | im 32]
-    const uint32_t lut_r = lds_addr(lut + r);  // LDS byte address of entry 0 of this lane's row
-    uint32_t entry_bytes;  // 128 (one LUT entry = 32 rows x 4 B), opaque so that
-    asm("s_mov_b32 %0, 128" : "=s"(entry_bytes));  // the address stays v_bfe + v_mad
+    char* stages = smem + dma_stages_at<BM>();
+    char* cbufs = smem + dma_codes_at<BM>();  // two k-steps of codes
+    // [entry][64 rows] LUT shared by a wave pair: this lane's row slot is
+    // 32 (wave & 1) + r; entry e at +256 e.  lut_slot holds the slot's LDS
+    // address of entry 0, whose byte 1 is zero (base is a multiple of 64 KB).
+    uint32_t* lut_pair = reinterpret_cast<uint32_t*>(smem + (wave < 2 ? 0 : dma_lut1_at<BM>()));
+    const int slot = 32 * (wave & 1) + r;
+    float* bias_s = reinterpret_cast<float*>(smem + dma_bias_at<BM>());  // [wave][re 32 | im 32]
+    const uint32_t lut_slot = lds_addr(lut_pair + slot);
 
-    // Activation DMA: wave w fills rows 32w .. 32w+31 of a stage with 4
-    // 1-KB loads of 8 rows; lane l writes row l >> 3, slot l & 7, which holds
-    // chunk (l & 7) ^ ((row >> 1) & 7).  The swizzle depends on the load's
-    // parity (row >> 1 = 16w + 4j + (l >> 4)), hence two lane offsets.
+    // Activation DMA: wave w fills rows RPW w .. RPW w + RPW - 1 of a stage
+    // with 1-KB loads of 8 rows; lane l writes row l >> 3, slot l & 7, which
+    // holds chunk (l & 7) ^ ((row >> 1) & 7).  The swizzle depends on the
+    // load's parity (row >> 1 = RPW w / 2 + 4j + (l >> 4)), hence two lane
+    // offsets.
     const int64_t ldx = 2 * (int64_t)a.K;  // fp16 elements per x row
     uint32_t voff[2];
 #pragma unroll
@@ -892,14 +930,14 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         const int chunk = (lane & 7) ^ ((4 * jp + (lane >> 4)) & 7);
         voff[jp] = (uint32_t)((lane >> 3) * ldx * 2 + (chunk >> 2) * (int64_t)a.K * 2 + (chunk & 3) * 16);
     }
-    const uint32_t lds_stages = lds_addr(stages) + 32 * wave * 128;
+    const uint32_t lds_stages = lds_addr(stages) + RPW * wave * 128;
     const char* xw = nullptr;      // this wave's first x row of the current tile
     const char* cw_src = nullptr;  // codes of the current tile's 32-row block
     auto issue_x = [&](int ks, int stage) {
         const char* src = xw + ks * 64;
         const uint32_t dst = lds_stages + stage * kDmaStage;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma_dwordx4(src + 8 * j * ldx * 2, voff[j & 1], dst + j * 1024);
+        for (int j = 0; j < RPW / 8; ++j) dma_dwordx4(src + 8 * j * ldx * 2, voff[j & 1], dst + j * 1024);
     };
     // Codes: one 1-KB block per wave and k-step; lane l fetches the uint4 of
     // MFMA lane l (row l & 31, half l >> 5) so the reads are consecutive.
@@ -916,6 +954,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     uint32_t aoff[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) aoff[s] = lds_addr(stages) + r * 128 + (((4 * g + s) ^ ((r >> 1) & 7)) * 16);
+    (void)kDmaLutWave;
 
     // Persistent: the grid holds two workgroups per CU and walks the tiles in
     // the same XCD-local order as a one-tile-per-workgroup launch (the grid
@@ -924,11 +963,11 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
     const int tile = xcd_tile(vb, total);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
-    const int64_t m0 = min((int64_t)mt * kDmaBM, a.M - kDmaBM);
+    const int64_t m0 = min((int64_t)mt * BM, a.M - BM);
     const int ntw = ntl * 4 + wave;
     const bool active = ntw < a.NT;
     const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
-    xw = reinterpret_cast<const char*>(a.x) + (m0 + 32 * wave) * ldx * 2;
+    xw = reinterpret_cast<const char*>(a.x) + (m0 + RPW * wave) * ldx * 2;
     cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)ntw_ld * a.KS * 64);
 
     floatx16 acc_re[MB], acc_im[MB];
@@ -936,7 +975,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
     int cur_blk = 0;
-    build_lut<CB>(lut, a.params, (int64_t)ntw_ld * 32 + r, true, a.nblk, 0, a.rot, r, g);
+    build_lut_slot<CB>(lut_pair, slot, a.params, (int64_t)ntw_ld * 32 + r, a.nblk, 0, a.rot, g);
     {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue
         const int64_t nn = (int64_t)ntw * 32 + r;
         const bool ok = a.bias && active && nn < a.N;
@@ -945,8 +984,11 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
     issue_codes(0, 0);
     issue_x(0, 0);
     issue_x(a.KS > 1 ? 1 : 0, 1);
-    // codes and stage 0 landed (at most the 4 newest loads in flight), LUT written
-    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    // codes and stage 0 landed (at most the newest k-step's loads in flight), LUT written
+    if (RPW == 32)
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
@@ -961,12 +1003,15 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
         auto read_sub = [&](int s, uint32_t (&U)[4], uint32_t (&W)[4], half8 (&ax)[MB]) {
             const uint32_t word = words[s];
+            const uint32_t pu = word & 0x0f0f0f0fu;         // U index of column e in byte e
+            const uint32_t pw = (word >> 4) & 0x0f0f0f0fu;  // W index
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {  // [entry][row] LUT (128-B entries): 32 lanes hit 32 banks
-                const uint32_t au = __umul24(__builtin_amdgcn_ubfe(word, 8 * e, 4), entry_bytes) + lut_r;
-                const uint32_t aw = __umul24(__builtin_amdgcn_ubfe(word, 8 * e + 4, 4), entry_bytes) + lut_r;
+            for (int e = 0; e < 4; ++e) {  // address = lut_slot with byte 1 := index (one v_perm_b32)
+                const uint32_t sel = 0x03020000u | ((4u + e) << 8);
+                const uint32_t au = __builtin_amdgcn_perm(pu, lut_slot, sel);
+                const uint32_t aw = __builtin_amdgcn_perm(pw, lut_slot, sel);
                 U[e] = *((lds_u32_t)au);
-                W[e] = *((lds_u32_t)aw + 16 * 32);
+                W[e] = *((lds_u32_t)aw + 16 * 64);  // W entries follow the 16 U entries
             }
 #pragma unroll
             for (int i = 0; i < MB; ++i) ax[i] = *((lds_h8_t)aoff[s] + (st * kDmaStage + i * 4096) / 16);
@@ -1029,17 +1074,20 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
             const int nb = (ks + 1) / a.block_ks;
             if (nb != cur_blk) {  // new scale block: this wave's LUT rows only
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                build_lut<CB>(lut, a.params, (int64_t)ntw_ld * 32 + r, true, a.nblk, nb, a.rot, r, g);
+                build_lut_slot<CB>(lut_pair, slot, a.params, (int64_t)ntw_ld * 32 + r, a.nblk, nb, a.rot, g);
                 cur_blk = nb;
             }
         }
-        // codes ks + 1 and stage ks + 1 landed: only the 4 newest loads
+        // codes ks + 1 and stage ks + 1 landed: only the newest RPW / 8 loads
         // (activations of ks + 2) may still be in flight; every LDS read of
         // this k-step is complete.  Near the end nothing is prefetched, so
         // everything must land.
-        if (ks + 2 < a.KS)
-            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
-        else
+        if (ks + 2 < a.KS) {
+            if (RPW == 32)
+                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+        } else
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -1100,7 +1148,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         }
       }
     } else {
-    char* tt = smem + wave * (kDmaEpiRows * kTRow);
+    char* tt = smem + wave * (EPI * kTRow);
     const int64_t nbase = (int64_t)ntw * 32;
     const int cq = lane & 7;  // 16-B chunk of a row: 0-3 real, 4-7 imaginary
     const int64_t col0 = (cq < 4 ? 0 : a.N) + nbase + 8 * (cq & 3);
@@ -1137,8 +1185,8 @@ __global__ void __launch_bounds__(256, 2) wide_linear_dma_kernel(WideArgs a) {
         __builtin_amdgcn_wave_barrier();
         if (active) {
 #pragma unroll
-            for (int row = lane >> 3; row < kDmaEpiRows; row += 8) {
-                const int64_t m = m0 + h * kDmaEpiRows + row;
+            for (int row = lane >> 3; row < EPI; row += 8) {
+                const int64_t m = m0 + h * EPI + row;
                 const uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
                 uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
                 if (a.vec_store && nfirst + 8 <= a.N) {
@@ -1369,27 +1417,31 @@ static hipError_t wide_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int YDT, int CB>
+template <int BM, int YDT, int CB>
 static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
+    constexpr int lds = dma_lds<BM>();
     std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_dma_kernel<YDT, CB>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kDmaLds);
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_dma_kernel<BM, YDT, CB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     });
     if (attr_err != hipSuccess) return attr_err;
-    a.tiles_m = (int)((a.M + kDmaBM - 1) / kDmaBM);
+    a.tiles_m = (int)((a.M + BM - 1) / BM);
     a.tiles_n = (int)((a.NT + 3) / 4);
     const int total = a.tiles_m * a.tiles_n;
-    const int slots = 2 * device_cus();  // two 74-KB workgroups per CU
+    const int slots = (BM == 128 ? 2 : 1) * device_cus();  // workgroups resident per CU
     const int grid = total < slots ? total : slots;
-    hipLaunchKernelGGL((wide_linear_dma_kernel<YDT, CB>), dim3(grid), dim3(256), kDmaLds, s, a);
+    hipLaunchKernelGGL((wide_linear_dma_kernel<BM, YDT, CB>), dim3(grid), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
 template <int XDT, int YDT, int CB>
 static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
-    if (XDT == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= kDmaBM) return wide_dma_go<YDT, CB>(a, s);
+#ifndef RPFQ_DMA_MIN_M
+#define RPFQ_DMA_MIN_M 128
+#endif
+    if (XDT == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M) return wide_dma_go<128, YDT, CB>(a, s);
     if (flags & RPFQ_FLAG_TILE_M128) return wide_go<128, XDT, YDT, CB>(a, s);
     if (a.M <= 32) return wide_go<32, XDT, YDT, CB>(a, s);
     if (a.M <= 64) return wide_go<64, XDT, YDT, CB>(a, s);
