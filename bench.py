@@ -122,6 +122,119 @@ def cpu_baseline(model, rows: dict, budget_s: float = 12.0):
                       f"decoded A_q (oracle/rpfq_oracle.py), {dt:.1f} s; excludes attention/LayerNorm"}
 
 
+# Complex layer shapes (K', N') of the ViT-B/16 and ViT-L/16 packed linears.
+STREAM_SHAPES = {
+    "vit_b.qkv": (384, 1152), "vit_b.proj": (384, 384), "vit_b.fc1": (384, 1536), "vit_b.fc2": (1536, 384),
+    "vit_l.qkv": (512, 1536), "vit_l.proj": (512, 512), "vit_l.fc1": (512, 2048), "vit_l.fc2": (2048, 512),
+}
+
+
+def stream_layer(k_c: int, n_c: int, seed: int, copies: int = 1):
+    """q2 (complex_phase_v2) layer of K' x N' with uniformly random axis codes
+    and per-(plane, row) scales ~U(0.01, 0.1), packed by rpfq_wide_pack.
+    copies > 1: one buffer of `copies` blobs of that layer, each with its own
+    random code bytes (every byte is a valid (U, W) index pair), for a
+    rotation over distinct weights.  Returns a list of PackedWide."""
+    import torch
+    from quant_models import _native as N
+    from quant_models import ops
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    planes = [torch.randint(0, 256, (n_c, k_c // 4), dtype=torch.uint8, device="cuda", generator=g)
+              for _ in range(4)]
+    sre = [torch.rand(n_c, 1, device="cuda", generator=g) * 0.09 + 0.01 for _ in range(4)]
+    sim = [torch.rand(n_c, 1, device="cuda", generator=g) * 0.09 + 0.01 for _ in range(4)]
+    pw = ops.PackedWide.from_planes(planes, sre, sim, n_c, k_c, N.CB_AXIS, 2, 0, None)
+    del planes, sre, sim
+    if copies == 1:
+        return [pw]
+    nb = pw.blob.numel()
+    codes_bytes = ((-(-n_c // 32)) * (-(-k_c // 32)) * 1024 + 255) // 256 * 256
+    big = torch.empty(copies, nb, dtype=torch.uint8, device="cuda")
+    big.copy_(pw.blob.expand(copies, nb))
+    big[:, :codes_bytes] = torch.randint(0, 256, (copies, codes_bytes), dtype=torch.uint8, device="cuda",
+                                         generator=g)
+    return [ops.PackedWide(n_c, k_c, N.CB_AXIS, 2, 0, big[i]) for i in range(copies)]
+
+
+def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, seed: int = 5):
+    """Batch-M weight streaming of one layer shape.
+    mode "stacked": one launch with N' stacked to >= gib GiB of codes (the
+    kernel's streaming rate at this K'); mode "rotate": >= gib GiB of distinct
+    blobs of the real K' x N' layer, one launch each, replayed from a HIP
+    graph (per-layer rate at batch M, launch gaps included).  Timed with HIP
+    events on the launch stream; bytes are algorithmic (ops.wide_bytes)."""
+    import torch
+    from quant_models import ops
+
+    dev = torch.device("cuda")
+    if mode == "stacked":
+        n_tot = -(-int(gib * (1 << 30)) // k_c)
+        n_tot = -(-n_tot // 32) * 32
+        layers = stream_layer(k_c, n_tot, seed)
+    else:
+        copies = -(-int(gib * (1 << 30)) // (k_c * n_c))
+        layers = stream_layer(k_c, n_c, seed, copies)
+    n_layer = layers[0].n_complex
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    x = torch.randn(m, 2 * k_c, device=dev, generator=g).to(torch.float16)
+    bias = torch.randn(2 * n_layer, device=dev, generator=g)
+    y = torch.empty(m, 2 * n_layer, dtype=torch.float16, device=dev)
+
+    def run_all():
+        for pw in layers:
+            pw.linear_into(x, bias, y)
+
+    run_all()  # warm up (kernel attributes, first-touch)
+    torch.cuda.synchronize()
+    ref = y.clone()
+    graph = None
+    if mode == "rotate":
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph, stream=s):
+                run_all()
+        torch.cuda.current_stream().wait_stream(s)
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, ref):
+            raise AssertionError("graph replay differs from the eager launches")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        graph.replay() if graph is not None else run_all()
+    e1.record()
+    torch.cuda.synchronize()
+    if not torch.equal(y, ref):
+        raise AssertionError("timed launches differ from the warm-up result")
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = len(layers) * ops.wide_bytes(m, n_layer, k_c)
+    code_bytes = len(layers) * n_layer * k_c
+    del layers
+    torch.cuda.empty_cache()
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"k_complex": k_c, "n_complex": n_layer, "m": m, "mode": mode, "launches": (1 if mode == "stacked"
+            else int(code_bytes // (k_c * n_layer))), "code_gib": round(code_bytes / (1 << 30), 3),
+            "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, reps: int = 10, out=None):
+    rows = []
+    for mode in modes:
+        for name, (k_c, n_c) in STREAM_SHAPES.items():
+            for m in ms:
+                row = {"shape": name, **stream_case(k_c, n_c, m, mode, gib, reps)}
+                rows.append(row)
+                print(json.dumps(row), flush=True)
+    if out:
+        with open(out, "w") as f:
+            json.dump(rows, f, indent=1)
+    return rows
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,7 +247,20 @@ def main() -> int:
     ap.add_argument("--layer-report", default=None, help="write per-shape kernel timings (JSON) here")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (counter calibration) and exit")
+    ap.add_argument("--stream-sweep", action="store_true",
+                    help="only run the batch-M weight-streaming sweep (M in {1,4,16}, ViT-B/L layer shapes, "
+                         ">= --stream-gib GiB of codes per timed pass) and exit")
+    ap.add_argument("--stream-gib", type=float, default=1.0)
+    ap.add_argument("--stream-modes", default="stacked,rotate")
+    ap.add_argument("--stream-ms", default="1,4,16")
+    ap.add_argument("--stream-out", default=None, help="write the sweep rows (JSON) here")
+    ap.add_argument("--no-stream-line", action="store_true",
+                    help="leave the batch-1 streaming summary out of the bench line")
     args = ap.parse_args()
+    if args.stream_sweep:
+        stream_sweep(tuple(int(v) for v in args.stream_ms.split(",")), tuple(args.stream_modes.split(",")),
+                     args.stream_gib, max(1, args.steps), args.stream_out)
+        return 0
     if args.copy_probe_mib:
         import torch
         src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -155,6 +281,14 @@ def main() -> int:
 
     name, batch, img, codebook, seed, desc = CONFIGS[args.config]
     batch = args.batch or batch
+    batch1 = None
+    if not args.no_stream_line:
+        # batch-1 weight streaming (HBM roof) at the ViT-B fc1 shape; runs before
+        # and outside the timed region of the model forward
+        k_c, n_c = STREAM_SHAPES["vit_b.fc1"]
+        batch1 = {"kernel": "rpfq::wide_linear_skinny_kernel (M <= 16)", "bound": "hbm", "peak": PEAK_HBM_GBS,
+                  "unit": "GB/s", "stacked": stream_case(k_c, n_c, 1, "stacked", 1.0, 10),
+                  "rotate": stream_case(k_c, n_c, 1, "rotate", 1.0, 5)}
     model = build_model(args.config)
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(torch.float16)
@@ -228,6 +362,8 @@ def main() -> int:
     if os.path.exists(traffic):
         with open(traffic) as f:
             line["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
+    if batch1 is not None:
+        line["batch1_stream"] = batch1
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(model, rows_per_image(model, x[:1]), args.cpu_budget)
     print(json.dumps(line), flush=True)

@@ -48,11 +48,14 @@ extern "C" {
 #define RPFQ_BF16 2
 
 /* rpfq_wide_linear flags.  Default (0): the kernel is chosen from the shape
- * (fp16 x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA; other
- * cases stage them through registers with a 32/64/128-row tile).
- * RPFQ_FLAG_TILE_M128 forces the register-staged 128-row kernel; every
- * kernel feeds the MFMA the same fp16 coefficients. */
+ * (M <= 16 streams the packed codes, one 32-row tile per wave, against all M
+ * rows; fp16 x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA;
+ * other cases stage them through registers with a 32/64/128-row tile).
+ * RPFQ_FLAG_TILE_M128 forces the register-staged 128-row kernel;
+ * RPFQ_FLAG_NO_STREAM keeps M <= 16 on the tiled kernels.  Every kernel
+ * feeds the MFMA the same fp16 coefficients. */
 #define RPFQ_FLAG_TILE_M128 1
+#define RPFQ_FLAG_NO_STREAM 2
 
 /* codebooks of the packed planes */
 #define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages

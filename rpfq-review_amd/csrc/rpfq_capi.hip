@@ -37,6 +37,9 @@ int check_desc(const rpfq_wide_desc* d) {
     if (d->n_complex <= 0 || d->k_complex <= 0)
         return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld must be positive",
                     (long long)d->n_complex, (long long)d->k_complex);
+    if (d->n_complex > (1LL << 30) || d->k_complex > (1LL << 24))
+        return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld exceed 2^30 / 2^24",
+                    (long long)d->n_complex, (long long)d->k_complex);
     if (d->k_complex % 8 != 0)
         return fail(RPFQ_ERR_ALIGN, "k_complex=%lld must be a multiple of 8", (long long)d->k_complex);
     if (d->block < 0 || (d->block > 0 && d->block % 32 != 0))
@@ -130,7 +133,8 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
-    if (flags & ~RPFQ_FLAG_TILE_M128) return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
+    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM))
+        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);

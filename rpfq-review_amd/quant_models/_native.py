@@ -27,6 +27,7 @@ ERRORS = {
 F32, F16, BF16 = 0, 1, 2
 CB_AXIS, CB_SIGN, CB_PSK16 = 0, 1, 2
 FLAG_TILE_M128 = 1  # force the register-staged 128-row kernel
+FLAG_NO_STREAM = 2  # keep M <= 16 on the tiled kernels (no weight-streaming kernel)
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 

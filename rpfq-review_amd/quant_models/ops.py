@@ -176,6 +176,24 @@ class PackedWide:
                 (m, self.n_complex, self.k_complex))
         return y.reshape(*lead, self.out_features)
 
+    def linear_into(self, x: torch.Tensor, bias: torch.Tensor | None, y: torch.Tensor, flags: int = 0) -> None:
+        """y[:] = U x + W conj(x) + bias for a contiguous [M, 2K'] x and a
+        preallocated contiguous [M, 2N'] y; bias float32 [2N'] or None.
+        Allocates nothing (usable under HIP graph capture)."""
+        N.require_device(x, bias, y)
+        m = x.shape[0]
+        if x.dim() != 2 or x.shape[1] != self.in_features or not x.is_contiguous():
+            raise ValueError(f"x must be a contiguous [M, {self.in_features}] tensor")
+        if y.shape != (m, self.out_features) or not y.is_contiguous():
+            raise ValueError(f"y must be a contiguous [{m}, {self.out_features}] tensor")
+        if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
+            raise TypeError("bias must be a contiguous float32 tensor")
+        lib = N.load()
+        N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x.data_ptr(),
+            N.dtype_code(x.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(y.dtype), int(flags),
+            N.stream_of(x)))
+
     def decode(self, round_fp16: bool = False) -> torch.Tensor:
         """Fused float32 weight A_q [2N', 2K'] (quant_i.py:534-544 layout)."""
         a = torch.empty(self.out_features, self.in_features, dtype=torch.float32, device=self.blob.device)

@@ -53,7 +53,8 @@ def test_wide_packed_bytes_geometry():
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("k_complex", 12, 3), ("n_complex", 0, 2), ("block", 48, 6), ("codebook", 9, 4), ("stages", 3, 4)])
+    ("k_complex", 12, 3), ("n_complex", 0, 2), ("block", 48, 6), ("codebook", 9, 4), ("stages", 3, 4),
+    ("n_complex", 2 ** 30 + 1, 2), ("k_complex", 2 ** 24 + 8, 2)])
 def test_wide_linear_rejects_bad_desc(field, value, code):
     L, N = lib()
     d = _desc(N)
@@ -72,7 +73,7 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 2, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4, None) == 6  # unknown flag bit
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 8, None) == 6
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 16, p, 1, 4, None, p, 1, 0, None) == 2
     assert L.rpfq_wide_linear(ctypes.byref(d), ctypes.c_void_p(258), 1 << 20, p, 1, 4, None, p, 1, 0, None) == 3

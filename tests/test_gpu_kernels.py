@@ -328,3 +328,66 @@ def test_wide_linear_kernels_consistent():
     scale = np.abs(x.float().cpu().numpy().astype(np.float64)) @ np.abs(
         O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)).T
     assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# weight-streaming kernel (M <= 16): the same operands, 16x16x32 MFMAs
+# ---------------------------------------------------------------------------
+SKINNY_CASES = CASES + [
+    (64, 1536, "axis", 2, 0, None),        # long K' (48 k-steps)
+    (40, 2048, "axis", 2, 256, None),      # long K' + per-(row, block) scales
+    (33, 1000, "psk16", 1, 0, None),       # K' % 32 != 0 (zeroed activation tail), 16-PSK
+]
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 7, 16])
+@pytest.mark.parametrize("case", SKINNY_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
+                                                    for c in SKINNY_CASES])
+def test_wide_linear_streaming(case, m):
+    r = rng(700 + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
+    # fp16 outputs through the 8-byte store path
+    y16 = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16).float().cpu().numpy()
+    check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+
+
+@pytest.mark.parametrize("m", [3, 12])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float16, torch.bfloat16), (torch.float32, torch.float16)])
+def test_wide_linear_streaming_dtypes(xdt, ydt, m):
+    r = rng(800 + m)
+    case = (160, 640, "axis", 2, 0, None)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(xdt)
+    y = pw.linear(x.to(DEV), None, out_dtype=ydt).float().cpu().numpy()
+    xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
+    out_ulp = {torch.float32: 1e-6, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
+    check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
+
+
+@pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640)])
+def test_wide_linear_streaming_persistent(m, n_c, k_c):
+    """Large N' (tens of thousands of one-wave workgroups) and K' beyond 16
+    k-steps: the streaming kernel and the tiled kernel (RPFQ_FLAG_NO_STREAM)
+    contract the same fp16 operands, so float32 outputs agree to
+    accumulation order."""
+    ops, N = qm()
+    r = rng(900 + m)
+    planes_np, packed, sre, sim, kinds, cb, nblk = make_wide(r, n_c, k_c)
+    pw = ops.PackedWide.from_planes([tdev(p) for p in packed], [tdev(s) for s in sre], [tdev(s) for s in sim],
+                                    n_c, k_c, cb, 2, 0, None)
+    x = torch.from_numpy(r.standard_normal((m, 2 * k_c)).astype(np.float32)).to(torch.float16).to(DEV)
+    bias = tdev(r.standard_normal(2 * n_c).astype(np.float32))
+    y0 = pw.linear(x, bias, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+    y1 = pw.linear(x, bias, out_dtype=torch.float32, flags=N.FLAG_NO_STREAM).cpu().numpy().astype(np.float64)
+    a16 = pw.decode(round_fp16=True).cpu().numpy().astype(np.float64)
+    xf = x.float().cpu().numpy().astype(np.float64)
+    scale = np.abs(xf) @ np.abs(a16).T + np.abs(bias.cpu().numpy())
+    assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)
+    # and the exact product of the decoded fp16 operands
+    assert np.all(np.abs(y0 - (xf @ a16.T + bias.cpu().numpy())) <= 1e-5 * scale + 1e-5)
