@@ -60,15 +60,21 @@ def rows_per_image(model, x):
     import torch
     from quant_models.inference import quant_layers
 
+    from quant_models import vision_transformer as vt
+
     rows, hooks = {}, []
     for name, layer in quant_layers(model):
         def hook(mod, inp, name=name):
             rows[name] = inp[0].numel() // inp[0].shape[-1] // x.shape[0]
         hooks.append(layer.register_forward_pre_hook(hook))
-    with torch.no_grad():
-        model(x[:1].repeat(x.shape[0], 1, 1, 1) if x.shape[0] > 1 else x)
-    for h in hooks:
-        h.remove()
+    fused, vt.FUSED_BLOCKS = vt.FUSED_BLOCKS, False  # module calls only, so every hook fires
+    try:
+        with torch.no_grad():
+            model(x[:1].repeat(x.shape[0], 1, 1, 1) if x.shape[0] > 1 else x)
+    finally:
+        vt.FUSED_BLOCKS = fused
+        for h in hooks:
+            h.remove()
     return rows
 
 

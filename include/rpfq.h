@@ -154,6 +154,35 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
                      void* y, int y_dtype, int flags, void* stream);
 
 /*
+ * rpfq_wide_linear with the block's residual add fused into the store:
+ *   y = residual + (U x + W conj(x) + bias)
+ * where the layer output is rounded to y_dtype first and the sum rounded
+ * again, so y is bit-identical to rpfq_wide_linear followed by an add in
+ * y_dtype (torch's `x + proj(...)`).  residual: [M, 2N'] of y_dtype, rows
+ * 16-byte aligned; it may be y itself (in place: every element is read and
+ * written by the same thread).  Other arguments as rpfq_wide_linear.
+ * Replaces the residual adds after attn.proj and mlp.fc2 of a ViT block
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:546 and :556
+ *   (runtime path :619, :625).
+ */
+int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
+                              const void* x, int x_dtype, int64_t M, const float* bias,
+                              const void* residual, void* y, int y_dtype, int flags, void* stream);
+
+/*
+ * LayerNorm over the last dimension (nn.LayerNorm with biased variance):
+ *   y = (x - mean) / sqrt(var + eps) * gamma + beta
+ * per row of x [M, C], statistics and the affine map in float32, then
+ * rounded to y_dtype.  gamma, beta: float32 [C] or NULL (1 / 0).  x, y,
+ * gamma and beta must be 16-byte aligned, C a multiple of 8 up to 4096; y
+ * may equal x.
+ * Replaces the norm1 / norm2 / final norm around the packed layers of a ViT
+ * block (RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:520, :549).
+ */
+int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma, const float* beta,
+                    float eps, void* y, int y_dtype, void* stream);
+
+/*
  * Activation fake quantization of a [M, in_features] feature block laid out
  * [re | im]: per row and per half, scale = qmax * (1 / max(max|x|, 1e-5)),
  * y = clamp(round_half_even(x * scale), -2^(bits-1), 2^(bits-1)-1) / scale,

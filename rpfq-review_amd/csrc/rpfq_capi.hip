@@ -141,9 +141,47 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     if (!aligned(packed, 256) || !aligned(x, 16))
         return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte and x 16-byte aligned");
     if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
-    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, y, y_dtype, flags,
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, nullptr, y, y_dtype, flags,
                                                reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear");
+}
+
+int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                              int x_dtype, int64_t M, const float* bias, const void* residual, void* y,
+                              int y_dtype, int flags, void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!packed || !x || !y || !residual) return fail(RPFQ_ERR_NULL, "packed/x/residual/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
+    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM))
+        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(residual, 16))
+        return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x and residual 16-byte aligned");
+    if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, residual, y, y_dtype, flags,
+                                               reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_linear_residual");
+}
+
+int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma, const float* beta,
+                    float eps, void* y, int y_dtype, void* stream) {
+    if (!x || !y) return fail(RPFQ_ERR_NULL, "x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0 || C <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld C=%lld must be positive", (long long)M, (long long)C);
+    if (C % 8 != 0 || C > 4096) return fail(RPFQ_ERR_SHAPE, "C=%lld must be a multiple of 8 and <= 4096", (long long)C);
+    if (M > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    if (!(eps >= 0.0f)) return fail(RPFQ_ERR_VALUE, "eps must be non-negative");
+    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(gamma, 16) || !aligned(beta, 16))
+        return fail(RPFQ_ERR_ALIGN, "x, y, gamma and beta must be 16-byte aligned");
+    return hip_status(rpfq::launch_layer_norm(x, x_dtype, M, C, gamma, beta, eps, y, y_dtype,
+                                              reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_layer_norm");
 }
 
 int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, int bits, void* y, int y_dtype,

@@ -13,9 +13,10 @@ namespace rpfq {
 //
 //  codes : [NT][KS][32 rows][32 bytes]   NT = ceil(N'/32), KS = ceil(K'/32)
 //          byte b of (row n, k-step ks) holds complex column
-//          k' = 32 ks + 16 s + 8 g + e  with  g = b / 16, s = (b / 8) & 1,
-//          e = b & 7, so MFMA lane group g streams its 16 bytes with one
-//          128-bit load per k-step.  Each byte is one complex element:
+//          k' = 32 ks + 8 s + 4 g + e  with  g = b / 16, s = (b / 4) & 3,
+//          e = b & 3, so MFMA lane group g streams its 16 bytes with one
+//          128-bit load per k-step (and each 4-byte word holds 4
+//          consecutive columns).  Each byte is one complex element:
 //          low nibble = U index, high nibble = W index.  AXIS/SIGN:
 //          index = c_s0 | c_s1 << 2; PSK16: index = 4-bit phase code.
 //          Padding (n >= N' or k' >= K') is 0.
@@ -68,8 +69,10 @@ hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const ui
                             int nplanes, const float* const* sre, const float* const* sim,
                             void* packed, hipStream_t s);
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
-                              const void* x, int xdt, int64_t M, const float* bias, void* y,
-                              int ydt, int flags, hipStream_t s);
+                              const void* x, int xdt, int64_t M, const float* bias, const void* res,
+                              void* y, int ydt, int flags, hipStream_t s);
+hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
+                             const float* beta, float eps, void* y, int ydt, hipStream_t s);
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt,
                             hipStream_t s);
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,

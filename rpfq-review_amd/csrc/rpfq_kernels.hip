@@ -142,6 +142,49 @@ __device__ __forceinline__ void store1(void* base, int64_t off, float v) {
 
 __device__ __forceinline__ half8 as_half8(uint4 v) { return __builtin_bit_cast(half8, v); }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// One element of y's dtype as float32.
+template <int YDT>
+__device__ __forceinline__ float load_y1(const void* base, int64_t off) {
+    if (YDT == RPFQ_F32) return reinterpret_cast<const float*>(base)[off];
+    if (YDT == RPFQ_F16) return (float)reinterpret_cast<const _Float16*>(base)[off];
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+}
+
+// Fused residual add, rounded as the unfused sequence rounds it: the layer
+// output v is first rounded to y's dtype, then res + that is rounded again by
+// the store (the sum of two fp16 values is exact in float32, so the store's
+// rounding equals an fp16 add; bf16 and float32 add in float32 as torch does).
+template <int YDT>
+__device__ __forceinline__ float with_res(float v, const void* res, int64_t off) {
+    if (!res) return v;
+    float r = v;
+    if (YDT == RPFQ_F16) r = (float)(_Float16)v;
+    if (YDT == RPFQ_BF16) r = bf16_to_f32(f32_to_bf16(v));
+    return load_y1<YDT>(res, off) + r;
+}
+
+// 8 (uint4) or 4 (uint2) packed 16-bit outputs plus the residual at `off`.
+__device__ __forceinline__ uint32_t add2_y(uint32_t v, uint32_t r, bool f16) {
+    if (f16) return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, r) + __builtin_bit_cast(half2v, v));
+    const float lo = bf16_to_f32(r & 0xffffu) + bf16_to_f32(v & 0xffffu);
+    const float hi = bf16_to_f32(r >> 16) + bf16_to_f32(v >> 16);
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+template <int YDT>
+__device__ __forceinline__ uint4 add_res8(uint4 v, const void* res, int64_t off) {
+    const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(res) + off);
+    const bool f16 = YDT == RPFQ_F16;
+    return make_uint4(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16), add2_y(v.z, r.z, f16), add2_y(v.w, r.w, f16));
+}
+template <int YDT>
+__device__ __forceinline__ uint2 add_res4(uint2 v, const void* res, int64_t off) {
+    const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(res) + off);
+    const bool f16 = YDT == RPFQ_F16;
+    return make_uint2(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16));
+}
+
 __device__ __forceinline__ half8 to_half8(const float* v) {
     uint4 u;
     u.x = pack_h2(v[0], v[1]);
@@ -461,6 +504,7 @@ struct WideArgs {
     const float4* params;
     RotParams rot;
     const float* bias;
+    const void* res;  // residual of y's dtype added to the output (NULL: none)
     void* y;
     int tiles_m, tiles_n;
     int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
@@ -478,8 +522,6 @@ constexpr int wide_lds_bytes() {
     return (2 * BM * kXRow + 4 * kLutWave) > (4 * BM * kTRow) ? (2 * BM * kXRow + 4 * kLutWave)
                                                                : (4 * BM * kTRow);
 }
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // Two floats -> packed fp16 pair (one v_cvt_pk_f16_f32, round to nearest even).
 __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
@@ -756,8 +798,8 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
             for (int v = 0; v < 16; ++v) {
                 const int64_t m = m0 + i * 32 + acc_row(v, g);
                 if (m < a.M) {
-                    store1<YDT>(a.y, m * ldy + n, acc_re[i][v] + br);
-                    store1<YDT>(a.y, m * ldy + a.N + n, acc_im[i][v] + bi);
+                    store1<YDT>(a.y, m * ldy + n, with_res<YDT>(acc_re[i][v] + br, a.res, m * ldy + n));
+                    store1<YDT>(a.y, m * ldy + a.N + n, with_res<YDT>(acc_im[i][v] + bi, a.res, m * ldy + a.N + n));
                 }
             }
         }
@@ -797,13 +839,19 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     for (int row = lane >> 3; row < BM; row += 8) {
         const int64_t m = m0 + row;
         if (m >= a.M) break;
-        const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tt) + row * TROW + q * 16);
+        uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tt) + row * TROW + q * 16);
         uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
         if (a.vec_store && nfirst + 8 <= a.N) {
+            if (a.res) v = add_res8<YDT>(v, a.res, m * ldy + col0);
             *reinterpret_cast<uint4*>(dst) = v;
         } else {
             const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
-            for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = h[t];
+            for (int t = 0; t < 8 && nfirst + t < a.N; ++t) {
+                uint16_t e = h[t];
+                if (a.res) e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + col0 + t],
+                                                 YDT == RPFQ_F16) & 0xffffu);
+                dst[t] = e;
+            }
         }
     }
 }
@@ -1132,6 +1180,16 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 }
                 float* yr = reinterpret_cast<float*>(a.y) + m * ldy + n0;
                 float* yi = reinterpret_cast<float*>(a.y) + m * ldy + a.N + n0;
+                if (a.res) {
+                    const float* rr = reinterpret_cast<const float*>(a.res) + m * ldy + n0;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        if (n0 + t < a.N) {
+                            vr[t] = rr[t] + vr[t];
+                            vi[t] = rr[a.N + t] + vi[t];
+                        }
+                    }
+                }
                 if (a.vec_store && n0 + 4 <= a.N) {
                     __builtin_nontemporal_store((f32x4){vr[0], vr[1], vr[2], vr[3]}, reinterpret_cast<f32x4*>(yr));
                     __builtin_nontemporal_store((f32x4){vi[0], vi[1], vi[2], vi[3]}, reinterpret_cast<f32x4*>(yi));
@@ -1153,8 +1211,18 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     const int cq = lane & 7;  // 16-B chunk of a row: 0-3 real, 4-7 imaginary
     const int64_t col0 = (cq < 4 ? 0 : a.N) + nbase + 8 * (cq & 3);
     const int64_t nfirst = nbase + 8 * (cq & 3);
+    // residual chunks of this lane's store rows are requested before the
+    // half tile goes through LDS, so their latency overlaps the transpose
+    const bool res_vec = a.res && active && a.vec_store && nfirst + 8 <= a.N;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+        uint4 rres[EPI / 8];
+        if (res_vec) {
+#pragma unroll
+            for (int j = 0; j < EPI / 8; ++j)
+                rres[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) +
+                                                          (m0 + h * EPI + (lane >> 3) + 8 * j) * ldy + col0);
+        }
 #pragma unroll
         for (int ii = 0; ii < MB / 2; ++ii) {
             const int i = h * (MB / 2) + ii;
@@ -1185,15 +1253,27 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         __builtin_amdgcn_wave_barrier();
         if (active) {
 #pragma unroll
-            for (int row = lane >> 3; row < EPI; row += 8) {
+            for (int j = 0; j < EPI / 8; ++j) {
+                const int row = (lane >> 3) + 8 * j;
                 const int64_t m = m0 + h * EPI + row;
-                const uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
+                uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
                 uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
                 if (a.vec_store && nfirst + 8 <= a.N) {
+                    if (res_vec) {
+                        const bool f16 = YDT == RPFQ_F16;
+                        v = make_uint4(add2_y(v.x, rres[j].x, f16), add2_y(v.y, rres[j].y, f16),
+                                       add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
+                    }
                     __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
                 } else {
                     const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
-                    for (int t = 0; t < 8 && nfirst + t < a.N; ++t) dst[t] = hv[t];
+                    for (int t = 0; t < 8 && nfirst + t < a.N; ++t) {
+                        uint16_t e = hv[t];
+                        if (a.res)
+                            e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + col0 + t],
+                                                  YDT == RPFQ_F16) & 0xffffu);
+                        dst[t] = e;
+                    }
                 }
             }
         }
@@ -1413,30 +1493,21 @@ __global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
             vi[v] = acc_im[h][v] + ((a.bias && ok) ? a.bias[a.N + n] : 0.0f);
         }
         const int64_t base = (int64_t)r16 * ldy + n0;
-        if (a.vec_store && n0 + 4 <= a.N) {
-            if (YDT == RPFQ_F32) {
-                *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.y) + base) =
-                    make_float4(vr[0], vr[1], vr[2], vr[3]);
-                *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.y) + base + a.N) =
-                    make_float4(vi[0], vi[1], vi[2], vi[3]);
-            } else if (YDT == RPFQ_F16) {
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) =
-                    make_uint2(cvt_pk(vr[0], vr[1]), cvt_pk(vr[2], vr[3]));
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base + a.N) =
-                    make_uint2(cvt_pk(vi[0], vi[1]), cvt_pk(vi[2], vi[3]));
-            } else {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    store1<YDT>(a.y, base + v, vr[v]);
-                    store1<YDT>(a.y, base + a.N + v, vi[v]);
-                }
+        if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
+            uint2 hr = make_uint2(cvt_pk(vr[0], vr[1]), cvt_pk(vr[2], vr[3]));
+            uint2 hi = make_uint2(cvt_pk(vi[0], vi[1]), cvt_pk(vi[2], vi[3]));
+            if (a.res) {
+                hr = add_res4<YDT>(hr, a.res, base);
+                hi = add_res4<YDT>(hi, a.res, base + a.N);
             }
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = hr;
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base + a.N) = hi;
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 if (n0 + v < a.N) {
-                    store1<YDT>(a.y, base + v, vr[v]);
-                    store1<YDT>(a.y, base + a.N + v, vi[v]);
+                    store1<YDT>(a.y, base + v, with_res<YDT>(vr[v], a.res, base + v));
+                    store1<YDT>(a.y, base + a.N + v, with_res<YDT>(vi[v], a.res, base + a.N + v));
                 }
             }
         }
@@ -1519,6 +1590,118 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const void* __restrict__
             float q = rintf(load1<XDT>(x, base + h * K + k) * scale);
             q = fminf(fmaxf(q, qmin), qmax);
             store1<YDT>(y, base + h * K + k, q / scale);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm (nn.LayerNorm over the last dimension, biased variance)
+// ---------------------------------------------------------------------------
+// TPR lanes per row (8 .. 64, so that no lane holds more than NC 8-element
+// chunks): lane l of a row holds chunks l, l + TPR, ... in registers, so the
+// row is read once; mean, then the variance of the held values about it
+// (two passes over registers, float32), then the affine map with gamma and
+// beta read as float4.
+template <int XDT>
+__device__ __forceinline__ void load8_ln(const void* base, int64_t off, float* v) {
+    if (XDT == RPFQ_F16) {
+        const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const half2v h = __builtin_bit_cast(half2v, w[i]);
+            v[2 * i] = (float)h.x;
+            v[2 * i + 1] = (float)h.y;
+        }
+    } else {
+        load8_f32<XDT>(base, off, v);
+    }
+}
+
+template <int YDT>
+__device__ __forceinline__ void store8_ln(void* base, int64_t off, const float* v) {
+    if (YDT == RPFQ_F32) {
+        float4* p = reinterpret_cast<float4*>(reinterpret_cast<float*>(base) + off);
+        p[0] = make_float4(v[0], v[1], v[2], v[3]);
+        p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else if (YDT == RPFQ_F16) {
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(base) + off) =
+            make_uint4(cvt_pk(v[0], v[1]), cvt_pk(v[2], v[3]), cvt_pk(v[4], v[5]), cvt_pk(v[6], v[7]));
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(base) + off) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int XDT, int YDT, int TPR, int NC>
+__global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict__ x, int64_t M, int C,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta, float eps, void* y) {
+    const int sub = threadIdx.x % TPR;
+    const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+    if (row >= M) return;  // whole groups leave together: TPR divides the wave
+    const int nch = C >> 3;
+    const int64_t base = row * C;
+    float v[NC][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = sub + TPR * j;
+        if (c < nch) {
+            load8_ln<XDT>(x, base + 8 * c, v[j]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += v[j][e];
+        }
+    }
+    const float mean = group_sum<TPR>(s) / (float)C;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        if (sub + TPR * j < nch) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = v[j][e] - mean;
+                s2 += d * d;
+            }
+        }
+    }
+    const float rstd = 1.0f / sqrtf(group_sum<TPR>(s2) / (float)C + eps);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = sub + TPR * j;
+        if (c < nch) {
+            float gk[8], bk[8];
+            if (gamma) {
+                const float4* gp = reinterpret_cast<const float4*>(gamma + 8 * c);
+                const float4 g0 = gp[0], g1 = gp[1];
+                gk[0] = g0.x; gk[1] = g0.y; gk[2] = g0.z; gk[3] = g0.w;
+                gk[4] = g1.x; gk[5] = g1.y; gk[6] = g1.z; gk[7] = g1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) gk[e] = 1.0f;
+            }
+            if (beta) {
+                const float4* bp = reinterpret_cast<const float4*>(beta + 8 * c);
+                const float4 b0 = bp[0], b1 = bp[1];
+                bk[0] = b0.x; bk[1] = b0.y; bk[2] = b0.z; bk[3] = b0.w;
+                bk[4] = b1.x; bk[5] = b1.y; bk[6] = b1.z; bk[7] = b1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bk[e] = 0.0f;
+            }
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (v[j][e] - mean) * rstd * gk[e] + bk[e];
+            store8_ln<YDT>(y, base + 8 * c, o);
         }
     }
 }
@@ -1716,7 +1899,8 @@ static hipError_t wide_x(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s
 }
 
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
-                              int xdt, int64_t M, const float* bias, void* y, int ydt, int flags, hipStream_t s) {
+                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
+                              hipStream_t s) {
     WideArgs a;
     a.x = x;
     a.M = M;
@@ -1730,6 +1914,7 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
     a.rot = rot_of(d);
     a.bias = bias;
+    a.res = res;
     a.y = y;
     a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);  // also covers 4-wide stores
     switch (d.codebook) {
@@ -1754,6 +1939,46 @@ hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bi
         case RPFQ_F32: return act_y<RPFQ_F32>(x, M, K, bits, y, ydt, s);
         case RPFQ_F16: return act_y<RPFQ_F16>(x, M, K, bits, y, ydt, s);
         default: return act_y<RPFQ_BF16>(x, M, K, bits, y, ydt, s);
+    }
+}
+
+template <int XDT, int YDT, int TPR, int NC>
+static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
+                            void* y, hipStream_t s) {
+    const dim3 grid((unsigned)((M + 256 / TPR - 1) / (256 / TPR)));
+    hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC>), grid, dim3(256), 0, s, x, M, C, gamma, beta, eps, y);
+    return hipGetLastError();
+}
+
+// Lanes per row: the smallest of 8, 16, 32, 64 that keeps every lane at <= 4
+// chunks (C <= 2048), else 64 lanes with up to 8 chunks (C <= 4096).
+template <int XDT, int YDT>
+static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, void* y,
+                        hipStream_t s) {
+    const int nch = C / 8;
+    if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, y, s);
+    if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, y, s);
+    if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, y, s);
+    if (nch <= 256) return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, y, s);
+    return ln_launch<XDT, YDT, 64, 8>(x, M, C, gamma, beta, eps, y, s);
+}
+
+template <int XDT>
+static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, void* y,
+                       int ydt, hipStream_t s) {
+    switch (ydt) {
+        case RPFQ_F32: return ln_go<XDT, RPFQ_F32>(x, M, C, gamma, beta, eps, y, s);
+        case RPFQ_F16: return ln_go<XDT, RPFQ_F16>(x, M, C, gamma, beta, eps, y, s);
+        default: return ln_go<XDT, RPFQ_BF16>(x, M, C, gamma, beta, eps, y, s);
+    }
+}
+
+hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
+                             float eps, void* y, int ydt, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return ln_y<RPFQ_F32>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
+        case RPFQ_F16: return ln_y<RPFQ_F16>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
+        default: return ln_y<RPFQ_BF16>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
     }
 }
 

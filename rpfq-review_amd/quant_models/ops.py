@@ -85,6 +85,28 @@ def act_quant(x: torch.Tensor, num_bits: int, out_dtype: torch.dtype | None = No
     return y.reshape(*lead, f)
 
 
+def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None, eps: float,
+               out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """nn.LayerNorm over the last dimension on the device (rpfq_layer_norm):
+    float32 statistics, output in out_dtype (default x.dtype).  weight/bias
+    are taken as float32."""
+    N.require_device(x, weight, bias)
+    c = x.shape[-1]
+    x2 = x.reshape(-1, c)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    y = torch.empty(x2.shape, dtype=out_dtype or x.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return y.reshape(x.shape)
+    w = None if weight is None else weight.detach().float().contiguous()
+    b = None if bias is None else bias.detach().float().contiguous()
+    lib = N.load()
+    N.check("rpfq_layer_norm", lib.rpfq_layer_norm(
+        x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], c, N.ptr(w), N.ptr(b), float(eps), y.data_ptr(),
+        N.dtype_code(y.dtype), N.stream_of(x2)))
+    return y.reshape(x.shape)
+
+
 @dataclass
 class PackedWide:
     """One widely-linear layer in the MI355X tiled layout (a device blob).
@@ -141,10 +163,14 @@ class PackedWide:
         return cls(n_complex, k_complex, codebook, stages, block, blob, rotation)
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
-               out_dtype: torch.dtype | None = None, flags: int = 0) -> torch.Tensor:
+               out_dtype: torch.dtype | None = None, flags: int = 0,
+               residual: torch.Tensor | None = None) -> torch.Tensor:
         """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
-        flags: 0 (kernel chosen from the shape) or _native.FLAG_TILE_M128."""
-        N.require_device(x, bias)
+        flags: 0 (kernel chosen from the shape), _native.FLAG_TILE_M128 or
+        _native.FLAG_NO_STREAM.  residual ([..., 2N'] of out_dtype): y =
+        residual + layer(x), fused into the kernel's store and rounded as the
+        unfused add would round it (rpfq_wide_linear_residual)."""
+        N.require_device(x, bias, residual)
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
         lead = x.shape[:-1]
@@ -154,6 +180,12 @@ class PackedWide:
         m = x2.shape[0]
         out_dtype = out_dtype or x.dtype
         y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
+        if residual is not None:
+            if residual.shape[:-1] != lead or residual.shape[-1] != self.out_features:
+                raise ValueError(f"residual must have shape {tuple(lead) + (self.out_features,)}")
+            r2 = residual.to(out_dtype).reshape(-1, self.out_features)
+            if not r2.is_contiguous() or r2.data_ptr() % 16:
+                r2 = r2.contiguous()
         if m == 0:
             return y.reshape(*lead, self.out_features)
         if bias is not None:
@@ -164,15 +196,23 @@ class PackedWide:
             ev0 = torch.cuda.Event(enable_timing=True)
             ev1 = torch.cuda.Event(enable_timing=True)
             ev0.record()
-        N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
-            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
-            N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), int(flags),
-            N.stream_of(x2)))
+        if residual is None:
+            N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
+                ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
+                N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), int(flags),
+                N.stream_of(x2)))
+        else:
+            N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
+                ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
+                N.dtype_code(x2.dtype), m, N.ptr(bias), r2.data_ptr(), y.data_ptr(), N.dtype_code(out_dtype),
+                int(flags), N.stream_of(x2)))
         if rec is not None:
             ev1.record()
-            rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex),
-                wide_bytes(m, self.n_complex, self.k_complex, x2.element_size(), y.element_size(),
-                           self.code_bytes * 8 // max(1, self.n_complex * self.k_complex)),
+            nbytes = wide_bytes(m, self.n_complex, self.k_complex, x2.element_size(), y.element_size(),
+                                self.code_bytes * 8 // max(1, self.n_complex * self.k_complex))
+            if residual is not None:
+                nbytes += m * self.out_features * y.element_size()
+            rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex), nbytes,
                 (m, self.n_complex, self.k_complex))
         return y.reshape(*lead, self.out_features)
 

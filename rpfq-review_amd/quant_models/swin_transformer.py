@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .vision_transformer import Mlp, PatchEmbed, _trunc_normal_
+from .vision_transformer import Mlp, PatchEmbed, _fused, _trunc_normal_, norm_fwd
 
 
 def window_partition(x: torch.Tensor, ws: int) -> torch.Tensor:
@@ -124,9 +124,12 @@ class SwinTransformerBlock(nn.Module):
 
     def forward(self, x):
         b, h, w, c = x.shape
-        x = x + self._attn(self.norm1(x))
+        x = x + self._attn(norm_fwd(self.norm1, x))
         x = x.reshape(b, -1, c)
-        x = x + self.mlp(self.norm2(x))
+        if _fused(self, x):  # the MLP residual add fused into fc2's store
+            x = self.mlp.forward_residual(norm_fwd(self.norm2, x), x)
+        else:
+            x = x + self.mlp(self.norm2(x))
         return x.reshape(b, h, w, c)
 
 
@@ -144,7 +147,7 @@ class PatchMerging(nn.Module):
     def forward(self, x):
         b, h, w, c = x.shape
         x = x.reshape(b, h // 2, 2, w // 2, 2, c).permute(0, 1, 3, 4, 2, 5).flatten(3)
-        return self.reduction(self.norm(x))
+        return self.reduction(norm_fwd(self.norm, x))
 
 
 class SwinTransformerStage(nn.Module):
@@ -210,7 +213,7 @@ class SwinTransformer(nn.Module):
                 nn.init.zeros_(m.bias)
 
     def forward_features(self, x):
-        return self.norm(self.layers(self.patch_embed(x)))
+        return norm_fwd(self.norm, self.layers(self.patch_embed(x)))
 
     def forward(self, x):
         return self.head(self.forward_features(x))

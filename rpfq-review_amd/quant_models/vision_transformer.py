@@ -12,9 +12,46 @@ norm1 -> qkv -> SDPA -> proj -> +res -> norm2 -> fc1 -> GELU(erf) -> fc2 -> +res
 """
 from __future__ import annotations
 
+import os
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+
+# Eval-mode device forward of a block uses the fused kernels: LayerNorm on the
+# HIP kernel and the residual add after attn.proj / mlp.fc2 fused into the
+# packed layer's store.  RPFQ_FUSED=0 keeps the module-by-module forward.
+FUSED_BLOCKS = os.environ.get("RPFQ_FUSED", "1") != "0"
+
+
+def _fused(module: nn.Module, x: torch.Tensor) -> bool:
+    return FUSED_BLOCKS and x.is_cuda and not module.training
+
+
+def norm_fwd(norm: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """norm(x), on the device LayerNorm kernel for eval-mode device tensors
+    (float32 copies of the affine parameters are cached on the module)."""
+    if not (_fused(norm, x) and type(norm) is nn.LayerNorm and norm.normalized_shape[-1] % 8 == 0
+            and len(norm.normalized_shape) == 1 and norm.normalized_shape[0] <= 4096):
+        return norm(x)
+    from . import ops
+
+    key = tuple((t.data_ptr(), t._version) if t is not None else None for t in (norm.weight, norm.bias))
+    cache = getattr(norm, "_rpfq_f32", None)
+    if cache is None or cache[0] != key:
+        cache = (key, None if norm.weight is None else norm.weight.detach().float().contiguous(),
+                 None if norm.bias is None else norm.bias.detach().float().contiguous())
+        norm._rpfq_f32 = cache
+    return ops.layer_norm(x, cache[1], cache[2], norm.eps)
+
+
+def linear_residual(layer: nn.Module, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual + layer(x), with the add fused into the packed layer's store
+    when the layer is a phase-quantized Linear on its HIP path."""
+    fwd = getattr(layer, "forward_residual", None)
+    if fwd is not None:
+        return fwd(x, residual)
+    return residual + layer(x)
 
 
 def _trunc_normal_(t: torch.Tensor, std: float = 0.02) -> torch.Tensor:
@@ -62,6 +99,10 @@ class Mlp(nn.Module):
     def forward(self, x):
         return self.drop2(self.fc2(self.norm(self.drop1(self.act(self.fc1(x))))))
 
+    def forward_residual(self, x, residual):
+        """residual + self(x) with the add fused into fc2 (eval mode)."""
+        return linear_residual(self.fc2, self.norm(self.drop1(self.act(self.fc1(x)))), residual)
+
 
 class Attention(nn.Module):
     def __init__(self, dim, num_heads=8, qkv_bias=False, attn_drop=0.0, proj_drop=0.0):
@@ -76,13 +117,19 @@ class Attention(nn.Module):
         self.proj = nn.Linear(dim, dim)
         self.proj_drop = nn.Dropout(proj_drop)
 
-    def forward(self, x):
+    def _mix(self, x):
         b, n, c = x.shape
         qkv = self.qkv(x).reshape(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)
         x = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
-        x = x.transpose(1, 2).reshape(b, n, c)
-        return self.proj_drop(self.proj(x))
+        return x.transpose(1, 2).reshape(b, n, c)
+
+    def forward(self, x):
+        return self.proj_drop(self.proj(self._mix(x)))
+
+    def forward_residual(self, x, residual):
+        """residual + self(x) with the add fused into proj (eval mode)."""
+        return linear_residual(self.proj, self._mix(x), residual)
 
 
 class Block(nn.Module):
@@ -97,6 +144,11 @@ class Block(nn.Module):
         self.ls2 = nn.Identity()
 
     def forward(self, x):
+        if _fused(self, x) and isinstance(self.ls1, nn.Identity) and isinstance(self.ls2, nn.Identity):
+            # audit_rpfq_vit_ios_parity.py:520-556 with the residual adds in
+            # the proj / fc2 stores and LayerNorm on the device kernel
+            x = self.attn.forward_residual(norm_fwd(self.norm1, x), x)
+            return self.mlp.forward_residual(norm_fwd(self.norm2, x), x)
         x = x + self.ls1(self.attn(self.norm1(x)))
         x = x + self.ls2(self.mlp(self.norm2(x)))
         return x
@@ -157,7 +209,7 @@ class VisionTransformer(nn.Module):
         x = torch.cat((self._prefix_tokens(x), x), dim=1) + self.pos_embed.to(x.dtype)
         x = self.norm_pre(self.pos_drop(x))
         x = self.blocks(x)
-        return self.norm(x)
+        return norm_fwd(self.norm, x)
 
     def forward_head(self, x, pre_logits: bool = False):
         x = self.head_drop(self.fc_norm(x[:, 0]))

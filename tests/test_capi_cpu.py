@@ -103,3 +103,24 @@ def test_wide_pack_plane_count():
     assert L.rpfq_wide_pack(ctypes.byref(d), arr, 3, arr, arr, p, 1 << 20, None) == 4
     d.codebook, d.stages = 2, 1
     assert L.rpfq_wide_pack(ctypes.byref(d), arr, 4, arr, arr, p, 1 << 20, None) == 4
+
+
+def test_residual_and_layer_norm_argument_errors():
+    L, N = lib()
+    d = _desc(N)
+    p = ctypes.c_void_p(256)
+    # NULL residual, bad dtype, bad flags, misaligned residual -- all before any HIP call
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, None, p, 1, 0, None) == 1
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 9, 0, None) == 5
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 8, None) == 6
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, ctypes.c_void_p(258), p, 1, 0,
+                                       None) == 3
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 16, p, 1, 4, None, p, p, 1, 0, None) == 2
+    assert L.rpfq_layer_norm(None, 1, 4, 64, None, None, 1e-6, p, 1, None) == 1
+    assert L.rpfq_layer_norm(p, 1, 4, 60, None, None, 1e-6, p, 1, None) == 2     # C % 8
+    assert L.rpfq_layer_norm(p, 1, 4, 8192, None, None, 1e-6, p, 1, None) == 2   # C > 4096
+    assert L.rpfq_layer_norm(p, 1, 0, 64, None, None, 1e-6, p, 1, None) == 2
+    assert L.rpfq_layer_norm(p, 5, 4, 64, None, None, 1e-6, p, 1, None) == 5
+    assert L.rpfq_layer_norm(p, 1, 4, 64, None, None, -1.0, p, 1, None) == 6
+    assert L.rpfq_layer_norm(ctypes.c_void_p(258), 1, 4, 64, None, None, 1e-6, p, 1, None) == 3
+    assert L.rpfq_layer_norm(p, 1, 4, 64, ctypes.c_void_p(260), None, 1e-6, p, 1, None) == 3

@@ -391,3 +391,70 @@ def test_wide_linear_streaming_persistent(m, n_c, k_c):
     assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)
     # and the exact product of the decoded fp16 operands
     assert np.all(np.abs(y0 - (xf @ a16.T + bias.cpu().numpy())) <= 1e-5 * scale + 1e-5)
+
+
+# ---------------------------------------------------------------------------
+# fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
+# followed by the add in y's dtype, on every kernel path
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,flags", [(3, 0), (16, 0), (33, 0), (130, 0), (300, 1), (129, 2)],
+                         ids=["stream3", "stream16", "reg33", "dma130", "reg128-300", "nostream129"])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float32])
+def test_wide_linear_residual_bit_exact(m, flags, ydt):
+    r = rng(1000 + m)
+    for case in (CASES[1], CASES[2]):  # N' % 8 == 0 (vector stores) and N' = 50 (element tail)
+        pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+        x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16).to(DEV)
+        bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+        res = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32) * 4).to(ydt).to(DEV)
+        y = pw.linear(x, bias, out_dtype=ydt, flags=flags)
+        yf = pw.linear(x, bias, out_dtype=ydt, flags=flags, residual=res)
+        assert torch.equal(yf, res + y), (case, m, flags, ydt)
+
+
+def test_wide_linear_residual_in_place():
+    """residual == y through the C ABI: every element is read before it is
+    written by the same thread."""
+    ops, N = qm()
+    import ctypes
+    r = rng(1100)
+    pw, *_ = build_packed(r, CASES[1])
+    lib = N.load()
+    for m in (4, 200):
+        x = torch.from_numpy(r.standard_normal((m, 768)).astype(np.float32)).to(torch.float16).to(DEV)
+        res = torch.from_numpy(r.standard_normal((m, 3072)).astype(np.float32)).to(torch.float16).to(DEV)
+        want = res + pw.linear(x, None, out_dtype=torch.float16)
+        y = res.clone()
+        N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
+            ctypes.byref(pw.desc), pw.blob.data_ptr(), pw.blob.numel(), x.data_ptr(), N.F16, m, None,
+            y.data_ptr(), y.data_ptr(), N.F16, 0, N.stream_of(x)))
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm (rpfq_layer_norm) against a float64 restatement of nn.LayerNorm
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,c", [(1, 8), (37, 96), (300, 768), (5, 1024), (9, 1536), (3, 4096)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)])
+def test_layer_norm(m, c, xdt, ydt):
+    ops, _ = qm()
+    r = rng(1200 + c)
+    x = torch.from_numpy((r.standard_normal((m, c)) * 3 + 1).astype(np.float32)).to(xdt)
+    g = torch.from_numpy(r.standard_normal(c).astype(np.float32))
+    b = torch.from_numpy(r.standard_normal(c).astype(np.float32))
+    y = ops.layer_norm(x.to(DEV), g.to(DEV), b.to(DEV), 1e-6, out_dtype=ydt).float().cpu().numpy().astype(np.float64)
+    xd = x.float().numpy().astype(np.float64)
+    mu = xd.mean(axis=1, keepdims=True)
+    var = ((xd - mu) ** 2).mean(axis=1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(var + 1e-6) * g.numpy() + b.numpy()
+    # float32 statistics (relative ~1e-6 of the normalized value) plus one
+    # rounding to y's dtype
+    ulp = {torch.float32: 2.0 ** -23, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[ydt]
+    tol = ulp * np.abs(ref) + 2e-5 * (np.abs(g.numpy()) * np.abs((xd - mu) / np.sqrt(var + 1e-6)) + 1)
+    assert np.all(np.abs(y - ref) <= tol)
+    # no affine parameters
+    y0 = ops.layer_norm(x.to(DEV), None, None, 1e-5, out_dtype=torch.float32).cpu().numpy()
+    ref0 = (xd - mu) / np.sqrt(var + 1e-5)
+    assert np.abs(y0 - ref0).max() <= 2e-5 * (np.abs(ref0).max() + 1)

@@ -108,7 +108,8 @@ def _reference_forward_cpu(model_gpu, name, x_cpu, state):
         return ref(x_cpu)
 
 
-@pytest.mark.parametrize("name", ["rpfq_deit_tiny_patch16_224_q", "rpfq_vit_tiny_patch16_224_q"])
+@pytest.mark.parametrize("name", ["rpfq_deit_tiny_patch16_224_q", "rpfq_vit_tiny_patch16_224_q",
+                                  "rpfq_swin_tiny_patch4_window7_224_q"])
 def test_end_to_end_logits(name):
     import quant_models as qm
     from quant_models.inference import load_synthetic_codes, prepare_inference
@@ -126,7 +127,7 @@ def test_end_to_end_logits(name):
     ref_state = {k: v.clone() for k, v in model.state_dict().items()}
     prepare_inference(model, DEV, torch.float16)
     g = torch.Generator().manual_seed(11)
-    x = torch.randn(64, 3, 224, 224, generator=g)
+    x = torch.randn(32 if "swin" in name else 64, 3, 224, 224, generator=g)
     with torch.no_grad():
         y = model(x.to(DEV, torch.float16)).float().cpu()
     # reference in float32 on the host with the same parameters and codes
@@ -139,3 +140,37 @@ def test_end_to_end_logits(name):
     confident = margin > 4 * err.max()
     assert bool(agree[confident].all())
     assert agree.mean() >= 0.99, f"top-1 agreement {agree.mean():.4f}"
+
+
+@pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_swin_tiny_patch4_window7_224_q"])
+def test_fused_blocks_match_unfused(name):
+    """Eval forward with the fused block path (device LayerNorm, residual adds
+    in the proj / fc2 stores) vs the module-by-module forward on the same GPU
+    model.  The residual adds are bit-identical by construction; LayerNorm
+    statistics are ordered differently from torch's, so the stated bound is
+    logits max-abs <= 1e-2 * max|logit| + 1e-3 with identical top-1 on
+    margin-confident samples."""
+    import quant_models as qm
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(3)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    load_synthetic_codes(model, 3)
+    prepare_inference(model, DEV, torch.float16)
+    x = torch.randn(16, 3, 224, 224, generator=torch.Generator().manual_seed(5)).to(DEV, torch.float16)
+    saved = vt.FUSED_BLOCKS
+    try:
+        with torch.no_grad():
+            vt.FUSED_BLOCKS = True
+            y_f = model(x).float().cpu()
+            vt.FUSED_BLOCKS = False
+            y_u = model(x).float().cpu()
+    finally:
+        vt.FUSED_BLOCKS = saved
+    err = (y_f - y_u).abs().max()
+    assert err <= 1e-2 * y_u.abs().max() + 1e-3, (err, y_u.abs().max())
+    top = y_u.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
