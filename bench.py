@@ -227,10 +227,13 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
             "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
-def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, reps: int = 10, out=None):
+def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, reps: int = 10, out=None,
+                 shapes=None):
     rows = []
     for mode in modes:
         for name, (k_c, n_c) in STREAM_SHAPES.items():
+            if shapes and name not in shapes:
+                continue
             for m in ms:
                 row = {"shape": name, **stream_case(k_c, n_c, m, mode, gib, reps)}
                 rows.append(row)
@@ -260,12 +263,21 @@ def main() -> int:
     ap.add_argument("--stream-modes", default="stacked,rotate")
     ap.add_argument("--stream-ms", default="1,4,16")
     ap.add_argument("--stream-out", default=None, help="write the sweep rows (JSON) here")
+    ap.add_argument("--stream-shapes", default=None,
+                    help="comma-separated subset of the sweep's layer shapes (e.g. vit_b.fc1)")
     ap.add_argument("--no-stream-line", action="store_true",
                     help="leave the batch-1 streaming summary out of the bench line")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one forward in a HIP graph and time its replays (launch-bound small batches)")
     args = ap.parse_args()
     if args.stream_sweep:
+        shapes = None if not args.stream_shapes else set(args.stream_shapes.split(","))
+        if shapes and not shapes <= set(STREAM_SHAPES):
+            print(f"unknown --stream-shapes {sorted(shapes - set(STREAM_SHAPES))}; known: {sorted(STREAM_SHAPES)}",
+                  file=sys.stderr)
+            return 2
         stream_sweep(tuple(int(v) for v in args.stream_ms.split(",")), tuple(args.stream_modes.split(",")),
-                     args.stream_gib, max(1, args.steps), args.stream_out)
+                     args.stream_gib, max(1, args.steps), args.stream_out, shapes)
         return 0
     if args.copy_probe_mib:
         import torch
@@ -299,10 +311,27 @@ def main() -> int:
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(torch.float16)
 
+    graph = None
     with torch.no_grad():
         for _ in range(args.warmup):
             model(x)
         torch.cuda.synchronize()
+        if args.graph:
+            eager = model(x).clone()
+            graph = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    gout = model(x)
+            torch.cuda.current_stream().wait_stream(s)
+            for _ in range(3):  # every replay, with eager work between, equals the eager forward
+                graph.replay()
+                torch.cuda.synchronize()
+                if not torch.equal(gout, eager):
+                    raise AssertionError("graph replay differs from the eager forward")
+                model(x)
+                torch.cuda.synchronize()
 
         launches = []
         ops.set_launch_recorder(lambda e0, e1, fl, by, shape: launches.append((e0, e1, fl, by, shape)))
@@ -310,7 +339,10 @@ def main() -> int:
         torch.cuda.synchronize()
         start.record()
         for _ in range(args.steps):
-            out = model(x)
+            if graph is not None:
+                graph.replay()
+            else:
+                out = model(x)
         end.record()
         torch.cuda.synchronize()
         ops.set_launch_recorder(None)
@@ -321,7 +353,8 @@ def main() -> int:
     kt = sum(e0.elapsed_time(e1) for e0, e1, *_ in launches)
     kf = sum(fl for _, _, fl, _, _ in launches)
     kb = sum(by for _, _, _, by, _ in launches)
-    achieved_tflops = kf / (kt / 1e3) / 1e12
+    # graph replays launch no recorded events: no per-launch roofline then
+    achieved_tflops = kf / (kt / 1e3) / 1e12 if kt > 0 else None
     per_shape = {}
     for e0, e1, fl, by, shape in launches:
         d = per_shape.setdefault(str(shape), [0, 0.0, fl, by])
@@ -347,25 +380,27 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic (N(0,1) images; random-init weights quantized by the reference axis rule, "
                 "synthetic per-row scales)",
-        "config": {"workload": f"{args.config}: {desc} forward, bs{batch}, {img}x{img}",
+        "config": {"workload": f"{args.config}: {desc} forward, bs{batch}, {img}x{img}"
+                               + (" (HIP graph replay)" if graph is not None else ""),
                    "batch": batch, "tokens": tokens, "packed_layers_per_step": len(launches) // args.steps},
         "roofline": {
             "bound": "mfma",
-            "achieved": round(achieved_tflops, 2),
+            "achieved": None if achieved_tflops is None else round(achieved_tflops, 2),
             "peak": PEAK_F16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(achieved_tflops / PEAK_F16_TFLOPS, 4),
+            "frac": None if achieved_tflops is None else round(achieved_tflops / PEAK_F16_TFLOPS, 4),
             "traffic": None,
             "kernel": "rpfq::wide_linear_dma_kernel (fp16 x, K' % 32 == 0, M >= 128; else "
                       "rpfq::wide_linear_kernel): all packed-layer launches in the timed region",
             "launches": len(launches),
             "avg_launch_us": round(1e3 * kt / max(1, len(launches)), 2),
-            "algorithmic_gbs": round(kb / (kt / 1e3) / 1e9, 1),
+            "algorithmic_gbs": round(kb / (kt / 1e3) / 1e9, 1) if kt > 0 else None,
         },
         "cpu_baseline": None,
     }
     traffic = os.path.join(ROOT, "profiles", f"wide_linear_{args.config}_traffic.json")
-    if os.path.exists(traffic):
+    # the committed counter summary covers the default batch of the eager forward
+    if os.path.exists(traffic) and batch == CONFIGS[args.config][1] and graph is None:
         with open(traffic) as f:
             line["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     if batch1 is not None:
