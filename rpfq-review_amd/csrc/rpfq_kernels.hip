@@ -1305,7 +1305,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 //     groups contribute 16 distinct columns per MFMA and 32 per k-step; the
 //     decoded pairs (A11, A12) / (A21, A22) of a column are directly the two
 //     k slots that meet (x_re, x_im) of the same column in B.
-//   * LUT: [entry][64 slots] fp16 (re, im) pairs at LDS address 0 (one wave
+//   * LUT: [entry][64 slots] fp16 (re, im) pairs at LDS address 0 (one tile
 //     per workgroup), each row held twice: row 16 h + r16 in slots
 //     32 h + 16 c + r16 (c = 0, 1), and lane group q reads copy c = q & 1,
 //     so the 32 lanes of a half-wave hit 32 distinct banks modulo 32.
@@ -1316,15 +1316,20 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 //     fragment straight from x (L2-resident) and interleaves them with
 //     v_perm_b32.  Rows past M read row M - 1: their MFMA columns are never
 //     stored.  Columns past K' (K' % 32 != 0 only) are zeroed.
-//   * waves are independent: codes and activations of k-step ks + SK_PF are
-//     requested before k-step ks is decoded, by unconditional loads in
-//     straight-line code (uniform base + constant lane offset) so the wait
-//     counts stay exact; occupancy hides the LDS latency of the decode.
+//   * split K for layers of few tiles: the 4 waves of a workgroup share one
+//     tile and its LUT, each walks a quarter of the k-steps, and wave 0 sums
+//     the partials through LDS (a small layer then covers 4x the SIMDs);
+//   * codes and activations of k-step ks + SK_PF are requested before k-step
+//     ks is decoded, by unconditional loads in straight-line code (uniform
+//     base + constant lane offset) so the wait counts stay exact; occupancy
+//     hides the LDS latency of the decode.
 #ifndef RPFQ_SK_PF
 #define RPFQ_SK_PF 4
 #endif
 constexpr int SK_PF = RPFQ_SK_PF;   // prefetch distance in k-steps
-constexpr int kSkLds = 32 * 64 * 4;  // 8 KB LUT
+constexpr int kSkLut = 32 * 64 * 4;  // 8 KB LUT
+constexpr int kSkRed = 3 * 16 * 64 * 4;  // partial sums of waves 1-3 (split-K)
+constexpr int kSkLds = kSkLut + kSkRed;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -1369,16 +1374,24 @@ __device__ __forceinline__ uint2 raw4_f16(uint2 v) {
 }
 
 // PB: per-(row, block) scales (the LUT is rebuilt at each block start);
-// KT: K' % 32 != 0 (activation columns past K' are zeroed).
-template <int XDT, int YDT, int CB, bool PB, bool KT>
-__global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
+// KT: K' % 32 != 0 (activation columns past K' are zeroed);
+// SPLIT (not with PB): split K -- the 4 waves of a workgroup share the
+// tile's LUT, take a quarter of the k-steps each, and wave 0 adds the three
+// other partial sums (through LDS, in a fixed order) before the epilogue.
+// Without SPLIT a workgroup is one wave streaming one tile's whole K.
+template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
+__global__ void __launch_bounds__(SPLIT ? 256 : 64, 4) wide_linear_skinny_kernel(WideArgs a) {
+    constexpr int NW = SPLIT ? 4 : 1;  // waves per tile
     extern __shared__ __align__(16) char smem[];
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, q = lane >> 4;
     const int R = lane & 31, g = lane >> 5;
     const int tile = blockIdx.x;
     const int KS = a.KS, K = a.K, M = (int)a.M;
+    const int chunk = (KS + NW - 1) / NW;
+    const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
 
     // uniform bases + constant lane offsets (global_load saddr + voffset)
     const uint2* ctile = reinterpret_cast<const uint2*>(a.codes) + (int64_t)tile * KS * 128;
@@ -1391,7 +1404,7 @@ __global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
         uint2 xr[2], xi[2];  // activations of MFMA t: 4 re, 4 im (raw 16-bit or fp16)
     };
     auto load_step = [&](int ks, Step& st) {
-        const int kc = ks < KS ? ks : KS - 1;
+        const int kc = ks < ke ? ks : (ke > 0 ? ke - 1 : 0);  // past the range: an L1 hit, unused
         const uint2* cp = ctile + kc * 128;
         st.c[0] = cp[coff];
         st.c[1] = cp[coff + 64];
@@ -1411,12 +1424,17 @@ __global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
     };
     Step ring[SK_PF];
 #pragma unroll
-    for (int i = 0; i < SK_PF; ++i) load_step(i, ring[i]);
+    for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
 
     int blk = 0;
-    {
+    if (wave == 0) {
         const float4* p = a.params + ((int64_t)tile * 32 + R) * a.nblk * 2;
         build_lut_sk<CB>(lut, p[0], p[1], a.rot, R, g);
+    }
+    if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     }
     // slot of (row group h, copy q & 1, row r16) in byte 0 of the address
     const uint32_t slot0 = (uint32_t)(16 * (q & 1) + r16) * 4;
@@ -1458,11 +1476,11 @@ __global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
             }
         }
     };
-    for (int ks0 = 0; ks0 < KS; ks0 += SK_PF) {
+    for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
 #pragma unroll
         for (int i = 0; i < SK_PF; ++i) {
             const int ks = ks0 + i;
-            if (ks >= KS) break;
+            if (ks >= ke) break;
             const Step cur = ring[i];
             load_step(ks + SK_PF, ring[i]);  // past the end: reloads the last k-step, unused
             if (PB) {  // per-(row, block) scales: new LUT at each block start
@@ -1474,6 +1492,33 @@ __global__ void __launch_bounds__(64, 4) wide_linear_skinny_kernel(WideArgs a) {
                 }
             }
             compute(ks, cur);
+        }
+    }
+
+    if (NW > 1) {  // waves 1-3 hand their partial sums to wave 0
+        float* red = reinterpret_cast<float*>(smem + kSkLut);
+        if (wave > 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                red[((wave - 1) * 16 + v) * 64 + lane] = acc_re[0][v];
+                red[((wave - 1) * 16 + 4 + v) * 64 + lane] = acc_re[1][v];
+                red[((wave - 1) * 16 + 8 + v) * 64 + lane] = acc_im[0][v];
+                red[((wave - 1) * 16 + 12 + v) * 64 + lane] = acc_im[1][v];
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < NW - 1; ++w) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                acc_re[0][v] += red[(w * 16 + v) * 64 + lane];
+                acc_re[1][v] += red[(w * 16 + 4 + v) * 64 + lane];
+                acc_im[0][v] += red[(w * 16 + 8 + v) * 64 + lane];
+                acc_im[1][v] += red[(w * 16 + 12 + v) * 64 + lane];
+            }
         }
     }
 
@@ -1852,17 +1897,26 @@ static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int XDT, int YDT, int CB, bool PB, bool KT>
+template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
 static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT>), dim3(a.NT), dim3(64), kSkLds, s, a);
+    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, SPLIT>), dim3(a.NT), dim3(SPLIT ? 256 : 64),
+                       SPLIT ? kSkLds : kSkLut, s, a);
     return hipGetLastError();
 }
 
+// Split K when the layer has too few tiles to give every SIMD a few waves
+// (a single layer at batch 1); a long stream of tiles runs one wave each.
+#ifndef RPFQ_SK_SPLIT_TILES
+#define RPFQ_SK_SPLIT_TILES 4096
+#endif
 template <int XDT, int YDT, int CB>
 static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
     const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
-    if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true>(a, s) : wide_sk_go<XDT, YDT, CB, true, false>(a, s);
-    return kt ? wide_sk_go<XDT, YDT, CB, false, true>(a, s) : wide_sk_go<XDT, YDT, CB, false, false>(a, s);
+    if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, false>(a, s)
+                      : wide_sk_go<XDT, YDT, CB, true, false, false>(a, s);
+    if (a.NT < RPFQ_SK_SPLIT_TILES)
+        return kt ? wide_sk_go<XDT, YDT, CB, false, true, true>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, true>(a, s);
+    return kt ? wide_sk_go<XDT, YDT, CB, false, true, false>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, false>(a, s);
 }
 
 template <int XDT, int YDT, int CB>

@@ -370,12 +370,14 @@ def test_wide_linear_streaming_dtypes(xdt, ydt, m):
     check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
 
 
-@pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640)])
+@pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640), (2, 131104, 64),
+                                       (12, 131072, 96), (1, 131200, 200)])
 def test_wide_linear_streaming_persistent(m, n_c, k_c):
-    """Large N' (tens of thousands of one-wave workgroups) and K' beyond 16
-    k-steps: the streaming kernel and the tiled kernel (RPFQ_FLAG_NO_STREAM)
-    contract the same fp16 operands, so float32 outputs agree to
-    accumulation order."""
+    """Large N': below 4096 tiles the split-K form (4 waves per tile), from
+    4096 tiles on one wave per tile (the last three cases), with K' tails and
+    K' beyond 16 k-steps.  The streaming kernel and the tiled kernel
+    (RPFQ_FLAG_NO_STREAM) contract the same fp16 operands, so float32
+    outputs agree to accumulation order."""
     ops, N = qm()
     r = rng(900 + m)
     planes_np, packed, sre, sim, kinds, cb, nblk = make_wide(r, n_c, k_c)
