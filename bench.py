@@ -39,7 +39,7 @@ CONFIGS = {
 }
 
 
-def build_model(cfg_name: str):
+def build_model(cfg_name: str, act_quant: bool = False):
     import torch
     import quant_models as qm
     from quant_models import _native as N
@@ -48,7 +48,7 @@ def build_model(cfg_name: str):
     name, _, img, codebook, seed, _ = CONFIGS[cfg_name]
     torch.manual_seed(seed)
     model = qm.create_model(name, img_size=img, quant_method_u="complex_phase_v2",
-                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+                            quant_method_w="complex_phase_v2", enable_act_quant=act_quant, enable_rotation=False)
     cb = N.CB_PSK16 if codebook == "psk16" else N.CB_AXIS
     load_synthetic_codes(model, seed, cb)
     prepare_inference(model, "cuda", torch.float16)
@@ -267,6 +267,8 @@ def main() -> int:
                     help="comma-separated subset of the sweep's layer shapes (e.g. vit_b.fc1)")
     ap.add_argument("--no-stream-line", action="store_true",
                     help="leave the batch-1 streaming summary out of the bench line")
+    ap.add_argument("--act-quant", action="store_true",
+                    help="build the model with 4-bit activation quantization (the reference layer's default)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one forward in a HIP graph and time its replays (launch-bound small batches)")
     args = ap.parse_args()
@@ -307,7 +309,7 @@ def main() -> int:
         batch1 = {"kernel": "rpfq::wide_linear_skinny_kernel (M <= 16)", "bound": "hbm", "peak": PEAK_HBM_GBS,
                   "unit": "GB/s", "stacked": stream_case(k_c, n_c, 1, "stacked", 1.0, 10),
                   "rotate": stream_case(k_c, n_c, 1, "rotate", 1.0, 5)}
-    model = build_model(args.config)
+    model = build_model(args.config, args.act_quant)
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(torch.float16)
 
@@ -381,6 +383,7 @@ def main() -> int:
         "data": "synthetic (N(0,1) images; random-init weights quantized by the reference axis rule, "
                 "synthetic per-row scales)",
         "config": {"workload": f"{args.config}: {desc} forward, bs{batch}, {img}x{img}"
+                               + (", 4-bit activation quantization" if args.act_quant else "")
                                + (" (HIP graph replay)" if graph is not None else ""),
                    "batch": batch, "tokens": tokens, "packed_layers_per_step": len(launches) // args.steps},
         "roofline": {

@@ -183,6 +183,19 @@ int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const floa
                     float eps, void* y, int y_dtype, void* stream);
 
 /*
+ * rpfq_layer_norm followed by the activation fake quantization of
+ * rpfq_act_quant on its output, in one pass over the rows: the LayerNorm
+ * output is rounded to y_dtype and then quantized per row and per half
+ * (C/2 columns each; C % 16 == 0), so y is bit-identical to the two calls in
+ * sequence.  bits: 2 .. 16.  The quantized input of the qkv and fc1 layers
+ * of a block with activation quantization on
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:520, :549 followed by
+ *   RPFQ-ViT-main/quant_models/quant_i.py:546-551.
+ */
+int rpfq_layer_norm_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma,
+                              const float* beta, float eps, int bits, void* y, int y_dtype, void* stream);
+
+/*
  * Activation fake quantization of a [M, in_features] feature block laid out
  * [re | im]: per row and per half, scale = qmax * (1 / max(max|x|, 1e-5)),
  * y = clamp(round_half_even(x * scale), -2^(bits-1), 2^(bits-1)-1) / scale,

@@ -54,6 +54,20 @@ int check_desc(const rpfq_wide_desc* d) {
     return RPFQ_OK;
 }
 
+int check_ln(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma, const float* beta, float eps,
+             void* y, int y_dtype) {
+    if (!x || !y) return fail(RPFQ_ERR_NULL, "x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0 || C <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld C=%lld must be positive", (long long)M, (long long)C);
+    if (C % 8 != 0 || C > 4096) return fail(RPFQ_ERR_SHAPE, "C=%lld must be a multiple of 8 and <= 4096", (long long)C);
+    if (M > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    if (!(eps >= 0.0f)) return fail(RPFQ_ERR_VALUE, "eps must be non-negative");
+    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(gamma, 16) || !aligned(beta, 16))
+        return fail(RPFQ_ERR_ALIGN, "x, y, gamma and beta must be 16-byte aligned");
+    return RPFQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -168,20 +182,25 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
                       "rpfq_wide_linear_residual");
 }
 
+
 int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma, const float* beta,
                     float eps, void* y, int y_dtype, void* stream) {
-    if (!x || !y) return fail(RPFQ_ERR_NULL, "x/y must not be NULL");
-    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
-        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
-    if (M <= 0 || C <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld C=%lld must be positive", (long long)M, (long long)C);
-    if (C % 8 != 0 || C > 4096) return fail(RPFQ_ERR_SHAPE, "C=%lld must be a multiple of 8 and <= 4096", (long long)C);
-    if (M > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
-    if (!(eps >= 0.0f)) return fail(RPFQ_ERR_VALUE, "eps must be non-negative");
-    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(gamma, 16) || !aligned(beta, 16))
-        return fail(RPFQ_ERR_ALIGN, "x, y, gamma and beta must be 16-byte aligned");
-    return hip_status(rpfq::launch_layer_norm(x, x_dtype, M, C, gamma, beta, eps, y, y_dtype,
+    int rc = check_ln(x, x_dtype, M, C, gamma, beta, eps, y, y_dtype);
+    if (rc) return rc;
+    return hip_status(rpfq::launch_layer_norm(x, x_dtype, M, C, gamma, beta, eps, 0, y, y_dtype,
                                               reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_layer_norm");
+}
+
+int rpfq_layer_norm_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma,
+                              const float* beta, float eps, int bits, void* y, int y_dtype, void* stream) {
+    int rc = check_ln(x, x_dtype, M, C, gamma, beta, eps, y, y_dtype);
+    if (rc) return rc;
+    if (C % 16 != 0) return fail(RPFQ_ERR_SHAPE, "C=%lld: each half must be a multiple of 8", (long long)C);
+    if (bits < 2 || bits > 16) return fail(RPFQ_ERR_BITS, "bits=%d unsupported (2..16)", bits);
+    return hip_status(rpfq::launch_layer_norm(x, x_dtype, M, C, gamma, beta, eps, bits, y, y_dtype,
+                                              reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_layer_norm_act_quant");
 }
 
 int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, int bits, void* y, int y_dtype,

@@ -1379,8 +1379,11 @@ __device__ __forceinline__ uint2 raw4_f16(uint2 v) {
 // tile's LUT, take a quarter of the k-steps each, and wave 0 adds the three
 // other partial sums (through LDS, in a fixed order) before the epilogue.
 // Without SPLIT a workgroup is one wave streaming one tile's whole K.
+#ifndef RPFQ_SK_OCC
+#define RPFQ_SK_OCC 4  // waves per SIMD the register budget is sized for
+#endif
 template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
-__global__ void __launch_bounds__(SPLIT ? 256 : 64, 4) wide_linear_skinny_kernel(WideArgs a) {
+__global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
     constexpr int NW = SPLIT ? 4 : 1;  // waves per tile
     extern __shared__ __align__(16) char smem[];
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
@@ -1687,67 +1690,133 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <int XDT, int YDT, int TPR, int NC>
+template <int TPR>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+template <int YDT>
+__device__ __forceinline__ float round_to(float v) {
+    if (YDT == RPFQ_F16) return (float)(_Float16)v;
+    if (YDT == RPFQ_BF16) return bf16_to_f32(f32_to_bf16(v));
+    return v;
+}
+
+// Row kernel for LayerNorm and / or activation fake quantization.
+// LN: y = (x - mean) / sqrt(var + eps) * gamma + beta (nn.LayerNorm);
+// AQ: per row and per half [0, C/2), [C/2, C): scale = qmax * (1 / max(max|v|,
+// 1e-5)), v = clamp(rint(v * scale), qmin, qmax) / scale in float32
+// (quant_i.py:438-455), applied to the LN output already rounded to y's
+// dtype, so LN + AQ is bit-identical to the two kernels in sequence.
+// Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
+// the two halves.
+template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ>
 __global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict__ x, int64_t M, int C,
                                                          const float* __restrict__ gamma,
-                                                         const float* __restrict__ beta, float eps, void* y) {
+                                                         const float* __restrict__ beta, float eps, int bits,
+                                                         void* y) {
     const int sub = threadIdx.x % TPR;
     const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
     if (row >= M) return;  // whole groups leave together: TPR divides the wave
     const int nch = C >> 3;
     const int64_t base = row * C;
     float v[NC][8];
-    float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = sub + TPR * j;
-        if (c < nch) {
-            load8_ln<XDT>(x, base + 8 * c, v[j]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s += v[j][e];
-        }
+        if (c < nch) load8_ln<XDT>(x, base + 8 * c, v[j]);
     }
-    const float mean = group_sum<TPR>(s) / (float)C;
-    float s2 = 0.0f;
+    if (LN) {
+        float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        if (sub + TPR * j < nch) {
+        for (int j = 0; j < NC; ++j)
+            if (sub + TPR * j < nch) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float d = v[j][e] - mean;
-                s2 += d * d;
+                for (int e = 0; e < 8; ++e) s += v[j][e];
+            }
+        const float mean = group_sum<TPR>(s) / (float)C;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            if (sub + TPR * j < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = v[j][e] - mean;
+                    s2 += d * d;
+                }
+            }
+        }
+        const float rstd = 1.0f / sqrtf(group_sum<TPR>(s2) / (float)C + eps);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = sub + TPR * j;
+            if (c < nch) {
+                float gk[8], bk[8];
+                if (gamma) {
+                    const float4* gp = reinterpret_cast<const float4*>(gamma + 8 * c);
+                    const float4 g0 = gp[0], g1 = gp[1];
+                    gk[0] = g0.x; gk[1] = g0.y; gk[2] = g0.z; gk[3] = g0.w;
+                    gk[4] = g1.x; gk[5] = g1.y; gk[6] = g1.z; gk[7] = g1.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) gk[e] = 1.0f;
+                }
+                if (beta) {
+                    const float4* bp = reinterpret_cast<const float4*>(beta + 8 * c);
+                    const float4 b0 = bp[0], b1 = bp[1];
+                    bk[0] = b0.x; bk[1] = b0.y; bk[2] = b0.z; bk[3] = b0.w;
+                    bk[4] = b1.x; bk[5] = b1.y; bk[6] = b1.z; bk[7] = b1.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) bk[e] = 0.0f;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float o = (v[j][e] - mean) * rstd * gk[e] + bk[e];
+                    v[j][e] = AQ ? round_to<YDT>(o) : o;
+                }
             }
         }
     }
-    const float rstd = 1.0f / sqrtf(group_sum<TPR>(s2) / (float)C + eps);
+    if (AQ) {
+        const int half_ch = nch >> 1;  // chunks of the real half
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = sub + TPR * j;
+            if (c < nch) {
+                float mx = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[j][e]));
+                if (c < half_ch) m0 = fmaxf(m0, mx); else m1 = fmaxf(m1, mx);
+            }
+        }
+        m0 = group_max<TPR>(m0);
+        m1 = group_max<TPR>(m1);
+        const float qmax = (float)((1 << (bits - 1)) - 1);
+        const float qmin = -(float)(1 << (bits - 1));
+        // torch evaluates `float(qmax) / tensor` as reciprocal(tensor) * qmax
+        const float sc0 = (1.0f / fmaxf(m0, 1e-5f)) * qmax, sc1 = (1.0f / fmaxf(m1, 1e-5f)) * qmax;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = sub + TPR * j;
+            if (c < nch) {
+                const float sc = c < half_ch ? sc0 : sc1;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float qv = rintf(v[j][e] * sc);
+                    qv = fminf(fmaxf(qv, qmin), qmax);
+                    v[j][e] = qv / sc;
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = sub + TPR * j;
-        if (c < nch) {
-            float gk[8], bk[8];
-            if (gamma) {
-                const float4* gp = reinterpret_cast<const float4*>(gamma + 8 * c);
-                const float4 g0 = gp[0], g1 = gp[1];
-                gk[0] = g0.x; gk[1] = g0.y; gk[2] = g0.z; gk[3] = g0.w;
-                gk[4] = g1.x; gk[5] = g1.y; gk[6] = g1.z; gk[7] = g1.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) gk[e] = 1.0f;
-            }
-            if (beta) {
-                const float4* bp = reinterpret_cast<const float4*>(beta + 8 * c);
-                const float4 b0 = bp[0], b1 = bp[1];
-                bk[0] = b0.x; bk[1] = b0.y; bk[2] = b0.z; bk[3] = b0.w;
-                bk[4] = b1.x; bk[5] = b1.y; bk[6] = b1.z; bk[7] = b1.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) bk[e] = 0.0f;
-            }
-            float o[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (v[j][e] - mean) * rstd * gk[e] + bk[e];
-            store8_ln<YDT>(y, base + 8 * c, o);
-        }
+        if (c < nch) store8_ln<YDT>(y, base + 8 * c, v[j]);
     }
 }
 
@@ -1988,7 +2057,14 @@ static hipError_t act_y(const void* x, int64_t M, int64_t K, int bits, void* y, 
     return hipGetLastError();
 }
 
+static hipError_t row_op(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
+                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s);
+
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt, hipStream_t s) {
+    // rows held in registers when no 8-element chunk straddles the halves
+    const bool vec = K % 8 == 0 && 2 * K <= 4096 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    if (vec) return row_op(x, xdt, M, 2 * K, nullptr, nullptr, 0.0f, 2, bits, y, ydt, s);
     switch (xdt) {
         case RPFQ_F32: return act_y<RPFQ_F32>(x, M, K, bits, y, ydt, s);
         case RPFQ_F16: return act_y<RPFQ_F16>(x, M, K, bits, y, ydt, s);
@@ -1998,42 +2074,56 @@ hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bi
 
 template <int XDT, int YDT, int TPR, int NC>
 static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                            void* y, hipStream_t s) {
+                            int mode, int bits, void* y, hipStream_t s) {
     const dim3 grid((unsigned)((M + 256 / TPR - 1) / (256 / TPR)));
-    hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC>), grid, dim3(256), 0, s, x, M, C, gamma, beta, eps, y);
+    if (mode == 1)
+        hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false>), grid, dim3(256), 0, s, x, M, C, gamma,
+                           beta, eps, bits, y);
+    else if (mode == 2)
+        hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true>), grid, dim3(256), 0, s, x, M, C, gamma,
+                           beta, eps, bits, y);
+    else
+        hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, true>), grid, dim3(256), 0, s, x, M, C, gamma,
+                           beta, eps, bits, y);
     return hipGetLastError();
 }
 
 // Lanes per row: the smallest of 8, 16, 32, 64 that keeps every lane at <= 4
 // chunks (C <= 2048), else 64 lanes with up to 8 chunks (C <= 4096).
+// mode: 1 LayerNorm, 2 activation quantization, 3 both.
 template <int XDT, int YDT>
-static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, void* y,
-                        hipStream_t s) {
+static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
+                        int mode, int bits, void* y, hipStream_t s) {
     const int nch = C / 8;
-    if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, y, s);
-    if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, y, s);
-    if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, y, s);
-    if (nch <= 256) return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, y, s);
-    return ln_launch<XDT, YDT, 64, 8>(x, M, C, gamma, beta, eps, y, s);
+    if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+    if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+    if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+    if (nch <= 256) return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+    return ln_launch<XDT, YDT, 64, 8>(x, M, C, gamma, beta, eps, mode, bits, y, s);
 }
 
 template <int XDT>
-static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, void* y,
-                       int ydt, hipStream_t s) {
+static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, int mode,
+                       int bits, void* y, int ydt, hipStream_t s) {
     switch (ydt) {
-        case RPFQ_F32: return ln_go<XDT, RPFQ_F32>(x, M, C, gamma, beta, eps, y, s);
-        case RPFQ_F16: return ln_go<XDT, RPFQ_F16>(x, M, C, gamma, beta, eps, y, s);
-        default: return ln_go<XDT, RPFQ_BF16>(x, M, C, gamma, beta, eps, y, s);
+        case RPFQ_F32: return ln_go<XDT, RPFQ_F32>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+        case RPFQ_F16: return ln_go<XDT, RPFQ_F16>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+        default: return ln_go<XDT, RPFQ_BF16>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+    }
+}
+
+static hipError_t row_op(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
+                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return ln_y<RPFQ_F32>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
+        case RPFQ_F16: return ln_y<RPFQ_F16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
+        default: return ln_y<RPFQ_BF16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
     }
 }
 
 hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
-                             float eps, void* y, int ydt, hipStream_t s) {
-    switch (xdt) {
-        case RPFQ_F32: return ln_y<RPFQ_F32>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
-        case RPFQ_F16: return ln_y<RPFQ_F16>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
-        default: return ln_y<RPFQ_BF16>(x, M, (int)C, gamma, beta, eps, y, ydt, s);
-    }
+                             float eps, int bits, void* y, int ydt, hipStream_t s) {
+    return row_op(x, xdt, M, C, gamma, beta, eps, bits > 0 ? 3 : 1, bits, y, ydt, s);
 }
 
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, float* out,

@@ -44,6 +44,7 @@ EXPORTED = (
     "rpfq_act_quant",
     "rpfq_wide_linear_residual",
     "rpfq_layer_norm",
+    "rpfq_layer_norm_act_quant",
 )
 
 
@@ -106,6 +107,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         lib.rpfq_wide_linear_residual.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, i32, i32, vp]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
+        lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
         for name in EXPORTED[2:]:
             if name != "rpfq_wide_packed_bytes":
                 getattr(lib, name).restype = i32

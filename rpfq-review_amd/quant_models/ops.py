@@ -86,10 +86,12 @@ def act_quant(x: torch.Tensor, num_bits: int, out_dtype: torch.dtype | None = No
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None, eps: float,
-               out_dtype: torch.dtype | None = None) -> torch.Tensor:
+               out_dtype: torch.dtype | None = None, act_bits: int = 0) -> torch.Tensor:
     """nn.LayerNorm over the last dimension on the device (rpfq_layer_norm):
     float32 statistics, output in out_dtype (default x.dtype).  weight/bias
-    are taken as float32."""
+    are taken as float32.  act_bits > 0: the output is also fake-quantized
+    per row and half (rpfq_layer_norm_act_quant, bit-identical to
+    act_quant(layer_norm(x)))."""
     N.require_device(x, weight, bias)
     c = x.shape[-1]
     x2 = x.reshape(-1, c)
@@ -101,9 +103,14 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
     w = None if weight is None else weight.detach().float().contiguous()
     b = None if bias is None else bias.detach().float().contiguous()
     lib = N.load()
-    N.check("rpfq_layer_norm", lib.rpfq_layer_norm(
-        x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], c, N.ptr(w), N.ptr(b), float(eps), y.data_ptr(),
-        N.dtype_code(y.dtype), N.stream_of(x2)))
+    if act_bits:
+        N.check("rpfq_layer_norm_act_quant", lib.rpfq_layer_norm_act_quant(
+            x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], c, N.ptr(w), N.ptr(b), float(eps), int(act_bits),
+            y.data_ptr(), N.dtype_code(y.dtype), N.stream_of(x2)))
+    else:
+        N.check("rpfq_layer_norm", lib.rpfq_layer_norm(
+            x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], c, N.ptr(w), N.ptr(b), float(eps), y.data_ptr(),
+            N.dtype_code(y.dtype), N.stream_of(x2)))
     return y.reshape(x.shape)
 
 

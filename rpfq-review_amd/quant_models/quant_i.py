@@ -331,14 +331,27 @@ class QATLinearComplexPhase(nn.Linear):
                 vs.append((q.rotation_angle.data_ptr(), q.rotation_angle._version))
         return tuple(vs)
 
-    def _packed_forward(self, x: torch.Tensor) -> torch.Tensor:
+    def _packed_forward(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         from . import ops
 
         pw = self.packed(x.device)
-        if self.act_quantizer is not None:
+        if self.act_quantizer is not None and not prequantized:
             x = ops.act_quant(x, self.act_quantizer.num_bits)
         bias = None if self.bias is None else self.bias.detach()
         return pw.linear(x, bias, out_dtype=x.dtype)
+
+    def packed_act_bits(self, x: torch.Tensor) -> int:
+        """Bits of the activation quantization the packed path would apply to
+        x (0 if none or if x does not take the packed path)."""
+        if self.act_quantizer is None or not (x.is_cuda and not self.training and self.use_packed):
+            return 0
+        return self.act_quantizer.num_bits
+
+    def forward_prequantized(self, x: torch.Tensor) -> torch.Tensor:
+        """forward() for an input the caller already fake-quantized exactly as
+        this layer's activation quantizer would (e.g. by
+        rpfq_layer_norm_act_quant); only valid when packed_act_bits(x) > 0."""
+        return self._packed_forward(x, prequantized=True)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda and not self.training and self.use_packed:

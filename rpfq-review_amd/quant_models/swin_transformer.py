@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .vision_transformer import Mlp, PatchEmbed, _fused, _trunc_normal_, norm_fwd
+from .vision_transformer import Mlp, PatchEmbed, _fused, _trunc_normal_, call_layer, norm_fwd, norm_quant_fwd
 
 
 def window_partition(x: torch.Tensor, ws: int) -> torch.Tensor:
@@ -127,7 +127,8 @@ class SwinTransformerBlock(nn.Module):
         x = x + self._attn(norm_fwd(self.norm1, x))
         x = x.reshape(b, -1, c)
         if _fused(self, x):  # the MLP residual add fused into fc2's store
-            x = self.mlp.forward_residual(norm_fwd(self.norm2, x), x)
+            hn, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
+            x = self.mlp.forward_residual(hn, x, q)
         else:
             x = x + self.mlp(self.norm2(x))
         return x.reshape(b, h, w, c)
@@ -147,7 +148,8 @@ class PatchMerging(nn.Module):
     def forward(self, x):
         b, h, w, c = x.shape
         x = x.reshape(b, h // 2, 2, w // 2, 2, c).permute(0, 1, 3, 4, 2, 5).flatten(3)
-        return self.reduction(norm_fwd(self.norm, x))
+        h, q = norm_quant_fwd(self.norm, x, self.reduction)
+        return call_layer(self.reduction, h, q)
 
 
 class SwinTransformerStage(nn.Module):

@@ -22,6 +22,9 @@ import torch.nn.functional as F
 # HIP kernel and the residual add after attn.proj / mlp.fc2 fused into the
 # packed layer's store.  RPFQ_FUSED=0 keeps the module-by-module forward.
 FUSED_BLOCKS = os.environ.get("RPFQ_FUSED", "1") != "0"
+# Within the fused path, a LayerNorm feeding a packed layer with activation
+# quantization also applies that quantization (rpfq_layer_norm_act_quant).
+FUSE_ACT_QUANT = os.environ.get("RPFQ_FUSE_AQ", "1") != "0"
 
 
 def _fused(module: nn.Module, x: torch.Tensor) -> bool:
@@ -36,13 +39,40 @@ def norm_fwd(norm: nn.Module, x: torch.Tensor) -> torch.Tensor:
         return norm(x)
     from . import ops
 
+    w, b = _ln_params(norm)
+    return ops.layer_norm(x, w, b, norm.eps)
+
+
+def _ln_params(norm: nn.LayerNorm):
+    """float32 copies of the affine parameters, cached on the module."""
     key = tuple((t.data_ptr(), t._version) if t is not None else None for t in (norm.weight, norm.bias))
     cache = getattr(norm, "_rpfq_f32", None)
     if cache is None or cache[0] != key:
         cache = (key, None if norm.weight is None else norm.weight.detach().float().contiguous(),
                  None if norm.bias is None else norm.bias.detach().float().contiguous())
         norm._rpfq_f32 = cache
-    return ops.layer_norm(x, cache[1], cache[2], norm.eps)
+    return cache[1], cache[2]
+
+
+def norm_quant_fwd(norm: nn.Module, x: torch.Tensor, layer: nn.Module):
+    """(h, prequantized): h = norm(x), with `layer`'s activation fake
+    quantization applied in the same device kernel when layer is a packed
+    phase-quantized Linear that quantizes its input; prequantized tells the
+    caller to run layer.forward_prequantized(h) instead of layer(h)."""
+    bits_of = getattr(layer, "packed_act_bits", None)
+    bits = bits_of(x) if bits_of is not None else 0
+    c = x.shape[-1]
+    if not (bits and FUSE_ACT_QUANT and _fused(norm, x) and type(norm) is nn.LayerNorm and c % 16 == 0
+            and c <= 4096 and len(norm.normalized_shape) == 1):
+        return norm_fwd(norm, x), False
+    from . import ops
+
+    w, b = _ln_params(norm)
+    return ops.layer_norm(x, w, b, norm.eps, act_bits=bits), True
+
+
+def call_layer(layer: nn.Module, h: torch.Tensor, prequantized: bool) -> torch.Tensor:
+    return layer.forward_prequantized(h) if prequantized else layer(h)
 
 
 def linear_residual(layer: nn.Module, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
@@ -99,9 +129,11 @@ class Mlp(nn.Module):
     def forward(self, x):
         return self.drop2(self.fc2(self.norm(self.drop1(self.act(self.fc1(x))))))
 
-    def forward_residual(self, x, residual):
-        """residual + self(x) with the add fused into fc2 (eval mode)."""
-        return linear_residual(self.fc2, self.norm(self.drop1(self.act(self.fc1(x)))), residual)
+    def forward_residual(self, x, residual, prequantized: bool = False):
+        """residual + self(x) with the add fused into fc2 (eval mode); x
+        already activation-quantized for fc1 if prequantized."""
+        h = call_layer(self.fc1, x, prequantized)
+        return linear_residual(self.fc2, self.norm(self.drop1(self.act(h))), residual)
 
 
 class Attention(nn.Module):
@@ -117,9 +149,10 @@ class Attention(nn.Module):
         self.proj = nn.Linear(dim, dim)
         self.proj_drop = nn.Dropout(proj_drop)
 
-    def _mix(self, x):
+    def _mix(self, x, prequantized: bool = False):
         b, n, c = x.shape
-        qkv = self.qkv(x).reshape(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        qkv = call_layer(self.qkv, x, prequantized).reshape(b, n, 3, self.num_heads, self.head_dim)
+        qkv = qkv.permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)
         x = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
         return x.transpose(1, 2).reshape(b, n, c)
@@ -127,9 +160,10 @@ class Attention(nn.Module):
     def forward(self, x):
         return self.proj_drop(self.proj(self._mix(x)))
 
-    def forward_residual(self, x, residual):
-        """residual + self(x) with the add fused into proj (eval mode)."""
-        return linear_residual(self.proj, self._mix(x), residual)
+    def forward_residual(self, x, residual, prequantized: bool = False):
+        """residual + self(x) with the add fused into proj (eval mode); x
+        already activation-quantized for qkv if prequantized."""
+        return linear_residual(self.proj, self._mix(x, prequantized), residual)
 
 
 class Block(nn.Module):
@@ -147,8 +181,10 @@ class Block(nn.Module):
         if _fused(self, x) and isinstance(self.ls1, nn.Identity) and isinstance(self.ls2, nn.Identity):
             # audit_rpfq_vit_ios_parity.py:520-556 with the residual adds in
             # the proj / fc2 stores and LayerNorm on the device kernel
-            x = self.attn.forward_residual(norm_fwd(self.norm1, x), x)
-            return self.mlp.forward_residual(norm_fwd(self.norm2, x), x)
+            h, q = norm_quant_fwd(self.norm1, x, self.attn.qkv)
+            x = self.attn.forward_residual(h, x, q)
+            h, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
+            return self.mlp.forward_residual(h, x, q)
         x = x + self.ls1(self.attn(self.norm1(x)))
         x = x + self.ls2(self.mlp(self.norm2(x)))
         return x

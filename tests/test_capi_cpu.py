@@ -124,3 +124,14 @@ def test_residual_and_layer_norm_argument_errors():
     assert L.rpfq_layer_norm(p, 1, 4, 64, None, None, -1.0, p, 1, None) == 6
     assert L.rpfq_layer_norm(ctypes.c_void_p(258), 1, 4, 64, None, None, 1e-6, p, 1, None) == 3
     assert L.rpfq_layer_norm(p, 1, 4, 64, ctypes.c_void_p(260), None, 1e-6, p, 1, None) == 3
+
+
+def test_layer_norm_act_quant_argument_errors():
+    L, _ = lib()
+    p = ctypes.c_void_p(256)
+    assert L.rpfq_layer_norm_act_quant(None, 1, 4, 64, None, None, 1e-6, 4, p, 1, None) == 1
+    assert L.rpfq_layer_norm_act_quant(p, 1, 4, 40, None, None, 1e-6, 4, p, 1, None) == 2   # C/2 % 8
+    assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, 1e-6, 1, p, 1, None) == 4   # bits
+    assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, 1e-6, 17, p, 1, None) == 4
+    assert L.rpfq_layer_norm_act_quant(p, 3, 4, 64, None, None, 1e-6, 4, p, 1, None) == 5
+    assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, -1.0, 4, p, 1, None) == 6

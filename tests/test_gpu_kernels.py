@@ -460,3 +460,35 @@ def test_layer_norm(m, c, xdt, ydt):
     y0 = ops.layer_norm(x.to(DEV), None, None, 1e-5, out_dtype=torch.float32).cpu().numpy()
     ref0 = (xd - mu) / np.sqrt(var + 1e-5)
     assert np.abs(y0 - ref0).max() <= 2e-5 * (np.abs(ref0).max() + 1)
+
+
+@pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 1024), (5, 3072)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16)])
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_layer_norm_act_quant_bit_exact(m, c, xdt, ydt, bits):
+    """rpfq_layer_norm_act_quant == rpfq_act_quant(rpfq_layer_norm(x)) bit for
+    bit (the LN output is rounded to y's dtype before it is quantized)."""
+    ops, _ = qm()
+    r = rng(1300 + c + bits)
+    x = torch.from_numpy((r.standard_normal((m, c)) * 2 + 0.5).astype(np.float32)).to(xdt).to(DEV)
+    g = tdev(r.standard_normal(c).astype(np.float32))
+    b = tdev(r.standard_normal(c).astype(np.float32))
+    fused = ops.layer_norm(x, g, b, 1e-6, out_dtype=ydt, act_bits=bits)
+    two = ops.act_quant(ops.layer_norm(x, g, b, 1e-6, out_dtype=ydt), bits)
+    assert torch.equal(fused, two)
+
+
+@pytest.mark.parametrize("k", [8, 384, 1536])
+def test_act_quant_row_kernel_matches_oracle(k):
+    """The register-resident act-quant kernel (K' % 8 == 0) is bit-exact with
+    the oracle's restatement of quant_i.py:438-455 in float32."""
+    ops, _ = qm()
+    r = rng(1400 + k)
+    xs = (r.standard_normal((41, 2 * k)) * 3).astype(np.float32)
+    xs[0, :] = 0.0           # all-zero row: the 1e-5 clamp
+    xs[1, :k] = 1.5          # ties at the half-scale points
+    for bits in (2, 4, 8):
+        ys = ops.act_quant(tdev(xs), bits).cpu().numpy()
+        qr, qi = O.act_quant(xs[:, :k], xs[:, k:], bits)
+        assert np.array_equal(ys, np.concatenate([qr, qi], axis=1))

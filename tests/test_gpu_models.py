@@ -174,3 +174,34 @@ def test_fused_blocks_match_unfused(name):
     top = y_u.topk(2, dim=1).values
     confident = (top[:, 0] - top[:, 1]) > 4 * err
     assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
+
+
+@pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_swin_tiny_patch4_window7_224_q"])
+def test_fused_act_quant_wiring(name):
+    """With activation quantization on, the fused block path feeds qkv / fc1
+    (and Swin's patch-merging reduction) from rpfq_layer_norm_act_quant and
+    skips their own quantization pass.  That kernel is bit-identical to
+    LayerNorm followed by act-quant, so the logits must equal those of the
+    same fused path with the LN + act-quant fusion switched off: a layer
+    quantized twice (or not at all) would change them."""
+    import quant_models as qm
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(4)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=True, enable_rotation=False)
+    load_synthetic_codes(model, 4)
+    prepare_inference(model, DEV, torch.float16)
+    x = torch.randn(8, 3, 224, 224, generator=torch.Generator().manual_seed(6)).to(DEV, torch.float16)
+    saved = vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT
+    try:
+        with torch.no_grad():
+            vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = True, True
+            y_f = model(x)
+            vt.FUSE_ACT_QUANT = False
+            y_u = model(x)
+    finally:
+        vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = saved
+    assert torch.isfinite(y_f).all()
+    assert torch.equal(y_f, y_u)
