@@ -244,6 +244,82 @@ def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, r
     return rows
 
 
+def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: bool, modes=("hip", "torch")):
+    """Quantization-aware training steps of the configured model (float32,
+    rotation at the family default, SGD): forward with every Linear
+    quantized from its float32 master weight, backward with straight-through
+    gradients, optimizer step.  'hip' runs the weight quantizer and the act
+    quant as HIP kernels (rpfq_quantize_wide, rpfq_act_quant); 'torch' runs
+    the reference formulation in torch ops on the GPU.  Also times the weight
+    quantization of all layers alone (no grad).  Prints one JSON line."""
+    import torch
+    import torch.nn.functional as F
+    import quant_models as qm
+    from quant_models import quant_i
+    from quant_models.inference import quant_layers
+
+    name, _, img, _, seed, desc = CONFIGS[cfg_name]
+    out = {}
+    for mode in modes:
+        quant_i.HIP_QAT = mode == "hip"
+        torch.manual_seed(seed)
+        model = qm.create_model(name, img_size=img, quant_method_u="complex_phase_v2",
+                                quant_method_w="complex_phase_v2", enable_act_quant=act_quant).cuda().train()
+        opt = torch.optim.SGD(model.parameters(), lr=1e-4, momentum=0.9)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        x = torch.randn(batch, 3, img, img, device="cuda", generator=g)
+        labels = torch.randint(0, 1000, (batch,), device="cuda", generator=g)
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            loss = F.cross_entropy(model(x), labels)
+            loss.backward()
+            opt.step()
+            return loss
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        layers = [layer for _, layer in quant_layers(model)]
+        probe = torch.zeros(1, device="cuda")
+        with torch.no_grad():
+            for _ in range(2):
+                for layer in layers:
+                    if mode == "hip":
+                        quant_i._HipWideQuantSTE.apply(layer.weight, layer.quantizer_u.rotation_angle,
+                                                       layer.quantizer_w.rotation_angle, layer._hip_qat_spec(probe))
+                    else:
+                        layer.quantized_weight()
+            torch.cuda.synchronize()
+            tq = time.perf_counter()
+            for layer in layers:
+                if mode == "hip":
+                    quant_i._HipWideQuantSTE.apply(layer.weight, layer.quantizer_u.rotation_angle,
+                                                   layer.quantizer_w.rotation_angle, layer._hip_qat_spec(probe))
+                else:
+                    layer.quantized_weight()
+            torch.cuda.synchronize()
+            tq = time.perf_counter() - tq
+        out[mode] = {"images_per_s": round(batch * steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 3),
+                     "weight_quant_ms": round(1e3 * tq, 3), "layers": len(layers), "final_loss": float(loss)}
+        print(f"# train {mode}: {out[mode]}", file=sys.stderr, flush=True)
+        del model, opt
+        torch.cuda.empty_cache()
+    quant_i.HIP_QAT = True
+    first = out[modes[0]]
+    print(json.dumps({"metric": f"QAT training images/s {desc}, float32, SGD", "value": first["images_per_s"],
+                      "unit": "images/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+                      "ms_per_step": first["ms_per_step"], "higher_is_better": True, "data": "synthetic",
+                      "config": {"workload": cfg_name, "batch": batch, "act_quant": act_quant, "mode": modes[0]},
+                      "modes": out}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,7 +347,13 @@ def main() -> int:
                     help="build the model with 4-bit activation quantization (the reference layer's default)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one forward in a HIP graph and time its replays (launch-bound small batches)")
+    ap.add_argument("--train", action="store_true",
+                    help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
+    ap.add_argument("--train-modes", default="hip,torch")
     args = ap.parse_args()
+    if args.train:
+        return train_bench(args.config, args.batch or 64, args.steps, args.warmup, args.act_quant,
+                           tuple(args.train_modes.split(",")))
     if args.stream_sweep:
         shapes = None if not args.stream_shapes else set(args.stream_shapes.split(","))
         if shapes and not shapes <= set(STREAM_SHAPES):

@@ -216,6 +216,50 @@ int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, i
 int rpfq_wide_decode(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                      float* a, int round_fp16, void* stream);
 
+/* weight quantizer kinds (training semantics) */
+#define RPFQ_QK_AXIS 0  /* dominant-axis stages, quant_i.py:36-81 (complex_phase_v1..v4) */
+#define RPFQ_QK_SIGN 1  /* quadrant-sign stages, quant_i.py:84-91 (complex_phase_new_v2) */
+
+/* Shape and methods of one QATLinearComplexPhase weight for rpfq_quantize_wide. */
+typedef struct rpfq_quant_desc {
+    int64_t n_complex; /* N' = out_features / 2 */
+    int64_t k_complex; /* K' = in_features / 2 */
+    int32_t kind[2];   /* RPFQ_QK_* of U and of W */
+    int32_t steps[2];  /* residual stages of U and of W, 1..4 */
+} rpfq_quant_desc;
+
+/* Bytes of the device workspace rpfq_quantize_wide needs (fixed, 64 KiB). */
+size_t rpfq_quantize_workspace_bytes(const rpfq_quant_desc* desc);
+
+/*
+ * Quantize one float32 master weight the way the reference's training
+ * forward does, on the GPU:
+ *   RPFQ-ViT-main/quant_models/quant_i.py:513-544 (2x2 split into U, W;
+ *   recombination into A_q) with ComplexWeightQuantizer.forward (:418-435,
+ *   optional rotation) over _residual_quantize (:94-118) of
+ *   _quantize_phase_axis (:65-81) or _quantize_sign_phase (:84-91).
+ * weight: float32 [2N', 2K'] row-major.
+ * rot:    NULL (no rotation) or float32 [4] = cos theta_u, sin theta_u,
+ *         cos theta_w, sin theta_w (device memory).
+ * a_q:    NULL or float32 [2N', 2K'] output: the quantized weight.
+ * scales: float32 [2][4][2] output: (U, W) x stage x (re, im) multipliers;
+ *         slots past a plane's stages are 0.
+ * codes:  NULL or uint8 [steps_u + steps_w][N'][K'/4] output: each stage's
+ *         2-bit codes in the exporter's packing (export…py:148-159; AXIS:
+ *         real_pos 1, imag_neg 2, imag_pos 3, else 0; SIGN: bit0 re >= 0,
+ *         bit1 im >= 0), ordered u_s0.., w_s0..; needs K' % 4 == 0.
+ *         With scale_re/scale_im of these planes taken from `scales`, they
+ *         are the input of rpfq_wide_pack (the rotation goes in the desc).
+ * work:   device buffer of rpfq_quantize_workspace_bytes(desc) bytes.
+ * Each scale is the reference's masked mean with the sum accumulated in
+ * float64 and rounded once to float32 (torch sums float32 in its own order:
+ * the two agree to about 1 ulp); codes and A_q follow from the scales
+ * bit-exactly.  Deterministic.  Asynchronous on `stream`; the buffers must
+ * not overlap.
+ */
+int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
+                       float* scales, uint8_t* codes, void* work, size_t work_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,11 @@ Parity status per function (how each one is pinned; see tests/test_oracle.py):
                                recompose_fp16 by its error bound against the
                                reference A_q and by sign/permutation identities.
 * ``linear_forward``        -- golden outputs of the reference layer.
+* ``quantize_sign_phase``, ``rotate_for_quant``, ``quantized_weight`` --
+                               golden A_q of the reference layer for every
+                               axis / sign method with rotation on and off
+                               (to the scale-sum ulp tolerance above), and
+                               closed-form sign cases.
 * ``psk16_*``               -- PARITY UNPINNED by the reference (the 16-PSK
                                codebook does not exist there); pinned only by
                                its closed form (unit modulus, 16 distinct
@@ -151,16 +156,37 @@ def quantize_phase_axis(w_re, w_im, min_val: float = 1e-5):
     return codes, s_re, s_im, q_re, q_im
 
 
-def residual_quantize(w_re, w_im, steps: int):
-    """Training-semantics residual stages (quant_i.py:94-118): returns the
-    summed quantized planes and the per-stage (codes, s_re, s_im)."""
+def quantize_sign_phase(w_re, w_im):
+    """Quadrant-sign stage (quant_i.py:84-91) -> (codes, s_re, s_im, q_re,
+    q_im): scale = mean |.| over the whole plane (float64 sum rounded to
+    float32, then torch's CPU mean: float32 sum / numel), clamped at 1e-6;
+    code bit0 = re >= 0, bit1 = im >= 0."""
+    w_re = np.asarray(w_re, dtype=F32)
+    w_im = np.asarray(w_im, dtype=F32)
+    n = F32(w_re.size)
+    s_re = max(F32(F32(np.sum(np.abs(w_re.astype(np.float64)))) / n), F32(1e-6))
+    s_im = max(F32(F32(np.sum(np.abs(w_im.astype(np.float64)))) / n), F32(1e-6))
+    pr, pi = w_re >= 0, w_im >= 0
+    q_re = np.where(pr, s_re, -s_re).astype(F32)
+    q_im = np.where(pi, s_im, -s_im).astype(F32)
+    codes = pr.astype(np.uint8) | (pi.astype(np.uint8) << 1)
+    return codes, F32(s_re), F32(s_im), q_re, q_im
+
+
+def residual_quantize(w_re, w_im, steps: int, kind: str = "axis"):
+    """Training-semantics residual stages (quant_i.py:94-118) of the axis
+    (:65-81) or quadrant-sign (:84-91) quantizer: returns the summed
+    quantized planes and the per-stage (codes, s_re, s_im)."""
     q_re = np.zeros_like(w_re, dtype=F32)
     q_im = np.zeros_like(w_im, dtype=F32)
     r_re = np.asarray(w_re, dtype=F32)
     r_im = np.asarray(w_im, dtype=F32)
     stages = []
     for _ in range(steps):
-        codes, s_re, s_im, st_re, st_im = quantize_phase_axis(r_re, r_im, 1e-5)
+        if kind == "sign":
+            codes, s_re, s_im, st_re, st_im = quantize_sign_phase(r_re, r_im)
+        else:
+            codes, s_re, s_im, st_re, st_im = quantize_phase_axis(r_re, r_im, 1e-5)
         q_re = q_re + st_re
         q_im = q_im + st_im
         r_re = r_re - st_re
@@ -438,6 +464,32 @@ def wide_linear(x, planes, bias=None, codebook: str = "axis", rotation=None, fp1
     if bias is not None:
         y = y + np.asarray(bias, np.float64)
     return y
+
+
+def rotate_for_quant(re, im, c, s):
+    """w * exp(-i theta) with float32 products rounded separately
+    (quant_i.py:429-430)."""
+    c, s = F32(c), F32(s)
+    return (re * c + im * s).astype(F32), (im * c - re * s).astype(F32)
+
+
+def quantized_weight(weight, kind_u: str, steps_u: int, kind_w: str, steps_w: int, rotation=None):
+    """A_q of QATLinearComplexPhase.forward (quant_i.py:513-544) for the
+    axis / quadrant-sign residual methods, with the optional global rotation
+    of ComplexWeightQuantizer.forward (:418-435).  rotation: None or
+    ((cos_u, sin_u), (cos_w, sin_w)) float32.  Returns (a_q, stages_u,
+    stages_w), stages as residual_quantize returns them."""
+    u_re, u_im, w_re, w_im = decompose(weight)
+    planes = []
+    for i, (re, im, kind, steps) in enumerate(((u_re, u_im, kind_u, steps_u), (w_re, w_im, kind_w, steps_w))):
+        if rotation is not None:
+            re, im = rotate_for_quant(re, im, *rotation[i])
+        q_re, q_im, st = residual_quantize(re, im, steps, kind)
+        if rotation is not None:
+            q_re, q_im = derotate(q_re, q_im, *rotation[i])
+        planes.append((q_re, q_im, st))
+    a_q = recompose(planes[0][0], planes[0][1], planes[1][0], planes[1][1])
+    return a_q, planes[0][2], planes[1][2]
 
 
 def linear_forward(x, weight, bias, steps_u: int, steps_w: int, act_bits: int | None):

@@ -232,4 +232,37 @@ int rpfq_wide_decode(const rpfq_wide_desc* desc, const void* packed, size_t pack
                       "rpfq_wide_decode");
 }
 
+size_t rpfq_quantize_workspace_bytes(const rpfq_quant_desc* desc) {
+    (void)desc;
+    return (size_t)rpfq::kQuantMaxBlocks * 8 * sizeof(double);
+}
+
+int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
+                       float* scales, uint8_t* codes, void* work, size_t work_bytes, void* stream) {
+    if (!desc) return fail(RPFQ_ERR_NULL, "desc is NULL");
+    if (desc->n_complex <= 0 || desc->k_complex <= 0)
+        return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld must be positive",
+                    (long long)desc->n_complex, (long long)desc->k_complex);
+    if (desc->n_complex > (1LL << 30) || desc->k_complex > (1LL << 24) ||
+        desc->n_complex * desc->k_complex > (1LL << 40))
+        return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld too large",
+                    (long long)desc->n_complex, (long long)desc->k_complex);
+    for (int p = 0; p < 2; ++p) {
+        if (desc->kind[p] != RPFQ_QK_AXIS && desc->kind[p] != RPFQ_QK_SIGN)
+            return fail(RPFQ_ERR_VALUE, "unknown quantizer kind %d", desc->kind[p]);
+        if (desc->steps[p] < 1 || desc->steps[p] > 4)
+            return fail(RPFQ_ERR_VALUE, "steps=%d unsupported (1..4)", desc->steps[p]);
+    }
+    if (!weight || !scales || !work) return fail(RPFQ_ERR_NULL, "weight/scales/work must not be NULL");
+    if (codes && desc->k_complex % 4 != 0)
+        return fail(RPFQ_ERR_ALIGN, "code planes need k_complex %% 4 == 0, got %lld", (long long)desc->k_complex);
+    if (work_bytes < rpfq_quantize_workspace_bytes(desc))
+        return fail(RPFQ_ERR_SHAPE, "workspace holds %zu bytes, need %zu", work_bytes,
+                    rpfq_quantize_workspace_bytes(desc));
+    if (!aligned(work, 8)) return fail(RPFQ_ERR_ALIGN, "workspace must be 8-byte aligned");
+    return hip_status(rpfq::launch_quantize_wide(*desc, weight, rot, a_q, scales, codes, work,
+                                                 reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_quantize_wide");
+}
+
 }  // extern "C"

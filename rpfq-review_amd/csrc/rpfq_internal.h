@@ -75,6 +75,11 @@ hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const
                              const float* beta, float eps, int bits, void* y, int ydt, hipStream_t s);
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt,
                             hipStream_t s);
+// weight quantizer (rpfq_quant.hip): reduction blocks per stage, and so the
+// workspace of rpfq_quantize_wide (kQuantMaxBlocks x 8 float64 partials)
+constexpr int kQuantMaxBlocks = 1024;
+hipError_t launch_quantize_wide(const rpfq_quant_desc& d, const float* weight, const float* rot, float* aq,
+                                float* scales, uint8_t* codes, void* work, hipStream_t s);
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               float* a, int round_fp16, hipStream_t s);
 

@@ -1,0 +1,311 @@
+// Training-semantics weight quantization of one QATLinearComplexPhase weight
+// on the GPU (RPFQ-ViT-main/quant_models/quant_i.py:513-544 with the
+// quantizers of :29-118 and the rotation of :425-435).
+//
+// Per element (n, k) of the complex planes the kernels recompute, in float32
+// and in the reference's op order:
+//   U = 0.5 (A11 + A22) + i 0.5 (A21 - A12),  W = 0.5 (A11 - A22) + i 0.5 (A12 + A21)
+//   optional w e^{-i theta}:  (re c + im s, im c - re s)
+//   residual stages q += step, r -= step (step from the stage's scale)
+//   optional q e^{+i theta}:  (re c - im s, im c + re s)
+//   A_q = [[Wre + Ure, Wim - Uim], [Wim + Uim, -Wre + Ure]]
+// A stage's scale is a mean over the whole plane, so each stage is one
+// reduction launch (per-block float64 partials of the masked |r| sums and
+// counts), one single-block finalize launch (fixed-order float64 sum,
+// rounded once to float32, then the reference's float32 division and clamp),
+// and the last launch writes A_q and the 2-bit code planes.  Nothing is
+// stored between launches except the partials and the scales: every launch
+// recomputes the earlier stages from the weight (a few VALU per stage), so
+// the weight is read once per launch and never written back.
+//
+// The float64 sums make each scale the float32 rounding of the exact sum
+// (the reference sums float32 in torch's order; both agree to ~1 ulp and the
+// CPU restatement uses the same float64 convention).  Results are
+// deterministic: the partition into blocks and the reduction order are fixed.
+#include "rpfq_internal.h"
+
+namespace rpfq {
+namespace {
+
+constexpr int kQThreads = 256;
+constexpr float kAxisFloor = 1e-5f;  // _safe_mean_abs min_val, quant_i.py:29
+constexpr float kSignFloor = 1e-6f;  // EPS, quant_i.py:26, :86-87
+
+struct QuantArgs {
+    const float* w;    // [2N, 2K] row-major
+    const float* rot;  // NULL or [cos_u, sin_u, cos_w, sin_w]
+    int64_t N, K;
+    int kind[2], steps[2];
+    float* scales;     // [2][4][2]: plane (U, W), stage, (re, im)
+    double* partial;   // [blocks][8]
+    float* aq;         // NULL or [2N, 2K]
+    uint8_t* codes;    // NULL or [steps_u + steps_w][N][K/4]
+    int stage;         // stage being reduced / finalized
+    int nblocks;       // reduction blocks
+};
+
+// Axis class of (re, im) as the exporter codes it (quant_i.py:36-62,
+// export_rpfq_vit_to_mlx.py:214-218): 1 real_pos, 0 real_neg, 3 imag_pos,
+// 2 imag_neg; 4 = no mask set (only for NaN input), stored as code 0.
+__device__ __forceinline__ int axis_class(float re, float im) {
+    float ar = fabsf(re), ai = fabsf(im);
+    if (ar > ai) return re >= 0.0f ? 1 : 0;
+    if (ai > ar) return im >= 0.0f ? 3 : 2;
+    if (re == 0.0f && im == 0.0f) return 1;  // zero tie -> real_pos
+    if (re > 0.0f && im > 0.0f) return 3;    // quadrant I tie -> imag_pos
+    if (re < 0.0f && im > 0.0f) return 0;    // quadrant II tie -> real_neg
+    if (re < 0.0f && im < 0.0f) return 2;    // quadrant III tie -> imag_neg
+    if (re > 0.0f && im < 0.0f) return 1;    // quadrant IV tie -> real_pos
+    return 4;
+}
+
+// One plane's running state: residual r and accumulated q.
+struct Plane {
+    float r_re, r_im, q_re, q_im;
+};
+
+// Applies stage t with scales (s_re, s_im); returns the code.
+template <int KIND>
+__device__ __forceinline__ uint32_t apply_stage(Plane& p, float s_re, float s_im) {
+    float v_re, v_im;
+    uint32_t code;
+    if (KIND == RPFQ_QK_SIGN) {  // quant_i.py:84-91
+        bool pr = p.r_re >= 0.0f, pi = p.r_im >= 0.0f;
+        v_re = pr ? s_re : -s_re;
+        v_im = pi ? s_im : -s_im;
+        code = (pr ? 1u : 0u) | (pi ? 2u : 0u);
+    } else {  // quant_i.py:65-81
+        int c = axis_class(p.r_re, p.r_im);
+        v_re = c == 1 ? s_re : (c == 0 ? -s_re : 0.0f);
+        v_im = c == 3 ? s_im : (c == 2 ? -s_im : 0.0f);
+        code = c == 4 ? 0u : (uint32_t)c;
+    }
+    p.q_re = p.q_re + v_re;  // quant_i.py:114-117
+    p.q_im = p.q_im + v_im;
+    p.r_re = p.r_re - v_re;
+    p.r_im = p.r_im - v_im;
+    return code;
+}
+
+__device__ __forceinline__ uint32_t apply_stage_k(int kind, Plane& p, float s_re, float s_im) {
+    return kind == RPFQ_QK_SIGN ? apply_stage<RPFQ_QK_SIGN>(p, s_re, s_im) : apply_stage<RPFQ_QK_AXIS>(p, s_re, s_im);
+}
+
+// U and W of element (n, k), rotated for quantization when rot is set
+// (quant_i.py:519-527, :429-430).
+__device__ __forceinline__ void load_planes(const QuantArgs& a, int64_t n, int64_t k, Plane& u, Plane& w) {
+    const int64_t row = 2 * a.K;
+    float a11 = a.w[n * row + k], a12 = a.w[n * row + a.K + k];
+    float a21 = a.w[(a.N + n) * row + k], a22 = a.w[(a.N + n) * row + a.K + k];
+    u.r_re = 0.5f * (a11 + a22);
+    u.r_im = 0.5f * (a21 - a12);
+    w.r_re = 0.5f * (a11 - a22);
+    w.r_im = 0.5f * (a12 + a21);
+    if (a.rot) {
+        float cu = a.rot[0], su = a.rot[1], cw = a.rot[2], sw = a.rot[3];
+        float ur = u.r_re * cu + u.r_im * su, ui = u.r_im * cu - u.r_re * su;
+        float wr = w.r_re * cw + w.r_im * sw, wi = w.r_im * cw - w.r_re * sw;
+        u.r_re = ur; u.r_im = ui;
+        w.r_re = wr; w.r_im = wi;
+    }
+    u.q_re = u.q_im = w.q_re = w.q_im = 0.0f;
+}
+
+// Masked |r| sums and counts of stage a.stage for U (0..3) and W (4..7):
+// (sum |re| over the real mask, count, sum |im| over the imaginary mask,
+// count); SIGN planes count every element.
+__global__ void __launch_bounds__(kQThreads) quant_reduce_kernel(QuantArgs a) {
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int64_t total = a.N * a.K;
+    const int st = a.stage;
+    for (int64_t e = (int64_t)blockIdx.x * kQThreads + threadIdx.x; e < total;
+         e += (int64_t)a.nblocks * kQThreads) {
+        int64_t n = e / a.K, k = e - n * a.K;
+        Plane pl[2];
+        load_planes(a, n, k, pl[0], pl[1]);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            if (a.steps[p] <= st) continue;
+#pragma unroll
+            for (int t = 0; t < 3; ++t)
+                if (t < st)
+                    apply_stage_k(a.kind[p], pl[p], a.scales[(p * 4 + t) * 2], a.scales[(p * 4 + t) * 2 + 1]);
+            if (a.kind[p] == RPFQ_QK_SIGN) {
+                acc[4 * p + 0] += (double)fabsf(pl[p].r_re);
+                acc[4 * p + 1] += 1.0;
+                acc[4 * p + 2] += (double)fabsf(pl[p].r_im);
+                acc[4 * p + 3] += 1.0;
+            } else {
+                int c = axis_class(pl[p].r_re, pl[p].r_im);
+                if (c == 0 || c == 1) {
+                    acc[4 * p + 0] += (double)fabsf(pl[p].r_re);
+                    acc[4 * p + 1] += 1.0;
+                } else if (c == 2 || c == 3) {
+                    acc[4 * p + 2] += (double)fabsf(pl[p].r_im);
+                    acc[4 * p + 3] += 1.0;
+                }
+            }
+        }
+    }
+    // fixed-order block reduction: wave butterfly, then the 4 waves in order
+    __shared__ double red[kQThreads / 64][8];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        double v = acc[j];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0) red[wv][j] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        double v = 0.0;
+        for (int i = 0; i < kQThreads / 64; ++i) v += red[i][threadIdx.x];
+        a.partial[(int64_t)blockIdx.x * 8 + threadIdx.x] = v;
+    }
+}
+
+// Sums the partials in a fixed order and writes stage a.stage's scales:
+// axis: max((float)sum / max((float)count, 1), 1e-5) (quant_i.py:29-33);
+// sign: max((float)sum / (float)(N K), 1e-6) (quant_i.py:86-87, torch's CPU
+// mean = sum / numel).  Stage 0 also clears every scale slot.
+__global__ void __launch_bounds__(kQThreads) quant_finalize_kernel(QuantArgs a) {
+    __shared__ double red[kQThreads / 64][8];
+    double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int b = threadIdx.x; b < a.nblocks; b += kQThreads)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += a.partial[(int64_t)b * 8 + j];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        double v = acc[j];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0) red[wv][j] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    double tot[8];
+    for (int j = 0; j < 8; ++j) {
+        double v = 0.0;
+        for (int i = 0; i < kQThreads / 64; ++i) v += red[i][j];
+        tot[j] = v;
+    }
+    if (a.stage == 0)
+        for (int i = 0; i < 16; ++i) a.scales[i] = 0.0f;
+    for (int p = 0; p < 2; ++p) {
+        if (a.steps[p] <= a.stage) continue;
+        float sc[2];
+        for (int h = 0; h < 2; ++h) {
+            float num = (float)tot[4 * p + 2 * h];
+            float m, floor_v;
+            if (a.kind[p] == RPFQ_QK_SIGN) {
+                m = num / (float)(a.N * a.K);
+                floor_v = kSignFloor;
+            } else {
+                float den = (float)tot[4 * p + 2 * h + 1];
+                m = num / (den < 1.0f ? 1.0f : den);
+                floor_v = kAxisFloor;
+            }
+            sc[h] = m < floor_v ? floor_v : m;  // clamp_min (NaN passes through)
+        }
+        a.scales[(p * 4 + a.stage) * 2] = sc[0];
+        a.scales[(p * 4 + a.stage) * 2 + 1] = sc[1];
+    }
+}
+
+// All stages with the final scales: A_q (rotated back, recombined) and the
+// code planes.  V consecutive columns per thread (V = 4 writes one packed
+// code byte per plane and stage).
+template <int V>
+__global__ void __launch_bounds__(kQThreads) quant_apply_kernel(QuantArgs a) {
+    const int64_t kv = a.K / V;
+    const int64_t total = a.N * kv;
+    const int64_t row = 2 * a.K;
+    const int64_t plane_bytes = a.N * (a.K / 4);
+    for (int64_t e = (int64_t)blockIdx.x * kQThreads + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * kQThreads) {
+        int64_t n = e / kv, k0 = (e - n * kv) * V;
+        uint32_t cbyte[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int64_t k = k0 + v;
+            Plane pl[2];
+            load_planes(a, n, k, pl[0], pl[1]);
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (t < a.steps[p]) {
+                        uint32_t c = apply_stage_k(a.kind[p], pl[p], a.scales[(p * 4 + t) * 2],
+                                                   a.scales[(p * 4 + t) * 2 + 1]);
+                        cbyte[p * 4 + t] |= c << (2 * v);
+                    }
+            float ur = pl[0].q_re, ui = pl[0].q_im, wr = pl[1].q_re, wi = pl[1].q_im;
+            if (a.rot) {  // quant_i.py:433-434
+                float cu = a.rot[0], su = a.rot[1], cw = a.rot[2], sw = a.rot[3];
+                float r0 = ur * cu - ui * su, i0 = ui * cu + ur * su;
+                float r1 = wr * cw - wi * sw, i1 = wi * cw + wr * sw;
+                ur = r0; ui = i0; wr = r1; wi = i1;
+            }
+            if (a.aq) {  // quant_i.py:534-544
+                a.aq[n * row + k] = wr + ur;
+                a.aq[n * row + a.K + k] = wi - ui;
+                a.aq[(a.N + n) * row + k] = wi + ui;
+                a.aq[(a.N + n) * row + a.K + k] = -wr + ur;
+            }
+        }
+        if (V == 4 && a.codes) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (t < a.steps[p]) {
+                        const int plane = p * a.steps[0] + t;
+                        a.codes[plane * plane_bytes + n * (a.K / 4) + k0 / 4] = (uint8_t)cbyte[p * 4 + t];
+                    }
+        }
+    }
+}
+
+int reduce_blocks(int64_t total) {
+    int64_t b = (total + kQThreads - 1) / kQThreads;
+    return (int)(b < kQuantMaxBlocks ? (b < 1 ? 1 : b) : kQuantMaxBlocks);
+}
+
+}  // namespace
+
+hipError_t launch_quantize_wide(const rpfq_quant_desc& d, const float* weight, const float* rot, float* aq,
+                                float* scales, uint8_t* codes, void* work, hipStream_t s) {
+    QuantArgs a;
+    a.w = weight;
+    a.rot = rot;
+    a.N = d.n_complex;
+    a.K = d.k_complex;
+    for (int p = 0; p < 2; ++p) {
+        a.kind[p] = d.kind[p];
+        a.steps[p] = d.steps[p];
+    }
+    a.scales = scales;
+    a.partial = static_cast<double*>(work);
+    a.aq = aq;
+    a.codes = codes;
+    a.nblocks = reduce_blocks(a.N * a.K);
+    const int max_steps = d.steps[0] > d.steps[1] ? d.steps[0] : d.steps[1];
+    for (int st = 0; st < max_steps; ++st) {
+        a.stage = st;
+        hipLaunchKernelGGL(quant_reduce_kernel, dim3(a.nblocks), dim3(kQThreads), 0, s, a);
+        hipLaunchKernelGGL(quant_finalize_kernel, dim3(1), dim3(kQThreads), 0, s, a);
+    }
+    if (aq || codes) {
+        const bool v4 = a.K % 4 == 0;
+        const int64_t items = a.N * (v4 ? a.K / 4 : a.K);
+        int64_t blocks = (items + kQThreads - 1) / kQThreads;
+        if (blocks > 8 * kQuantMaxBlocks) blocks = 8 * kQuantMaxBlocks;
+        if (v4)
+            hipLaunchKernelGGL(quant_apply_kernel<4>, dim3((unsigned)blocks), dim3(kQThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL(quant_apply_kernel<1>, dim3((unsigned)blocks), dim3(kQThreads), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rpfq

@@ -26,6 +26,7 @@ ERRORS = {
 }
 F32, F16, BF16 = 0, 1, 2
 CB_AXIS, CB_SIGN, CB_PSK16 = 0, 1, 2
+QK_AXIS, QK_SIGN = 0, 1  # weight quantizer kinds of rpfq_quantize_wide
 FLAG_TILE_M128 = 1  # force the register-staged 128-row kernel
 FLAG_NO_STREAM = 2  # keep M <= 16 on the tiled kernels (no weight-streaming kernel)
 
@@ -45,6 +46,8 @@ EXPORTED = (
     "rpfq_wide_linear_residual",
     "rpfq_layer_norm",
     "rpfq_layer_norm_act_quant",
+    "rpfq_quantize_workspace_bytes",
+    "rpfq_quantize_wide",
 )
 
 
@@ -60,6 +63,17 @@ class WideDesc(ctypes.Structure):
         ("rotate", ctypes.c_int32),
         ("rot_u", ctypes.c_float * 2),
         ("rot_w", ctypes.c_float * 2),
+    ]
+
+
+class QuantDesc(ctypes.Structure):
+    """Mirror of struct rpfq_quant_desc."""
+
+    _fields_ = [
+        ("n_complex", ctypes.c_int64),
+        ("k_complex", ctypes.c_int64),
+        ("kind", ctypes.c_int32 * 2),
+        ("steps", ctypes.c_int32 * 2),
     ]
 
 
@@ -108,8 +122,12 @@ def load() -> ctypes.CDLL:
         lib.rpfq_wide_linear_residual.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, i32, i32, vp]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
+        qp = ctypes.POINTER(QuantDesc)
+        lib.rpfq_quantize_workspace_bytes.argtypes = [qp]
+        lib.rpfq_quantize_workspace_bytes.restype = sz
+        lib.rpfq_quantize_wide.argtypes = [qp, vp, vp, vp, vp, vp, vp, sz, vp]
         for name in EXPORTED[2:]:
-            if name != "rpfq_wide_packed_bytes":
+            if name not in ("rpfq_wide_packed_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32
         _lib = lib
         return lib

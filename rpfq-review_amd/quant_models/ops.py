@@ -257,6 +257,129 @@ class PackedWide:
         bits = 8 if self.codebook == N.CB_PSK16 else 4 * self.stages
         return self.n_complex * self.k_complex * bits // 8
 
+    @property
+    def device(self) -> torch.device:
+        return self.blob.device
+
+
+@dataclass
+class PackedStages:
+    """A layer whose U and W carry more than two residual stages
+    (complex_phase_v3 / v4, quant_i.py:145-166), run as stage groups of at
+    most two stages each: group 0 holds stages (0, 1) of U and W, group 1
+    stages (2[, 3]).  The layer is linear in its stages, so
+
+        y = G1 x + (G0 x + bias)
+
+    with the inner sum added in group 1's store (rpfq_wide_linear_residual).
+    Each group's fused fp16 coefficients satisfy the single-group bound
+    against that group's float32 stage sum, and the intermediate G0 x + bias
+    is rounded once to y's dtype."""
+
+    groups: list
+
+    @property
+    def n_complex(self) -> int:
+        return self.groups[0].n_complex
+
+    @property
+    def k_complex(self) -> int:
+        return self.groups[0].k_complex
+
+    @property
+    def in_features(self) -> int:
+        return self.groups[0].in_features
+
+    @property
+    def out_features(self) -> int:
+        return self.groups[0].out_features
+
+    @property
+    def stages(self) -> int:
+        return sum(g.stages for g in self.groups)
+
+    @property
+    def device(self) -> torch.device:
+        return self.groups[0].device
+
+    @property
+    def code_bytes(self) -> int:
+        return sum(g.code_bytes for g in self.groups)
+
+    def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype | None = None, flags: int = 0,
+               residual: torch.Tensor | None = None) -> torch.Tensor:
+        """PackedWide.linear over all stage groups (one launch per group)."""
+        y = self.groups[0].linear(x, bias, out_dtype, flags, residual)
+        for g in self.groups[1:]:
+            y = g.linear(x, None, y.dtype, flags, residual=y)
+        return y
+
+    def decode(self, round_fp16: bool = False) -> torch.Tensor:
+        """Sum of the groups' fused weights (float32)."""
+        a = self.groups[0].decode(round_fp16)
+        for g in self.groups[1:]:
+            a += g.decode(round_fp16)
+        return a
+
+
+def pack_layer(planes, scale_re, scale_im, n_complex: int, k_complex: int, codebook: int = N.CB_AXIS,
+               stages: int = 2, block: int = 0, rotation=None):
+    """PackedWide for stages <= 2, else PackedStages over groups of two
+    stages.  planes / scales ordered u_s0..u_s{S-1}, w_s0..w_s{S-1} (AXIS,
+    SIGN) as PackedWide.from_planes takes them."""
+    if stages <= 2 or codebook == N.CB_PSK16:
+        return PackedWide.from_planes(planes, scale_re, scale_im, n_complex, k_complex, codebook, stages, block,
+                                      rotation)
+    if len(planes) != 2 * stages:
+        raise ValueError(f"expected {2 * stages} planes, got {len(planes)}")
+    groups = []
+    for lo in range(0, stages, 2):
+        hi = min(lo + 2, stages)
+        idx = list(range(lo, hi)) + list(range(stages + lo, stages + hi))
+        groups.append(PackedWide.from_planes([planes[i] for i in idx], [scale_re[i] for i in idx],
+                                             [scale_im[i] for i in idx], n_complex, k_complex, codebook,
+                                             hi - lo, block, rotation))
+    return PackedStages(groups)
+
+
+QUANT_KINDS = {"axis": N.QK_AXIS, "sign": N.QK_SIGN}
+
+
+def quantize_wide(weight: torch.Tensor, kind_u: str, steps_u: int, kind_w: str, steps_w: int,
+                  rot: torch.Tensor | None = None, want_aq: bool = True, want_codes: bool = False):
+    """Training-semantics quantization of a float32 [2N', 2K'] master weight
+    on the GPU (rpfq_quantize_wide; quant_i.py:513-544).
+
+    rot: None or a float32 device tensor [cos_u, sin_u, cos_w, sin_w].
+    Returns (a_q [2N', 2K'] float32 or None, scales [2, 4, 2] float32 (U/W,
+    stage, re/im), codes [steps_u + steps_w, N', K'/4] uint8 or None)."""
+    N.require_device(weight, rot)
+    if weight.dtype != torch.float32 or weight.dim() != 2:
+        raise TypeError("weight must be a 2-D float32 tensor")
+    out_f, in_f = weight.shape
+    if out_f % 2 or in_f % 2:
+        raise ValueError("Complex-phase QAT requires even in/out features.")
+    weight = weight.contiguous()
+    d = N.QuantDesc()
+    d.n_complex, d.k_complex = out_f // 2, in_f // 2
+    d.kind[0], d.kind[1] = QUANT_KINDS[kind_u], QUANT_KINDS[kind_w]
+    d.steps[0], d.steps[1] = int(steps_u), int(steps_w)
+    if rot is not None:
+        rot = rot.detach().reshape(4).float().contiguous()
+    dev = weight.device
+    lib = N.load()
+    work = torch.empty(lib.rpfq_quantize_workspace_bytes(ctypes.byref(d)), dtype=torch.uint8, device=dev)
+    scales = torch.empty(2, 4, 2, dtype=torch.float32, device=dev)
+    a_q = torch.empty_like(weight) if want_aq else None
+    codes = None
+    if want_codes:
+        codes = torch.empty(steps_u + steps_w, d.n_complex, d.k_complex // 4, dtype=torch.uint8, device=dev)
+    N.check("rpfq_quantize_wide", lib.rpfq_quantize_wide(
+        ctypes.byref(d), weight.data_ptr(), N.ptr(rot), N.ptr(a_q), scales.data_ptr(), N.ptr(codes),
+        work.data_ptr(), work.numel(), N.stream_of(weight)))
+    return a_q, scales, codes
+
 
 def make_desc(n_complex, k_complex, codebook, stages, block, rotation) -> N.WideDesc:
     d = N.WideDesc()

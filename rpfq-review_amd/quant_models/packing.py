@@ -178,6 +178,8 @@ def rotate_back(re, im, cos_t, sin_t):
 STAGES_OF = {
     "complex_phase_v1": ("axis", 1),
     "complex_phase_v2": ("axis", 2),
+    "complex_phase_v3": ("axis", 3),
+    "complex_phase_v4": ("axis", 4),
     "complex_phase_new_v2": ("sign", 2),
 }
 
@@ -227,6 +229,45 @@ def quantize_layer(weight: torch.Tensor, method_u: str, method_w: str, rot_u=Non
     rotation = None
     if rot_u is not None:
         rotation = ((float(rot_u[0]), float(rot_u[1])), (float(rot_w[0]), float(rot_w[1])))
+    cb = N.CB_AXIS if kind_u == "axis" else N.CB_SIGN
+    return LayerCodes(planes, sre, sim, n_c, k_c, cb, steps_u, 0, rotation)
+
+
+def quantize_layer_device(weight: torch.Tensor, method_u: str, method_w: str, rot_u=None, rot_w=None) -> LayerCodes:
+    """quantize_layer on the GPU (rpfq_quantize_wide): the weight stays on
+    its device and the planes and scales come back as device tensors.
+
+    Codes follow from the scales bit-exactly; each scale is the float32
+    rounding of the exact masked sum (float64 accumulation) where the host
+    path reproduces torch's float32 CPU summation order, so the two agree to
+    about 1 ulp per scale."""
+    from . import ops
+
+    if method_u not in STAGES_OF or method_w not in STAGES_OF:
+        raise NotImplementedError(
+            f"packed HIP path supports {sorted(STAGES_OF)}; got U={method_u}, W={method_w}")
+    kind_u, steps_u = STAGES_OF[method_u]
+    kind_w, steps_w = STAGES_OF[method_w]
+    if kind_u != kind_w or steps_u != steps_w:
+        raise NotImplementedError("packed HIP path needs the same method for U and W")
+    if (rot_u is None) != (rot_w is None):
+        raise ValueError("rotation must be set for both U and W or neither")
+    dev = weight.device
+    rot = None
+    rotation = None
+    if rot_u is not None:
+        vals = [float(rot_u[0]), float(rot_u[1]), float(rot_w[0]), float(rot_w[1])]
+        rot = torch.tensor(vals, dtype=torch.float32, device=dev)
+        rotation = ((vals[0], vals[1]), (vals[2], vals[3]))
+    _, scales, codes = ops.quantize_wide(weight.detach().float(), kind_u, steps_u, kind_w, steps_w, rot=rot,
+                                         want_aq=False, want_codes=True)
+    n_c, k_c = weight.shape[0] // 2, weight.shape[1] // 2
+    planes, sre, sim = [], [], []
+    for p, steps in ((0, steps_u), (1, steps_w)):
+        for t in range(steps):
+            planes.append(codes[p * steps_u + t])
+            sre.append(scales[p, t, 0].reshape(1, 1).expand(n_c, 1).contiguous())
+            sim.append(scales[p, t, 1].reshape(1, 1).expand(n_c, 1).contiguous())
     cb = N.CB_AXIS if kind_u == "axis" else N.CB_SIGN
     return LayerCodes(planes, sre, sim, n_c, k_c, cb, steps_u, 0, rotation)
 

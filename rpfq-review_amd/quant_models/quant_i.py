@@ -16,12 +16,17 @@ Execution:
   (codes + scales, re-packed when the weight changes) and every call runs the
   gfx950 kernels of librpfq.so through the C ABI.  There is no host fallback:
   if the library is missing the call raises.
-* training mode (any device) or host tensors -> quantization-aware forward in
-  torch with straight-through gradients, the reference's training semantics.
+* training mode on device tensors -> the quantization-aware forward with the
+  weight quantized by the rpfq_quantize_wide kernels and activations by the
+  act-quant kernel, straight-through gradients, F.linear on the float32 A_q
+  (RPFQ_HIP_QAT=0 selects the torch formulation below);
+* host tensors (or complex_phase_next_v1) -> the same forward in torch ops,
+  the reference's training semantics.
 """
 from __future__ import annotations
 
 import math
+import os
 from typing import Dict, Tuple
 
 import torch
@@ -244,6 +249,91 @@ class ComplexActivationQuantizer(nn.Module):
         return ActivationQuantSTE.apply(x_real, x_imag, self.num_bits)
 
 
+# ---------------------------------------------------------------------------
+# HIP training path: the same quantizers as device kernels, straight-through
+# gradients (quant_i.py:128-130, :452-455)
+# ---------------------------------------------------------------------------
+HIP_QAT = os.environ.get("RPFQ_HIP_QAT", "1") != "0"
+# eval packing on the GPU quantizer instead of the host (float64-sum scales,
+# ~1 ulp from the host's torch CPU order; no host round trip of the weight)
+DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
+
+_HIP_KINDS = {
+    "complex_phase_v1": ("axis", 1),
+    "complex_phase_v2": ("axis", 2),
+    "complex_phase_v3": ("axis", 3),
+    "complex_phase_v4": ("axis", 4),
+    "complex_phase_new_v2": ("sign", 2),
+}
+
+
+def rotation_grad(grad_aq: torch.Tensor, weight: torch.Tensor, a_q: torch.Tensor):
+    """d loss / d theta of the U and W rotations under the straight-through
+    quantizer.  With out = q e^{+i theta}, q = Q(w e^{-i theta}) and dQ = I,
+    d out / d theta = (w_im - out_im, out_re - w_re) per element, so
+    grad_theta = sum(g_re (w_im - out_im) + g_im (out_re - w_re)), with g the
+    gradient of the plane (G11 + G22, G21 - G12 for U; G11 - G22, G12 + G21
+    for W from the 2x2 blocks of grad_aq, quant_i.py:534-544) and out the
+    plane of A_q (recovered by the same split as the weight)."""
+    g11, g12, g21, g22 = _blocks(grad_aq)
+    gu = (g11 + g22, g21 - g12)
+    gw = (g11 - g22, g12 + g21)
+    u_re, u_im, w_re, w_im = P.split_blocks(weight)
+    ou_re, ou_im, ow_re, ow_im = P.split_blocks(a_q)
+    th_u = (gu[0] * (u_im - ou_im) + gu[1] * (ou_re - u_re)).sum()
+    th_w = (gw[0] * (w_im - ow_im) + gw[1] * (ow_re - w_re)).sum()
+    return th_u, th_w
+
+
+def _blocks(a: torch.Tensor):
+    no, ni = a.shape[0] // 2, a.shape[1] // 2
+    return a[:no, :ni], a[:no, ni:], a[no:, :ni], a[no:, ni:]
+
+
+class _HipWideQuantSTE(torch.autograd.Function):
+    """A_q from the float32 master weight by rpfq_quantize_wide; backward:
+    the weight gets the A_q gradient unchanged (split and recombination are
+    inverse linear maps and the quantizer is straight-through), the rotation
+    angles get rotation_grad."""
+
+    @staticmethod
+    def forward(ctx, weight, theta_u, theta_w, spec):
+        from . import ops
+
+        rot = None
+        if theta_u is not None:
+            tu, tw = theta_u.detach().float().reshape(1), theta_w.detach().float().reshape(1)
+            rot = torch.cat((torch.cos(tu), torch.sin(tu), torch.cos(tw), torch.sin(tw)))
+        a_q, _, _ = ops.quantize_wide(weight.detach(), *spec, rot=rot)
+        ctx.rotated = theta_u is not None
+        if ctx.rotated:
+            ctx.save_for_backward(weight, a_q)
+        return a_q
+
+    @staticmethod
+    def backward(ctx, grad):
+        if not ctx.rotated:
+            return grad, None, None, None
+        weight, a_q = ctx.saved_tensors
+        th_u, th_w = rotation_grad(grad.float(), weight.detach(), a_q)
+        return grad, th_u.reshape(1), th_w.reshape(1), None
+
+
+class _HipActQuantSTE(torch.autograd.Function):
+    """ActivationQuantSTE (quant_i.py:438-455) by the rpfq_act_quant kernel
+    for float32 activations (bit-exact); identity gradient."""
+
+    @staticmethod
+    def forward(ctx, x, num_bits):
+        from . import ops
+
+        return ops.act_quant(x, num_bits)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None
+
+
 class QATLinearComplexPhase(nn.Linear):
     """Complex-structured quantized linear layer (quant_i.py:475-554).
 
@@ -266,6 +356,7 @@ class QATLinearComplexPhase(nn.Linear):
         self.act_quantizer = ComplexActivationQuantizer(num_bits=act_num_bits) if enable_act_quant else None
         # packed HIP state (not part of the state dict)
         self.use_packed = True
+        self.pack_on_device = DEVICE_PACK
         self._packed = None
         self._packed_key = None
         self._override = None
@@ -278,7 +369,29 @@ class QATLinearComplexPhase(nn.Linear):
         wq_re, wq_im = self.quantizer_w(w_re, w_im)
         return P.join_blocks(uq_re, uq_im, wq_re, wq_im)
 
+    def _hip_qat_spec(self, x: torch.Tensor):
+        """(kind_u, steps_u, kind_w, steps_w) when the training forward runs
+        on the HIP quantizer, else None (host tensors, next_v1, disabled)."""
+        if not (HIP_QAT and self.use_packed and x.is_cuda and self.weight.dtype == torch.float32):
+            return None
+        ku = _HIP_KINDS.get(self.quantizer_u.quant_method)
+        kw = _HIP_KINDS.get(self.quantizer_w.quant_method)
+        if ku is None or kw is None:
+            return None
+        return ku + kw
+
     def _qat_forward(self, x: torch.Tensor) -> torch.Tensor:
+        spec = self._hip_qat_spec(x)
+        if spec is not None:
+            q_weight = _HipWideQuantSTE.apply(self.weight, self.quantizer_u.rotation_angle,
+                                              self.quantizer_w.rotation_angle, spec)
+            if self.act_quantizer is not None:
+                if x.dtype == torch.float32:
+                    x = _HipActQuantSTE.apply(x, self.act_quantizer.num_bits)
+                else:  # reduced-precision activations: the reference's per-op rounding
+                    h = self.in_features // 2
+                    x = torch.cat(self.act_quantizer(x[..., :h], x[..., h:]), dim=-1)
+            return F.linear(x, q_weight, self.bias)
         q_weight = self.quantized_weight()
         if self.act_quantizer is not None:
             h = self.in_features // 2
@@ -300,14 +413,17 @@ class QATLinearComplexPhase(nn.Linear):
     def packed(self, device: torch.device):
         """The layer's PackedWide on `device`, packing on first use and again
         whenever the float32 weight changed."""
-        from .ops import PackedWide
+        from .ops import pack_layer
 
         key = ("override", id(self._override)) if self._override is not None else \
             (self.weight.data_ptr(), self.weight._version, self._rotation_version())
-        if self._packed is not None and self._packed_key == key and self._packed.blob.device == device:
+        if self._packed is not None and self._packed_key == key and self._packed.device == device:
             return self._packed
         if self._override is not None:
             lc = self._override
+        elif self.pack_on_device and self.weight.is_cuda:
+            lc = P.quantize_layer_device(self.weight, self.quantizer_u.quant_method, self.quantizer_w.quant_method,
+                                         self.quantizer_u.rotation_cos_sin(), self.quantizer_w.rotation_cos_sin())
         else:
             # offline step, on the host in float32 like the reference's
             # exporter, so codes and scales are bit-identical to the
@@ -316,11 +432,9 @@ class QATLinearComplexPhase(nn.Linear):
             rot_w = self.quantizer_w.rotation_cos_sin()
             lc = P.quantize_layer(self.weight.detach().cpu(), self.quantizer_u.quant_method,
                                   self.quantizer_w.quant_method, rot_u, rot_w)
-        self._packed = PackedWide.from_planes([p.to(device) for p in lc.planes],
-                                              [s.to(device) for s in lc.scale_re],
-                                              [s.to(device) for s in lc.scale_im],
-                                              lc.n_complex, lc.k_complex, lc.codebook, lc.stages, lc.block,
-                                              lc.rotation)
+        self._packed = pack_layer([p.to(device) for p in lc.planes], [s.to(device) for s in lc.scale_re],
+                                  [s.to(device) for s in lc.scale_im], lc.n_complex, lc.k_complex, lc.codebook,
+                                  lc.stages, lc.block, lc.rotation)
         self._packed_key = key
         return self._packed
 

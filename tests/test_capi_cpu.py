@@ -135,3 +135,28 @@ def test_layer_norm_act_quant_argument_errors():
     assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, 1e-6, 17, p, 1, None) == 4
     assert L.rpfq_layer_norm_act_quant(p, 3, 4, 64, None, None, 1e-6, 4, p, 1, None) == 5
     assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, -1.0, 4, p, 1, None) == 6
+
+
+def test_quantize_wide_argument_errors():
+    L, N = lib()
+    p = ctypes.c_void_p(256)
+    d = N.QuantDesc()
+    d.n_complex, d.k_complex = 32, 48
+    d.kind[0], d.kind[1], d.steps[0], d.steps[1] = 0, 1, 2, 2
+    ws = L.rpfq_quantize_workspace_bytes(ctypes.byref(d))
+    assert ws == 1024 * 8 * 8
+    assert L.rpfq_quantize_wide(None, p, None, p, p, None, p, ws, None) == 1
+    assert L.rpfq_quantize_wide(ctypes.byref(d), None, None, p, p, None, p, ws, None) == 1   # weight
+    assert L.rpfq_quantize_wide(ctypes.byref(d), p, None, p, None, None, p, ws, None) == 1   # scales
+    assert L.rpfq_quantize_wide(ctypes.byref(d), p, None, p, p, None, p, ws - 8, None) == 2  # workspace
+    for field, idx, value in (("kind", 0, 2), ("kind", 1, -1), ("steps", 0, 0), ("steps", 1, 5)):
+        bad = N.QuantDesc()
+        ctypes.pointer(bad)[0] = d
+        getattr(bad, field)[idx] = value
+        assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, None, p, ws, None) == 6, (field, idx)
+    bad = N.QuantDesc()
+    ctypes.pointer(bad)[0] = d
+    bad.k_complex = 50
+    assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, p, p, ws, None) == 3  # codes need K' % 4
+    bad.k_complex = 0
+    assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, None, p, ws, None) == 2

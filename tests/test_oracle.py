@@ -203,6 +203,47 @@ def test_linear_forward_golden(golden, method, steps, act):
     assert np.allclose(y, golden[f"fwd_y_{tag}"], rtol=1e-5, atol=1e-5)
 
 
+def _rot_cos_sin():
+    """float32 (cos, sin) of the golden layers' rotation angles (0.3 for U,
+    -0.2 for W) evaluated by torch on the CPU, as the reference did."""
+    import torch
+
+    out = []
+    for t in (0.3, -0.2):
+        th = torch.full((1,), t, dtype=torch.float32)
+        out.append((np.float32(torch.cos(th).item()), np.float32(torch.sin(th).item())))
+    return tuple(out)
+
+
+@pytest.mark.parametrize("method,kind,steps", [("complex_phase_v1", "axis", 1), ("complex_phase_v2", "axis", 2),
+                                               ("complex_phase_v3", "axis", 3), ("complex_phase_v4", "axis", 4),
+                                               ("complex_phase_new_v2", "sign", 2)])
+@pytest.mark.parametrize("rot", [0, 1])
+def test_quantized_weight_golden(golden, method, kind, steps, rot):
+    a_q, st_u, st_w = O.quantized_weight(golden["w_weight"], kind, steps, kind, steps,
+                                         _rot_cos_sin() if rot else None)
+    assert len(st_u) == steps and len(st_w) == steps
+    ref = golden[f"fwd_aq_{method}_a0_r{rot}"]
+    # float64 scale sums vs torch's float32 order: <= 2 ulp per scale (ulp
+    # ~1.9e-9 here), summed over the stages of U and W
+    assert np.allclose(a_q, ref, rtol=0, atol=4 * steps * 2e-9)
+    # a wrong sign, axis or rotation direction moves entries by a whole scale
+    assert np.abs(a_q - ref).max() < 1e-6
+
+
+def test_quantize_sign_phase_closed_form():
+    re = np.array([[0.5, -0.25], [-0.0, 0.0]], np.float32)
+    im = np.array([[-1.0, 0.75], [0.0, -0.5]], np.float32)
+    codes, s_re, s_im, q_re, q_im = O.quantize_sign_phase(re, im)
+    assert s_re == np.float32(0.75 / 4) and s_im == np.float32(2.25 / 4)
+    # bit0 = re >= 0 (-0 counts as >= 0), bit1 = im >= 0
+    assert codes.tolist() == [[1, 2], [3, 1]]
+    assert q_re.tolist() == [[s_re, -s_re], [s_re, s_re]] and q_im.tolist() == [[-s_im, s_im], [s_im, -s_im]]
+    # an all-zero plane takes the 1e-6 floor
+    _, s0, _, _, _ = O.quantize_sign_phase(np.zeros((2, 2), np.float32), np.ones((2, 2), np.float32))
+    assert s0 == np.float32(1e-6)
+
+
 # -- 16-PSK (build-defined codebook: parity unpinned by the reference) -------------
 def test_psk16_closed_form():
     cb = O.psk16_codebook().astype(np.float64)

@@ -108,6 +108,30 @@ def test_qat_layer_forward_matches_reference(golden, method, act, rot):
     assert torch.allclose(y, torch.from_numpy(golden[f"fwd_y_{tag}"]), rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("method,steps", [("complex_phase_v3", 3), ("complex_phase_v4", 4)])
+@pytest.mark.parametrize("rot", [0, 1])
+def test_quantize_layer_more_stages_match_golden(golden, method, steps, rot):
+    """v3 / v4: the packer's 2*steps planes and scales decode (all stages
+    summed in order, then de-rotated) to the reference's A_q bit for bit."""
+    from quant_models.quant_i import QATLinearComplexPhase
+
+    layer = QATLinearComplexPhase(quant_method_u=method, quant_method_w=method, enable_act_quant=False,
+                                  enable_rotation=bool(rot), in_features=96, out_features=64)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(golden["w_weight"]))
+        if rot:
+            layer.quantizer_u.rotation_angle.fill_(0.3)
+            layer.quantizer_w.rotation_angle.fill_(-0.2)
+    lc = P().quantize_layer(layer.weight, method, method, layer.quantizer_u.rotation_cos_sin(),
+                            layer.quantizer_w.rotation_cos_sin())
+    assert lc.stages == steps and len(lc.planes) == 2 * steps
+    kinds = "u" * steps + "w" * steps
+    planes = [(O.unpack_codes(p.numpy()), a.numpy()[:, 0], b.numpy()[:, 0], k)
+              for p, a, b, k in zip(lc.planes, lc.scale_re, lc.scale_im, kinds)]
+    a_q = O.wide_weight(planes, rotation=lc.rotation)
+    assert np.array_equal(a_q, golden[f"fwd_aq_{method}_a0_r{rot}"])
+
+
 def test_layer_errors():
     from quant_models.quant_i import ComplexWeightQuantizer, QATLinearComplexPhase
 
