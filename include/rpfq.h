@@ -64,6 +64,10 @@ extern "C" {
                             bit0 = (re >= 0), bit1 = (im >= 0) */
 #define RPFQ_CB_PSK16 2  /* 4-bit code c -> exp(i 2 pi c / 16); build-defined,
                             no counterpart in the reference */
+#define RPFQ_CB_TABLE 3  /* 4-bit index into a per-row table of 16 complex
+                            values for U and 16 for W: the learnable grouped
+                            codebook of complex_phase_next_v1 (quant_i.py:193-351;
+                            index = codeword | (e_re >= 0) << 2 | (e_im >= 0) << 3) */
 
 /* Descriptor of one packed widely-linear layer. */
 typedef struct rpfq_wide_desc {
@@ -72,7 +76,7 @@ typedef struct rpfq_wide_desc {
     int64_t block;     /* scale block along K' in complex columns: 0 = one
                           scale per row, else a multiple of 32 */
     int32_t codebook;  /* RPFQ_CB_* */
-    int32_t stages;    /* residual stages per U/W: 1 or 2 (AXIS/SIGN); 1 (PSK16) */
+    int32_t stages;    /* residual stages per U/W: 1 or 2 (AXIS/SIGN); 1 (PSK16, TABLE) */
     int32_t rotate;    /* 1: de-rotate the quantized U/W by (cos,sin) below,
                           quant_i.py:425-435 */
     float rot_u[2];    /* cos(theta_u), sin(theta_u) as float32 */
@@ -126,10 +130,12 @@ size_t rpfq_wide_packed_bytes(const rpfq_wide_desc* desc);
  *   and the fused cache of kernels/phase_linear_cache.cpp:84-131.
  * planes (AXIS/SIGN): 2*stages code planes ordered u_s0[, u_s1], w_s0[, w_s1],
  *   each [N', K'/4] uint8 in the exporter's packing (export…py:148-159);
- * planes (PSK16): u, w, each [N', K'/2] uint8 (low nibble first).
+ * planes (PSK16, TABLE): u, w, each [N', K'/2] uint8 (low nibble first).
  * scale_re[p] / scale_im[p]: float32 [N', nblk] multipliers of plane p
  *   (the training scale, or 1/gamma of the exporter); PSK16 uses scale_re
  *   only (magnitude).  nblk = 1 if desc->block == 0 else ceil(K'/block).
+ *   TABLE: scale_re[p] / scale_im[p] are the real / imaginary parts of the
+ *   [N', 16] float32 value table of plane p (U, W); block and rotate are 0.
  * packed: device buffer of rpfq_wide_packed_bytes(desc) bytes.
  */
 int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int nplanes,

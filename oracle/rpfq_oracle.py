@@ -388,7 +388,10 @@ def wide_parts(planes, codebook: str = "axis", rotation=None):
     'u' or 'w', stage order preserved; the per-stage float32 values are summed
     as the reference does (quant_i.py:111-118: q = 0 + step0 + step1), then
     optionally de-rotated (quant_i.py:433-434).  codebook 'axis' | 'sign' |
-    'psk16' (for 'psk16' s_re is the magnitude and s_im is ignored)."""
+    'psk16' (for 'psk16' s_re is the magnitude and s_im is ignored) |
+    'table' (codes index per-row [N, 16] value tables s_re / s_im: the
+    packed form of complex_phase_next_v1's grouped quantizer,
+    quant_i.py:193-351; one plane each for U and W)."""
     acc = {}
     for codes, s_re, s_im, kind in planes:
         if codebook == "psk16":
@@ -399,6 +402,9 @@ def wide_parts(planes, codebook: str = "axis", rotation=None):
             v_im = (cb[..., 1] * mag).astype(F32)
         elif codebook == "sign":
             v_re, v_im = sign_codes_values(codes, s_re, s_im)
+        elif codebook == "table":  # s_re / s_im: per-row [N, 16] value tables, codes = indices
+            v_re = np.take_along_axis(np.asarray(s_re, F32), np.asarray(codes, np.int64), axis=1)
+            v_im = np.take_along_axis(np.asarray(s_im, F32), np.asarray(codes, np.int64), axis=1)
         else:
             v_re, v_im = dequant_codes(codes, s_re, s_im, gamma=False)
         q_re, q_im = acc.get(kind, (np.zeros_like(v_re), np.zeros_like(v_im)))

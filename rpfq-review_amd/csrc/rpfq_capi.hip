@@ -44,10 +44,13 @@ int check_desc(const rpfq_wide_desc* d) {
         return fail(RPFQ_ERR_ALIGN, "k_complex=%lld must be a multiple of 8", (long long)d->k_complex);
     if (d->block < 0 || (d->block > 0 && d->block % 32 != 0))
         return fail(RPFQ_ERR_VALUE, "block=%lld must be 0 or a multiple of 32", (long long)d->block);
-    if (d->codebook != RPFQ_CB_AXIS && d->codebook != RPFQ_CB_SIGN && d->codebook != RPFQ_CB_PSK16)
+    if (d->codebook != RPFQ_CB_AXIS && d->codebook != RPFQ_CB_SIGN && d->codebook != RPFQ_CB_PSK16 &&
+        d->codebook != RPFQ_CB_TABLE)
         return fail(RPFQ_ERR_BITS, "unknown codebook %d", d->codebook);
-    if (d->codebook == RPFQ_CB_PSK16 && d->stages != 1)
-        return fail(RPFQ_ERR_BITS, "PSK16 layers have one stage, got %d", d->stages);
+    if ((d->codebook == RPFQ_CB_PSK16 || d->codebook == RPFQ_CB_TABLE) && d->stages != 1)
+        return fail(RPFQ_ERR_BITS, "PSK16 / TABLE layers have one stage, got %d", d->stages);
+    if (d->codebook == RPFQ_CB_TABLE && (d->block != 0 || d->rotate != 0))
+        return fail(RPFQ_ERR_VALUE, "TABLE layers take block = 0 and rotate = 0 (the table holds final values)");
     if (d->stages != 1 && d->stages != 2)
         return fail(RPFQ_ERR_BITS, "stages=%d unsupported (1 or 2)", d->stages);
     if (d->rotate != 0 && d->rotate != 1) return fail(RPFQ_ERR_VALUE, "rotate must be 0 or 1");
@@ -123,7 +126,7 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
     int rc = check_desc(desc);
     if (rc) return rc;
     if (!planes || !scale_re || !packed) return fail(RPFQ_ERR_NULL, "planes/scale_re/packed must not be NULL");
-    int want = desc->codebook == RPFQ_CB_PSK16 ? 2 : 2 * desc->stages;
+    int want = (desc->codebook == RPFQ_CB_PSK16 || desc->codebook == RPFQ_CB_TABLE) ? 2 : 2 * desc->stages;
     if (nplanes != want) return fail(RPFQ_ERR_BITS, "expected %d planes, got %d", want, nplanes);
     if (desc->codebook != RPFQ_CB_PSK16 && !scale_im) return fail(RPFQ_ERR_NULL, "scale_im must not be NULL");
     for (int p = 0; p < nplanes; ++p) {

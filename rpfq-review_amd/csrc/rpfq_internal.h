@@ -23,6 +23,8 @@ namespace rpfq {
 //  params: [NT*32 rows][nblk][8] float32 at an offset rounded up to 256 B:
 //          AXIS/SIGN: u_s0 (re,im), u_s1 (re,im), w_s0 (re,im), w_s1 (re,im)
 //          multipliers; PSK16: [s_u, 0, 0, 0, s_w, 0, 0, 0].  Padded rows 0.
+//          TABLE: [NT*32 rows][32] (re, im) float32 pairs, entries 0..15 the
+//          U values of indices 0..15, 16..31 the W values (nblk = 1).
 // ---------------------------------------------------------------------------
 struct WideGeom {
     int64_t N, K;        // complex dims
@@ -48,7 +50,8 @@ inline WideGeom wide_geom(const rpfq_wide_desc& d) {
     }
     size_t codes = (size_t)g.NT * g.KS * 1024;
     g.codes_bytes = (codes + 255) & ~(size_t)255;
-    g.total_bytes = g.codes_bytes + (size_t)g.NT * 32 * g.nblk * 8 * sizeof(float);
+    const size_t row_floats = d.codebook == RPFQ_CB_TABLE ? 64 : (size_t)g.nblk * 8;
+    g.total_bytes = g.codes_bytes + (size_t)g.NT * 32 * row_floats * sizeof(float);
     return g;
 }
 

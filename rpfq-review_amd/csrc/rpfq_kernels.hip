@@ -442,7 +442,7 @@ __global__ void wide_pack_codes_kernel(PackArgs a) {
     int64_t k = ks * 32 + 8 * s + 4 * gg + e;
     uint32_t out = 0;
     if (n < a.N && k < a.K) {
-        if (a.codebook == RPFQ_CB_PSK16) {
+        if (a.codebook == RPFQ_CB_PSK16 || a.codebook == RPFQ_CB_TABLE) {
             int64_t kb = a.K >> 1;
             uint32_t cu = (a.planes[0][n * kb + (k >> 1)] >> (4 * (k & 1))) & 15u;
             uint32_t cw = (a.planes[1][n * kb + (k >> 1)] >> (4 * (k & 1))) & 15u;
@@ -464,6 +464,21 @@ __global__ void wide_pack_codes_kernel(PackArgs a) {
         }
     }
     a.codes[idx] = (uint8_t)out;
+}
+
+// TABLE: row n's 16 U then 16 W (re, im) values; padded rows 0.
+__global__ void wide_pack_table_kernel(PackArgs a) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t total = a.NT * 32 * 32;
+    if (idx >= total) return;
+    int64_t n = idx >> 5;
+    int e = (int)(idx & 31), p = e >> 4, i = e & 15;
+    float re = 0.0f, im = 0.0f;
+    if (n < a.N) {
+        re = a.sre[p][n * 16 + i];
+        im = a.sim[p][n * 16 + i];
+    }
+    reinterpret_cast<float2*>(a.params)[idx] = make_float2(re, im);
 }
 
 __global__ void wide_pack_params_kernel(PackArgs a) {
@@ -548,7 +563,7 @@ template <int CB>
 __device__ __forceinline__ void build_lut(uint32_t* lut, const float4* params, int64_t n, bool active, int nblk,
                                           int blk, const RotParams& rot, int r, int g) {
     float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
-    if (active) {
+    if (CB != RPFQ_CB_TABLE && active) {
         const float4* p = params + (n * nblk + blk) * 2;
         pu = p[0];
         pw = p[1];
@@ -556,8 +571,15 @@ __device__ __forceinline__ void build_lut(uint32_t* lut, const float4* params, i
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         uint32_t idx = (uint32_t)(g + 2 * j);
-        float2 u = lut_entry<CB>(idx, pu);
-        float2 w = lut_entry<CB>(idx, pw);
+        float2 u, w;
+        if constexpr (CB == RPFQ_CB_TABLE) {
+            const float2* t = reinterpret_cast<const float2*>(params) + n * 32;
+            u = active ? t[idx] : make_float2(0.0f, 0.0f);
+            w = active ? t[16 + idx] : make_float2(0.0f, 0.0f);
+        } else {
+            u = lut_entry<CB>(idx, pu);
+            w = lut_entry<CB>(idx, pw);
+        }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);
             w = derotate(w, rot.cw, rot.sw);
@@ -929,13 +951,24 @@ __device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, ui
 template <int CB>
 __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, const float4* params, int64_t n,
                                                int nblk, int blk, const RotParams& rot, int g) {
-    const float4* p = params + (n * nblk + blk) * 2;
-    const float4 pu = p[0], pw = p[1];
+    float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
+    if constexpr (CB != RPFQ_CB_TABLE) {
+        const float4* p = params + (n * nblk + blk) * 2;
+        pu = p[0];
+        pw = p[1];
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t idx = (uint32_t)(g + 2 * j);
-        float2 u = lut_entry<CB>(idx, pu);
-        float2 w = lut_entry<CB>(idx, pw);
+        float2 u, w;
+        if constexpr (CB == RPFQ_CB_TABLE) {
+            const float2* t = reinterpret_cast<const float2*>(params) + n * 32;
+            u = t[idx];
+            w = t[16 + idx];
+        } else {
+            u = lut_entry<CB>(idx, pu);
+            w = lut_entry<CB>(idx, pw);
+        }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);
             w = derotate(w, rot.cw, rot.sw);
@@ -1337,14 +1370,24 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // entry idx in slots 32 (R >> 4) + (R & 15) and + 16; lane group g writes
 // the even or odd indices.
 template <int CB>
-__device__ __forceinline__ void build_lut_sk(uint32_t* lut, float4 pu, float4 pw, const RotParams& rot, int R,
-                                             int g) {
+__device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, const RotParams& rot, int R, int g) {
     const int s0 = 32 * (R >> 4) + (R & 15);
+    float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
+    if constexpr (CB != RPFQ_CB_TABLE) {
+        pu = p[0];
+        pw = p[1];
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t idx = (uint32_t)(g + 2 * j);
-        float2 u = lut_entry<CB>(idx, pu);
-        float2 w = lut_entry<CB>(idx, pw);
+        float2 u, w;
+        if constexpr (CB == RPFQ_CB_TABLE) {  // p = the row's 32 (re, im) values
+            u = reinterpret_cast<const float2*>(p)[idx];
+            w = reinterpret_cast<const float2*>(p)[16 + idx];
+        } else {
+            u = lut_entry<CB>(idx, pu);
+            w = lut_entry<CB>(idx, pw);
+        }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);
             w = derotate(w, rot.cw, rot.sw);
@@ -1431,8 +1474,8 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
 
     int blk = 0;
     if (wave == 0) {
-        const float4* p = a.params + ((int64_t)tile * 32 + R) * a.nblk * 2;
-        build_lut_sk<CB>(lut, p[0], p[1], a.rot, R, g);
+        const float4* p = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
+        build_lut_sk<CB>(lut, p, a.rot, R, g);
     }
     if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1491,7 +1534,7 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
                 if (nb != blk) {
                     blk = nb;
                     const float4* p = a.params + (((int64_t)tile * 32 + R) * a.nblk + nb) * 2;
-                    build_lut_sk<CB>(lut, p[0], p[1], a.rot, R, g);
+                    build_lut_sk<CB>(lut, p, a.rot, R, g);
                 }
             }
             compute(ks, cur);
@@ -1574,10 +1617,17 @@ __global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const floa
     int s = (int)(kk >> 3), gg = (int)((kk >> 2) & 1), e = (int)(kk & 3);
     int b = gg * 16 + s * 4 + e;
     uint32_t byte = codes[((nt * KS + ks) * 32 + rr) * 32 + b];
-    int64_t blk = ks / block_ks;
-    const float4* p = params + (n * nblk + blk) * 2;
-    float2 U = lut_entry<CB>(byte & 15u, p[0]);
-    float2 W = lut_entry<CB>(byte >> 4, p[1]);
+    float2 U, W;
+    if constexpr (CB == RPFQ_CB_TABLE) {
+        const float2* t = reinterpret_cast<const float2*>(params) + n * 32;
+        U = t[byte & 15u];
+        W = t[16 + (byte >> 4)];
+    } else {
+        int64_t blk = ks / block_ks;
+        const float4* p = params + (n * nblk + blk) * 2;
+        U = lut_entry<CB>(byte & 15u, p[0]);
+        W = lut_entry<CB>(byte >> 4, p[1]);
+    }
     if (rot.rotate) {
         U = derotate(U, rot.cu, rot.su);
         W = derotate(W, rot.cw, rot.sw);
@@ -1903,6 +1953,11 @@ hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const ui
     hipLaunchKernelGGL(wide_pack_codes_kernel, dim3(grid1d(nc, 256)), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (d.codebook == RPFQ_CB_TABLE) {
+        int64_t nt = g.NT * 32 * 32;
+        hipLaunchKernelGGL(wide_pack_table_kernel, dim3(grid1d(nt, 256)), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     int64_t np = g.NT * 32 * g.nblk;
     hipLaunchKernelGGL(wide_pack_params_kernel, dim3(grid1d(np, 256)), dim3(256), 0, s, a);
     return hipGetLastError();
@@ -2043,6 +2098,7 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     switch (d.codebook) {
         case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
         case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_TABLE: return wide_x<RPFQ_CB_TABLE>(a, xdt, ydt, flags, s);
         default: return wide_x<RPFQ_CB_AXIS>(a, xdt, ydt, flags, s);
     }
 }
@@ -2140,6 +2196,10 @@ hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const 
             break;
         case RPFQ_CB_PSK16:
             hipLaunchKernelGGL(wide_decode_kernel<RPFQ_CB_PSK16>, grid, dim3(256), 0, s, codes, params, g.N, g.K,
+                               g.KS, g.nblk, g.block_ks, rot, out, round_fp16);
+            break;
+        case RPFQ_CB_TABLE:
+            hipLaunchKernelGGL(wide_decode_kernel<RPFQ_CB_TABLE>, grid, dim3(256), 0, s, codes, params, g.N, g.K,
                                g.KS, g.nblk, g.block_ks, rot, out, round_fp16);
             break;
         default:

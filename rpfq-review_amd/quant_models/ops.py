@@ -253,8 +253,8 @@ class PackedWide:
     @property
     def code_bytes(self) -> int:
         """Algorithmic bytes of the packed codes: 2*stages planes of 2 bits
-        (AXIS/SIGN) or 2 planes of 4 bits (PSK16) per complex element."""
-        bits = 8 if self.codebook == N.CB_PSK16 else 4 * self.stages
+        (AXIS/SIGN) or 2 planes of 4 bits (PSK16, TABLE) per complex element."""
+        bits = 8 if self.codebook in (N.CB_PSK16, N.CB_TABLE) else 4 * self.stages
         return self.n_complex * self.k_complex * bits // 8
 
     @property
@@ -328,7 +328,7 @@ def pack_layer(planes, scale_re, scale_im, n_complex: int, k_complex: int, codeb
     """PackedWide for stages <= 2, else PackedStages over groups of two
     stages.  planes / scales ordered u_s0..u_s{S-1}, w_s0..w_s{S-1} (AXIS,
     SIGN) as PackedWide.from_planes takes them."""
-    if stages <= 2 or codebook == N.CB_PSK16:
+    if stages <= 2 or codebook in (N.CB_PSK16, N.CB_TABLE):
         return PackedWide.from_planes(planes, scale_re, scale_im, n_complex, k_complex, codebook, stages, block,
                                       rotation)
     if len(planes) != 2 * stages:

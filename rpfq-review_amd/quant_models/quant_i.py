@@ -113,7 +113,9 @@ class LearnableGroupedPhaseQuant(nn.Module):
         else:
             self.register_parameter("rotation_angles", None)
 
-    def forward(self, w_real: torch.Tensor, w_imag: torch.Tensor) -> TensorPair:
+    def _fit(self, w_real, w_imag, phase_angles, rotation_angles):
+        """Steps 1-5 of the reference forward (quant_i.py:286-331): grouped,
+        rotated planes, chosen codeword, group magnitudes and residual signs."""
         if w_real.shape != w_imag.shape:
             raise ValueError("w_real and w_imag must have the same shape.")
         rows, cols = w_real.shape
@@ -127,33 +129,76 @@ class LearnableGroupedPhaseQuant(nn.Module):
         wr = wr.reshape(groups, gs, cols)
         wi = wi.reshape(groups, gs, cols)
         valid = valid.reshape(groups, gs, 1)
+        c = s = None
         if self.enable_rotation:
-            c, s = torch.cos(self.rotation_angles), torch.sin(self.rotation_angles)
+            c, s = torch.cos(rotation_angles), torch.sin(rotation_angles)
             rr, ri = wr * c + wi * s, wi * c - wr * s
         else:
             rr, ri = wr, wi
         inv = torch.rsqrt((rr.square() + ri.square()).clamp_min(EPS))
-        book = torch.stack((torch.cos(self.phase_angles), torch.sin(self.phase_angles)), dim=-1)
+        book = torch.stack((torch.cos(phase_angles), torch.sin(phase_angles)), dim=-1)
         sim = (rr * inv).unsqueeze(-1) * book[:, 0].view(1, 1, 1, -1) + \
               (ri * inv).unsqueeze(-1) * book[:, 1].view(1, 1, 1, -1)
-        chosen = book[sim.argmax(dim=-1)]
+        idx = sim.argmax(dim=-1)
+        chosen = book[idx]
         d_re, d_im = chosen[..., 0], chosen[..., 1]
         num = ((rr * d_re + ri * d_im) * valid).sum(dim=(1, 2), keepdim=True)
         den = (((d_re.square() + d_im.square()) * valid).sum(dim=(1, 2), keepdim=True)).clamp_min(EPS)
         alpha = num / den
         q_re, q_im = alpha * d_re, alpha * d_im
+        fit = {"rows": rows, "cols": cols, "c": c, "s": s, "book": book, "idx": idx, "alpha": alpha,
+               "q_re": q_re, "q_im": q_im}
         if self.use_residual:
             e_re, e_im = rr - q_re, ri - q_im
             count = (valid.sum(dim=(1, 2), keepdim=True) * e_re.shape[-1]).clamp_min(1.0)
-            b_re = (e_re.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
-            b_im = (e_im.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
-            q_re = q_re + b_re * torch.where(e_re >= 0, 1.0, -1.0).to(e_re.dtype)
-            q_im = q_im + b_im * torch.where(e_im >= 0, 1.0, -1.0).to(e_im.dtype)
+            fit["b_re"] = (e_re.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
+            fit["b_im"] = (e_im.abs() * valid).sum(dim=(1, 2), keepdim=True) / count
+            fit["pos_re"], fit["pos_im"] = e_re >= 0, e_im >= 0
+        return fit
+
+    def forward(self, w_real: torch.Tensor, w_imag: torch.Tensor) -> TensorPair:
+        f = self._fit(w_real, w_imag, self.phase_angles, self.rotation_angles)
+        q_re, q_im = f["q_re"], f["q_im"]
+        if self.use_residual:
+            q_re = q_re + f["b_re"] * torch.where(f["pos_re"], 1.0, -1.0).to(q_re.dtype)
+            q_im = q_im + f["b_im"] * torch.where(f["pos_im"], 1.0, -1.0).to(q_im.dtype)
         if self.enable_rotation:
+            c, s = f["c"], f["s"]
             q_re, q_im = q_re * c - q_im * s, q_im * c + q_re * s
-        q_re = q_re.reshape(-1, cols)[:rows]
-        q_im = q_im.reshape(-1, cols)[:rows]
+        q_re = q_re.reshape(-1, f["cols"])[:f["rows"]]
+        q_im = q_im.reshape(-1, f["cols"])[:f["rows"]]
         return q_re + (w_real - w_real.detach()), q_im + (w_imag - w_imag.detach())
+
+    def table(self, w_real: torch.Tensor, w_imag: torch.Tensor):
+        """Packed form of forward() on host copies of the weight and the
+        learned parameters: a 4-bit index per weight (codeword |
+        (residual re >= 0) << 2 | (residual im >= 0) << 3) and per row the 16
+        values the indices stand for, each formed by forward()'s float32 ops
+        in forward()'s order (alpha d + beta sign, rotation back, + 0), so
+        table[row][index] equals forward()'s value bit for bit.
+        Returns (index uint8 [rows, cols], table_re, table_im float32 [rows, 16])."""
+        if self.n_codewords != 4 or not self.use_residual:
+            raise NotImplementedError("packed next_v1 needs 4 codewords and the residual sign step")
+        pa = self.phase_angles.detach().cpu()
+        ra = self.rotation_angles.detach().cpu() if self.rotation_angles is not None else None
+        f = self._fit(w_real.detach().cpu().float(), w_imag.detach().cpu().float(), pa, ra)
+        rows, cols = f["rows"], f["cols"]
+        idx = (f["idx"].to(torch.uint8) | (f["pos_re"].to(torch.uint8) << 2) | (f["pos_im"].to(torch.uint8) << 3))
+        e = torch.arange(16)
+        d = f["book"][e & 3]                                   # [16, 2]
+        sg_re = torch.where(((e >> 2) & 1) == 1, 1.0, -1.0)
+        sg_im = torch.where(((e >> 3) & 1) == 1, 1.0, -1.0)
+        alpha = f["alpha"].reshape(-1, 1)                      # [groups, 1]
+        t_re = alpha * d[:, 0].view(1, 16) + f["b_re"].reshape(-1, 1) * sg_re.view(1, 16)
+        t_im = alpha * d[:, 1].view(1, 16) + f["b_im"].reshape(-1, 1) * sg_im.view(1, 16)
+        if self.enable_rotation:
+            c, s = f["c"].reshape(-1, 1), f["s"].reshape(-1, 1)
+            t_re, t_im = t_re * c - t_im * s, t_im * c + t_re * s
+        t_re, t_im = t_re + 0.0, t_im + 0.0  # forward()'s "+ (w - w.detach())" (turns -0 into +0)
+        gs = self.group_size
+        t_re = t_re.repeat_interleave(gs, dim=0)[:rows].contiguous()
+        t_im = t_im.repeat_interleave(gs, dim=0)[:rows].contiguous()
+        return idx.reshape(-1, cols)[:rows].contiguous(), t_re, t_im
 
 
 SUPPORTED_QUANT_METHODS = (
@@ -421,6 +466,8 @@ class QATLinearComplexPhase(nn.Linear):
             return self._packed
         if self._override is not None:
             lc = self._override
+        elif self.quantizer_u.is_module_quantizer or self.quantizer_w.is_module_quantizer:
+            lc = self._table_codes()
         elif self.pack_on_device and self.weight.is_cuda:
             lc = P.quantize_layer_device(self.weight, self.quantizer_u.quant_method, self.quantizer_w.quant_method,
                                          self.quantizer_u.rotation_cos_sin(), self.quantizer_w.rotation_cos_sin())
@@ -438,11 +485,27 @@ class QATLinearComplexPhase(nn.Linear):
         self._packed_key = key
         return self._packed
 
+    def _table_codes(self) -> "P.LayerCodes":
+        """complex_phase_next_v1 in the TABLE codebook: 4-bit indices and the
+        per-row value tables of both learned grouped quantizers (host)."""
+        if not (self.quantizer_u.is_module_quantizer and self.quantizer_w.is_module_quantizer):
+            raise NotImplementedError("packed HIP path needs complex_phase_next_v1 for both U and W")
+        from . import _native as N
+
+        u_re, u_im, w_re, w_im = P.split_blocks(self.weight.detach().cpu().float())
+        iu, tu_re, tu_im = self.quantizer_u.quant_fn.table(u_re, u_im)
+        iw, tw_re, tw_im = self.quantizer_w.quant_fn.table(w_re, w_im)
+        return P.LayerCodes([P.pack4(iu), P.pack4(iw)], [tu_re, tw_re], [tu_im, tw_im], u_re.shape[0],
+                            u_re.shape[1], N.CB_TABLE, 1, 0, None)
+
     def _rotation_version(self):
         vs = []
         for q in (self.quantizer_u, self.quantizer_w):
-            if q.rotation_angle is not None:
-                vs.append((q.rotation_angle.data_ptr(), q.rotation_angle._version))
+            params = [q.rotation_angle] if q.rotation_angle is not None else []
+            if q.is_module_quantizer:
+                params = [p for p in (q.quant_fn.phase_angles, q.quant_fn.rotation_angles) if p is not None]
+            for p in params:
+                vs.append((p.data_ptr(), p._version))
         return tuple(vs)
 
     def _packed_forward(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:

@@ -160,3 +160,18 @@ def test_quantize_wide_argument_errors():
     assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, p, p, ws, None) == 3  # codes need K' % 4
     bad.k_complex = 0
     assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, None, p, ws, None) == 2
+
+
+def test_table_codebook_desc_rules():
+    L, N = lib()
+    d = _desc(N, n=64, k=64, cb=N.CB_TABLE, stages=1)
+    # codes 2 x 2 tiles x 1 KB, then 64 rows x 32 (re, im) float32 pairs
+    assert L.rpfq_wide_packed_bytes(ctypes.byref(d)) == 2 * 2 * 1024 + 64 * 64 * 4
+    buf = ctypes.create_string_buffer(64)
+    for field, value, code in (("stages", 2, 4), ("block", 256, 6), ("rotate", 1, 6)):
+        bad = _desc(N, n=64, k=64, cb=N.CB_TABLE, stages=1)
+        setattr(bad, field, value)
+        assert L.rpfq_wide_linear(ctypes.byref(bad), buf, 1 << 20, buf, 1, 4, None, buf, 1, 0, None) == code, field
+    p = ctypes.c_void_p(256)
+    arr = (ctypes.c_void_p * 4)(p, p, p, p)
+    assert L.rpfq_wide_pack(ctypes.byref(d), arr, 4, arr, arr, p, 1 << 20, None) == 4  # two planes (u, w)

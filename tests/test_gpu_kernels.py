@@ -142,10 +142,18 @@ def test_phase_linear_half_inputs(dt):
 def make_wide(r, n_c, k_c, codebook="axis", stages=2, per_row=True, block=0):
     """Random planes + per-(plane,row[,block]) scales in the oracle format."""
     _, N = qm()
-    nplanes = 2 if codebook == "psk16" else 2 * stages
+    nplanes = 2 if codebook in ("psk16", "table") else 2 * stages
     nblk = 1 if block == 0 else -(-k_c // block)
     planes_np, sre, sim, packed = [], [], [], []
     for p in range(nplanes):
+        if codebook == "table":  # 4-bit indices into per-row tables of 16 signed values
+            c = r.integers(0, 16, size=(n_c, k_c), dtype=np.uint8)
+            packed.append(O.pack_codes4(c))
+            sgn = lambda: np.where(r.random((n_c, 16)) < 0.5, -1.0, 1.0)  # noqa: E731
+            planes_np.append(c)
+            sre.append((r.uniform(0.01, 0.2, size=(n_c, 16)) * sgn()).astype(np.float32))
+            sim.append((r.uniform(0.01, 0.2, size=(n_c, 16)) * sgn()).astype(np.float32))
+            continue
         if codebook == "psk16":
             c = r.integers(0, 16, size=(n_c, k_c), dtype=np.uint8)
             packed.append(O.pack_codes4(c))
@@ -161,12 +169,15 @@ def make_wide(r, n_c, k_c, codebook="axis", stages=2, per_row=True, block=0):
         sre.append(s1)
         sim.append(s2)
     kinds = (["u"] * (nplanes // 2)) + (["w"] * (nplanes // 2))
-    cb = {"axis": N.CB_AXIS, "sign": N.CB_SIGN, "psk16": N.CB_PSK16}[codebook]
+    cb = {"axis": N.CB_AXIS, "sign": N.CB_SIGN, "psk16": N.CB_PSK16, "table": N.CB_TABLE}[codebook]
     return planes_np, packed, sre, sim, kinds, cb, nblk
 
 
-def oracle_planes(planes_np, sre, sim, kinds, k_c, block):
-    """Expand per-block scales to per-element for the oracle."""
+def oracle_planes(planes_np, sre, sim, kinds, k_c, block, codebook="axis"):
+    """Expand per-block scales to per-element for the oracle (value tables
+    of the 'table' codebook pass through)."""
+    if codebook == "table":
+        return list(zip(planes_np, sre, sim, kinds))
     out = []
     bs = block if block else k_c
     for c, a, b, kind in zip(planes_np, sre, sim, kinds):
@@ -189,6 +200,7 @@ CASES = [
     (64, 64, "sign", 2, 0, None),          # new_v2
     (96, 128, "psk16", 1, 0, None),        # 16-PSK
     (128, 96, "axis", 2, 0, ((0.95533645, 0.29552022), (0.98006660, -0.19866933))),  # rotation
+    (100, 96, "table", 1, 0, None),        # next_v1: per-row value tables
 ]
 
 
@@ -201,7 +213,7 @@ def build_packed(r, case):
     rotation = None
     if rot is not None:
         rotation = tuple((np.float32(c), np.float32(s)) for c, s in rot)
-    oplanes = oracle_planes(planes_np, sre, sim, kinds, k_c, block)
+    oplanes = oracle_planes(planes_np, sre, sim, kinds, k_c, block, codebook)
     a_ref = O.wide_weight(oplanes, codebook, rotation)
     build_packed.last_oplanes, build_packed.last_rotation = oplanes, rotation
     return pw, oplanes, a_ref, codebook, rotation
@@ -302,8 +314,8 @@ def test_wide_linear_matches_reference_android_runtime():
 
 @pytest.mark.parametrize("flags", [0, 1])
 @pytest.mark.parametrize("m", [33, 128, 300, 513])
-@pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[4], CASES[7]],
-                         ids=["1536x384", "50x48", "130x512-b256", "rot"])
+@pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[4], CASES[7], CASES[8]],
+                         ids=["1536x384", "50x48", "130x512-b256", "rot", "table"])
 def test_wide_linear_kernels_agree(case, m, flags):
     """The LDS-DMA kernel (flags 0, fp16 x, K' % 32 == 0, M >= 128) and the
     register-staged kernel (RPFQ_FLAG_TILE_M128) meet the same bound, with

@@ -165,3 +165,41 @@ def test_synthetic_layer_shapes_and_ranges():
     assert float(s.min()) >= 0.01 and float(s.max()) <= 0.1
     lc16 = P().synthetic_layer(w, g, codebook=2)
     assert len(lc16.planes) == 2 and lc16.planes[0].shape == (32, 24)
+
+
+@pytest.mark.parametrize("rot", [0, 1])
+@pytest.mark.parametrize("rows", [64, 50])
+def test_next_v1_table_matches_forward(rot, rows):
+    """complex_phase_next_v1's packed form: table[row][index] reproduces the
+    grouped quantizer's forward bit for bit (rotation, ragged last group)."""
+    from quant_models.quant_i import LearnableGroupedPhaseQuant
+
+    torch.manual_seed(rows + rot)
+    q = LearnableGroupedPhaseQuant(n_rows=rows, group_size=32, enable_rotation=bool(rot))
+    with torch.no_grad():
+        q.phase_angles.add_(torch.randn(4) * 0.2)
+        if rot:
+            q.rotation_angles.normal_(0.0, 0.5)
+    re, im = torch.randn(rows, 40) * 0.05, torch.randn(rows, 40) * 0.05
+    with torch.no_grad():
+        q_re, q_im = q(re, im)
+    idx, t_re, t_im = q.table(re, im)
+    assert idx.dtype == torch.uint8 and int(idx.max()) < 16 and t_re.shape == (rows, 16)
+    assert torch.equal(torch.gather(t_re, 1, idx.long()), q_re)
+    assert torch.equal(torch.gather(t_im, 1, idx.long()), q_im)
+
+
+def test_next_v1_layer_codes_reproduce_golden(golden):
+    """The layer's TABLE codes decode (oracle, 'table' codebook) to the
+    reference's golden A_q of complex_phase_next_v1."""
+    from quant_models.quant_i import QATLinearComplexPhase
+
+    layer = QATLinearComplexPhase(quant_method_u="complex_phase_next_v1", quant_method_w="complex_phase_next_v1",
+                                  enable_act_quant=False, enable_rotation=False, in_features=96, out_features=64)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(golden["w_weight"]))
+    lc = layer._table_codes()
+    assert lc.codebook == 3 and lc.stages == 1 and [tuple(p.shape) for p in lc.planes] == [(32, 24)] * 2
+    planes = [(O.unpack_codes4(p.numpy()), a.numpy(), b.numpy(), k)
+              for p, a, b, k in zip(lc.planes, lc.scale_re, lc.scale_im, "uw")]
+    assert np.array_equal(O.wide_weight(planes, "table"), golden["fwd_aq_complex_phase_next_v1_a0_r0"])
