@@ -1040,7 +1040,19 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // Persistent: the grid holds two workgroups per CU and walks the tiles in
     // the same XCD-local order as a one-tile-per-workgroup launch (the grid
     // size is a multiple of 8, so vb & 7 stays this workgroup's XCD).
+    // K-step ks of every tile uses activation stage (ks + 2) % 3, so k-step 0
+    // sits in stage 2, which (with codes buffer 0) lies outside the epilogue's
+    // LDS rows: the next tile's first codes and activations are requested
+    // before the epilogue and land while it runs.
     const int total = a.tiles_m * a.tiles_n;
+    auto tile_src = [&](int vb_t) {  // this wave's x rows and code block of tile vb_t
+        const int t = xcd_tile(vb_t, total);
+        const int mt_t = t / a.tiles_n;
+        const int ntw_t = (t - mt_t * a.tiles_n) * 4 + wave;
+        const int64_t m0_t = min((int64_t)mt_t * BM, a.M - BM);
+        xw = reinterpret_cast<const char*>(a.x) + (m0_t + RPW * wave) * ldx * 2;
+        cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)(ntw_t < a.NT ? ntw_t : a.NT - 1) * a.KS * 64);
+    };
     for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
     const int tile = xcd_tile(vb, total);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
@@ -1048,13 +1060,18 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     const int ntw = ntl * 4 + wave;
     const bool active = ntw < a.NT;
     const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
-    xw = reinterpret_cast<const char*>(a.x) + (m0 + RPW * wave) * ldx * 2;
-    cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)ntw_ld * a.KS * 64);
+    tile_src(vb);
 
     floatx16 acc_re[MB], acc_im[MB];
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
+    if (vb == (int)blockIdx.x) {  // later tiles had these requested before the previous epilogue
+        issue_codes(0, 0);
+        issue_x(0, 2);
+    }
+    issue_x(a.KS > 1 ? 1 : 0, 0);
+    // the LUT and bias are written while the loads are in flight
     int cur_blk = 0;
     build_lut_slot<CB>(lut_pair, slot, a.params, (int64_t)ntw_ld * 32 + r, a.nblk, 0, a.rot, g);
     {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue
@@ -1062,10 +1079,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         const bool ok = a.bias && active && nn < a.N;
         bias_s[wave * 64 + g * 32 + r] = ok ? a.bias[g * (int64_t)a.N + nn] : 0.0f;
     }
-    issue_codes(0, 0);
-    issue_x(0, 0);
-    issue_x(a.KS > 1 ? 1 : 0, 1);
-    // codes and stage 0 landed (at most the newest k-step's loads in flight), LUT written
+    // codes and stage 2 landed (at most the newest k-step's loads in flight), LUT written
     if (RPW == 32)
         asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
     else
@@ -1175,12 +1189,19 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     };
     int ks = 0;
     for (; ks + 3 <= a.KS; ks += 3) {
-        kstep(ks, 0);
-        kstep(ks + 1, 1);
-        kstep(ks + 2, 2);
+        kstep(ks, 2);
+        kstep(ks + 1, 0);
+        kstep(ks + 2, 1);
     }
-    if (ks < a.KS) kstep(ks, 0);
-    if (ks + 1 < a.KS) kstep(ks + 1, 1);
+    if (ks < a.KS) kstep(ks, 2);
+    if (ks + 1 < a.KS) kstep(ks + 1, 0);
+    // every stage and code buffer is free (the last k-step drained its loads
+    // and reads before its barrier): request the next tile's k-step 0
+    if (vb + (int)gridDim.x < total) {
+        tile_src(vb + (int)gridDim.x);
+        issue_codes(0, 0);
+        issue_x(0, 2);
+    }
     // Epilogue.  The accumulators hold the transposed tile: lane (r, g) of
     // subtile i has, for x row 32 i + r, outputs n = 32 ntw + 8 q + 4 g + t at
     // element 4 q + t.  Each 4 consecutive outputs go to LDS as one 8-B write
