@@ -1044,6 +1044,8 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // sits in stage 2, which (with codes buffer 0) lies outside the epilogue's
     // LDS rows: the next tile's first codes and activations are requested
     // before the epilogue and land while it runs.
+    static_assert(4 * (BM / 2) * kTRow <= kDmaLutPair + 2 * dma_stage<BM>(),
+                  "the epilogue rows end before activation stage 2");
     const int total = a.tiles_m * a.tiles_n;
     auto tile_src = [&](int vb_t) {  // this wave's x rows and code block of tile vb_t
         const int t = xcd_tile(vb_t, total);
@@ -1056,7 +1058,12 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
     const int tile = xcd_tile(vb, total);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
+    // the last m-tile is shifted back to end at row M (M % BM != 0); rows
+    // below m_own belong to the previous m-tile and are not stored again, so
+    // every output row is read (residual) and written by one workgroup only
+    // (y may alias the residual)
     const int64_t m0 = min((int64_t)mt * BM, a.M - BM);
+    const int64_t m_own = (int64_t)mt * BM;
     const int ntw = ntl * 4 + wave;
     const bool active = ntw < a.NT;
     const int ntw_ld = active ? ntw : a.NT - 1;  // inactive waves decode a valid tile, store nothing
@@ -1223,6 +1230,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
             const int64_t m = m0 + 32 * i + r;
+            if (m < m_own) continue;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t n0 = nb0 + 8 * q;
@@ -1310,6 +1318,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
             for (int j = 0; j < EPI / 8; ++j) {
                 const int row = (lane >> 3) + 8 * j;
                 const int64_t m = m0 + h * EPI + row;
+                if (m < m_own) continue;
                 uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
                 uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
                 if (a.vec_store && nfirst + 8 <= a.N) {

@@ -428,13 +428,16 @@ def test_wide_linear_residual_bit_exact(m, flags, ydt):
 
 def test_wide_linear_residual_in_place():
     """residual == y through the C ABI: every element is read before it is
-    written by the same thread."""
+    written by the same thread, and by one workgroup only -- also the rows
+    of the last m-tile that the DMA kernel shifts back over the previous
+    one (M % 128 != 0), over several rounds of the persistent grid
+    (M = 40,037: 3,756 tiles)."""
     ops, N = qm()
     import ctypes
     r = rng(1100)
     pw, *_ = build_packed(r, CASES[1])
     lib = N.load()
-    for m in (4, 200):
+    for m in (4, 200, 40037):
         x = torch.from_numpy(r.standard_normal((m, 768)).astype(np.float32)).to(torch.float16).to(DEV)
         res = torch.from_numpy(r.standard_normal((m, 3072)).astype(np.float32)).to(torch.float16).to(DEV)
         want = res + pw.linear(x, None, out_dtype=torch.float16)
