@@ -1044,7 +1044,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // sits in stage 2, which (with codes buffer 0) lies outside the epilogue's
     // LDS rows: the next tile's first codes and activations are requested
     // before the epilogue and land while it runs.
-    static_assert(4 * (BM / 2) * kTRow <= kDmaLutPair + 2 * dma_stage<BM>(),
+    static_assert(4 * ((BM / 2) * kTRow + 64) <= kDmaLutPair + 2 * dma_stage<BM>(),
                   "the epilogue rows end before activation stage 2");
     const int total = a.tiles_m * a.tiles_n;
     auto tile_src = [&](int vb_t) {  // this wave's x rows and code block of tile vb_t
@@ -1268,22 +1268,36 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         }
       }
     } else {
-    char* tt = smem + wave * (EPI * kTRow);
-    const int64_t nbase = (int64_t)ntw * 32;
-    const int cq = lane & 7;  // 16-B chunk of a row: 0-3 real, 4-7 imaginary
-    const int64_t col0 = (cq < 4 ? 0 : a.N) + nbase + 8 * (cq & 3);
-    const int64_t nfirst = nbase + 8 * (cq & 3);
+    // Half a tile at a time: each wave writes its 32 output rows to LDS
+    // ([row][re 32 | im 32] fp16, wave regions kEpiWave apart); after a
+    // workgroup barrier each wave stores EPI / 4 token rows across all four
+    // waves' columns.  A token row of the tile is 128 re + 128 im outputs,
+    // i.e. whole 128-B lines of y, so no line is written in halves at two
+    // different times.  Lane l: row 2 j + (l >> 5), 16-B chunk c = l & 31
+    // (c < 16: re outputs 8 c.., else im outputs 8 (c - 16)..); the 64-B pad
+    // of the wave regions keeps the 8 lanes of a read on 32 distinct banks.
+    constexpr int kEpiWave = EPI * kTRow + 64;
+    char* tt = smem + wave * kEpiWave;
+    const int c = lane & 31;
+    const int64_t ncol = (int64_t)ntl * 128 + 8 * (c & 15);  // first output column (complex row) of the chunk
+    const int64_t gcol = (c < 16 ? 0 : a.N) + ncol;
+    const char* tsrc = smem + ((c & 15) >> 2) * kEpiWave + (c < 16 ? 0 : 64) + (c & 3) * 16;
+    const bool chunk_vec = a.vec_store && ncol + 8 <= a.N;
     // residual chunks of this lane's store rows are requested before the
     // half tile goes through LDS, so their latency overlaps the transpose
-    const bool res_vec = a.res && active && a.vec_store && nfirst + 8 <= a.N;
+    const bool res_vec = a.res && chunk_vec;
+    constexpr int RPS = EPI / 8;  // store instructions per wave and half (2 rows each)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        uint4 rres[EPI / 8];
+        uint4 rres[RPS];
         if (res_vec) {
 #pragma unroll
-            for (int j = 0; j < EPI / 8; ++j)
-                rres[j] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) +
-                                                          (m0 + h * EPI + (lane >> 3) + 8 * j) * ldy + col0);
+            for (int j = 0; j < RPS; ++j) {
+                const int64_t m = m0 + h * EPI + (EPI / 4) * wave + 2 * j + (lane >> 5);
+                rres[j] = m >= m_own ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) +
+                                                                        m * ldy + gcol)
+                                     : make_uint4(0, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int ii = 0; ii < MB / 2; ++ii) {
@@ -1311,37 +1325,39 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 *reinterpret_cast<uint2*>(trow + 64 + (8 * q + 4 * g) * 2) = pi;
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
-        __builtin_amdgcn_wave_barrier();
-        if (active) {
+        // every wave's rows of this half are in LDS
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
 #pragma unroll
-            for (int j = 0; j < EPI / 8; ++j) {
-                const int row = (lane >> 3) + 8 * j;
-                const int64_t m = m0 + h * EPI + row;
-                if (m < m_own) continue;
-                uint4 v = *reinterpret_cast<const uint4*>(tt + row * kTRow + cq * 16);
-                uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
-                if (a.vec_store && nfirst + 8 <= a.N) {
-                    if (res_vec) {
-                        const bool f16 = YDT == RPFQ_F16;
-                        v = make_uint4(add2_y(v.x, rres[j].x, f16), add2_y(v.y, rres[j].y, f16),
-                                       add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
-                    }
-                    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
-                } else {
-                    const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
-                    for (int t = 0; t < 8 && nfirst + t < a.N; ++t) {
-                        uint16_t e = hv[t];
-                        if (a.res)
-                            e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + col0 + t],
-                                                  YDT == RPFQ_F16) & 0xffffu);
-                        dst[t] = e;
-                    }
+        for (int j = 0; j < RPS; ++j) {
+            const int row = (EPI / 4) * wave + 2 * j + (lane >> 5);
+            const int64_t m = m0 + h * EPI + row;
+            if (m < m_own || ncol >= a.N) continue;
+            uint4 v = *reinterpret_cast<const uint4*>(tsrc + row * kTRow);
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + gcol;
+            if (chunk_vec) {
+                if (res_vec) {
+                    const bool f16 = YDT == RPFQ_F16;
+                    v = make_uint4(add2_y(v.x, rres[j].x, f16), add2_y(v.y, rres[j].y, f16),
+                                   add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
+                }
+                __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
+            } else {
+                const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
+                for (int t = 0; t < 8 && ncol + t < a.N; ++t) {
+                    uint16_t e = hv[t];
+                    if (a.res)
+                        e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + gcol + t],
+                                              YDT == RPFQ_F16) & 0xffffu);
+                    dst[t] = e;
                 }
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads of this half done before the next overwrite
-        __builtin_amdgcn_wave_barrier();
+        // all reads of this half done before the next half overwrites the rows
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     }
     }
     // every wave is done with this tile's LDS before the next tile refills it
