@@ -342,6 +342,27 @@ def test_wide_linear_kernels_consistent():
     assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)
 
 
+def test_wide_linear_many_rounds():
+    """M = 50,432 on a 1536 x 384 layer (4,728 tiles: 9.2 rounds of the
+    persistent grid, the last m-tile shifted back): the DMA kernel agrees
+    with the register-staged kernel to float32 accumulation order, and the
+    fused residual stays bit-identical to the separate add."""
+    r = rng(650)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, CASES[1])
+    m = 50432
+    x = torch.from_numpy(r.standard_normal((m, 768)).astype(np.float32)).to(torch.float16).to(DEV)
+    bias = tdev(r.standard_normal(3072).astype(np.float32))
+    y0 = pw.linear(x, bias, out_dtype=torch.float32, flags=0).double()
+    y1 = pw.linear(x, bias, out_dtype=torch.float32, flags=1).double()
+    a16 = torch.from_numpy(O.wide_weight(oplanes, codebook, rotation, fp16=True)).to(DEV).double()
+    scale = x.double().abs() @ a16.abs().T + bias.double().abs()
+    assert bool(((y0 - y1).abs() <= 2e-6 * scale + 1e-6).all())
+    res = torch.from_numpy(r.standard_normal((m, 3072)).astype(np.float32)).to(torch.float16).to(DEV)
+    want = res + pw.linear(x, bias, out_dtype=torch.float16)
+    got = pw.linear(x, bias, out_dtype=torch.float16, residual=res)
+    assert torch.equal(got, want)
+
+
 # ---------------------------------------------------------------------------
 # weight-streaming kernel (M <= 16): the same operands, 16x16x32 MFMAs
 # ---------------------------------------------------------------------------
