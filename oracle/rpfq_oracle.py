@@ -32,6 +32,9 @@ Parity status per function (how each one is pinned; see tests/test_oracle.py):
                                recompose_fp16 by its error bound against the
                                reference A_q and by sign/permutation identities.
 * ``linear_forward``        -- golden outputs of the reference layer.
+* ``wide_parts(..., "table")`` -- the per-row value tables of the packed
+                               next_v1 form: the golden next_v1 A_q of the
+                               reference layer, bit-exact.
 * ``quantize_sign_phase``, ``rotate_for_quant``, ``quantized_weight`` --
                                golden A_q of the reference layer for every
                                axis / sign method with rotation on and off
