@@ -244,6 +244,31 @@ def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, r
     return rows
 
 
+def layer_probe(n_c: int, k_c: int, m: int, steps: int) -> int:
+    """One q2 layer of N' x K' (uniformly random code bytes, per-row scales)
+    on m fp16 rows: `steps` launches of the packed kernel, timed with HIP
+    events; prints one JSON line."""
+    import torch
+
+    pw = stream_layer(k_c, n_c, 1)[0]
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(m, 2 * k_c, device="cuda", generator=g).half()
+    y = torch.empty(m, 2 * n_c, device="cuda", dtype=torch.float16)
+    pw.linear_into(x, None, y)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        pw.linear_into(x, None, y)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / max(1, steps)
+    flops = 2 * m * 2 * k_c * 2 * n_c
+    print(json.dumps({"layer_probe": [n_c, k_c], "m": m, "launches": steps + 1, "avg_us": round(us, 2),
+                      "tflops": round(flops / us / 1e6, 1)}))
+    return 0
+
+
 def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: bool, modes=("hip", "torch")):
     """Quantization-aware training steps of the configured model (float32,
     rotation at the family default, SGD): forward with every Linear
@@ -347,10 +372,15 @@ def main() -> int:
                     help="build the model with 4-bit activation quantization (the reference layer's default)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one forward in a HIP graph and time its replays (launch-bound small batches)")
+    ap.add_argument("--layer-probe", default=None, metavar="NC,KC",
+                    help="time one q2 layer of N' x K' complex (random codes) on 50,432 fp16 rows instead "
+                         "(--steps launches; for counter runs)")
     ap.add_argument("--train", action="store_true",
                     help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
     ap.add_argument("--train-modes", default="hip,torch")
     args = ap.parse_args()
+    if args.layer_probe:
+        return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
     if args.train:
         return train_bench(args.config, args.batch or 64, args.steps, args.warmup, args.act_quant,
                            tuple(args.train_modes.split(",")))
