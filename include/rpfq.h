@@ -255,7 +255,8 @@ size_t rpfq_quantize_workspace_bytes(const rpfq_quant_desc* desc);
  *         real_pos 1, imag_neg 2, imag_pos 3, else 0; SIGN: bit0 re >= 0,
  *         bit1 im >= 0), ordered u_s0.., w_s0..; needs K' % 4 == 0.
  *         With scale_re/scale_im of these planes taken from `scales`, they
- *         are the input of rpfq_wide_pack (the rotation goes in the desc).
+ *         are the input of rpfq_wide_pack (the rotation goes in the desc);
+ *         codes also need 16-byte aligned weight and a_q.
  * work:   device buffer of rpfq_quantize_workspace_bytes(desc) bytes.
  * Each scale is the reference's masked mean with the sum accumulated in
  * float64 and rounded once to float32 (torch sums float32 in its own order:

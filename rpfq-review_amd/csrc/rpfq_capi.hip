@@ -259,6 +259,8 @@ int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const f
     if (!weight || !scales || !work) return fail(RPFQ_ERR_NULL, "weight/scales/work must not be NULL");
     if (codes && desc->k_complex % 4 != 0)
         return fail(RPFQ_ERR_ALIGN, "code planes need k_complex %% 4 == 0, got %lld", (long long)desc->k_complex);
+    if (codes && (!aligned(weight, 16) || (a_q && !aligned(a_q, 16))))
+        return fail(RPFQ_ERR_ALIGN, "code planes need 16-byte aligned weight and a_q");
     if (work_bytes < rpfq_quantize_workspace_bytes(desc))
         return fail(RPFQ_ERR_SHAPE, "workspace holds %zu bytes, need %zu", work_bytes,
                     rpfq_quantize_workspace_bytes(desc));

@@ -111,38 +111,96 @@ __device__ __forceinline__ void load_planes(const QuantArgs& a, int64_t n, int64
     u.q_re = u.q_im = w.q_re = w.q_im = 0.0f;
 }
 
+// V consecutive columns k0.. of U and W (V = 4: one 16-B load per quadrant
+// of the weight; K % 4 == 0 keeps the loads aligned).
+template <int V>
+__device__ __forceinline__ void load_planes_v(const QuantArgs& a, int64_t n, int64_t k0, Plane (&u)[V],
+                                              Plane (&w)[V]) {
+    if constexpr (V == 4) {
+        const int64_t row = 2 * a.K;
+        const float4 q11 = *reinterpret_cast<const float4*>(a.w + n * row + k0);
+        const float4 q12 = *reinterpret_cast<const float4*>(a.w + n * row + a.K + k0);
+        const float4 q21 = *reinterpret_cast<const float4*>(a.w + (a.N + n) * row + k0);
+        const float4 q22 = *reinterpret_cast<const float4*>(a.w + (a.N + n) * row + a.K + k0);
+        const float v11[4] = {q11.x, q11.y, q11.z, q11.w}, v12[4] = {q12.x, q12.y, q12.z, q12.w};
+        const float v21[4] = {q21.x, q21.y, q21.z, q21.w}, v22[4] = {q22.x, q22.y, q22.z, q22.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            u[v].r_re = 0.5f * (v11[v] + v22[v]);
+            u[v].r_im = 0.5f * (v21[v] - v12[v]);
+            w[v].r_re = 0.5f * (v11[v] - v22[v]);
+            w[v].r_im = 0.5f * (v12[v] + v21[v]);
+            if (a.rot) {
+                const float cu = a.rot[0], su = a.rot[1], cw = a.rot[2], sw = a.rot[3];
+                const float ur = u[v].r_re * cu + u[v].r_im * su, ui = u[v].r_im * cu - u[v].r_re * su;
+                const float wr = w[v].r_re * cw + w[v].r_im * sw, wi = w[v].r_im * cw - w[v].r_re * sw;
+                u[v].r_re = ur; u[v].r_im = ui;
+                w[v].r_re = wr; w[v].r_im = wi;
+            }
+            u[v].q_re = u[v].q_im = w[v].q_re = w[v].q_im = 0.0f;
+        }
+    } else {
+        load_planes(a, n, k0, u[0], w[0]);
+    }
+}
+
+// Row and first column of work item `it` (V columns each); 32-bit division
+// when the item count allows it.
+template <int V>
+__device__ __forceinline__ void item_nk(const QuantArgs& a, int64_t it, bool small, int64_t& n, int64_t& k0) {
+    const int64_t kv = a.K / V;
+    if (small) {
+        const uint32_t ni = (uint32_t)it / (uint32_t)kv;
+        n = ni;
+        k0 = ((int64_t)((uint32_t)it - ni * (uint32_t)kv)) * V;
+    } else {
+        n = it / kv;
+        k0 = (it - n * kv) * V;
+    }
+}
+
 // Masked |r| sums and counts of stage a.stage for U (0..3) and W (4..7):
 // (sum |re| over the real mask, count, sum |im| over the imaginary mask,
 // count); SIGN planes count every element.
+template <int V>
 __global__ void __launch_bounds__(kQThreads) quant_reduce_kernel(QuantArgs a) {
     double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int64_t total = a.N * a.K;
+    const int64_t items = a.N * (a.K / V);
+    const bool small = items < (1LL << 31);
     const int st = a.stage;
-    for (int64_t e = (int64_t)blockIdx.x * kQThreads + threadIdx.x; e < total;
-         e += (int64_t)a.nblocks * kQThreads) {
-        int64_t n = e / a.K, k = e - n * a.K;
-        Plane pl[2];
-        load_planes(a, n, k, pl[0], pl[1]);
+    float sc[16];  // scales of the finished stages (finalized by earlier launches)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            if (a.steps[p] <= st) continue;
+    for (int i = 0; i < 16; ++i) sc[i] = a.scales[i];
+    for (int64_t it = (int64_t)blockIdx.x * kQThreads + threadIdx.x; it < items;
+         it += (int64_t)a.nblocks * kQThreads) {
+        int64_t n, k0;
+        item_nk<V>(a, it, small, n, k0);
+        Plane u[V], w[V];
+        load_planes_v<V>(a, n, k0, u, w);
 #pragma unroll
-            for (int t = 0; t < 3; ++t)
-                if (t < st)
-                    apply_stage_k(a.kind[p], pl[p], a.scales[(p * 4 + t) * 2], a.scales[(p * 4 + t) * 2 + 1]);
-            if (a.kind[p] == RPFQ_QK_SIGN) {
-                acc[4 * p + 0] += (double)fabsf(pl[p].r_re);
-                acc[4 * p + 1] += 1.0;
-                acc[4 * p + 2] += (double)fabsf(pl[p].r_im);
-                acc[4 * p + 3] += 1.0;
-            } else {
-                int c = axis_class(pl[p].r_re, pl[p].r_im);
-                if (c == 0 || c == 1) {
-                    acc[4 * p + 0] += (double)fabsf(pl[p].r_re);
+        for (int v = 0; v < V; ++v) {
+            Plane* pl[2] = {&u[v], &w[v]};
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                if (a.steps[p] <= st) continue;
+                Plane& q = *pl[p];
+#pragma unroll
+                for (int t = 0; t < 3; ++t)
+                    if (t < st) apply_stage_k(a.kind[p], q, sc[(p * 4 + t) * 2], sc[(p * 4 + t) * 2 + 1]);
+                if (a.kind[p] == RPFQ_QK_SIGN) {
+                    acc[4 * p + 0] += (double)fabsf(q.r_re);
                     acc[4 * p + 1] += 1.0;
-                } else if (c == 2 || c == 3) {
-                    acc[4 * p + 2] += (double)fabsf(pl[p].r_im);
+                    acc[4 * p + 2] += (double)fabsf(q.r_im);
                     acc[4 * p + 3] += 1.0;
+                } else {
+                    const int c = axis_class(q.r_re, q.r_im);
+                    if (c == 0 || c == 1) {
+                        acc[4 * p + 0] += (double)fabsf(q.r_re);
+                        acc[4 * p + 1] += 1.0;
+                    } else if (c == 2 || c == 3) {
+                        acc[4 * p + 2] += (double)fabsf(q.r_im);
+                        acc[4 * p + 3] += 1.0;
+                    }
                 }
             }
         }
@@ -217,40 +275,61 @@ __global__ void __launch_bounds__(kQThreads) quant_finalize_kernel(QuantArgs a) 
 // code byte per plane and stage).
 template <int V>
 __global__ void __launch_bounds__(kQThreads) quant_apply_kernel(QuantArgs a) {
-    const int64_t kv = a.K / V;
-    const int64_t total = a.N * kv;
+    const int64_t items = a.N * (a.K / V);
+    const bool small = items < (1LL << 31);
     const int64_t row = 2 * a.K;
     const int64_t plane_bytes = a.N * (a.K / 4);
-    for (int64_t e = (int64_t)blockIdx.x * kQThreads + threadIdx.x; e < total;
-         e += (int64_t)gridDim.x * kQThreads) {
-        int64_t n = e / kv, k0 = (e - n * kv) * V;
+    float sc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = a.scales[i];
+    for (int64_t it = (int64_t)blockIdx.x * kQThreads + threadIdx.x; it < items;
+         it += (int64_t)gridDim.x * kQThreads) {
+        int64_t n, k0;
+        item_nk<V>(a, it, small, n, k0);
+        Plane u[V], w[V];
+        load_planes_v<V>(a, n, k0, u, w);
         uint32_t cbyte[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float o11[V], o12[V], o21[V], o22[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const int64_t k = k0 + v;
-            Plane pl[2];
-            load_planes(a, n, k, pl[0], pl[1]);
+            Plane* pl[2] = {&u[v], &w[v]};
 #pragma unroll
             for (int p = 0; p < 2; ++p)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
                     if (t < a.steps[p]) {
-                        uint32_t c = apply_stage_k(a.kind[p], pl[p], a.scales[(p * 4 + t) * 2],
-                                                   a.scales[(p * 4 + t) * 2 + 1]);
+                        const uint32_t c = apply_stage_k(a.kind[p], *pl[p], sc[(p * 4 + t) * 2],
+                                                         sc[(p * 4 + t) * 2 + 1]);
                         cbyte[p * 4 + t] |= c << (2 * v);
                     }
-            float ur = pl[0].q_re, ui = pl[0].q_im, wr = pl[1].q_re, wi = pl[1].q_im;
+            float ur = u[v].q_re, ui = u[v].q_im, wr = w[v].q_re, wi = w[v].q_im;
             if (a.rot) {  // quant_i.py:433-434
-                float cu = a.rot[0], su = a.rot[1], cw = a.rot[2], sw = a.rot[3];
-                float r0 = ur * cu - ui * su, i0 = ui * cu + ur * su;
-                float r1 = wr * cw - wi * sw, i1 = wi * cw + wr * sw;
+                const float cu = a.rot[0], su = a.rot[1], cw = a.rot[2], sw = a.rot[3];
+                const float r0 = ur * cu - ui * su, i0 = ui * cu + ur * su;
+                const float r1 = wr * cw - wi * sw, i1 = wi * cw + wr * sw;
                 ur = r0; ui = i0; wr = r1; wi = i1;
             }
-            if (a.aq) {  // quant_i.py:534-544
-                a.aq[n * row + k] = wr + ur;
-                a.aq[n * row + a.K + k] = wi - ui;
-                a.aq[(a.N + n) * row + k] = wi + ui;
-                a.aq[(a.N + n) * row + a.K + k] = -wr + ur;
+            o11[v] = wr + ur;  // quant_i.py:534-544
+            o12[v] = wi - ui;
+            o21[v] = wi + ui;
+            o22[v] = -wr + ur;
+        }
+        if (a.aq) {
+            float* r0p = a.aq + n * row + k0;
+            float* r1p = a.aq + (a.N + n) * row + k0;
+            if constexpr (V == 4) {
+                *reinterpret_cast<float4*>(r0p) = make_float4(o11[0], o11[1], o11[2], o11[3]);
+                *reinterpret_cast<float4*>(r0p + a.K) = make_float4(o12[0], o12[1], o12[2], o12[3]);
+                *reinterpret_cast<float4*>(r1p) = make_float4(o21[0], o21[1], o21[2], o21[3]);
+                *reinterpret_cast<float4*>(r1p + a.K) = make_float4(o22[0], o22[1], o22[2], o22[3]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    r0p[v] = o11[v];
+                    r0p[a.K + v] = o12[v];
+                    r1p[v] = o21[v];
+                    r1p[a.K + v] = o22[v];
+                }
             }
         }
         if (V == 4 && a.codes) {
@@ -288,15 +367,20 @@ hipError_t launch_quantize_wide(const rpfq_quant_desc& d, const float* weight, c
     a.partial = static_cast<double*>(work);
     a.aq = aq;
     a.codes = codes;
-    a.nblocks = reduce_blocks(a.N * a.K);
+    // four columns per thread (16-B loads and stores) when the rows allow it
+    const bool v4 = a.K % 4 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(aq) % 16 == 0;
+    a.nblocks = reduce_blocks(a.N * (v4 ? a.K / 4 : a.K));
     const int max_steps = d.steps[0] > d.steps[1] ? d.steps[0] : d.steps[1];
     for (int st = 0; st < max_steps; ++st) {
         a.stage = st;
-        hipLaunchKernelGGL(quant_reduce_kernel, dim3(a.nblocks), dim3(kQThreads), 0, s, a);
+        if (v4)
+            hipLaunchKernelGGL(quant_reduce_kernel<4>, dim3(a.nblocks), dim3(kQThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL(quant_reduce_kernel<1>, dim3(a.nblocks), dim3(kQThreads), 0, s, a);
         hipLaunchKernelGGL(quant_finalize_kernel, dim3(1), dim3(kQThreads), 0, s, a);
     }
     if (aq || codes) {
-        const bool v4 = a.K % 4 == 0;
         const int64_t items = a.N * (v4 ? a.K / 4 : a.K);
         int64_t blocks = (items + kQThreads - 1) / kQThreads;
         if (blocks > 8 * kQuantMaxBlocks) blocks = 8 * kQuantMaxBlocks;

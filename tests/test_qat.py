@@ -127,6 +127,27 @@ def test_quantize_wide_ties_and_zeros(kind):
 
 
 @pytest.mark.gpu
+def test_quantize_wide_unaligned_weight():
+    """A weight that is not 16-byte aligned takes the one-column-per-thread
+    path: the same A_q and scales; code planes are refused."""
+    from quant_models import _native as N
+    from quant_models import ops
+
+    r = np.random.default_rng(9)
+    w = (r.standard_normal((2 * 96, 2 * 64)) * 0.02).astype(np.float32)
+    buf = torch.zeros(w.size + 1, dtype=torch.float32, device=DEV)
+    wd = buf[1:].view(w.shape)
+    wd.copy_(torch.from_numpy(w))
+    assert wd.data_ptr() % 16 != 0
+    a_q, scales, _ = ops.quantize_wide(wd, "axis", 2, "axis", 2)
+    ref, st_u, _ = O.quantized_weight(w, "axis", 2, "axis", 2)
+    assert np.array_equal(a_q.cpu().numpy(), ref)
+    assert scales.cpu().numpy()[0, 1, 0] == st_u[1][1]
+    with pytest.raises(N.RPFQError, match="aligned"):
+        ops.quantize_wide(wd, "axis", 2, "axis", 2, want_codes=True)
+
+
+@pytest.mark.gpu
 def test_quantize_wide_argument_errors():
     from quant_models import _native as N
     from quant_models import ops
