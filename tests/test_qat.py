@@ -231,3 +231,63 @@ def test_hip_training_step_matches_torch_formulation(method, act, rot):
             a = getattr(gpu, q).rotation_angle.grad.cpu()
             b = getattr(cpu, q).rotation_angle.grad
             assert torch.allclose(a, b, rtol=1e-3, atol=1e-4 * float(b.abs().max()))
+
+
+# ---------------------------------------------------------------------------
+# torch.ops.rpfq.* (the reference's operator contract, kernel.py:599-605)
+# ---------------------------------------------------------------------------
+def test_rpfq_ops_registered_with_fake_shapes():
+    import quant_models  # noqa: F401  (registers the operators)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x, w, b = torch.empty(3, 5, 96), torch.empty(64, 96), torch.empty(64)
+        assert torch.ops.rpfq.qat_linear(x, w, b, "complex_phase_v2", "complex_phase_v2", 4).shape == (3, 5, 64)
+        blob = torch.empty(4096, dtype=torch.uint8)
+        assert torch.ops.rpfq.wide_linear(x, blob, 32, 48, 0, 2, 0, None, b).shape == (3, 5, 64)
+        assert torch.ops.rpfq.act_quant(x, 4).shape == (3, 5, 96)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("method,act", [("complex_phase_v2", 4), ("complex_phase_new_v2", 0), ("complex_phase_v3", 4)])
+def test_rpfq_qat_linear_op_matches_layer(method, act):
+    """torch.ops.rpfq.qat_linear == the HIP training forward of
+    QATLinearComplexPhase (rotation off), and its registered backward gives
+    the layer's autograd gradients."""
+    import quant_models  # noqa: F401
+    from quant_models.quant_i import QATLinearComplexPhase
+
+    torch.manual_seed(4)
+    layer = QATLinearComplexPhase(quant_method_u=method, quant_method_w=method, enable_act_quant=act > 0,
+                                  act_num_bits=act or 4, enable_rotation=False, in_features=192,
+                                  out_features=128).to(DEV).train()
+    x = torch.randn(7, 192, device=DEV)
+    gy = torch.randn(7, 128, device=DEV)
+    x1 = x.clone().requires_grad_(True)
+    y1 = layer(x1)
+    (y1 * gy).sum().backward()
+    w = layer.weight.detach().clone().requires_grad_(True)
+    b = layer.bias.detach().clone().requires_grad_(True)
+    x2 = x.clone().requires_grad_(True)
+    y2 = torch.ops.rpfq.qat_linear(x2, w, b, method, method, act)
+    assert torch.equal(y2, y1)
+    (y2 * gy).sum().backward()
+    for a, ref in ((x2.grad, x1.grad), (w.grad, layer.weight.grad), (b.grad, layer.bias.grad)):
+        assert torch.allclose(a, ref, rtol=1e-5, atol=1e-6 * float(ref.abs().max()))
+
+
+@pytest.mark.gpu
+def test_rpfq_wide_linear_op_matches_packed(golden):
+    import quant_models  # noqa: F401
+    from quant_models import ops
+    from quant_models import packing as P
+
+    lc = P.quantize_layer(torch.from_numpy(golden["w_weight"]), "complex_phase_v2", "complex_phase_v2")
+    pw = ops.pack_layer([p.to(DEV) for p in lc.planes], [s.to(DEV) for s in lc.scale_re],
+                        [s.to(DEV) for s in lc.scale_im], lc.n_complex, lc.k_complex, lc.codebook, lc.stages)
+    x = torch.randn(9, 96, device=DEV).half()
+    bias = torch.randn(64, device=DEV)
+    y_op = torch.ops.rpfq.wide_linear(x, pw.blob, pw.n_complex, pw.k_complex, pw.codebook, pw.stages, pw.block,
+                                      None, bias)
+    assert torch.equal(y_op, pw.linear(x, bias))
+    assert torch.equal(torch.ops.rpfq.act_quant(x.float(), 4), ops.act_quant(x.float(), 4))
