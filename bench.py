@@ -404,8 +404,8 @@ def main() -> int:
                           "launches": args.steps}))
         return 0
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is a design "
-              "note in DESIGN.md, not a benchmark of this build", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is part of "
+              "this build's design, not of what it benchmarks", file=sys.stderr)
         return 2
 
     import torch
