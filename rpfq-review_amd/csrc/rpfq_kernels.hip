@@ -523,6 +523,7 @@ struct WideArgs {
     void* y;
     int tiles_m, tiles_n;
     int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
+    int wg_epi;     // DMA epilogue: workgroup-wide full-line stores (else per wave)
 };
 
 // LDS activation row: 32 complex columns as (re, im) fp16 pairs = 128 B,
@@ -1269,31 +1270,41 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
       }
     } else {
     // Half a tile at a time: each wave writes its 32 output rows to LDS
-    // ([row][re 32 | im 32] fp16, wave regions kEpiWave apart); after a
-    // workgroup barrier each wave stores EPI / 4 token rows across all four
-    // waves' columns.  A token row of the tile is 128 re + 128 im outputs,
-    // i.e. whole 128-B lines of y, so no line is written in halves at two
-    // different times.  Lane l: row 2 j + (l >> 5), 16-B chunk c = l & 31
-    // (c < 16: re outputs 8 c.., else im outputs 8 (c - 16)..); the 64-B pad
-    // of the wave regions keeps the 8 lanes of a read on 32 distinct banks.
+    // ([row][re 32 | im 32] fp16, wave regions kEpiWave apart), then stores
+    // them as 16-B chunks (8 per lane and half) in one of two patterns:
+    //  * workgroup-wide (a.wg_epi, whole tiles of 128 output columns and a
+    //    k-loop long enough to hide two workgroup barriers per half): after a
+    //    barrier each wave stores EPI / 4 token rows across all four waves'
+    //    columns, so every store covers whole 128-B lines of y (a row of the
+    //    tile is 128 re + 128 im outputs).  Lane l: row 2 j + (l >> 5), chunk
+    //    c = l & 31 (c < 16: re outputs 8 c.., else im outputs 8 (c - 16)..);
+    //  * per wave: each wave stores its own rows, 8 lanes per row (chunks
+    //    0-3 re, 4-7 im), half lines of y, with no workgroup barrier (short
+    //    k-loops, where the barriers would cost more than the lines save).
+    // The 64-B pad of the wave regions keeps the 8 lanes of a workgroup-wide
+    // read on 32 distinct banks.
     constexpr int kEpiWave = EPI * kTRow + 64;
     char* tt = smem + wave * kEpiWave;
-    const int c = lane & 31;
-    const int64_t ncol = (int64_t)ntl * 128 + 8 * (c & 15);  // first output column (complex row) of the chunk
-    const int64_t gcol = (c < 16 ? 0 : a.N) + ncol;
-    const char* tsrc = smem + ((c & 15) >> 2) * kEpiWave + (c < 16 ? 0 : 64) + (c & 3) * 16;
+    const bool wg = a.wg_epi != 0;
+    const int c = wg ? (lane & 31) : (lane & 7);
+    const bool im_chunk = wg ? c >= 16 : c >= 4;
+    const int64_t ncol = wg ? (int64_t)ntl * 128 + 8 * (c & 15) : (int64_t)ntw * 32 + 8 * (c & 3);
+    const int64_t gcol = (im_chunk ? a.N : 0) + ncol;
+    const char* tsrc = wg ? smem + ((c & 15) >> 2) * kEpiWave + (im_chunk ? 64 : 0) + (c & 3) * 16 : tt + c * 16;
+    const int row0 = wg ? (EPI / 4) * wave + (lane >> 5) : (lane >> 3);
+    const int rstep = wg ? 2 : 8;
     const bool chunk_vec = a.vec_store && ncol + 8 <= a.N;
     // residual chunks of this lane's store rows are requested before the
     // half tile goes through LDS, so their latency overlaps the transpose
     const bool res_vec = a.res && chunk_vec;
-    constexpr int RPS = EPI / 8;  // store instructions per wave and half (2 rows each)
+    constexpr int RPS = EPI / 8;  // store instructions per wave and half
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         uint4 rres[RPS];
         if (res_vec) {
 #pragma unroll
             for (int j = 0; j < RPS; ++j) {
-                const int64_t m = m0 + h * EPI + (EPI / 4) * wave + 2 * j + (lane >> 5);
+                const int64_t m = m0 + h * EPI + row0 + rstep * j;
                 rres[j] = m >= m_own ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) +
                                                                         m * ldy + gcol)
                                      : make_uint4(0, 0, 0, 0);
@@ -1325,13 +1336,13 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 *reinterpret_cast<uint2*>(trow + 64 + (8 * q + 4 * g) * 2) = pi;
             }
         }
-        // every wave's rows of this half are in LDS
+        // the rows of this half are in LDS (every wave's, or this wave's)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
+        if (wg) __builtin_amdgcn_s_barrier(); else __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int j = 0; j < RPS; ++j) {
-            const int row = (EPI / 4) * wave + 2 * j + (lane >> 5);
+            const int row = row0 + rstep * j;
             const int64_t m = m0 + h * EPI + row;
             if (m < m_own || ncol >= a.N) continue;
             uint4 v = *reinterpret_cast<const uint4*>(tsrc + row * kTRow);
@@ -1356,7 +1367,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         }
         // all reads of this half done before the next half overwrites the rows
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
+        if (wg) __builtin_amdgcn_s_barrier(); else __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
     }
     }
@@ -2141,6 +2152,9 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     a.res = res;
     a.y = y;
     a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);  // also covers 4-wide stores
+    // whole 128-column tiles and >= 8 k-steps (ViT-B/L, not DeiT-Ti's K' = 96 / N' = 96 layers):
+    // full-line stores pay for the two workgroup barriers per half tile
+    a.wg_epi = (g.N % 128 == 0) && (g.KS >= 8);
     switch (d.codebook) {
         case RPFQ_CB_SIGN: return wide_x<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
         case RPFQ_CB_PSK16: return wide_x<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
