@@ -175,3 +175,42 @@ def test_table_codebook_desc_rules():
     p = ctypes.c_void_p(256)
     arr = (ctypes.c_void_p * 4)(p, p, p, p)
     assert L.rpfq_wide_pack(ctypes.byref(d), arr, 4, arr, arr, p, 1 << 20, None) == 4  # two planes (u, w)
+
+
+def test_header_compiles_as_c99_and_links(tmp_path):
+    """A native C caller (the Android runtime's role): include/rpfq.h is plain
+    C99, the library links, and the validation paths answer from C."""
+    import shutil
+    import subprocess
+
+    L, N = lib()
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "caller.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "rpfq.h"
+int main(void) {
+    rpfq_wide_desc d = {0};
+    d.n_complex = 64; d.k_complex = 64; d.block = 0; d.codebook = RPFQ_CB_AXIS; d.stages = 2; d.rotate = 0;
+    if (rpfq_abi_version() != RPFQ_ABI_VERSION) return 1;
+    if (rpfq_wide_packed_bytes(&d) == 0) return 2;
+    d.k_complex = 12;                                  /* not a multiple of 8 */
+    if (rpfq_wide_packed_bytes(&d) != 0) return 3;
+    if (rpfq_wide_linear(&d, 0, 0, 0, RPFQ_F16, 4, 0, 0, RPFQ_F16, 0, 0) != RPFQ_ERR_ALIGN) return 4;
+    if (rpfq_last_error()[0] == 0) return 5;
+    rpfq_quant_desc q = {0};
+    q.n_complex = 8; q.k_complex = 8; q.kind[0] = q.kind[1] = RPFQ_QK_AXIS; q.steps[0] = 5; q.steps[1] = 1;
+    if (rpfq_quantize_wide(&q, 0, 0, 0, 0, 0, 0, 0, 0) == RPFQ_OK) return 6;
+    printf("ok\n");
+    return 0;
+}
+''')
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(N.library_path())
+    cmd = [cc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe),
+           "-L", libdir, "-lrpfq", f"-Wl,-rpath,{libdir}", "-Wl,-rpath,/opt/rocm/lib", "-L", "/opt/rocm/lib"]
+    subprocess.run(cmd, check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stdout, out.stderr)
