@@ -48,14 +48,20 @@ extern "C" {
 #define RPFQ_BF16 2
 
 /* rpfq_wide_linear flags.  Default (0): the kernel is chosen from the shape
- * (M <= 16 streams the packed codes, one 32-row tile per wave, against all M
- * rows; fp16 x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA;
- * other cases stage them through registers with a 32/64/128-row tile).
+ * (M <= 16, and small-M launches where a cost model predicts it faster --
+ * e.g. a ViT-B layer at one image -- stream the packed codes, 32-row tiles
+ * against 16-row chunks of x; fp16 x with K' % 32 == 0 and M >= 128 stages
+ * activations by LDS DMA; other cases stage them through registers with a
+ * 32/64/128-row tile).
  * RPFQ_FLAG_TILE_M128 forces the register-staged 128-row kernel;
- * RPFQ_FLAG_NO_STREAM keeps M <= 16 on the tiled kernels.  Every kernel
- * feeds the MFMA the same fp16 coefficients. */
+ * RPFQ_FLAG_NO_STREAM keeps every M on the tiled kernels;
+ * RPFQ_FLAG_STREAM forces the streaming kernel for any M (one workgroup per
+ * 16-row chunk of x and 32-row tile of the codes; at most 2^24 of them,
+ * else RPFQ_ERR_SHAPE; not combinable with the other two, RPFQ_ERR_VALUE).
+ * Every kernel feeds the MFMA the same fp16 coefficients. */
 #define RPFQ_FLAG_TILE_M128 1
 #define RPFQ_FLAG_NO_STREAM 2
+#define RPFQ_FLAG_STREAM 4
 
 /* codebooks of the packed planes */
 #define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages

@@ -142,6 +142,19 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
                       "rpfq_wide_pack");
 }
 
+// Kernel-choice flags: known bits, no contradictory pair, and a streaming
+// launch (one workgroup per 16-row chunk and 32-row tile) within the grid.
+static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M) {
+    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM))
+        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
+    if ((flags & RPFQ_FLAG_STREAM) && (flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)))
+        return fail(RPFQ_ERR_VALUE, "flags=%d: RPFQ_FLAG_STREAM excludes the tiled-kernel flags", flags);
+    if ((flags & RPFQ_FLAG_STREAM) && (int64_t)g.NT * ((M + 15) / 16) > ((int64_t)1 << 24))
+        return fail(RPFQ_ERR_SHAPE, "M=%lld: RPFQ_FLAG_STREAM allows at most 2^24 (chunk, tile) workgroups",
+                    (long long)M);
+    return 0;
+}
+
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
                      int x_dtype, int64_t M, const float* bias, void* y, int y_dtype, int flags, void* stream) {
     int rc = check_desc(desc);
@@ -150,9 +163,8 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
-    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM))
-        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if ((rc = check_flags(flags, g, M))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16))
@@ -172,9 +184,8 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
-    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM))
-        return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if ((rc = check_flags(flags, g, M))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(residual, 16))

@@ -1381,11 +1381,12 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 
 
 // ---------------------------------------------------------------------------
-// widely-linear layer for M <= 16 rows: weight streaming
+// widely-linear layer for small M: weight streaming
 // ---------------------------------------------------------------------------
 // The packed codes are the only large operand, so each wave streams one
-// 32-row tile of them (KS contiguous 1-KB blocks) and contracts it with all
-// M activation rows on v_mfma_f32_16x16x32_f16: the decoded weights are the
+// 32-row tile of them (KS contiguous 1-KB blocks) and contracts it with a
+// chunk of up to 16 activation rows on v_mfma_f32_16x16x32_f16 (workgroup
+// = chunk x tiles + tile; M <= 16 is one chunk): the decoded weights are the
 // A operand (16 output rows x 16 complex columns as (re, im) fp16 pairs),
 // the activations the B operand (its 16 columns are the x rows).
 //   * codes: lane (r16 = lane & 15, q = lane >> 4) loads 8 B of rows r16 and
@@ -1491,8 +1492,13 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
     const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, q = lane >> 4;
     const int R = lane & 31, g = lane >> 5;
-    const int tile = blockIdx.x;
-    const int KS = a.KS, K = a.K, M = (int)a.M;
+    // workgroup -> (16-row chunk of x, 32-row tile of the codes), chunk-major
+    const int mc = (int)(blockIdx.x / (unsigned)a.NT);
+    const int tile = (int)blockIdx.x - mc * a.NT;
+    const int KS = a.KS, K = a.K;
+    const int64_t m0 = 16 * (int64_t)mc;                  // first x row of the chunk
+    const int M = (int)min((int64_t)16, a.M - m0);        // rows of the chunk
+    const void* xc = reinterpret_cast<const char*>(a.x) + m0 * 2 * K * (XDT == RPFQ_F32 ? 4 : 2);
     const int chunk = (KS + NW - 1) / NW;
     const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
 
@@ -1516,12 +1522,12 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
             if (KT) {
                 const int col = 32 * kc + xcol + 8 * t;
                 const int off = xoff - xcol + (col < K ? col : 0);  // K' tail: in bounds, zeroed at use
-                st.xr[t] = load4_raw<XDT>(a.x, off);
-                st.xi[t] = load4_raw<XDT>(a.x, off + K);
+                st.xr[t] = load4_raw<XDT>(xc, off);
+                st.xi[t] = load4_raw<XDT>(xc, off + K);
             } else {
                 const int64_t xb = 32 * (int64_t)kc + 8 * t;
-                st.xr[t] = load4_raw<XDT>(a.x, xb + xoff);
-                st.xi[t] = load4_raw<XDT>(a.x, xb + K + xoff);
+                st.xr[t] = load4_raw<XDT>(xc, xb + xoff);
+                st.xi[t] = load4_raw<XDT>(xc, xb + K + xoff);
             }
         }
     };
@@ -1640,7 +1646,7 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
             vr[v] = acc_re[h][v] + ((a.bias && ok) ? a.bias[n] : 0.0f);
             vi[v] = acc_im[h][v] + ((a.bias && ok) ? a.bias[a.N + n] : 0.0f);
         }
-        const int64_t base = (int64_t)r16 * ldy + n0;
+        const int64_t base = (m0 + r16) * ldy + n0;
         if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
             uint2 hr = make_uint2(cvt_pk(vr[0], vr[1]), cvt_pk(vr[2], vr[3]));
             uint2 hi = make_uint2(cvt_pk(vi[0], vi[1]), cvt_pk(vi[2], vi[3]));
@@ -2078,15 +2084,18 @@ static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Workgroups of the streaming kernel: one per (16-row chunk, 32-row tile).
+static int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
+
 template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
 static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, SPLIT>), dim3(a.NT), dim3(SPLIT ? 256 : 64),
-                       SPLIT ? kSkLds : kSkLut, s, a);
+    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, SPLIT>), dim3((unsigned)sk_groups(a)),
+                       dim3(SPLIT ? 256 : 64), SPLIT ? kSkLds : kSkLut, s, a);
     return hipGetLastError();
 }
 
-// Split K when the layer has too few tiles to give every SIMD a few waves
-// (a single layer at batch 1); a long stream of tiles runs one wave each.
+// Split K when the launch has too few workgroups to give every SIMD a few
+// waves (a single layer at batch 1); a long stream of tiles runs one wave each.
 #ifndef RPFQ_SK_SPLIT_TILES
 #define RPFQ_SK_SPLIT_TILES 4096
 #endif
@@ -2095,9 +2104,30 @@ static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
     const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
     if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, false>(a, s)
                       : wide_sk_go<XDT, YDT, CB, true, false, false>(a, s);
-    if (a.NT < RPFQ_SK_SPLIT_TILES)
+    if (sk_groups(a) < RPFQ_SK_SPLIT_TILES)
         return kt ? wide_sk_go<XDT, YDT, CB, false, true, true>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, true>(a, s);
     return kt ? wide_sk_go<XDT, YDT, CB, false, true, false>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, false>(a, s);
+}
+
+// Kernel choice for a small M.  A tiled kernel gives each workgroup one
+// 128-row x 128-column output tile through all of K, so while the launch is
+// at most one tile deep it costs about one tile's latency, ~5 + KS us on
+// MI355X whatever M and N'.  The streaming kernel spreads its (16-row chunk,
+// 32-row tile) groups over every SIMD: with split K ~4.5 us + groups x
+// (7.7 + 0.49 KS) ns; with per-(row, block) scales (one wave per group
+// through all of K) ~(2 + 0.55 KS) us while the groups fit ~900 at once,
+// proportionally longer past that.  The fits are from fp16 ViT-B/L and
+// DeiT-Ti layer shapes at M = 24 .. 1576; streaming is taken where it is
+// predicted 10% faster, and always for M <= 16.
+static bool stream_pays(const WideArgs& a) {
+    if (a.M <= 16) return true;
+    const int64_t tiles = ((a.M + 127) / 128) * ((a.NT + 3) / 4);
+    if (tiles > 2 * (int64_t)device_cus()) return false;  // more than one round of the tiled grid
+    const double groups = (double)sk_groups(a);
+    const double t_stream = a.nblk > 1 ? (2.0 + 0.55 * a.KS) * (groups > 900.0 ? groups / 900.0 : 1.0)
+                                       : 4.5 + groups * (0.0077 + 0.00049 * a.KS);
+    const double t_tiled = 5.0 + a.KS;
+    return t_stream < 0.9 * t_tiled;
 }
 
 template <int XDT, int YDT, int CB>
@@ -2105,7 +2135,7 @@ static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
 #ifndef RPFQ_DMA_MIN_M
 #define RPFQ_DMA_MIN_M 128
 #endif
-    if (a.M <= 16 && !(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)))
+    if ((flags & RPFQ_FLAG_STREAM) || (!(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)) && stream_pays(a)))
         return wide_sk<XDT, YDT, CB>(a, s);
     flags &= ~RPFQ_FLAG_NO_STREAM;
     if (XDT == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M) return wide_dma_go<128, YDT, CB>(a, s);

@@ -28,7 +28,8 @@ F32, F16, BF16 = 0, 1, 2
 CB_AXIS, CB_SIGN, CB_PSK16, CB_TABLE = 0, 1, 2, 3
 QK_AXIS, QK_SIGN = 0, 1  # weight quantizer kinds of rpfq_quantize_wide
 FLAG_TILE_M128 = 1  # force the register-staged 128-row kernel
-FLAG_NO_STREAM = 2  # keep M <= 16 on the tiled kernels (no weight-streaming kernel)
+FLAG_NO_STREAM = 2  # keep every M on the tiled kernels (no weight-streaming kernel)
+FLAG_STREAM = 4  # force the weight-streaming kernel for any M (16-row chunks)
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 

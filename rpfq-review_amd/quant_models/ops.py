@@ -173,8 +173,8 @@ class PackedWide:
                out_dtype: torch.dtype | None = None, flags: int = 0,
                residual: torch.Tensor | None = None) -> torch.Tensor:
         """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
-        flags: 0 (kernel chosen from the shape), _native.FLAG_TILE_M128 or
-        _native.FLAG_NO_STREAM.  residual ([..., 2N'] of out_dtype): y =
+        flags: 0 (kernel chosen from the shape), _native.FLAG_TILE_M128,
+        _native.FLAG_NO_STREAM or _native.FLAG_STREAM.  residual ([..., 2N'] of out_dtype): y =
         residual + layer(x), fused into the kernel's store and rounded as the
         unfused add would round it (rpfq_wide_linear_residual)."""
         N.require_device(x, bias, residual)

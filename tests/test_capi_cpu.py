@@ -73,8 +73,12 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4, None) == 6  # unknown flag bit
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 8, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 8, None) == 6  # unknown flag bit
+    # RPFQ_FLAG_STREAM with a tiled-kernel flag; a streaming grid past 2^24 workgroups
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 1, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 2, None) == 6
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 1 << 30, None, p, 1, 4, None) == 2
+    assert "2^24" in L.rpfq_last_error().decode()
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 16, p, 1, 4, None, p, 1, 0, None) == 2
     assert L.rpfq_wide_linear(ctypes.byref(d), ctypes.c_void_p(258), 1 << 20, p, 1, 4, None, p, 1, 0, None) == 3
     assert "aligned" in L.rpfq_last_error().decode()

@@ -251,16 +251,19 @@ def test_wide_decode_bit_exact(case):
     assert np.array_equal(a16, O.wide_weight(build_packed.last_oplanes, case[2], build_packed.last_rotation, fp16=True))
 
 
+@pytest.mark.parametrize("flags", [0, 2], ids=["auto", "tiled"])
 @pytest.mark.parametrize("m", [1, 5, 31, 64, 65, 128, 129, 300])
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
                                              for c in CASES])
-def test_wide_linear(case, m):
+def test_wide_linear(case, m, flags):
+    """flags 0: the kernel the shape selects (streaming for the small
+    launches); 2 (RPFQ_FLAG_NO_STREAM): the tiled kernels at every M."""
     r = rng(200 + m)
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
     k_in = 2 * case[1]
     x = torch.from_numpy(r.standard_normal((m, k_in)).astype(np.float32)).to(torch.float16)
     bias = r.standard_normal(2 * case[0]).astype(np.float32)
-    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32, flags=flags).cpu().numpy()
     xf = x.float().numpy().astype(np.float64)
     check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
 
@@ -312,14 +315,14 @@ def test_wide_linear_matches_reference_android_runtime():
     assert np.all(np.abs(y - y_ref) <= (2 * u + u * u) * (ax @ mag.T) + 1e-5 * scale + 1e-4)
 
 
-@pytest.mark.parametrize("flags", [0, 1])
+@pytest.mark.parametrize("flags", [2, 1])
 @pytest.mark.parametrize("m", [33, 128, 300, 513])
 @pytest.mark.parametrize("case", [CASES[1], CASES[2], CASES[4], CASES[7], CASES[8]],
                          ids=["1536x384", "50x48", "130x512-b256", "rot", "table"])
 def test_wide_linear_kernels_agree(case, m, flags):
-    """The LDS-DMA kernel (flags 0, fp16 x, K' % 32 == 0, M >= 128) and the
-    register-staged kernel (RPFQ_FLAG_TILE_M128) meet the same bound, with
-    fp16 outputs through the LDS-transposed epilogue."""
+    """The LDS-DMA kernel (RPFQ_FLAG_NO_STREAM, fp16 x, K' % 32 == 0,
+    M >= 128) and the register-staged kernel (RPFQ_FLAG_TILE_M128) meet the
+    same bound, with fp16 outputs through the LDS-transposed epilogue."""
     r = rng(500 + m)
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
     x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
@@ -335,7 +338,7 @@ def test_wide_linear_kernels_consistent():
     r = rng(600)
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, CASES[1])
     x = torch.from_numpy(r.standard_normal((1000, 768)).astype(np.float32)).to(torch.float16).to(DEV)
-    y0 = pw.linear(x, None, out_dtype=torch.float32, flags=0).cpu().numpy().astype(np.float64)
+    y0 = pw.linear(x, None, out_dtype=torch.float32, flags=2).cpu().numpy().astype(np.float64)
     y1 = pw.linear(x, None, out_dtype=torch.float32, flags=1).cpu().numpy().astype(np.float64)
     scale = np.abs(x.float().cpu().numpy().astype(np.float64)) @ np.abs(
         O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)).T
@@ -389,6 +392,24 @@ def test_wide_linear_streaming(case, m):
     check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
+@pytest.mark.parametrize("m", [17, 45, 197])
+@pytest.mark.parametrize("case", SKINNY_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
+                                                    for c in SKINNY_CASES])
+def test_wide_linear_stream_chunks(case, m):
+    """RPFQ_FLAG_STREAM past 16 rows: one workgroup per (16-row chunk, tile),
+    ragged last chunk, against the oracle; float32 and fp16 outputs."""
+    ops, N = qm()
+    r = rng(750 + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    xf = x.float().numpy().astype(np.float64)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32, flags=N.FLAG_STREAM).cpu().numpy()
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
+    y16 = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16, flags=N.FLAG_STREAM).float().cpu().numpy()
+    check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+
+
 @pytest.mark.parametrize("m", [3, 12])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
                                      (torch.float16, torch.bfloat16), (torch.float32, torch.float16)])
@@ -432,8 +453,9 @@ def test_wide_linear_streaming_persistent(m, n_c, k_c):
 # fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
 # followed by the add in y's dtype, on every kernel path
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("m,flags", [(3, 0), (16, 0), (33, 0), (130, 0), (300, 1), (129, 2)],
-                         ids=["stream3", "stream16", "reg33", "dma130", "reg128-300", "nostream129"])
+@pytest.mark.parametrize("m,flags", [(3, 0), (16, 0), (33, 2), (130, 2), (300, 1), (129, 2), (197, 4), (197, 0)],
+                         ids=["stream3", "stream16", "reg33", "dma130", "reg128-300", "nostream129", "stream197",
+                              "auto197"])
 @pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float32])
 def test_wide_linear_residual_bit_exact(m, flags, ydt):
     r = rng(1000 + m)
@@ -449,25 +471,26 @@ def test_wide_linear_residual_bit_exact(m, flags, ydt):
 
 def test_wide_linear_residual_in_place():
     """residual == y through the C ABI: every element is read before it is
-    written by the same thread, and by one workgroup only -- also the rows
-    of the last m-tile that the DMA kernel shifts back over the previous
-    one (M % 128 != 0), over several rounds of the persistent grid
-    (M = 40,037: 3,756 tiles)."""
+    written by the same thread, and by one workgroup only -- on the
+    streaming kernel (M = 4, 200 by default) and on the DMA kernel, also the
+    rows of the last m-tile that it shifts back over the previous one
+    (M % 128 != 0), over several rounds of the persistent grid (M = 40,037:
+    3,756 tiles)."""
     ops, N = qm()
     import ctypes
     r = rng(1100)
     pw, *_ = build_packed(r, CASES[1])
     lib = N.load()
-    for m in (4, 200, 40037):
+    for m, flags in ((4, 0), (200, 0), (200, N.FLAG_NO_STREAM), (40037, 0)):
         x = torch.from_numpy(r.standard_normal((m, 768)).astype(np.float32)).to(torch.float16).to(DEV)
         res = torch.from_numpy(r.standard_normal((m, 3072)).astype(np.float32)).to(torch.float16).to(DEV)
-        want = res + pw.linear(x, None, out_dtype=torch.float16)
+        want = res + pw.linear(x, None, out_dtype=torch.float16, flags=flags)
         y = res.clone()
         N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
             ctypes.byref(pw.desc), pw.blob.data_ptr(), pw.blob.numel(), x.data_ptr(), N.F16, m, None,
-            y.data_ptr(), y.data_ptr(), N.F16, 0, N.stream_of(x)))
+            y.data_ptr(), y.data_ptr(), N.F16, flags, N.stream_of(x)))
         torch.cuda.synchronize()
-        assert torch.equal(y, want)
+        assert torch.equal(y, want), (m, flags)
 
 
 # ---------------------------------------------------------------------------
