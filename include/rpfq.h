@@ -62,6 +62,12 @@ extern "C" {
 #define RPFQ_FLAG_TILE_M128 1
 #define RPFQ_FLAG_NO_STREAM 2
 #define RPFQ_FLAG_STREAM 4
+/* RPFQ_FLAG_GELU (rpfq_wide_linear only; the residual entry point rejects
+ * it, RPFQ_ERR_VALUE): y = gelu(layer output), exact erf GELU applied in the
+ * store to the output rounded to y's dtype, computed in float32 and rounded
+ * again -- equal to torch.nn.functional.gelu (approximate='none') of the
+ * unfused output, as the ViT MLP applies it after fc1 (timm Mlp, nn.GELU). */
+#define RPFQ_FLAG_GELU 8
 
 /* codebooks of the packed planes */
 #define RPFQ_CB_AXIS 0   /* 2-bit {-1,+1,-i,+i} axis codes, residual stages
@@ -159,11 +165,28 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  * reference does (stage sums, de-rotation) and rounded to fp16; each fused
  * coefficient (A11 = Wre + Ure, A12 = Wim - Uim, A21 = Wim + Uim,
  * A22 = -Wre + Ure) is one correctly rounded fp16 add of those; the MFMA
- * accumulates in float32.  flags: 0 or RPFQ_FLAG_TILE_M128.
+ * accumulates in float32.  flags: the RPFQ_FLAG_* bits above.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                      const void* x, int x_dtype, int64_t M, const float* bias,
                      void* y, int y_dtype, int flags, void* stream);
+
+/* kernels of rpfq_wide_linear (rpfq_wide_linear_kernel) */
+#define RPFQ_KERNEL_STREAM 0  /* weight streaming, 16-row chunks of x */
+#define RPFQ_KERNEL_DMA 1     /* 128-row tiles, activations staged by LDS DMA */
+#define RPFQ_KERNEL_TILED 2   /* 32/64/128-row tiles staged through registers */
+
+/*
+ * *kernel := the RPFQ_KERNEL_* that rpfq_wide_linear runs for this layer, M,
+ * dtypes and flags (no GPU work; same validation as rpfq_wide_linear minus
+ * the buffers).  For callers choosing whether to fuse an epilogue op: the
+ * fused GELU pays on the streaming kernel, while on the DMA kernel its
+ * float32 erf in the per-tile epilogue costs about what the separate
+ * (memory-bound) GELU pass does.  No counterpart in the reference: the
+ * kernel choice is this library's.
+ */
+int rpfq_wide_linear_kernel(const rpfq_wide_desc* desc, int64_t M, int x_dtype, int y_dtype, int flags,
+                            int* kernel);
 
 /*
  * rpfq_wide_linear with the block's residual add fused into the store:

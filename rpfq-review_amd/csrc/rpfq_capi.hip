@@ -142,11 +142,14 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
                       "rpfq_wide_pack");
 }
 
-// Kernel-choice flags: known bits, no contradictory pair, and a streaming
-// launch (one workgroup per 16-row chunk and 32-row tile) within the grid.
-static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M) {
-    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM))
+// Flags: known bits, no contradictory pair, GELU only without a residual,
+// and a streaming launch (one workgroup per 16-row chunk and 32-row tile)
+// within the grid.
+static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M, bool residual) {
+    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM | RPFQ_FLAG_GELU))
         return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
+    if (residual && (flags & RPFQ_FLAG_GELU))
+        return fail(RPFQ_ERR_VALUE, "RPFQ_FLAG_GELU is not defined with a residual");
     if ((flags & RPFQ_FLAG_STREAM) && (flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)))
         return fail(RPFQ_ERR_VALUE, "flags=%d: RPFQ_FLAG_STREAM excludes the tiled-kernel flags", flags);
     if ((flags & RPFQ_FLAG_STREAM) && (int64_t)g.NT * ((M + 15) / 16) > ((int64_t)1 << 24))
@@ -164,7 +167,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M))) return rc;
+    if ((rc = check_flags(flags, g, M, false))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16))
@@ -173,6 +176,21 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, nullptr, y, y_dtype, flags,
                                                reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear");
+}
+
+int rpfq_wide_linear_kernel(const rpfq_wide_desc* desc, int64_t M, int x_dtype, int y_dtype, int flags,
+                            int* kernel) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!kernel) return fail(RPFQ_ERR_NULL, "kernel must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if ((rc = check_flags(flags, g, M, false))) return rc;
+    if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    *kernel = rpfq::wide_linear_kernel_choice(g, x_dtype, M, y_dtype, flags);
+    return RPFQ_OK;
 }
 
 int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
@@ -185,7 +203,7 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M))) return rc;
+    if ((rc = check_flags(flags, g, M, true))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(residual, 16))

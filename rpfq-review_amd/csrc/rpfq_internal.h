@@ -74,6 +74,7 @@ hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const ui
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               const void* x, int xdt, int64_t M, const float* bias, const void* res,
                               void* y, int ydt, int flags, hipStream_t s);
+int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags);  // RPFQ_KERNEL_*
 hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
                              const float* beta, float eps, int bits, void* y, int ydt, hipStream_t s);
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt,

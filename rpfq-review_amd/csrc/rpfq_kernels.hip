@@ -185,6 +185,60 @@ __device__ __forceinline__ uint2 add_res4(uint2 v, const void* res, int64_t off)
     return make_uint2(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16));
 }
 
+// Fused activation of the stored output (WideArgs::act = 1): exact GELU
+// (approximate = 'none') of the value already rounded to y's dtype, computed
+// in float32 by the formula of torch's GELU kernel for 16-bit and float32
+// tensors, x * 0.5 * (1 + erf(x * sqrt(1/2))), and rounded to y's dtype by
+// the store.  The empty asm keeps that float32 rounding: without it the
+// backend may fold the last multiply and the fp16 conversion into one
+// v_fma_mixlo_f16 (a single rounding), which changes the result where the
+// exact value lies near an fp16 rounding tie, and differently per kernel.
+__device__ __forceinline__ float gelu_f(float x) {
+    float g = x * 0.5f * (1.0f + erff(x * 0.707106781186547524f));
+    asm volatile("" : "+v"(g));
+    return g;
+}
+
+template <int YDT>
+__device__ __forceinline__ float act_y(float v, int act) {
+    if (!act) return v;
+    if (YDT == RPFQ_F16) v = (float)(_Float16)v;
+    if (YDT == RPFQ_BF16) v = bf16_to_f32(f32_to_bf16(v));
+    return gelu_f(v);
+}
+// two packed 16-bit outputs of y's dtype
+__device__ __forceinline__ uint32_t gelu2_y(uint32_t v, bool f16) {
+    if (f16) {
+        const half2v h = __builtin_bit_cast(half2v, v);
+        const half2v o = {(_Float16)gelu_f((float)h.x), (_Float16)gelu_f((float)h.y)};
+        return __builtin_bit_cast(uint32_t, o);
+    }
+    return (uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v & 0xffffu))) |
+           ((uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v >> 16))) << 16);
+}
+__device__ __forceinline__ uint4 gelu8_y(uint4 v, bool f16) {
+    return make_uint4(gelu2_y(v.x, f16), gelu2_y(v.y, f16), gelu2_y(v.z, f16), gelu2_y(v.w, f16));
+}
+__device__ __forceinline__ uint16_t gelu1_y(uint16_t e, bool f16) {
+    if (f16) return __builtin_bit_cast(uint16_t, (_Float16)gelu_f((float)__builtin_bit_cast(_Float16, e)));
+    return f32_to_bf16(gelu_f(bf16_to_f32(e)));
+}
+// The same 8 outputs one at a time in a rolled loop (the 16-bit values shift
+// through the four words), so only one erf body is live: unrolled, the DMA
+// kernel's allocator pays for the epilogue's GELU with spills in its k-loop.
+__device__ __forceinline__ uint4 gelu8_rolled(uint4 v, bool f16) {
+    uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+#pragma unroll 1
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t o = gelu1_y((uint16_t)(w0 & 0xffffu), f16);
+        w0 = (w0 >> 16) | (w1 << 16);
+        w1 = (w1 >> 16) | (w2 << 16);
+        w2 = (w2 >> 16) | (w3 << 16);
+        w3 = (w3 >> 16) | (o << 16);
+    }
+    return make_uint4(w0, w1, w2, w3);
+}
+
 __device__ __forceinline__ half8 to_half8(const float* v) {
     uint4 u;
     u.x = pack_h2(v[0], v[1]);
@@ -524,6 +578,7 @@ struct WideArgs {
     int tiles_m, tiles_n;
     int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
     int wg_epi;     // DMA epilogue: workgroup-wide full-line stores (else per wave)
+    int act;        // 1: exact GELU of the rounded output (no residual), 0: none
 };
 
 // LDS activation row: 32 complex columns as (re, im) fp16 pairs = 128 B,
@@ -821,8 +876,9 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
             for (int v = 0; v < 16; ++v) {
                 const int64_t m = m0 + i * 32 + acc_row(v, g);
                 if (m < a.M) {
-                    store1<YDT>(a.y, m * ldy + n, with_res<YDT>(acc_re[i][v] + br, a.res, m * ldy + n));
-                    store1<YDT>(a.y, m * ldy + a.N + n, with_res<YDT>(acc_im[i][v] + bi, a.res, m * ldy + a.N + n));
+                    store1<YDT>(a.y, m * ldy + n, with_res<YDT>(act_y<YDT>(acc_re[i][v] + br, a.act), a.res, m * ldy + n));
+                    store1<YDT>(a.y, m * ldy + a.N + n,
+                                with_res<YDT>(act_y<YDT>(acc_im[i][v] + bi, a.act), a.res, m * ldy + a.N + n));
                 }
             }
         }
@@ -866,6 +922,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
         uint16_t* dst = reinterpret_cast<uint16_t*>(a.y) + m * ldy + col0;
         if (a.vec_store && nfirst + 8 <= a.N) {
             if (a.res) v = add_res8<YDT>(v, a.res, m * ldy + col0);
+            if (a.act) v = gelu8_y(v, YDT == RPFQ_F16);
             *reinterpret_cast<uint4*>(dst) = v;
         } else {
             const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
@@ -873,6 +930,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
                 uint16_t e = h[t];
                 if (a.res) e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + col0 + t],
                                                  YDT == RPFQ_F16) & 0xffffu);
+                if (a.act) e = gelu1_y(e, YDT == RPFQ_F16);
                 dst[t] = e;
             }
         }
@@ -979,7 +1037,9 @@ __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, con
     }
 }
 
-template <int BM, int YDT, int CB>
+// ACT (compile time, = WideArgs::act): the fused GELU's code stays out of
+// the plain instantiation, whose k-loop runs at the edge of the register file.
+template <int BM, int YDT, int CB, int ACT>
 __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int MB = BM / 32;
@@ -1238,8 +1298,8 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 float vr[4], vi[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    vr[t] = acc_re[i][4 * q + t] + bre[4 * q + t];
-                    vi[t] = acc_im[i][4 * q + t] + bim[4 * q + t];
+                    vr[t] = act_y<YDT>(acc_re[i][4 * q + t] + bre[4 * q + t], ACT);
+                    vi[t] = act_y<YDT>(acc_im[i][4 * q + t] + bim[4 * q + t], ACT);
                 }
                 float* yr = reinterpret_cast<float*>(a.y) + m * ldy + n0;
                 float* yi = reinterpret_cast<float*>(a.y) + m * ldy + a.N + n0;
@@ -1353,6 +1413,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     v = make_uint4(add2_y(v.x, rres[j].x, f16), add2_y(v.y, rres[j].y, f16),
                                    add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
                 }
+                if constexpr (ACT != 0) v = gelu8_rolled(v, YDT == RPFQ_F16);
                 __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
             } else {
                 const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
@@ -1361,6 +1422,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     if (a.res)
                         e = (uint16_t)(add2_y(e, reinterpret_cast<const uint16_t*>(a.res)[m * ldy + gcol + t],
                                               YDT == RPFQ_F16) & 0xffffu);
+                    if constexpr (ACT != 0) e = gelu1_y(e, YDT == RPFQ_F16);
                     dst[t] = e;
                 }
             }
@@ -1654,14 +1716,18 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
                 hr = add_res4<YDT>(hr, a.res, base);
                 hi = add_res4<YDT>(hi, a.res, base + a.N);
             }
+            if (a.act) {
+                hr = make_uint2(gelu2_y(hr.x, true), gelu2_y(hr.y, true));
+                hi = make_uint2(gelu2_y(hi.x, true), gelu2_y(hi.y, true));
+            }
             *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = hr;
             *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base + a.N) = hi;
         } else {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 if (n0 + v < a.N) {
-                    store1<YDT>(a.y, base + v, with_res<YDT>(vr[v], a.res, base + v));
-                    store1<YDT>(a.y, base + a.N + v, with_res<YDT>(vi[v], a.res, base + a.N + v));
+                    store1<YDT>(a.y, base + v, with_res<YDT>(act_y<YDT>(vr[v], a.act), a.res, base + v));
+                    store1<YDT>(a.y, base + a.N + v, with_res<YDT>(act_y<YDT>(vi[v], a.act), a.res, base + a.N + v));
                 }
             }
         }
@@ -2065,13 +2131,13 @@ static hipError_t wide_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int BM, int YDT, int CB>
-static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
+template <int BM, int YDT, int CB, int ACT>
+static hipError_t wide_dma_act(WideArgs& a, hipStream_t s) {
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     constexpr int lds = dma_lds<BM>();
     std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_dma_kernel<BM, YDT, CB>),
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_linear_dma_kernel<BM, YDT, CB, ACT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     });
     if (attr_err != hipSuccess) return attr_err;
@@ -2080,8 +2146,14 @@ static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
     const int total = a.tiles_m * a.tiles_n;
     const int slots = (BM == 128 ? 2 : 1) * device_cus();  // workgroups resident per CU
     const int grid = total < slots ? total : slots;
-    hipLaunchKernelGGL((wide_linear_dma_kernel<BM, YDT, CB>), dim3(grid), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((wide_linear_dma_kernel<BM, YDT, CB, ACT>), dim3(grid), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+template <int BM, int YDT, int CB>
+static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
+    if constexpr (YDT == RPFQ_BF16) return wide_dma_act<BM, YDT, CB, 0>(a, s);  // GELU: not routed here
+    else return a.act ? wide_dma_act<BM, YDT, CB, 1>(a, s) : wide_dma_act<BM, YDT, CB, 0>(a, s);
 }
 
 // Workgroups of the streaming kernel: one per (16-row chunk, 32-row tile).
@@ -2130,15 +2202,28 @@ static bool stream_pays(const WideArgs& a) {
     return t_stream < 0.9 * t_tiled;
 }
 
-template <int XDT, int YDT, int CB>
-static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
 #ifndef RPFQ_DMA_MIN_M
 #define RPFQ_DMA_MIN_M 128
 #endif
+// The kernel a launch runs (RPFQ_KERNEL_*), from the shape, dtypes and the
+// kernel-choice flags (the GELU bit already moved into a.act).
+static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
     if ((flags & RPFQ_FLAG_STREAM) || (!(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)) && stream_pays(a)))
-        return wide_sk<XDT, YDT, CB>(a, s);
+        return RPFQ_KERNEL_STREAM;
     flags &= ~RPFQ_FLAG_NO_STREAM;
-    if (XDT == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M) return wide_dma_go<128, YDT, CB>(a, s);
+    // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
+    // spill in its k-loop, so they take the register-staged kernel)
+    if (xdt == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M && !(a.act && ydt == RPFQ_BF16))
+        return RPFQ_KERNEL_DMA;
+    return RPFQ_KERNEL_TILED;
+}
+
+template <int XDT, int YDT, int CB>
+static hipError_t wide_bm(WideArgs& a, int flags, hipStream_t s) {
+    const int k = choose_kernel(a, XDT, YDT, flags);
+    if (k == RPFQ_KERNEL_STREAM) return wide_sk<XDT, YDT, CB>(a, s);
+    if (k == RPFQ_KERNEL_DMA) return wide_dma_go<128, YDT, CB>(a, s);
+    flags &= ~RPFQ_FLAG_NO_STREAM;
     if (flags & RPFQ_FLAG_TILE_M128) return wide_go<128, XDT, YDT, CB>(a, s);
     if (a.M <= 32) return wide_go<32, XDT, YDT, CB>(a, s);
     if (a.M <= 64) return wide_go<64, XDT, YDT, CB>(a, s);
@@ -2163,11 +2248,9 @@ static hipError_t wide_x(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s
     }
 }
 
-hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
-                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
-                              hipStream_t s) {
-    WideArgs a;
-    a.x = x;
+// Shape fields of the launch arguments (what the kernel choice reads).
+static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
+    WideArgs a = {};
     a.M = M;
     a.K = (int)g.K;
     a.N = (int)g.N;
@@ -2175,6 +2258,20 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     a.KS = (int)g.KS;
     a.nblk = (int)g.nblk;
     a.block_ks = (int)g.block_ks;
+    a.act = (flags & RPFQ_FLAG_GELU) ? 1 : 0;  // an epilogue op, not a kernel choice
+    return a;
+}
+
+int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags) {
+    return choose_kernel(wide_shape(g, M, flags), xdt, ydt, flags & ~RPFQ_FLAG_GELU);
+}
+
+hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
+                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
+                              hipStream_t s) {
+    WideArgs a = wide_shape(g, M, flags);
+    flags &= ~RPFQ_FLAG_GELU;
+    a.x = x;
     a.codes = reinterpret_cast<const uint4*>(packed);
     a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
     a.rot = rot_of(d);

@@ -30,6 +30,8 @@ QK_AXIS, QK_SIGN = 0, 1  # weight quantizer kinds of rpfq_quantize_wide
 FLAG_TILE_M128 = 1  # force the register-staged 128-row kernel
 FLAG_NO_STREAM = 2  # keep every M on the tiled kernels (no weight-streaming kernel)
 FLAG_STREAM = 4  # force the weight-streaming kernel for any M (16-row chunks)
+FLAG_GELU = 8  # exact GELU of the rounded output, fused into the store (no residual)
+KERNEL_STREAM, KERNEL_DMA, KERNEL_TILED = 0, 1, 2  # rpfq_wide_linear_kernel
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -45,6 +47,7 @@ EXPORTED = (
     "rpfq_wide_decode",
     "rpfq_act_quant",
     "rpfq_wide_linear_residual",
+    "rpfq_wide_linear_kernel",
     "rpfq_layer_norm",
     "rpfq_layer_norm_act_quant",
     "rpfq_quantize_workspace_bytes",
@@ -121,6 +124,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_wide_decode.argtypes = [dp, vp, sz, vp, i32, vp]
         lib.rpfq_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         lib.rpfq_wide_linear_residual.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, i32, i32, vp]
+        lib.rpfq_wide_linear_kernel.argtypes = [dp, i64, i32, i32, i32, ctypes.POINTER(i32)]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
         qp = ctypes.POINTER(QuantDesc)

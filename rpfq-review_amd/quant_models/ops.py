@@ -171,13 +171,19 @@ class PackedWide:
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, flags: int = 0,
-               residual: torch.Tensor | None = None) -> torch.Tensor:
+               residual: torch.Tensor | None = None, gelu: bool = False) -> torch.Tensor:
         """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
         flags: 0 (kernel chosen from the shape), _native.FLAG_TILE_M128,
         _native.FLAG_NO_STREAM or _native.FLAG_STREAM.  residual ([..., 2N'] of out_dtype): y =
         residual + layer(x), fused into the kernel's store and rounded as the
-        unfused add would round it (rpfq_wide_linear_residual)."""
+        unfused add would round it (rpfq_wide_linear_residual).  gelu: y =
+        F.gelu(layer(x)) (exact erf GELU in the store, equal to the unfused
+        op; not with a residual)."""
         N.require_device(x, bias, residual)
+        if gelu:
+            if residual is not None:
+                raise ValueError("gelu and residual cannot be fused together")
+            flags = int(flags) | N.FLAG_GELU
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
         lead = x.shape[:-1]
@@ -222,6 +228,15 @@ class PackedWide:
             rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex), nbytes,
                 (m, self.n_complex, self.k_complex))
         return y.reshape(*lead, self.out_features)
+
+    def kernel_for(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype, flags: int = 0) -> int:
+        """The kernel linear() runs for m rows (N.KERNEL_STREAM / _DMA /
+        _TILED; rpfq_wide_linear_kernel, no GPU work)."""
+        out = ctypes.c_int32(-1)
+        N.check("rpfq_wide_linear_kernel", N.load().rpfq_wide_linear_kernel(
+            ctypes.byref(self.desc), int(m), N.dtype_code(x_dtype), N.dtype_code(y_dtype), int(flags),
+            ctypes.byref(out)))
+        return out.value
 
     def linear_into(self, x: torch.Tensor, bias: torch.Tensor | None, y: torch.Tensor, flags: int = 0) -> None:
         """y[:] = U x + W conj(x) + bias for a contiguous [M, 2K'] x and a

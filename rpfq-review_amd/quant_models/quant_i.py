@@ -535,6 +535,27 @@ class QATLinearComplexPhase(nn.Linear):
             return self._packed_forward(x)
         return self._qat_forward(x)
 
+    def forward_gelu(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
+        """F.gelu(self(x)) (exact erf GELU); x already activation-quantized
+        for this layer if prequantized.  On the packed HIP path the GELU runs
+        in the kernel's store (within 1 ulp of the unfused op) where the
+        launch takes the streaming kernel; on the tiled kernels the float32
+        erf in the per-tile epilogue costs about what torch's separate GELU
+        pass does, so there the GELU stays a separate op."""
+        if x.is_cuda and not self.training and self.use_packed:
+            from . import _native as N
+            from . import ops
+
+            pw = self.packed(x.device)
+            if self.act_quantizer is not None and not prequantized:
+                x = ops.act_quant(x, self.act_quantizer.num_bits)
+            bias = None if self.bias is None else self.bias.detach()
+            m = x.numel() // x.shape[-1]
+            if m and pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) == N.KERNEL_STREAM:
+                return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
+            return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
+        return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
+
     def forward_residual(self, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
         """residual + self(x).  On the packed HIP path the add is fused into
         the kernel's store (bit-identical to the unfused add in x's dtype);

@@ -25,6 +25,9 @@ FUSED_BLOCKS = os.environ.get("RPFQ_FUSED", "1") != "0"
 # Within the fused path, a LayerNorm feeding a packed layer with activation
 # quantization also applies that quantization (rpfq_layer_norm_act_quant).
 FUSE_ACT_QUANT = os.environ.get("RPFQ_FUSE_AQ", "1") != "0"
+# Within the fused path, the MLP's exact GELU runs in fc1's store when fc1 is
+# a packed phase-quantized Linear (rpfq_wide_linear with RPFQ_FLAG_GELU).
+FUSE_GELU = os.environ.get("RPFQ_FUSE_GELU", "1") != "0"
 
 
 def _fused(module: nn.Module, x: torch.Tensor) -> bool:
@@ -130,10 +133,15 @@ class Mlp(nn.Module):
         return self.drop2(self.fc2(self.norm(self.drop1(self.act(self.fc1(x))))))
 
     def forward_residual(self, x, residual, prequantized: bool = False):
-        """residual + self(x) with the add fused into fc2 (eval mode); x
+        """residual + self(x) with the add fused into fc2 and an exact GELU
+        into fc1's store when fc1 is a phase-quantized Linear (eval mode); x
         already activation-quantized for fc1 if prequantized."""
-        h = call_layer(self.fc1, x, prequantized)
-        return linear_residual(self.fc2, self.norm(self.drop1(self.act(h))), residual)
+        fc1_gelu = getattr(self.fc1, "forward_gelu", None)
+        if FUSE_GELU and fc1_gelu is not None and type(self.act) is nn.GELU and self.act.approximate == "none":
+            h = fc1_gelu(x, prequantized)
+        else:
+            h = self.act(call_layer(self.fc1, x, prequantized))
+        return linear_residual(self.fc2, self.norm(self.drop1(h)), residual)
 
 
 class Attention(nn.Module):

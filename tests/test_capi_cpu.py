@@ -73,7 +73,7 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 8, None) == 6  # unknown flag bit
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 16, None) == 6  # unknown flag bit
     # RPFQ_FLAG_STREAM with a tiled-kernel flag; a streaming grid past 2^24 workgroups
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 1, None) == 6
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 2, None) == 6
@@ -116,7 +116,9 @@ def test_residual_and_layer_norm_argument_errors():
     # NULL residual, bad dtype, bad flags, misaligned residual -- all before any HIP call
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 9, 0, None) == 5
-    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 8, None) == 6
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 16, None) == 6
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 8, None) == 6  # GELU
+    assert "GELU" in L.rpfq_last_error().decode()
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, ctypes.c_void_p(258), p, 1, 0,
                                        None) == 3
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 16, p, 1, 4, None, p, p, 1, 0, None) == 2
@@ -218,3 +220,30 @@ int main(void) {
     subprocess.run(cmd, check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stdout, out.stderr)
+
+
+def test_wide_linear_kernel_choice():
+    """rpfq_wide_linear_kernel (no GPU work): the streaming kernel for a few
+    rows and for small one-tile-deep launches, the DMA kernel for large fp16
+    launches, the register-staged kernel for float32 x, bf16 output with
+    GELU, or RPFQ_FLAG_TILE_M128; the flags force their kernels."""
+    L, N = lib()
+    d = _desc(N, n=1536, k=384)  # ViT-B fc1
+
+    def kernel(m, xdt=1, ydt=1, flags=0):
+        out = ctypes.c_int32(-1)
+        assert L.rpfq_wide_linear_kernel(ctypes.byref(d), m, xdt, ydt, flags, ctypes.byref(out)) == 0
+        return out.value
+    assert kernel(1) == N.KERNEL_STREAM and kernel(16) == N.KERNEL_STREAM
+    assert kernel(197) == N.KERNEL_STREAM  # one image: 624 (chunk, tile) groups vs one 128-row tile deep
+    assert kernel(50432) == N.KERNEL_DMA
+    assert kernel(50432, flags=N.FLAG_GELU) == N.KERNEL_DMA
+    assert kernel(50432, ydt=2, flags=N.FLAG_GELU) == N.KERNEL_TILED
+    assert kernel(50432, xdt=0) == N.KERNEL_TILED
+    assert kernel(300, flags=N.FLAG_TILE_M128) == N.KERNEL_TILED
+    assert kernel(197, flags=N.FLAG_NO_STREAM) == N.KERNEL_DMA
+    assert kernel(50432, flags=N.FLAG_STREAM) == N.KERNEL_STREAM
+    out = ctypes.c_int32(-1)
+    assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 0, None) == 1
+    assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 0, 1, 1, 0, ctypes.byref(out)) == 2
+    assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 16, ctypes.byref(out)) == 6

@@ -241,3 +241,51 @@ def test_fused_act_quant_wiring(name):
         vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = saved
     assert torch.isfinite(y_f).all()
     assert torch.equal(y_f, y_u)
+
+
+@pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_swin_tiny_patch4_window7_224_q"])
+def test_fused_gelu_wiring(name):
+    """The fused block path runs the MLP's exact GELU in fc1's store
+    (RPFQ_FLAG_GELU), within 1 fp16 ulp of torch's GELU of the unfused fc1
+    output (rarely off at all): the logits stay within 1e-2 * max|logit| +
+    1e-3 of the same path with the GELU fusion off, with identical top-1 on
+    margin-confident samples.  A GELU skipped or applied twice moves them by
+    orders of magnitude more."""
+    import quant_models as qm
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(5)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    load_synthetic_codes(model, 5)
+    prepare_inference(model, DEV, torch.float16)
+    # one image: fc1 takes the streaming kernel, where the GELU is fused
+    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(7)).to(DEV, torch.float16)
+    from quant_models import ops
+    fused = []
+    linear = ops.PackedWide.linear
+
+    def counting(self, *args, **kw):
+        fused.append(bool(kw.get("gelu", False)))
+        return linear(self, *args, **kw)
+    saved = vt.FUSED_BLOCKS, vt.FUSE_GELU
+    try:
+        ops.PackedWide.linear = counting
+        with torch.no_grad():
+            vt.FUSED_BLOCKS, vt.FUSE_GELU = True, True
+            y_f = model(x)
+            n_fused = sum(fused)
+            vt.FUSE_GELU = False
+            y_u = model(x)
+    finally:
+        ops.PackedWide.linear = linear
+        vt.FUSED_BLOCKS, vt.FUSE_GELU = saved
+    assert n_fused >= 2, n_fused
+    assert torch.isfinite(y_f).all()
+    y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
+    err = (y_f - y_u).abs().max()
+    assert err <= 1e-2 * y_u.abs().max() + 1e-3, (err, y_u.abs().max())
+    top = y_u.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
