@@ -418,7 +418,7 @@ def main() -> int:
         # batch-1 weight streaming (HBM roof) at the ViT-B fc1 shape; runs before
         # and outside the timed region of the model forward
         k_c, n_c = STREAM_SHAPES["vit_b.fc1"]
-        batch1 = {"kernel": "rpfq::wide_linear_skinny_kernel (M <= 16)", "bound": "hbm", "peak": PEAK_HBM_GBS,
+        batch1 = {"kernel": "rpfq::wide_linear_skinny_kernel (M = 1)", "bound": "hbm", "peak": PEAK_HBM_GBS,
                   "unit": "GB/s", "stacked": stream_case(k_c, n_c, 1, "stacked", 1.0, 10),
                   "rotate": stream_case(k_c, n_c, 1, "rotate", 1.0, 5)}
     model = build_model(args.config, args.act_quant)
@@ -505,8 +505,9 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": None if achieved_tflops is None else round(achieved_tflops / PEAK_F16_TFLOPS, 4),
             "traffic": None,
-            "kernel": "rpfq::wide_linear_dma_kernel (fp16 x, K' % 32 == 0, M >= 128; else "
-                      "rpfq::wide_linear_kernel): all packed-layer launches in the timed region",
+            "kernel": "rpfq::wide_linear_dma_kernel (fp16 x, K' % 32 == 0, M >= 128, launches over one tile "
+                      "deep; small launches rpfq::wide_linear_skinny_kernel, else rpfq::wide_linear_kernel): "
+                      "all packed-layer launches in the timed region (none under --graph)",
             "launches": len(launches),
             "avg_launch_us": round(1e3 * kt / max(1, len(launches)), 2),
             "algorithmic_gbs": round(kb / (kt / 1e3) / 1e9, 1) if kt > 0 else None,
