@@ -1470,8 +1470,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 //     v_perm_b32.  Rows past M read row M - 1: their MFMA columns are never
 //     stored.  Columns past K' (K' % 32 != 0 only) are zeroed.
 //   * split K for layers of few tiles: the 4 waves of a workgroup share one
-//     tile and its LUT, each walks a quarter of the k-steps, and wave 0 sums
-//     the partials through LDS (a small layer then covers 4x the SIMDs);
+//     tile and its LUT (each builds a quarter of it), each walks a quarter
+//     of the k-steps, and wave 0 sums the partials through LDS (a small
+//     layer then covers 4x the SIMDs);
 //   * codes and activations of k-step ks + SK_PF are requested before k-step
 //     ks is decoded, by unconditional loads in straight-line code (uniform
 //     base + constant lane offset) so the wait counts stay exact; occupancy
@@ -1489,8 +1490,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // LUT of the skinny kernel from row R's parameters (pu, pw), R = lane & 31:
 // entry idx in slots 32 (R >> 4) + (R & 15) and + 16; lane group g writes
 // the even or odd indices.
-template <int CB>
-__device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, const RotParams& rot, int R, int g) {
+// NJ of the 8 (even or odd) indices from j0 on: a whole LUT (NJ = 8), or the
+// quarter one wave of a split-K workgroup builds (NJ = 2, j0 = 2 wave).
+template <int CB, int NJ = 8>
+__device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, const RotParams& rot, int R, int g,
+                                             int j0 = 0) {
     const int s0 = 32 * (R >> 4) + (R & 15);
     float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
     if constexpr (CB != RPFQ_CB_TABLE) {
@@ -1498,8 +1502,8 @@ __device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, con
         pw = p[1];
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t idx = (uint32_t)(g + 2 * j);
+    for (int jj = 0; jj < NJ; ++jj) {
+        const uint32_t idx = (uint32_t)(g + 2 * (j0 + jj));
         float2 u, w;
         if constexpr (CB == RPFQ_CB_TABLE) {  // p = the row's 32 (re, im) values
             u = reinterpret_cast<const float2*>(p)[idx];
@@ -1598,9 +1602,12 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
     for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
 
     int blk = 0;
-    if (wave == 0) {
+    {  // split K: each of the 4 waves builds a quarter of the shared LUT
         const float4* p = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
-        build_lut_sk<CB>(lut, p, a.rot, R, g);
+        if (NW == 1)
+            build_lut_sk<CB>(lut, p, a.rot, R, g);
+        else
+            build_lut_sk<CB, 2>(lut, p, a.rot, R, g, 2 * wave);
     }
     if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
