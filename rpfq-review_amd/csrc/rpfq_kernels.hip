@@ -2339,12 +2339,18 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
 }
 
 // Lanes per row: the smallest of 8, 16, 32, 64 that keeps every lane at <= 4
-// chunks (C <= 2048), else 64 lanes with up to 8 chunks (C <= 4096).
+// chunks (C <= 2048), else 64 lanes with up to 8 chunks (C <= 4096); 64
+// lanes whenever that smallest choice would launch fewer than 256
+// workgroups (a batch-1 forward: 197 rows), so the launch spreads over the
+// CUs and each lane's chain of loads and reductions is shorter.
 // mode: 1 LayerNorm, 2 activation quantization, 3 both.
 template <int XDT, int YDT>
 static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
                         int mode, int bits, void* y, hipStream_t s) {
     const int nch = C / 8;
+    const int tpr = nch <= 32 ? 8 : nch <= 64 ? 16 : nch <= 128 ? 32 : 64;
+    if (nch <= 256 && tpr < 64 && M * tpr < 256 * 256)
+        return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
     if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
     if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
     if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
