@@ -404,7 +404,7 @@ def test_wide_linear_streaming(case, m):
     check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
-@pytest.mark.parametrize("m", [17, 45, 197])
+@pytest.mark.parametrize("m", [17, 45, 197, 300])
 @pytest.mark.parametrize("case", SKINNY_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
                                                     for c in SKINNY_CASES])
 def test_wide_linear_stream_chunks(case, m):
@@ -465,9 +465,10 @@ def test_wide_linear_streaming_persistent(m, n_c, k_c):
 # fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
 # followed by the add in y's dtype, on every kernel path
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("m,flags", [(3, 0), (16, 0), (33, 2), (130, 2), (300, 1), (129, 2), (197, 4), (197, 0)],
+@pytest.mark.parametrize("m,flags", [(3, 0), (16, 0), (33, 2), (130, 2), (300, 1), (129, 2), (197, 4), (197, 0),
+                                     (300, 4)],
                          ids=["stream3", "stream16", "reg33", "dma130", "reg128-300", "nostream129", "stream197",
-                              "auto197"])
+                              "auto197", "stream300"])
 @pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float32])
 def test_wide_linear_residual_bit_exact(m, flags, ydt):
     r = rng(1000 + m)
