@@ -1469,10 +1469,10 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 //     fragment straight from x (L2-resident) and interleaves them with
 //     v_perm_b32.  Rows past M read row M - 1: their MFMA columns are never
 //     stored.  Columns past K' (K' % 32 != 0 only) are zeroed.
-//   * split K for layers of few tiles: the 4 waves of a workgroup share one
-//     tile and its LUT (each builds a quarter of it), each walks a quarter
-//     of the k-steps, and wave 0 sums the partials through LDS (a small
-//     layer then covers 4x the SIMDs);
+//   * split K for layers of few tiles: the NW = 2 or 4 waves of a workgroup
+//     share one tile and its LUT (each builds 1 / NW of it), each walks
+//     1 / NW of the k-steps, and wave 0 sums the partials through LDS (a
+//     small layer then covers NW times the SIMDs);
 //   * codes and activations of k-step ks + SK_PF are requested before k-step
 //     ks is decoded, by unconditional loads in straight-line code (uniform
 //     base + constant lane offset) so the wait counts stay exact; occupancy
@@ -1482,8 +1482,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 #endif
 constexpr int SK_PF = RPFQ_SK_PF;   // prefetch distance in k-steps
 constexpr int kSkLut = 32 * 64 * 4;  // 8 KB LUT
-constexpr int kSkRed = 3 * 16 * 64 * 4;  // partial sums of waves 1-3 (split-K)
-constexpr int kSkLds = kSkLut + kSkRed;
+// LDS of a workgroup of NW waves: the LUT, and with split K the partial sums
+// of waves 1 .. NW-1
+constexpr int sk_lds(int nw) { return kSkLut + (nw - 1) * 16 * 64 * 4; }
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -1491,7 +1492,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // entry idx in slots 32 (R >> 4) + (R & 15) and + 16; lane group g writes
 // the even or odd indices.
 // NJ of the 8 (even or odd) indices from j0 on: a whole LUT (NJ = 8), or the
-// quarter one wave of a split-K workgroup builds (NJ = 2, j0 = 2 wave).
+// part one wave of a split-K workgroup of NW waves builds (NJ = 8 / NW,
+// j0 = NJ wave).
 template <int CB, int NJ = 8>
 __device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, const RotParams& rot, int R, int g,
                                              int j0 = 0) {
@@ -1542,16 +1544,15 @@ __device__ __forceinline__ uint2 raw4_f16(uint2 v) {
 
 // PB: per-(row, block) scales (the LUT is rebuilt at each block start);
 // KT: K' % 32 != 0 (activation columns past K' are zeroed);
-// SPLIT (not with PB): split K -- the 4 waves of a workgroup share the
-// tile's LUT, take a quarter of the k-steps each, and wave 0 adds the three
+// NW (1 with PB): waves per workgroup.  NW = 2 or 4 splits K: the waves
+// share the tile's LUT, take 1 / NW of the k-steps each, and wave 0 adds the
 // other partial sums (through LDS, in a fixed order) before the epilogue.
-// Without SPLIT a workgroup is one wave streaming one tile's whole K.
+// NW = 1: one wave streams the tile's whole K.
 #ifndef RPFQ_SK_OCC
 #define RPFQ_SK_OCC 4  // waves per SIMD the register budget is sized for
 #endif
-template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
-__global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
-    constexpr int NW = SPLIT ? 4 : 1;  // waves per tile
+template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
+__global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
     const int lane = threadIdx.x & 63;
@@ -1602,12 +1603,12 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
     for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
 
     int blk = 0;
-    {  // split K: each of the 4 waves builds a quarter of the shared LUT
+    {  // split K: each wave builds 1 / NW of the shared LUT
         const float4* p = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
         if (NW == 1)
             build_lut_sk<CB>(lut, p, a.rot, R, g);
         else
-            build_lut_sk<CB, 2>(lut, p, a.rot, R, g, 2 * wave);
+            build_lut_sk<CB, 8 / NW>(lut, p, a.rot, R, g, (8 / NW) * wave);
     }
     if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1673,7 +1674,7 @@ __global__ void __launch_bounds__(SPLIT ? 256 : 64, RPFQ_SK_OCC) wide_linear_ski
         }
     }
 
-    if (NW > 1) {  // waves 1-3 hand their partial sums to wave 0
+    if (NW > 1) {  // waves 1 .. NW-1 hand their partial sums to wave 0
         float* red = reinterpret_cast<float*>(smem + kSkLut);
         if (wave > 0) {
 #pragma unroll
@@ -2166,26 +2167,35 @@ static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
 // Workgroups of the streaming kernel: one per (16-row chunk, 32-row tile).
 static int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
 
-template <int XDT, int YDT, int CB, bool PB, bool KT, bool SPLIT>
+template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
 static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, SPLIT>), dim3((unsigned)sk_groups(a)),
-                       dim3(SPLIT ? 256 : 64), SPLIT ? kSkLds : kSkLut, s, a);
+    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, NW>), dim3((unsigned)sk_groups(a)),
+                       dim3(64 * NW), sk_lds(NW), s, a);
     return hipGetLastError();
 }
 
 // Split K when the launch has too few workgroups to give every SIMD a few
-// waves (a single layer at batch 1); a long stream of tiles runs one wave each.
+// waves (a single layer at batch 1): over 4 waves below 400 workgroups, over
+// 2 from there (less LUT building and reduction per k-step once the groups
+// alone fill the SIMDs; ViT-B/16 batch-1 forward 0.834 -> 0.772 ms, and 2
+// waves already from 128 groups measured slower); a long stream of tiles
+// runs one wave each.
 #ifndef RPFQ_SK_SPLIT_TILES
 #define RPFQ_SK_SPLIT_TILES 4096
+#endif
+#ifndef RPFQ_SK_NW2_GROUPS
+#define RPFQ_SK_NW2_GROUPS 400
 #endif
 template <int XDT, int YDT, int CB>
 static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
     const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
-    if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, false>(a, s)
-                      : wide_sk_go<XDT, YDT, CB, true, false, false>(a, s);
-    if (sk_groups(a) < RPFQ_SK_SPLIT_TILES)
-        return kt ? wide_sk_go<XDT, YDT, CB, false, true, true>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, true>(a, s);
-    return kt ? wide_sk_go<XDT, YDT, CB, false, true, false>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, false>(a, s);
+    if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, true, false, 1>(a, s);
+    const int64_t groups = sk_groups(a);
+    if (groups >= RPFQ_SK_NW2_GROUPS && groups < RPFQ_SK_SPLIT_TILES)
+        return kt ? wide_sk_go<XDT, YDT, CB, false, true, 2>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 2>(a, s);
+    if (groups < RPFQ_SK_SPLIT_TILES)
+        return kt ? wide_sk_go<XDT, YDT, CB, false, true, 4>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 4>(a, s);
+    return kt ? wide_sk_go<XDT, YDT, CB, false, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 1>(a, s);
 }
 
 // Kernel choice for a small M.  A tiled kernel gives each workgroup one
