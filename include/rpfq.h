@@ -219,10 +219,12 @@ int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const floa
 
 /*
  * rpfq_layer_norm followed by the activation fake quantization of
- * rpfq_act_quant on its output, in one pass over the rows: the LayerNorm
- * output is rounded to y_dtype and then quantized per row and per half
- * (C/2 columns each; C % 16 == 0), so y is bit-identical to the two calls in
- * sequence.  bits: 2 .. 16.  The quantized input of the qkv and fc1 layers
+ * rpfq_act_quant on its output, in one pass over the rows: the float32
+ * LayerNorm output is quantized per row and per half (C/2 columns each;
+ * C % 16 == 0) and only the quantized value is rounded to y_dtype, as the
+ * reference quantizes its float32 LayerNorm output; y is bit-identical to
+ * rpfq_layer_norm with float32 output followed by rpfq_act_quant with
+ * y_dtype output.  bits: 2 .. 16.  The quantized input of the qkv and fc1 layers
  * of a block with activation quantization on
  *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:520, :549 followed by
  *   RPFQ-ViT-main/quant_models/quant_i.py:546-551.

@@ -310,14 +310,6 @@ def psk16_codebook() -> np.ndarray:
     return np.array(out, dtype=F32) + F32(0.0)  # -0 -> +0
 
 
-def psk16_quantize(w_re, w_im):
-    """Nearest of 16 phases; per-row magnitude scale = mean |w| of the row."""
-    w = np.asarray(w_re, np.float64) + 1j * np.asarray(w_im, np.float64)
-    codes = (np.round(np.angle(w) / (2 * math.pi / 16)) % 16).astype(np.uint8)
-    scale = np.maximum(np.abs(w).mean(axis=1), 1e-6).astype(F32)
-    return codes, scale
-
-
 # --------------------------------------------------------------------------
 # activation fake-quant (quant_i.py:438-455)
 # --------------------------------------------------------------------------

@@ -1,0 +1,349 @@
+// Device helpers shared by the HIP kernel translation units: codebooks,
+// element I/O, the fused-coefficient decode and the LUT builders.
+//
+// Arithmetic order of the decoded coefficients follows the reference exactly
+// (RPFQ-ViT-main/quant_models/quant_i.py:111-118 stage sums, :534-544
+// recombination) so the float32 coefficient is bit-identical to A_q; it is
+// rounded once to fp16 for the MFMA.
+#pragma once
+
+#include "rpfq_internal.h"
+
+namespace rpfq {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// codebooks
+// ---------------------------------------------------------------------------
+// 16-PSK: exact octant symmetry from three float32 constants
+// (cos pi/8, sin pi/8, sqrt(2)/2 rounded to nearest float32).
+#define PSK_C1 0x1.d906bcp-1f  /* float32(cos pi/8) */
+#define PSK_S1 0x1.87de2ap-2f  /* float32(sin pi/8) */
+#define PSK_R2 0x1.6a09e6p-1f  /* float32(sqrt(2)/2) */
+static __constant__ float kPskCos[16] = {1.0f,    PSK_C1,  PSK_R2,  PSK_S1,  0.0f,    -PSK_S1, -PSK_R2, -PSK_C1,
+                                  -1.0f,   -PSK_C1, -PSK_R2, -PSK_S1, 0.0f,    PSK_S1,  PSK_R2,  PSK_C1};
+static __constant__ float kPskSin[16] = {0.0f,    PSK_S1,  PSK_R2,  PSK_C1,  1.0f,    PSK_C1,  PSK_R2,  PSK_S1,
+                                  0.0f,    -PSK_S1, -PSK_R2, -PSK_C1, -1.0f,   -PSK_C1, -PSK_R2, -PSK_S1};
+
+// 2-bit axis code -> value, codes 00=-1, 01=+1, 10=-i, 11=+i
+// (export_rpfq_vit_to_mlx.py:598-603; phase_linear.cpp:143-154).
+__device__ __forceinline__ float2 axis_val(uint32_t c, float sr, float si) {
+    float2 v;
+    v.x = (c & 2u) ? 0.0f : ((c & 1u) ? sr : -sr);
+    v.y = (c & 2u) ? ((c & 1u) ? si : -si) : 0.0f;
+    return v;
+}
+
+// 2-bit quadrant-sign code: bit0 = re >= 0, bit1 = im >= 0 (quant_i.py:84-91).
+__device__ __forceinline__ float2 sign_val(uint32_t c, float sr, float si) {
+    float2 v;
+    v.x = (c & 1u) ? sr : -sr;
+    v.y = (c & 2u) ? si : -si;
+    return v;
+}
+
+// Quantized complex value of one U (or W) index under the per-row
+// parameters p = (s0 re, s0 im, s1 re, s1 im).  Stages are summed in the
+// reference's order q = step0 + step1 (quant_i.py:111-118).
+template <int CB>
+__device__ __forceinline__ float2 lut_entry(uint32_t idx, float4 p) {
+    if (CB == RPFQ_CB_PSK16) {
+        return make_float2(p.x * kPskCos[idx], p.x * kPskSin[idx]);
+    }
+    float2 v0, v1;
+    if (CB == RPFQ_CB_SIGN) {
+        v0 = sign_val(idx & 3u, p.x, p.y);
+        v1 = sign_val(idx >> 2, p.z, p.w);
+    } else {
+        v0 = axis_val(idx & 3u, p.x, p.y);
+        v1 = axis_val(idx >> 2, p.z, p.w);
+    }
+    return make_float2(v0.x + v1.x, v0.y + v1.y);
+}
+
+// De-rotation after quantization (quant_i.py:433-434); built without
+// contraction (-ffp-contract=off) so each product rounds as in torch.
+__device__ __forceinline__ float2 derotate(float2 q, float c, float s) {
+    float a = q.x * c;
+    float b = q.y * s;
+    float d = q.y * c;
+    float e = q.x * s;
+    return make_float2(a - b, d + e);
+}
+
+// ---------------------------------------------------------------------------
+// element I/O
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// 8 consecutive elements at element offset `off` -> 8 fp16 in a uint4.
+template <int XDT>
+__device__ __forceinline__ uint4 load8_f16(const void* base, int64_t off) {
+    if (XDT == RPFQ_F16) {
+        return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    } else if (XDT == RPFQ_BF16) {
+        uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        uint4 o;
+        o.x = pack_h2(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16));
+        o.y = pack_h2(bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16));
+        o.z = pack_h2(bf16_to_f32(v.z & 0xffffu), bf16_to_f32(v.z >> 16));
+        o.w = pack_h2(bf16_to_f32(v.w & 0xffffu), bf16_to_f32(v.w >> 16));
+        return o;
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+        float4 a = p[0], b = p[1];
+        uint4 o;
+        o.x = pack_h2(a.x, a.y);
+        o.y = pack_h2(a.z, a.w);
+        o.z = pack_h2(b.x, b.y);
+        o.w = pack_h2(b.z, b.w);
+        return o;
+    }
+}
+
+// float32 -> (hi, lo) fp16 pair with x ~= hi + lo (relative error ~2^-22).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    _Float16 la = (_Float16)(a - (float)ha), lb = (_Float16)(b - (float)hb);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+}
+
+template <int YDT>
+__device__ __forceinline__ void store1(void* base, int64_t off, float v) {
+    if (YDT == RPFQ_F32) {
+        reinterpret_cast<float*>(base)[off] = v;
+    } else if (YDT == RPFQ_F16) {
+        reinterpret_cast<_Float16*>(base)[off] = (_Float16)v;
+    } else {
+        reinterpret_cast<uint16_t*>(base)[off] = f32_to_bf16(v);
+    }
+}
+
+__device__ __forceinline__ half8 as_half8(uint4 v) { return __builtin_bit_cast(half8, v); }
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// One element of y's dtype as float32.
+template <int YDT>
+__device__ __forceinline__ float load_y1(const void* base, int64_t off) {
+    if (YDT == RPFQ_F32) return reinterpret_cast<const float*>(base)[off];
+    if (YDT == RPFQ_F16) return (float)reinterpret_cast<const _Float16*>(base)[off];
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[off]);
+}
+
+// Fused residual add, rounded as the unfused sequence rounds it: the layer
+// output v is first rounded to y's dtype, then res + that is rounded again by
+// the store (the sum of two fp16 values is exact in float32, so the store's
+// rounding equals an fp16 add; bf16 and float32 add in float32 as torch does).
+template <int YDT>
+__device__ __forceinline__ float with_res(float v, const void* res, int64_t off) {
+    if (!res) return v;
+    float r = v;
+    if (YDT == RPFQ_F16) r = (float)(_Float16)v;
+    if (YDT == RPFQ_BF16) r = bf16_to_f32(f32_to_bf16(v));
+    return load_y1<YDT>(res, off) + r;
+}
+
+// 8 (uint4) or 4 (uint2) packed 16-bit outputs plus the residual at `off`.
+__device__ __forceinline__ uint32_t add2_y(uint32_t v, uint32_t r, bool f16) {
+    if (f16) return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, r) + __builtin_bit_cast(half2v, v));
+    const float lo = bf16_to_f32(r & 0xffffu) + bf16_to_f32(v & 0xffffu);
+    const float hi = bf16_to_f32(r >> 16) + bf16_to_f32(v >> 16);
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+template <int YDT>
+__device__ __forceinline__ uint4 add_res8(uint4 v, const void* res, int64_t off) {
+    const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(res) + off);
+    const bool f16 = YDT == RPFQ_F16;
+    return make_uint4(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16), add2_y(v.z, r.z, f16), add2_y(v.w, r.w, f16));
+}
+template <int YDT>
+__device__ __forceinline__ uint2 add_res4(uint2 v, const void* res, int64_t off) {
+    const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(res) + off);
+    const bool f16 = YDT == RPFQ_F16;
+    return make_uint2(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16));
+}
+
+// Fused activation of the stored output (WideArgs::act = 1): exact GELU
+// (approximate = 'none') of the value already rounded to y's dtype, computed
+// in float32 by the formula of torch's GELU kernel for 16-bit and float32
+// tensors, x * 0.5 * (1 + erf(x * sqrt(1/2))), and rounded to y's dtype by
+// the store.  The empty asm keeps that float32 rounding: without it the
+// backend may fold the last multiply and the fp16 conversion into one
+// v_fma_mixlo_f16 (a single rounding), which changes the result where the
+// exact value lies near an fp16 rounding tie, and differently per kernel.
+__device__ __forceinline__ float gelu_f(float x) {
+    float g = x * 0.5f * (1.0f + erff(x * 0.707106781186547524f));
+    asm volatile("" : "+v"(g));
+    return g;
+}
+
+template <int YDT>
+__device__ __forceinline__ float act_y(float v, int act) {
+    if (!act) return v;
+    if (YDT == RPFQ_F16) v = (float)(_Float16)v;
+    if (YDT == RPFQ_BF16) v = bf16_to_f32(f32_to_bf16(v));
+    return gelu_f(v);
+}
+// two packed 16-bit outputs of y's dtype
+__device__ __forceinline__ uint32_t gelu2_y(uint32_t v, bool f16) {
+    if (f16) {
+        const half2v h = __builtin_bit_cast(half2v, v);
+        const half2v o = {(_Float16)gelu_f((float)h.x), (_Float16)gelu_f((float)h.y)};
+        return __builtin_bit_cast(uint32_t, o);
+    }
+    return (uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v & 0xffffu))) |
+           ((uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v >> 16))) << 16);
+}
+__device__ __forceinline__ uint4 gelu8_y(uint4 v, bool f16) {
+    return make_uint4(gelu2_y(v.x, f16), gelu2_y(v.y, f16), gelu2_y(v.z, f16), gelu2_y(v.w, f16));
+}
+__device__ __forceinline__ uint16_t gelu1_y(uint16_t e, bool f16) {
+    if (f16) return __builtin_bit_cast(uint16_t, (_Float16)gelu_f((float)__builtin_bit_cast(_Float16, e)));
+    return f32_to_bf16(gelu_f(bf16_to_f32(e)));
+}
+// The same 8 outputs one at a time in a rolled loop (the 16-bit values shift
+// through the four words), so only one erf body is live: unrolled, the DMA
+// kernel's allocator pays for the epilogue's GELU with spills in its k-loop.
+__device__ __forceinline__ uint4 gelu8_rolled(uint4 v, bool f16) {
+    uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+#pragma unroll 1
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t o = gelu1_y((uint16_t)(w0 & 0xffffu), f16);
+        w0 = (w0 >> 16) | (w1 << 16);
+        w1 = (w1 >> 16) | (w2 << 16);
+        w2 = (w2 >> 16) | (w3 << 16);
+        w3 = (w3 >> 16) | (o << 16);
+    }
+    return make_uint4(w0, w1, w2, w3);
+}
+
+__device__ __forceinline__ half8 to_half8(const float* v) {
+    uint4 u;
+    u.x = pack_h2(v[0], v[1]);
+    u.y = pack_h2(v[2], v[3]);
+    u.z = pack_h2(v[4], v[5]);
+    u.w = pack_h2(v[6], v[7]);
+    return as_half8(u);
+}
+
+// Workgroup id -> tile id so that each XCD (ids are dealt round-robin over 8
+// XCDs) owns one contiguous run of tiles; consecutive tiles share an M-tile
+// and hit the same L2.
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+    int xcd = bid & 7, local = bid >> 3;
+    int q = total >> 3, r = total & 7;
+    return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+// Row i of the 32x32 MFMA accumulator element v held by lane group g (lane/32).
+__device__ __forceinline__ int acc_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }
+// LDS activation row: 32 complex columns as (re, im) fp16 pairs = 128 B,
+// padded to 144 B so the 8 lanes of a 128-bit read hit distinct banks.
+constexpr int kXRow = 144;
+constexpr int kLutWave = 32 * 32 * 4;  // 32 entries x 32 rows x fp16 pair
+
+constexpr int kTRow = 64 * 2 + 16;     // epilogue tile row: 64 fp16 outputs (+16 pad)
+
+template <int BM>
+constexpr int wide_lds_bytes() {
+    return (2 * BM * kXRow + 4 * kLutWave) > (4 * BM * kTRow) ? (2 * BM * kXRow + 4 * kLutWave)
+                                                               : (4 * BM * kTRow);
+}
+
+// Two floats -> packed fp16 pair (one v_cvt_pk_f16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+    half2v h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Fused fp16 coefficient pairs of one code byte from its U and W entries
+// (fp16 (re, im) pairs): p1 = (A11, A12) = (Wre + Ure, Wim - Uim),
+// p2 = (A21, A22) = (Wim + Uim, -Wre + Ure), each one correctly rounded fp16
+// add in the reference's recombination order (quant_i.py:534-537); one
+// v_pk_add_f16 per pair.
+__device__ __forceinline__ void fuse_h(uint32_t U, uint32_t W, uint32_t& p1, uint32_t& p2) {
+    const half2v u = __builtin_bit_cast(half2v, U), w = __builtin_bit_cast(half2v, W);
+    p1 = __builtin_bit_cast(uint32_t, w + (half2v){u.x, -u.y});
+    p2 = __builtin_bit_cast(uint32_t, (half2v){w.y, -w.x} + (half2v){u.y, u.x});
+}
+
+// Builds the wave's LUT for scale block `blk`: entries 0..15 hold U(idx),
+// 16..31 hold W(idx) as fp16 (re, im) pairs, each for the wave's 32 rows;
+// layout [entry][row] so the 32 lanes of a lookup touch 32 consecutive
+// dwords (no bank conflicts).
+template <int CB>
+__device__ __forceinline__ void build_lut(uint32_t* lut, const float4* params, int64_t n, bool active, int nblk,
+                                          int blk, const RotParams& rot, int r, int g) {
+    float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
+    if (CB != RPFQ_CB_TABLE && active) {
+        const float4* p = params + (n * nblk + blk) * 2;
+        pu = p[0];
+        pw = p[1];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t idx = (uint32_t)(g + 2 * j);
+        float2 u, w;
+        if constexpr (CB == RPFQ_CB_TABLE) {
+            const float2* t = reinterpret_cast<const float2*>(params) + n * 32;
+            u = active ? t[idx] : make_float2(0.0f, 0.0f);
+            w = active ? t[16 + idx] : make_float2(0.0f, 0.0f);
+        } else {
+            u = lut_entry<CB>(idx, pu);
+            w = lut_entry<CB>(idx, pw);
+        }
+        if (rot.rotate) {
+            u = derotate(u, rot.cu, rot.su);
+            w = derotate(w, rot.cw, rot.sw);
+        }
+        lut[idx * 32 + r] = cvt_pk(u.x, u.y);
+        lut[(16 + idx) * 32 + r] = cvt_pk(w.x, w.y);
+    }
+}
+
+// 8 consecutive activations -> 8 floats (bf16 / f32 sources).
+template <int XDT>
+__device__ __forceinline__ void load8_f32(const void* base, int64_t off, float* v) {
+    if (XDT == RPFQ_BF16) {
+        uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+            v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        }
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+}
+
+// LDS address-space views and the LDS byte address of a shared pointer.
+typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const half8* lds_h8_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
+}
+
+}  // namespace rpfq

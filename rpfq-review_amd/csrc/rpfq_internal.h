@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/rpfq.h"
 
 namespace rpfq {
@@ -60,6 +62,53 @@ struct RotParams {
     float cu, su, cw, sw;
 };
 
+inline RotParams rot_of(const rpfq_wide_desc& d) {
+    RotParams r;
+    r.rotate = d.rotate;
+    r.cu = d.rot_u[0];
+    r.su = d.rot_u[1];
+    r.cw = d.rot_w[0];
+    r.sw = d.rot_w[1];
+    return r;
+}
+
+// Launch arguments of the widely-linear GEMM kernels.
+struct WideArgs {
+    const void* x;
+    int64_t M;
+    int K, N, NT, KS, nblk, block_ks;
+    const uint4* codes;
+    const float4* params;
+    RotParams rot;
+    const float* bias;
+    const void* res;  // residual of y's dtype added to the output (NULL: none)
+    void* y;
+    int tiles_m, tiles_n;
+    int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
+    int wg_epi;     // DMA epilogue: workgroup-wide full-line stores (else per wave)
+    int act;        // 1: exact GELU of the rounded output (no residual), 0: none
+};
+
+// Compute units of the current device (cached per device, thread-safe;
+// 256 on MI355X), rounded down to a multiple of 4 so a persistent grid of
+// 2 workgroups per CU stays a multiple of 8 (XCD-local tile order).
+int device_cus();
+
+// hipFuncSetAttribute(kernel, MaxDynamicSharedMemorySize, bytes) once per
+// device: `done` holds one bit per device index (< 64; devices past that
+// set the attribute on every call).  Concurrent first calls may both set
+// it, which is harmless (the call is idempotent).
+hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t>& done);
+
+// Widely-linear GEMM launchers, one translation unit per codebook (CB):
+// wide_dma.hip (fp16 x, LDS DMA, M >= 128), wide_stream.hip (weight
+// streaming), wide_tiled.hip (register-staged tiles, bm = 32, 64 or 128).
+template <int CB> hipError_t launch_wide_dma(WideArgs& a, int ydt, hipStream_t s);
+template <int CB> hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, hipStream_t s);
+template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int ydt, hipStream_t s);
+// workgroups of the streaming kernel: one per (16-row chunk, 32-row tile)
+inline int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
+
 // launchers (rpfq_kernels.hip); return hipError_t
 hipError_t launch_unpack(const uint8_t* codes, int bits, int64_t rows, int64_t k,
                          const uint16_t* gre, const uint16_t* gim, int64_t nblk, int64_t block,
@@ -71,6 +120,7 @@ hipError_t launch_phase_linear(const void* xr, const void* xi, int xdt, int conj
 hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const uint8_t* const* planes,
                             int nplanes, const float* const* sre, const float* const* sim,
                             void* packed, hipStream_t s);
+// dispatch (wide_dispatch.hip)
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               const void* x, int xdt, int64_t M, const float* bias, const void* res,
                               void* y, int ydt, int flags, hipStream_t s);

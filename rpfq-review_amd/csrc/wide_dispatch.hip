@@ -1,0 +1,121 @@
+// Kernel choice and launch of the widely-linear layer (rpfq_wide_linear):
+// the shape, dtypes and flags pick the streaming, LDS-DMA or register-staged
+// kernel; each lives in its own translation unit per codebook.
+#include <mutex>
+
+#include "rpfq_internal.h"
+
+namespace rpfq {
+
+int device_cus() {
+    static std::atomic<int> cached[64];  // zero-initialised (static storage)
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    int n = dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        if (dev < 64) cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n & ~3;  // keep the grid a multiple of 8 (XCD-local tile order)
+}
+
+hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 64;
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
+
+// Kernel choice for a small M.  A tiled kernel gives each workgroup one
+// 128-row x 128-column output tile through all of K, so while the launch is
+// at most one tile deep it costs about one tile's latency, ~5 + KS us on
+// MI355X whatever M and N'.  The streaming kernel spreads its (16-row chunk,
+// 32-row tile) groups over every SIMD: with split K ~4.5 us + groups x
+// (7.7 + 0.49 KS) ns; with per-(row, block) scales (one wave per group
+// through all of K) ~(2 + 0.55 KS) us while the groups fit ~900 at once,
+// proportionally longer past that.  The fits are from fp16 ViT-B/L and
+// DeiT-Ti layer shapes at M = 24 .. 1576; streaming is taken where it is
+// predicted 10% faster, and always for M <= 16.
+static bool stream_pays(const WideArgs& a) {
+    if (a.M <= 16) return true;
+    const int64_t tiles = ((a.M + 127) / 128) * ((a.NT + 3) / 4);
+    if (tiles > 2 * (int64_t)device_cus()) return false;  // more than one round of the tiled grid
+    const double groups = (double)sk_groups(a);
+    const double t_stream = a.nblk > 1 ? (2.0 + 0.55 * a.KS) * (groups > 900.0 ? groups / 900.0 : 1.0)
+                                       : 4.5 + groups * (0.0077 + 0.00049 * a.KS);
+    const double t_tiled = 5.0 + a.KS;
+    return t_stream < 0.9 * t_tiled;
+}
+
+#ifndef RPFQ_DMA_MIN_M
+#define RPFQ_DMA_MIN_M 128
+#endif
+// The kernel a launch runs (RPFQ_KERNEL_*), from the shape, dtypes and the
+// kernel-choice flags (the GELU bit already moved into a.act).
+static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
+    if ((flags & RPFQ_FLAG_STREAM) || (!(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)) && stream_pays(a)))
+        return RPFQ_KERNEL_STREAM;
+    flags &= ~RPFQ_FLAG_NO_STREAM;
+    // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
+    // spill in its k-loop, so they take the register-staged kernel)
+    if (xdt == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M && !(a.act && ydt == RPFQ_BF16))
+        return RPFQ_KERNEL_DMA;
+    return RPFQ_KERNEL_TILED;
+}
+
+template <int CB>
+static hipError_t wide_cb(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s) {
+    const int k = choose_kernel(a, xdt, ydt, flags);
+    if (k == RPFQ_KERNEL_STREAM) return launch_wide_stream<CB>(a, xdt, ydt, s);
+    if (k == RPFQ_KERNEL_DMA) return launch_wide_dma<CB>(a, ydt, s);
+    flags &= ~RPFQ_FLAG_NO_STREAM;
+    const int bm = (flags & RPFQ_FLAG_TILE_M128) ? 128 : a.M <= 32 ? 32 : a.M <= 64 ? 64 : 128;
+    return launch_wide_tiled<CB>(a, bm, xdt, ydt, s);
+}
+
+// Shape fields of the launch arguments (what the kernel choice reads).
+static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
+    WideArgs a = {};
+    a.M = M;
+    a.K = (int)g.K;
+    a.N = (int)g.N;
+    a.NT = (int)g.NT;
+    a.KS = (int)g.KS;
+    a.nblk = (int)g.nblk;
+    a.block_ks = (int)g.block_ks;
+    a.act = (flags & RPFQ_FLAG_GELU) ? 1 : 0;  // an epilogue op, not a kernel choice
+    return a;
+}
+
+int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags) {
+    return choose_kernel(wide_shape(g, M, flags), xdt, ydt, flags & ~RPFQ_FLAG_GELU);
+}
+
+hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
+                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
+                              hipStream_t s) {
+    WideArgs a = wide_shape(g, M, flags);
+    flags &= ~RPFQ_FLAG_GELU;
+    a.x = x;
+    a.codes = reinterpret_cast<const uint4*>(packed);
+    a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
+    a.rot = rot_of(d);
+    a.bias = bias;
+    a.res = res;
+    a.y = y;
+    a.vec_store = (g.N % 8 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);  // also covers 4-wide stores
+    // whole 128-column tiles and >= 8 k-steps (ViT-B/L, not DeiT-Ti's K' = 96 / N' = 96 layers):
+    // full-line stores pay for the two workgroup barriers per half tile
+    a.wg_epi = (g.N % 128 == 0) && (g.KS >= 8);
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN: return wide_cb<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_PSK16: return wide_cb<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_TABLE: return wide_cb<RPFQ_CB_TABLE>(a, xdt, ydt, flags, s);
+        default: return wide_cb<RPFQ_CB_AXIS>(a, xdt, ydt, flags, s);
+    }
+}
+
+}  // namespace rpfq

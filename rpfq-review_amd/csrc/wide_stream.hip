@@ -1,0 +1,364 @@
+// Widely-linear layer for small M: weight streaming.  Compiled once per
+// codebook (RPFQ_CB_SEL).
+#include "rpfq_device.h"
+
+#ifndef RPFQ_CB_SEL
+#error "compile once per codebook with -DRPFQ_CB_SEL=<RPFQ_CB_*>"
+#endif
+
+namespace rpfq {
+
+
+
+// ---------------------------------------------------------------------------
+// widely-linear layer for small M: weight streaming
+// ---------------------------------------------------------------------------
+// The packed codes are the only large operand, so each wave streams one
+// 32-row tile of them (KS contiguous 1-KB blocks) and contracts it with a
+// chunk of up to 16 activation rows on v_mfma_f32_16x16x32_f16 (workgroup
+// = chunk x tiles + tile; M <= 16 is one chunk): the decoded weights are the
+// A operand (16 output rows x 16 complex columns as (re, im) fp16 pairs),
+// the activations the B operand (its 16 columns are the x rows).
+//   * codes: lane (r16 = lane & 15, q = lane >> 4) loads 8 B of rows r16 and
+//     16 + r16 per k-step: bytes 8q .. 8q+7 of the row's 32, i.e. the dwords
+//     s = 2 (q & 1) + t (t = 0, 1) of lane group g = q >> 1, which hold the
+//     complex columns 8 s + 4 g + e.  MFMA t takes dword t, so the four lane
+//     groups contribute 16 distinct columns per MFMA and 32 per k-step; the
+//     decoded pairs (A11, A12) / (A21, A22) of a column are directly the two
+//     k slots that meet (x_re, x_im) of the same column in B.
+//   * LUT: [entry][64 slots] fp16 (re, im) pairs at LDS address 0 (one tile
+//     per workgroup), each row held twice: row 16 h + r16 in slots
+//     32 h + 16 c + r16 (c = 0, 1), and lane group q reads copy c = q & 1,
+//     so the 32 lanes of a half-wave hit 32 distinct banks modulo 32.
+//     Entry e sits at e * 256 + 4 slot: one v_perm_b32 puts the index
+//     nibble into byte 1 of the slot address, and the W entries (e >= 16)
+//     are reached through the ds_read immediate offset.
+//   * activations: lane (m, q) loads the 4 re and 4 im values of its B
+//     fragment straight from x (L2-resident) and interleaves them with
+//     v_perm_b32.  Rows past M read row M - 1: their MFMA columns are never
+//     stored.  Columns past K' (K' % 32 != 0 only) are zeroed.
+//   * split K for layers of few tiles: the NW = 2 or 4 waves of a workgroup
+//     share one tile and its LUT (each builds 1 / NW of it), each walks
+//     1 / NW of the k-steps, and wave 0 sums the partials through LDS (a
+//     small layer then covers NW times the SIMDs);
+//   * codes and activations of k-step ks + SK_PF are requested before k-step
+//     ks is decoded, by unconditional loads in straight-line code (uniform
+//     base + constant lane offset) so the wait counts stay exact; occupancy
+//     hides the LDS latency of the decode.
+#ifndef RPFQ_SK_PF
+#define RPFQ_SK_PF 4
+#endif
+constexpr int SK_PF = RPFQ_SK_PF;   // prefetch distance in k-steps
+constexpr int kSkLut = 32 * 64 * 4;  // 8 KB LUT
+// LDS of a workgroup of NW waves: the LUT, and with split K the partial sums
+// of waves 1 .. NW-1
+constexpr int sk_lds(int nw) { return kSkLut + (nw - 1) * 16 * 64 * 4; }
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// LUT of the skinny kernel from row R's parameters (pu, pw), R = lane & 31:
+// entry idx in slots 32 (R >> 4) + (R & 15) and + 16; lane group g writes
+// the even or odd indices.
+// NJ of the 8 (even or odd) indices from j0 on: a whole LUT (NJ = 8), or the
+// part one wave of a split-K workgroup of NW waves builds (NJ = 8 / NW,
+// j0 = NJ wave).
+template <int CB, int NJ = 8>
+__device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, const RotParams& rot, int R, int g,
+                                             int j0 = 0) {
+    const int s0 = 32 * (R >> 4) + (R & 15);
+    float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
+    if constexpr (CB != RPFQ_CB_TABLE) {
+        pu = p[0];
+        pw = p[1];
+    }
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+        const uint32_t idx = (uint32_t)(g + 2 * (j0 + jj));
+        float2 u, w;
+        if constexpr (CB == RPFQ_CB_TABLE) {  // p = the row's 32 (re, im) values
+            u = reinterpret_cast<const float2*>(p)[idx];
+            w = reinterpret_cast<const float2*>(p)[16 + idx];
+        } else {
+            u = lut_entry<CB>(idx, pu);
+            w = lut_entry<CB>(idx, pw);
+        }
+        if (rot.rotate) {
+            u = derotate(u, rot.cu, rot.su);
+            w = derotate(w, rot.cw, rot.sw);
+        }
+        const uint32_t hu = cvt_pk(u.x, u.y), hw = cvt_pk(w.x, w.y);
+        lut[idx * 64 + s0] = hu;
+        lut[idx * 64 + s0 + 16] = hu;
+        lut[(16 + idx) * 64 + s0] = hw;
+        lut[(16 + idx) * 64 + s0 + 16] = hw;
+    }
+}
+
+// 4 consecutive activations at element offset `off`: the raw 16-bit values
+// (fp16, bf16; converted at use so the load stays in flight) or, for
+// float32, 4 fp16 converted on load.
+template <int XDT>
+__device__ __forceinline__ uint2 load4_raw(const void* base, int64_t off) {
+    if (XDT != RPFQ_F32) return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + off);
+    const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+    return make_uint2(pack_h2(f.x, f.y), pack_h2(f.z, f.w));
+}
+template <int XDT>
+__device__ __forceinline__ uint2 raw4_f16(uint2 v) {
+    if (XDT != RPFQ_BF16) return v;
+    return make_uint2(pack_h2(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16)),
+                      pack_h2(bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16)));
+}
+
+// PB: per-(row, block) scales (the LUT is rebuilt at each block start);
+// KT: K' % 32 != 0 (activation columns past K' are zeroed);
+// NW (1 with PB): waves per workgroup.  NW = 2 or 4 splits K: the waves
+// share the tile's LUT, take 1 / NW of the k-steps each, and wave 0 adds the
+// other partial sums (through LDS, in a fixed order) before the epilogue.
+// NW = 1: one wave streams the tile's whole K.
+#ifndef RPFQ_SK_OCC
+#define RPFQ_SK_OCC 4  // waves per SIMD the register budget is sized for
+#endif
+template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
+__global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
+    const int lane = threadIdx.x & 63;
+    const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, q = lane >> 4;
+    const int R = lane & 31, g = lane >> 5;
+    // workgroup -> (16-row chunk of x, 32-row tile of the codes), chunk-major
+    const int mc = (int)(blockIdx.x / (unsigned)a.NT);
+    const int tile = (int)blockIdx.x - mc * a.NT;
+    const int KS = a.KS, K = a.K;
+    const int64_t m0 = 16 * (int64_t)mc;                  // first x row of the chunk
+    const int M = (int)min((int64_t)16, a.M - m0);        // rows of the chunk
+    const void* xc = reinterpret_cast<const char*>(a.x) + m0 * 2 * K * (XDT == RPFQ_F32 ? 4 : 2);
+    const int chunk = (KS + NW - 1) / NW;
+    const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
+
+    // uniform bases + constant lane offsets (global_load saddr + voffset)
+    const uint2* ctile = reinterpret_cast<const uint2*>(a.codes) + (int64_t)tile * KS * 128;
+    const int coff = r16 * 4 + q;
+    const bool m_ok = r16 < M;
+    const int xoff = (m_ok ? r16 : M - 1) * 2 * K + 16 * (q & 1) + 4 * (q >> 1);  // + 32 ks + 8 t
+    const int xcol = 16 * (q & 1) + 4 * (q >> 1);
+    struct Step {
+        uint2 c[2];          // code dwords (t = 0, 1) of rows r16 and 16 + r16
+        uint2 xr[2], xi[2];  // activations of MFMA t: 4 re, 4 im (raw 16-bit or fp16)
+    };
+    auto load_step = [&](int ks, Step& st) {
+        const int kc = ks < ke ? ks : (ke > 0 ? ke - 1 : 0);  // past the range: an L1 hit, unused
+        const uint2* cp = ctile + kc * 128;
+        st.c[0] = cp[coff];
+        st.c[1] = cp[coff + 64];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (KT) {
+                const int col = 32 * kc + xcol + 8 * t;
+                const int off = xoff - xcol + (col < K ? col : 0);  // K' tail: in bounds, zeroed at use
+                st.xr[t] = load4_raw<XDT>(xc, off);
+                st.xi[t] = load4_raw<XDT>(xc, off + K);
+            } else {
+                const int64_t xb = 32 * (int64_t)kc + 8 * t;
+                st.xr[t] = load4_raw<XDT>(xc, xb + xoff);
+                st.xi[t] = load4_raw<XDT>(xc, xb + K + xoff);
+            }
+        }
+    };
+    Step ring[SK_PF];
+#pragma unroll
+    for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
+
+    int blk = 0;
+    {  // split K: each wave builds 1 / NW of the shared LUT
+        const float4* p = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
+        if (NW == 1)
+            build_lut_sk<CB>(lut, p, a.rot, R, g);
+        else
+            build_lut_sk<CB, 8 / NW>(lut, p, a.rot, R, g, (8 / NW) * wave);
+    }
+    if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+    // slot of (row group h, copy q & 1, row r16) in byte 0 of the address
+    const uint32_t slot0 = (uint32_t)(16 * (q & 1) + r16) * 4;
+
+    floatx4 acc_re[2], acc_im[2];
+    acc_re[0] = acc_re[1] = acc_im[0] = acc_im[1] = floatx4{0, 0, 0, 0};
+    auto compute = [&](int ks, const Step& st) {
+        half8 bx[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint2 re = raw4_f16<XDT>(st.xr[t]), im = raw4_f16<XDT>(st.xi[t]);
+            uint4 b = make_uint4(__builtin_amdgcn_perm(im.x, re.x, 0x05040100u),
+                                 __builtin_amdgcn_perm(im.x, re.x, 0x07060302u),
+                                 __builtin_amdgcn_perm(im.y, re.y, 0x05040100u),
+                                 __builtin_amdgcn_perm(im.y, re.y, 0x07060302u));
+            if (KT && 32 * ks + xcol + 8 * t >= K) b = make_uint4(0, 0, 0, 0);
+            bx[t] = as_half8(b);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t slot = slot0 + 128 * h;
+            const uint32_t words[2] = {st.c[h].x, st.c[h].y};
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t pu = words[t] & 0x0f0f0f0fu;
+                const uint32_t pw = (words[t] >> 4) & 0x0f0f0f0fu;
+                uint32_t p1[4], p2[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t sel = 0x03020000u | ((4u + e) << 8);
+                    const uint32_t U = *((lds_u32_t)__builtin_amdgcn_perm(pu, slot, sel));
+                    const uint32_t W = *((lds_u32_t)__builtin_amdgcn_perm(pw, slot, sel) + 16 * 64);
+                    fuse_h(U, W, p1[e], p2[e]);
+                }
+                const half8 are = as_half8(make_uint4(p1[0], p1[1], p1[2], p1[3]));
+                const half8 aim = as_half8(make_uint4(p2[0], p2[1], p2[2], p2[3]));
+                acc_re[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(are, bx[t], acc_re[h], 0, 0, 0);
+                acc_im[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aim, bx[t], acc_im[h], 0, 0, 0);
+            }
+        }
+    };
+    for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
+#pragma unroll
+        for (int i = 0; i < SK_PF; ++i) {
+            const int ks = ks0 + i;
+            if (ks >= ke) break;
+            const Step cur = ring[i];
+            load_step(ks + SK_PF, ring[i]);  // past the end: reloads the last k-step, unused
+            if (PB) {  // per-(row, block) scales: new LUT at each block start
+                const int nb = ks / a.block_ks;
+                if (nb != blk) {
+                    blk = nb;
+                    const float4* p = a.params + (((int64_t)tile * 32 + R) * a.nblk + nb) * 2;
+                    build_lut_sk<CB>(lut, p, a.rot, R, g);
+                }
+            }
+            compute(ks, cur);
+        }
+    }
+
+    if (NW > 1) {  // waves 1 .. NW-1 hand their partial sums to wave 0
+        float* red = reinterpret_cast<float*>(smem + kSkLut);
+        if (wave > 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                red[((wave - 1) * 16 + v) * 64 + lane] = acc_re[0][v];
+                red[((wave - 1) * 16 + 4 + v) * 64 + lane] = acc_re[1][v];
+                red[((wave - 1) * 16 + 8 + v) * 64 + lane] = acc_im[0][v];
+                red[((wave - 1) * 16 + 12 + v) * 64 + lane] = acc_im[1][v];
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < NW - 1; ++w) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                acc_re[0][v] += red[(w * 16 + v) * 64 + lane];
+                acc_re[1][v] += red[(w * 16 + 4 + v) * 64 + lane];
+                acc_im[0][v] += red[(w * 16 + 8 + v) * 64 + lane];
+                acc_im[1][v] += red[(w * 16 + 12 + v) * 64 + lane];
+            }
+        }
+    }
+
+    // Epilogue: lane (m = r16, q) holds outputs n = 32 tile + 16 h + 4 q + v
+    // of x row m; rows past M and outputs past N' store nothing.
+    if (!m_ok) return;
+    const int64_t ldy = 2 * (int64_t)a.N;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t n0 = (int64_t)tile * 32 + 16 * h + 4 * q;
+        float vr[4], vi[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t n = n0 + v;
+            const bool ok = n < a.N;
+            vr[v] = acc_re[h][v] + ((a.bias && ok) ? a.bias[n] : 0.0f);
+            vi[v] = acc_im[h][v] + ((a.bias && ok) ? a.bias[a.N + n] : 0.0f);
+        }
+        const int64_t base = (m0 + r16) * ldy + n0;
+        if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
+            uint2 hr = make_uint2(cvt_pk(vr[0], vr[1]), cvt_pk(vr[2], vr[3]));
+            uint2 hi = make_uint2(cvt_pk(vi[0], vi[1]), cvt_pk(vi[2], vi[3]));
+            if (a.res) {
+                hr = add_res4<YDT>(hr, a.res, base);
+                hi = add_res4<YDT>(hi, a.res, base + a.N);
+            }
+            if (a.act) {
+                hr = make_uint2(gelu2_y(hr.x, true), gelu2_y(hr.y, true));
+                hi = make_uint2(gelu2_y(hi.x, true), gelu2_y(hi.y, true));
+            }
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = hr;
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base + a.N) = hi;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (n0 + v < a.N) {
+                    store1<YDT>(a.y, base + v, with_res<YDT>(act_y<YDT>(vr[v], a.act), a.res, base + v));
+                    store1<YDT>(a.y, base + a.N + v, with_res<YDT>(act_y<YDT>(vi[v], a.act), a.res, base + a.N + v));
+                }
+            }
+        }
+    }
+}
+
+template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
+static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, NW>), dim3((unsigned)sk_groups(a)),
+                       dim3(64 * NW), sk_lds(NW), s, a);
+    return hipGetLastError();
+}
+
+// Split K when the launch has too few workgroups to give every SIMD a few
+// waves (a single layer at batch 1): over 4 waves below 400 workgroups, over
+// 2 from there (less LUT building and reduction per k-step once the groups
+// alone fill the SIMDs; ViT-B/16 batch-1 forward 0.834 -> 0.772 ms, and 2
+// waves already from 128 groups measured slower); a long stream of tiles
+// runs one wave each.
+#ifndef RPFQ_SK_SPLIT_TILES
+#define RPFQ_SK_SPLIT_TILES 4096
+#endif
+#ifndef RPFQ_SK_NW2_GROUPS
+#define RPFQ_SK_NW2_GROUPS 400
+#endif
+template <int XDT, int YDT, int CB>
+static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
+    const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
+    if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, true, false, 1>(a, s);
+    const int64_t groups = sk_groups(a);
+    if (groups >= RPFQ_SK_NW2_GROUPS && groups < RPFQ_SK_SPLIT_TILES)
+        return kt ? wide_sk_go<XDT, YDT, CB, false, true, 2>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 2>(a, s);
+    if (groups < RPFQ_SK_SPLIT_TILES)
+        return kt ? wide_sk_go<XDT, YDT, CB, false, true, 4>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 4>(a, s);
+    return kt ? wide_sk_go<XDT, YDT, CB, false, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 1>(a, s);
+}
+
+template <int XDT, int CB>
+static hipError_t stream_y(WideArgs& a, int ydt, hipStream_t s) {
+    switch (ydt) {
+        case RPFQ_F32: return wide_sk<XDT, RPFQ_F32, CB>(a, s);
+        case RPFQ_F16: return wide_sk<XDT, RPFQ_F16, CB>(a, s);
+        default: return wide_sk<XDT, RPFQ_BF16, CB>(a, s);
+    }
+}
+
+template <int CB>
+hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return stream_y<RPFQ_F32, CB>(a, ydt, s);
+        case RPFQ_F16: return stream_y<RPFQ_F16, CB>(a, ydt, s);
+        default: return stream_y<RPFQ_BF16, CB>(a, ydt, s);
+    }
+}
+
+template hipError_t launch_wide_stream<RPFQ_CB_SEL>(WideArgs&, int, int, hipStream_t);
+
+}  // namespace rpfq

@@ -13,6 +13,17 @@ import torch
 
 from . import _native as N
 
+
+def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """t itself when it is contiguous with a 16-byte aligned start (what the
+    C ABI requires of row-major operands), else a fresh contiguous copy: a
+    contiguous view at an odd offset is copied too, since contiguous() would
+    return it unchanged."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 # Optional per-launch timing hook: when set, PackedWide.linear records HIP
 # events around each wide-linear launch on the launch stream and hands
 # (start_event, end_event, flops, algorithmic_bytes, shape) to the recorder.
@@ -89,14 +100,13 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
                out_dtype: torch.dtype | None = None, act_bits: int = 0) -> torch.Tensor:
     """nn.LayerNorm over the last dimension on the device (rpfq_layer_norm):
     float32 statistics, output in out_dtype (default x.dtype).  weight/bias
-    are taken as float32.  act_bits > 0: the output is also fake-quantized
-    per row and half (rpfq_layer_norm_act_quant, bit-identical to
-    act_quant(layer_norm(x)))."""
+    are taken as float32.  act_bits > 0: the float32 LayerNorm output is
+    fake-quantized per row and half before the rounding to out_dtype
+    (rpfq_layer_norm_act_quant, bit-identical to
+    act_quant(layer_norm(x, out_dtype=float32), out_dtype=out_dtype))."""
     N.require_device(x, weight, bias)
     c = x.shape[-1]
-    x2 = x.reshape(-1, c)
-    if not x2.is_contiguous() or x2.data_ptr() % 16:
-        x2 = x2.contiguous()
+    x2 = _aligned_rows(x.reshape(-1, c))
     y = torch.empty(x2.shape, dtype=out_dtype or x.dtype, device=x.device)
     if x2.shape[0] == 0:
         return y.reshape(x.shape)
@@ -187,18 +197,14 @@ class PackedWide:
         if x.shape[-1] != self.in_features:
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
         lead = x.shape[:-1]
-        x2 = x.reshape(-1, self.in_features)
-        if not x2.is_contiguous() or x2.data_ptr() % 16:
-            x2 = x2.contiguous()
+        x2 = _aligned_rows(x.reshape(-1, self.in_features))
         m = x2.shape[0]
         out_dtype = out_dtype or x.dtype
         y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
         if residual is not None:
             if residual.shape[:-1] != lead or residual.shape[-1] != self.out_features:
                 raise ValueError(f"residual must have shape {tuple(lead) + (self.out_features,)}")
-            r2 = residual.to(out_dtype).reshape(-1, self.out_features)
-            if not r2.is_contiguous() or r2.data_ptr() % 16:
-                r2 = r2.contiguous()
+            r2 = _aligned_rows(residual.to(out_dtype).reshape(-1, self.out_features))
         if m == 0:
             return y.reshape(*lead, self.out_features)
         if bias is not None:

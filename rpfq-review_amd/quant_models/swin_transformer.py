@@ -61,9 +61,10 @@ class WindowAttention(nn.Module):
         bias = self.relative_position_bias_table[self.relative_position_index.view(-1)].view(n, n, -1)
         return bias.permute(2, 0, 1).contiguous().unsqueeze(0)  # 1, heads, N, N
 
-    def forward(self, x, mask=None):
+    def forward(self, x, mask=None, prequantized: bool = False):
         bw, n, c = x.shape
-        qkv = self.qkv(x).reshape(bw, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        qkv = call_layer(self.qkv, x, prequantized).reshape(bw, n, 3, self.num_heads, self.head_dim)
+        qkv = qkv.permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)
         bias = self._rel_bias().to(q.dtype)
         if mask is not None:
@@ -108,7 +109,11 @@ class SwinTransformerBlock(nn.Module):
         mask = win.unsqueeze(1) - win.unsqueeze(2)
         return mask.masked_fill(mask != 0, float(-100.0)).masked_fill(mask == 0, 0.0)
 
-    def _attn(self, x):
+    def _attn(self, x, prequantized: bool = False):
+        """Shifted-window attention of normalised tokens x; prequantized: x
+        already carries qkv's activation quantization (per token row, so the
+        padding, roll and window partition below commute with it: zero rows
+        quantize to zero)."""
         b, h0, w0, c = x.shape
         h, w = self.padded
         if (h, w) != (h0, w0):  # pad to whole windows, cropped below
@@ -116,7 +121,7 @@ class SwinTransformerBlock(nn.Module):
         if self.shift_size:
             x = torch.roll(x, shifts=(-self.shift_size, -self.shift_size), dims=(1, 2))
         win = window_partition(x, self.window_size)
-        win = self.attn(win, mask=self.attn_mask)
+        win = self.attn(win, mask=self.attn_mask, prequantized=prequantized)
         x = window_reverse(win, self.window_size, h, w)
         if self.shift_size:
             x = torch.roll(x, shifts=(self.shift_size, self.shift_size), dims=(1, 2))
@@ -124,7 +129,8 @@ class SwinTransformerBlock(nn.Module):
 
     def forward(self, x):
         b, h, w, c = x.shape
-        x = x + self._attn(norm_fwd(self.norm1, x))
+        hn, q = norm_quant_fwd(self.norm1, x, self.attn.qkv)
+        x = x + self._attn(hn, q)
         x = x.reshape(b, -1, c)
         if _fused(self, x):  # the MLP residual add fused into fc2's store
             hn, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)

@@ -344,6 +344,63 @@ def test_wide_linear_kernels_agree(case, m, flags):
     check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
+# The packed layer shapes (N', K') the headline models run on the tiled
+# kernels at batch >= 1: ViT-B/16 qkv, proj, fc1, fc2 and ViT-L/16 fc2 (axis
+# codes, 2 stages) and ViT-L/16 qkv / fc2 in 16-PSK.
+REAL_SHAPES = [
+    (1152, 384, "axis", 2, 0, None),
+    (384, 384, "axis", 2, 0, None),
+    (1536, 384, "axis", 2, 0, None),
+    (384, 1536, "axis", 2, 0, None),
+    (512, 2048, "axis", 2, 0, None),
+    (1536, 512, "psk16", 1, 0, None),
+    (512, 2048, "psk16", 1, 0, None),
+]
+
+
+@pytest.mark.parametrize("flags", [0, 2], ids=["auto", "tiled"])
+@pytest.mark.parametrize("m", [128, 300, 1000])
+@pytest.mark.parametrize("case", REAL_SHAPES, ids=[f"{c[0]}x{c[1]}-{c[2]}" for c in REAL_SHAPES])
+def test_wide_linear_model_shapes(case, m, flags):
+    """The model layer shapes against the oracle at M = 128, 300, 1000 (the
+    LDS-DMA kernel under RPFQ_FLAG_NO_STREAM and, by default, whichever
+    kernel the shape selects), K' up to 2048 (64 k-steps), fp16 and float32
+    outputs."""
+    r = rng(1500 + m + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    xf = x.float().numpy().astype(np.float64)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32, flags=flags).cpu().numpy()
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
+    y16 = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16, flags=flags).float().cpu().numpy()
+    check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+
+
+@pytest.mark.parametrize("case", [REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[1], REAL_SHAPES[0]],
+                         ids=["fc1", "fc2", "proj", "qkv"])
+def test_wide_linear_full_batch_rows(case):
+    """ViT-B/16 at batch 256 (M = 50,432 rows): the DMA kernel's output on
+    sampled rows against the oracle -- the first m-tile, the last m-tile
+    (shifted back to end at row M), 256 random rows -- with fp16 outputs as
+    the model stores them.  proj and fc2 (N' = 384: 1,182 tiles, 2.31 rounds
+    of the persistent grid) cover a partial last round."""
+    r = rng(1600 + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    m = 50432
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16).to(DEV)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    ops, N = qm()
+    assert pw.kernel_for(m, torch.float16, torch.float16) == N.KERNEL_DMA
+    y = pw.linear(x, tdev(bias), out_dtype=torch.float16)
+    rows = np.unique(np.concatenate([np.arange(128), np.arange(m - 128, m),
+                                     r.choice(m, size=256, replace=False)]))
+    idx = torch.from_numpy(rows).to(DEV)
+    ys = y.index_select(0, idx).float().cpu().numpy()
+    xf = x.index_select(0, idx).float().cpu().numpy().astype(np.float64)
+    check_against_oracle(ys, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+
+
 def test_wide_linear_kernels_consistent():
     """Both kernels contract the same fp16 operands (they differ only in the
     k order inside each MFMA), so float32 outputs agree to accumulation order."""
@@ -436,13 +493,16 @@ def test_wide_linear_streaming_dtypes(xdt, ydt, m):
     check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
 
 
-@pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640), (2, 131104, 64),
-                                       (12, 131072, 96), (1, 131200, 200)])
+@pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640), (3, 16500, 200),
+                                       (4, 3000, 2048), (2, 131104, 64), (12, 131072, 96), (1, 131200, 200)])
 def test_wide_linear_streaming_persistent(m, n_c, k_c):
-    """Large N': below 4096 tiles the split-K form (4 waves per tile), from
-    4096 tiles on one wave per tile (the last three cases), with K' tails and
-    K' beyond 16 k-steps.  The streaming kernel and the tiled kernel
-    (RPFQ_FLAG_NO_STREAM) contract the same fp16 operands, so float32
+    """Large N' on the streaming kernel's three forms: split K over 2 waves
+    per tile for 400 .. 4095 workgroups (66000 x 96 at M = 8: 2063 groups;
+    70000 x 64: 2188; 16500 x 640: 516; 16500 x 200: 516 with a K' tail),
+    over 4 waves below 400 (3000 x 2048: 94 groups, 64 k-steps), and one
+    wave per tile from 4096 workgroups (the 131,072+ row cases), with K'
+    tails and K' beyond 16 k-steps.  The streaming kernel and the tiled
+    kernel (RPFQ_FLAG_NO_STREAM) contract the same fp16 operands, so float32
     outputs agree to accumulation order."""
     ops, N = qm()
     r = rng(900 + m)
@@ -537,6 +597,29 @@ def test_wide_linear_residual_in_place():
         assert torch.equal(y, want), (m, flags)
 
 
+def test_misaligned_views_are_copied():
+    """Contiguous views that start off the C ABI's 16-byte row alignment (an
+    odd element offset into a flat buffer) are copied before the call, for
+    x, the residual and the LayerNorm input: results equal those of aligned
+    copies of the same data."""
+    ops, _ = qm()
+    r = rng(1700)
+    pw, *_ = build_packed(r, CASES[1])
+    m = 5
+    flat = tdev(r.standard_normal(m * 768 + 1).astype(np.float16))
+    x = flat[1:].view(m, 768)
+    assert x.is_contiguous() and x.data_ptr() % 16 != 0
+    assert torch.equal(pw.linear(x, None, out_dtype=torch.float32), pw.linear(x.clone(), None, out_dtype=torch.float32))
+    rflat = tdev(r.standard_normal(m * 3072 + 3).astype(np.float16))
+    res = rflat[3:].view(m, 3072)
+    assert res.data_ptr() % 16 != 0
+    assert torch.equal(pw.linear(x, None, out_dtype=torch.float16, residual=res),
+                       pw.linear(x.clone(), None, out_dtype=torch.float16, residual=res.clone()))
+    g = tdev(r.standard_normal(768).astype(np.float32))
+    b = tdev(r.standard_normal(768).astype(np.float32))
+    assert torch.equal(ops.layer_norm(x, g, b, 1e-6), ops.layer_norm(x.clone(), g, b, 1e-6))
+
+
 # ---------------------------------------------------------------------------
 # LayerNorm (rpfq_layer_norm) against a float64 restatement of nn.LayerNorm
 # ---------------------------------------------------------------------------
@@ -570,16 +653,23 @@ def test_layer_norm(m, c, xdt, ydt):
                                      (torch.bfloat16, torch.bfloat16)])
 @pytest.mark.parametrize("bits", [2, 4, 8])
 def test_layer_norm_act_quant_bit_exact(m, c, xdt, ydt, bits):
-    """rpfq_layer_norm_act_quant == rpfq_act_quant(rpfq_layer_norm(x)) bit for
-    bit (the LN output is rounded to y's dtype before it is quantized)."""
+    """rpfq_layer_norm_act_quant == rpfq_act_quant(rpfq_layer_norm(x) in
+    float32) rounded to y's dtype, bit for bit: the float32 LN output is
+    quantized (as the reference quantizes its float32 LayerNorm output) and
+    only the quantized value is rounded."""
     ops, _ = qm()
     r = rng(1300 + c + bits)
     x = torch.from_numpy((r.standard_normal((m, c)) * 2 + 0.5).astype(np.float32)).to(xdt).to(DEV)
     g = tdev(r.standard_normal(c).astype(np.float32))
     b = tdev(r.standard_normal(c).astype(np.float32))
     fused = ops.layer_norm(x, g, b, 1e-6, out_dtype=ydt, act_bits=bits)
-    two = ops.act_quant(ops.layer_norm(x, g, b, 1e-6, out_dtype=ydt), bits)
+    two = ops.act_quant(ops.layer_norm(x, g, b, 1e-6, out_dtype=torch.float32), bits, out_dtype=ydt)
     assert torch.equal(fused, two)
+    # and the quantization itself is the oracle's on that float32 LN output
+    ln = ops.layer_norm(x, g, b, 1e-6, out_dtype=torch.float32).cpu().numpy()
+    qr, qi = O.act_quant(ln[:, :c // 2], ln[:, c // 2:], bits)
+    ref = torch.from_numpy(np.concatenate([qr, qi], axis=1)).to(ydt)
+    assert torch.equal(fused.cpu(), ref)
 
 
 @pytest.mark.parametrize("k", [8, 384, 1536])
