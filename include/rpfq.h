@@ -12,7 +12,8 @@
  *   - argument validation happens on the host before any HIP call, so every
  *     shape / null / alignment / enum error is reported without a GPU;
  *   - the library holds no mutable global state: calls are reentrant and
- *     may be issued from several threads on different streams.
+ *     may be issued from several threads on different streams (the one
+ *     exception, rpfq_quantize_wide_noalloc, says so at its declaration).
  *
  * Feature layout: a "wide" (widely-linear) layer maps x = [x_re | x_im]
  * ([M, 2K'] row-major) to y = [y_re | y_im] ([M, 2N']) with
@@ -297,6 +298,22 @@ size_t rpfq_quantize_workspace_bytes(const rpfq_quant_desc* desc);
  */
 int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
                        float* scales, uint8_t* codes, void* work, size_t work_bytes, void* stream);
+
+/*
+ * rpfq_quantize_wide without a workspace argument and without any device
+ * allocation: the float64 partials live in a static device array of this
+ * library (64 KiB per GPU, held until the process ends), so the call makes
+ * no hipMalloc / hipFree and calls no allocating routine.  Inputs, outputs
+ * and results are those of rpfq_quantize_wide (bit-identical); shapes whose
+ * workspace would exceed the array are rejected (RPFQ_ERR_SHAPE).  Every
+ * call on a GPU shares that GPU's array, so calls that overlap on one GPU
+ * (concurrent streams, several host threads) race; calls ordered on one
+ * stream do not.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving or training
+ * loops, harnesses that forbid allocation).
+ */
+int rpfq_quantize_wide_noalloc(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
+                               float* scales, uint8_t* codes, void* stream);
 
 #ifdef __cplusplus
 }

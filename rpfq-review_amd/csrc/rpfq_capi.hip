@@ -269,8 +269,10 @@ size_t rpfq_quantize_workspace_bytes(const rpfq_quant_desc* desc) {
     return (size_t)rpfq::kQuantMaxBlocks * 8 * sizeof(double);
 }
 
-int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
-                       float* scales, uint8_t* codes, void* work, size_t work_bytes, void* stream) {
+// Shape, method and pointer checks shared by rpfq_quantize_wide and its
+// no-allocation variant (everything but the workspace).
+static int check_quantize(const rpfq_quant_desc* desc, const float* weight, const float* a_q, const float* scales,
+                          const uint8_t* codes) {
     if (!desc) return fail(RPFQ_ERR_NULL, "desc is NULL");
     if (desc->n_complex <= 0 || desc->k_complex <= 0)
         return fail(RPFQ_ERR_SHAPE, "n_complex=%lld k_complex=%lld must be positive",
@@ -285,11 +287,19 @@ int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const f
         if (desc->steps[p] < 1 || desc->steps[p] > 4)
             return fail(RPFQ_ERR_VALUE, "steps=%d unsupported (1..4)", desc->steps[p]);
     }
-    if (!weight || !scales || !work) return fail(RPFQ_ERR_NULL, "weight/scales/work must not be NULL");
+    if (!weight || !scales) return fail(RPFQ_ERR_NULL, "weight/scales must not be NULL");
     if (codes && desc->k_complex % 4 != 0)
         return fail(RPFQ_ERR_ALIGN, "code planes need k_complex %% 4 == 0, got %lld", (long long)desc->k_complex);
     if (codes && (!aligned(weight, 16) || (a_q && !aligned(a_q, 16))))
         return fail(RPFQ_ERR_ALIGN, "code planes need 16-byte aligned weight and a_q");
+    return RPFQ_OK;
+}
+
+int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
+                       float* scales, uint8_t* codes, void* work, size_t work_bytes, void* stream) {
+    int rc = check_quantize(desc, weight, a_q, scales, codes);
+    if (rc) return rc;
+    if (!work) return fail(RPFQ_ERR_NULL, "work must not be NULL");
     if (work_bytes < rpfq_quantize_workspace_bytes(desc))
         return fail(RPFQ_ERR_SHAPE, "workspace holds %zu bytes, need %zu", work_bytes,
                     rpfq_quantize_workspace_bytes(desc));
@@ -297,6 +307,22 @@ int rpfq_quantize_wide(const rpfq_quant_desc* desc, const float* weight, const f
     return hip_status(rpfq::launch_quantize_wide(*desc, weight, rot, a_q, scales, codes, work,
                                                  reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_quantize_wide");
+}
+
+int rpfq_quantize_wide_noalloc(const rpfq_quant_desc* desc, const float* weight, const float* rot, float* a_q,
+                               float* scales, uint8_t* codes, void* stream) {
+    int rc = check_quantize(desc, weight, a_q, scales, codes);
+    if (rc) return rc;
+    const size_t need = rpfq_quantize_workspace_bytes(desc), have = rpfq::quant_scratch_bytes();
+    if (need > have)
+        return fail(RPFQ_ERR_SHAPE, "rpfq_quantize_wide_noalloc: needs %zu bytes of scratch, the static device "
+                    "array holds %zu", need, have);
+    void* work = nullptr;
+    rc = hip_status(rpfq::quant_scratch_ptr(&work), "rpfq_quantize_wide_noalloc (scratch address)");
+    if (rc) return rc;
+    return hip_status(rpfq::launch_quantize_wide(*desc, weight, rot, a_q, scales, codes, work,
+                                                 reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_quantize_wide_noalloc");
 }
 
 }  // extern "C"

@@ -134,6 +134,10 @@ hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bi
 constexpr int kQuantMaxBlocks = 1024;
 hipError_t launch_quantize_wide(const rpfq_quant_desc& d, const float* weight, const float* rot, float* aq,
                                 float* scales, uint8_t* codes, void* work, hipStream_t s);
+// the static device scratch of rpfq_quantize_wide_noalloc: its size, and its
+// device address on the current device (resolved once per device)
+size_t quant_scratch_bytes();
+hipError_t quant_scratch_ptr(void** out);
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               float* a, int round_fp16, hipStream_t s);
 

@@ -22,6 +22,8 @@
 // (the reference sums float32 in torch's order; both agree to ~1 ulp and the
 // CPU restatement uses the same float64 convention).  Results are
 // deterministic: the partition into blocks and the reduction order are fixed.
+#include <mutex>
+
 #include "rpfq_internal.h"
 
 namespace rpfq {
@@ -345,12 +347,42 @@ __global__ void __launch_bounds__(kQThreads) quant_apply_kernel(QuantArgs a) {
     }
 }
 
+// Device scratch of rpfq_quantize_wide_noalloc: the per-block float64
+// partials of one stage (kQuantMaxBlocks x 8 doubles = 64 KiB per device,
+// held until the process ends).  Host code never passes `scratch` itself to
+// a kernel (its name is a host-side stand-in there): quant_scratch_ptr() resolves
+// the device address once per device.
+static __device__ __align__(256) double scratch[kQuantMaxBlocks * 8];
+
 int reduce_blocks(int64_t total) {
     int64_t b = (total + kQThreads - 1) / kQThreads;
     return (int)(b < kQuantMaxBlocks ? (b < 1 ? 1 : b) : kQuantMaxBlocks);
 }
 
 }  // namespace
+
+size_t quant_scratch_bytes() { return sizeof(scratch); }
+
+hipError_t quant_scratch_ptr(void** out) {
+    static std::atomic<void*> ptrs[64];  // per device, zero-initialised
+    static std::mutex mu;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    void* p = ptrs[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(mu);
+        p = ptrs[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with device `dev` current
+            if (e != hipSuccess) return e;
+            ptrs[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
 
 hipError_t launch_quantize_wide(const rpfq_quant_desc& d, const float* weight, const float* rot, float* aq,
                                 float* scales, uint8_t* codes, void* work, hipStream_t s) {

@@ -52,6 +52,7 @@ EXPORTED = (
     "rpfq_layer_norm_act_quant",
     "rpfq_quantize_workspace_bytes",
     "rpfq_quantize_wide",
+    "rpfq_quantize_wide_noalloc",
 )
 
 
@@ -131,6 +132,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_quantize_workspace_bytes.argtypes = [qp]
         lib.rpfq_quantize_workspace_bytes.restype = sz
         lib.rpfq_quantize_wide.argtypes = [qp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.rpfq_quantize_wide_noalloc.argtypes = [qp, vp, vp, vp, vp, vp, vp]
         for name in EXPORTED[2:]:
             if name not in ("rpfq_wide_packed_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32

@@ -168,6 +168,26 @@ def test_quantize_wide_argument_errors():
     assert L.rpfq_quantize_wide(ctypes.byref(bad), p, None, p, p, None, p, ws, None) == 2
 
 
+def test_quantize_wide_noalloc_argument_errors():
+    """The no-allocation quantizer validates like rpfq_quantize_wide (no
+    workspace argument), before any HIP call."""
+    L, N = lib()
+    p = ctypes.c_void_p(256)
+    d = N.QuantDesc()
+    d.n_complex, d.k_complex = 32, 48
+    d.kind[0], d.kind[1], d.steps[0], d.steps[1] = 0, 1, 2, 2
+    assert L.rpfq_quantize_wide_noalloc(None, p, None, p, p, None, None) == 1
+    assert L.rpfq_quantize_wide_noalloc(ctypes.byref(d), None, None, p, p, None, None) == 1  # weight
+    assert L.rpfq_quantize_wide_noalloc(ctypes.byref(d), p, None, p, None, None, None) == 1  # scales
+    bad = N.QuantDesc()
+    ctypes.pointer(bad)[0] = d
+    bad.steps[1] = 5
+    assert L.rpfq_quantize_wide_noalloc(ctypes.byref(bad), p, None, p, p, None, None) == 6
+    bad.steps[1], bad.k_complex = 2, 50
+    assert L.rpfq_quantize_wide_noalloc(ctypes.byref(bad), p, None, p, p, p, None) == 3  # codes need K' % 4
+    assert "k_complex" in L.rpfq_last_error().decode()
+
+
 def test_table_codebook_desc_rules():
     L, N = lib()
     d = _desc(N, n=64, k=64, cb=N.CB_TABLE, stages=1)
