@@ -128,6 +128,168 @@ def cpu_baseline(model, rows: dict, budget_s: float = 12.0):
                       f"decoded A_q (oracle/rpfq_oracle.py), {dt:.1f} s; excludes attention/LayerNorm"}
 
 
+def config1_inputs(seed: int = 0):
+    """X planes N(0,1) float32 [1576, 768]; 2-bit codes
+    U{0..3} [3072, 768] packed low-bits-first [3072, 192]; per-output-channel
+    scale s ~ U(0.01, 0.1) held as the exporter's fp16 gamma = fp16(1/s)
+    (so the packed format carries it exactly), shared by re and im."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    m, k, n = 1576, 768, 3072
+    xr = rng.standard_normal((m, k)).astype(np.float32)
+    xi = rng.standard_normal((m, k)).astype(np.float32)
+    codes = rng.integers(0, 4, size=(n, k), dtype=np.uint8)
+    c = codes.reshape(n, k // 4, 4)
+    packed = (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).astype(np.uint8)
+    s = rng.uniform(0.01, 0.1, size=(n, 1))
+    gamma = (1.0 / s).astype(np.float16)
+    return xr, xi, codes, packed, gamma
+
+
+def config1_cpu_baseline(xr, xi, codes, gamma, budget_s: float = 12.0):
+    """The reference's own CPU primitive on config 1: phaseLinearReference
+    (RPFQ-ViTAndroid/app/src/main/cpp/ops/phase_linear.cpp:119-164, U-branch
+    feed (xr, -xi), compiled from the reference sources into oracle/_ref),
+    single-threaded as the reference runs it, on the first T tokens with T
+    sized to ~budget_s from a short probe; TFLOP/s of the algorithmic 8 M K N.
+    Falls back to the numpy oracle (oracle.phase_linear) without oracle/_ref."""
+    import numpy as np
+    from oracle import ref_lib
+
+    k, n = xr.shape[1], codes.shape[0]
+    lib = ref_lib.load()
+    kind = "reference" if lib is not None else "port"
+
+    def run(t):
+        if lib is not None:
+            return ref_lib.phase_linear(xr[:t], -xi[:t], codes, gamma, gamma, k)
+        from oracle import rpfq_oracle as O
+        inv = O.inv_gamma(gamma)[:, 0]
+        return O.phase_linear(xr[:t], xi[:t], codes, inv, inv, conj_input=False)
+
+    t0 = time.perf_counter()
+    run(2)
+    probe = max(time.perf_counter() - t0, 1e-4) / 2
+    t = int(min(xr.shape[0], max(2, budget_s / probe)))
+    t0 = time.perf_counter()
+    run(t)
+    dt = time.perf_counter() - t0
+    return {"value": round(8.0 * t * k * n / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"{t} of 1576 tokens x K={k} x N={n}, "
+                      + ("phaseLinearReference (oracle/_ref, compiled from the reference's Android C++)"
+                         if lib is not None else "numpy oracle.phase_linear") + f", {dt:.1f} s"}
+
+
+def bench_config1(steps: int, warmup: int, cpu: bool, budget_s: float) -> int:
+    """Config 1: one phase-quantized complex Linear at the ViT-B fc1 shape
+    through rpfq_phase_linear (phase_linear_kernel: ternary fp16 MFMA
+    operands, the float32 planes split into fp16 hi + lo terms, scales in
+    the epilogue), U-branch semantics y = W x (conj_x = 0).  A step is one
+    launch over the resident [1576, 768] planes; value = TFLOP/s of the
+    algorithmic 8 M K N."""
+    import ctypes
+
+    import torch
+    from quant_models import _native as N
+
+    xr, xi, codes, packed, gamma = config1_inputs()
+    m, k = xr.shape
+    n = codes.shape[0]
+    dev = torch.device("cuda")
+    txr, txi = torch.from_numpy(xr).to(dev), torch.from_numpy(xi).to(dev)
+    tcodes = torch.from_numpy(packed).to(dev)
+    tg = torch.from_numpy(gamma).to(dev)
+    yr = torch.empty(m, n, dtype=torch.float32, device=dev)
+    yi = torch.empty_like(yr)
+    lib = N.load()
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        N.check("rpfq_phase_linear", lib.rpfq_phase_linear(
+            txr.data_ptr(), txi.data_ptr(), N.F32, 0, m, k, tcodes.data_ptr(), tg.data_ptr(), tg.data_ptr(), 0,
+            n, yr.data_ptr(), yi.data_ptr(), N.F32, stream.cuda_stream or None))
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 8.0 * m * k * n
+    nbytes = 8 * m * k + k * n // 4 + 4 * n + 8 * m * n
+    tflops = flops / (ms / 1e3) / 1e12
+    line = {
+        "metric": "complex-GEMM TFLOP/s, config 1 (phase-quantized complex Linear 768->3072, M = 1576, "
+                  "float32 planes, U-branch) on 1 MI355X",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 in/out (fp16 hi + lo MFMA operands, f32 accumulate)",
+        "data": "synthetic (numpy default_rng(0): N(0,1) planes, uniform 2-bit codes, fp16 gammas of U(0.01, 0.1))",
+        "config": {"workload": "cplx_fc1: BASELINE config 1, M=1576 (8 images x 197 tokens), K=768, N=3072 "
+                               "complex, per-output-channel scales", "m": m, "k": k, "n": n},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_F16_TFLOPS, 4), "traffic": None,
+                     "kernel": "rpfq::phase_linear_kernel<64, F32, F32, false> (one launch per step; float32 x "
+                               "runs two fp16 MFMA passes, hi and lo, so the MFMA executes 2x the algorithmic "
+                               "flops)",
+                     "algorithmic_bytes": nbytes, "algorithmic_gbs": round(nbytes / (ms / 1e3) / 1e9, 1)},
+        "cpu_baseline": config1_cpu_baseline(xr, xi, codes, gamma, budget_s) if cpu else None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_as_is(model, rows: dict, batch: int, gemm_rate: float, act_bits: int, budget_s: float = 12.0):
+    """Variant (i), the reference layer's per-call work as it is
+    (QATLinearComplexPhase.forward, quant_i.py:513-554): every call
+    requantizes the float32 master weight (oracle.quantized_weight: 2x2
+    split, two residual axis stages for U and W, recombination), applies the
+    activation quantization when the model has it (oracle.act_quant), then
+    the float32 GEMM -- timed for one forward of B images (B = the bench
+    batch, or fewer so it fits ~budget_s at the GEMM-only rate); images/s."""
+    import numpy as np
+    from oracle import rpfq_oracle as O
+    from quant_models.inference import quant_layers
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = len(os.sched_getaffinity(0))
+    b = int(max(1, min(batch, 0.5 * budget_s * gemm_rate)))
+    rng = np.random.default_rng(1)
+    layers = [(layer.weight.detach().float().cpu().numpy(), rows[name]) for name, layer in quant_layers(model)]
+    xs = {}
+    for w, r in layers:
+        if xs.get(w.shape[1], np.empty((0, 0))).shape[0] < r * b:
+            xs[w.shape[1]] = rng.standard_normal((r * b, w.shape[1])).astype(np.float32)
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    if ctx:
+        ctx.__enter__()
+    try:
+        t0 = time.perf_counter()
+        for w, r in layers:
+            a_q, _, _ = O.quantized_weight(w, "axis", 2, "axis", 2)
+            x = xs[w.shape[1]][:r * b]
+            if act_bits:
+                h = x.shape[1] // 2
+                x = np.concatenate(O.act_quant(x[:, :h], x[:, h:], act_bits), axis=1)
+            _ = x @ a_q.T
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return {"value": round(b / dt, 3), "unit": "images/s", "cores": cores, "kind": "port",
+            "sample": f"one forward of {b} image(s) x {len(layers)} packed layers: per-call requantization of the "
+                      f"float32 master weight + " + (f"{act_bits}-bit act quant + " if act_bits else "")
+                      + f"float32 numpy GEMM (oracle/rpfq_oracle.py), {dt:.1f} s"}
+
+
 # Complex layer shapes (K', N') of the ViT-B/16 and ViT-L/16 packed linears.
 STREAM_SHAPES = {
     "vit_b.qkv": (384, 1152), "vit_b.proj": (384, 384), "vit_b.fc1": (384, 1536), "vit_b.fc2": (1536, 384),
@@ -350,7 +512,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="vit_b16_q2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="vit_b16_q2", choices=sorted(CONFIGS) + ["cplx_fc1"])
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -407,6 +569,8 @@ def main() -> int:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is part of "
               "this build's design, not of what it benchmarks", file=sys.stderr)
         return 2
+    if args.config == "cplx_fc1":
+        return bench_config1(args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
 
     import torch
     from quant_models import ops
@@ -522,7 +686,10 @@ def main() -> int:
     if batch1 is not None:
         line["batch1_stream"] = batch1
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(model, rows_per_image(model, x[:1]), args.cpu_budget)
+        rows = rows_per_image(model, x[:1])
+        line["cpu_baseline"] = cpu_baseline(model, rows, args.cpu_budget)
+        line["cpu_baseline"]["as_is"] = cpu_baseline_as_is(model, rows, batch, line["cpu_baseline"]["value"],
+                                                           4 if args.act_quant else 0, args.cpu_budget)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -387,7 +387,8 @@ def test_fused_act_quant_wiring(name):
     n_layers = sum(1 for _ in quant_layers(model))
     x = torch.randn(8, 3, 224, 224, generator=torch.Generator().manual_seed(6)).to(DEV, torch.float16)
     calls, pre = [], []
-    act_quant, fwd_pre = ops.act_quant, QATLinearComplexPhase.forward_prequantized
+    act_quant = ops.act_quant
+    fwd_pre, fwd_gelu = QATLinearComplexPhase.forward_prequantized, QATLinearComplexPhase.forward_gelu
 
     def counting(*args, **kw):
         calls.append(1)
@@ -396,10 +397,16 @@ def test_fused_act_quant_wiring(name):
     def recording(self, h):
         pre.append(h.reshape(-1, h.shape[-1])[:64].float().cpu())
         return fwd_pre(self, h)
+
+    def recording_gelu(self, h, prequantized=False):  # fc1 of the fused MLP
+        if prequantized:
+            pre.append(h.reshape(-1, h.shape[-1])[:64].float().cpu())
+        return fwd_gelu(self, h, prequantized)
     saved = vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT
     try:
         ops.act_quant = counting
         QATLinearComplexPhase.forward_prequantized = recording
+        QATLinearComplexPhase.forward_gelu = recording_gelu
         with torch.no_grad():
             vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = True, True
             y_f = model(x)
@@ -415,6 +422,7 @@ def test_fused_act_quant_wiring(name):
     finally:
         ops.act_quant = act_quant
         QATLinearComplexPhase.forward_prequantized = fwd_pre
+        QATLinearComplexPhase.forward_gelu = fwd_gelu
         vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = saved
     assert n_unfused == n_module == n_layers, (n_unfused, n_module, n_layers)
     blocks = sum(1 for m in model.modules() if hasattr(m, "mlp") and hasattr(m, "norm2"))
