@@ -47,10 +47,25 @@ __device__ __forceinline__ float2 sign_val(uint32_t c, float sr, float si) {
 // Quantized complex value of one U (or W) index under the per-row
 // parameters p = (s0 re, s0 im, s1 re, s1 im).  Stages are summed in the
 // reference's order q = step0 + step1 (quant_i.py:111-118).
+// 16-PSK unit value e^{i pi idx / 8} from the octant constants by selects
+// (no memory access): r = idx & 3 within the quadrant, q = idx >> 2 quarter
+// turns.  Negation as 0 - v keeps the zeros +0, so every value equals
+// (kPskCos[idx], kPskSin[idx]) bit for bit.
+__device__ __forceinline__ float2 psk16_unit(uint32_t idx) {
+    const uint32_t r = idx & 3u, q = (idx >> 2) & 3u;
+    const float c = r == 0 ? 1.0f : r == 1 ? PSK_C1 : r == 2 ? PSK_R2 : PSK_S1;
+    const float s = r == 0 ? 0.0f : r == 1 ? PSK_S1 : r == 2 ? PSK_R2 : PSK_C1;
+    float2 v;
+    v.x = q == 0 ? c : q == 1 ? 0.0f - s : q == 2 ? 0.0f - c : s;
+    v.y = q == 0 ? s : q == 1 ? c : q == 2 ? 0.0f - s : 0.0f - c;
+    return v;
+}
+
 template <int CB>
 __device__ __forceinline__ float2 lut_entry(uint32_t idx, float4 p) {
     if (CB == RPFQ_CB_PSK16) {
-        return make_float2(p.x * kPskCos[idx], p.x * kPskSin[idx]);
+        const float2 u = psk16_unit(idx);
+        return make_float2(p.x * u.x, p.x * u.y);
     }
     float2 v0, v1;
     if (CB == RPFQ_CB_SIGN) {
@@ -61,6 +76,19 @@ __device__ __forceinline__ float2 lut_entry(uint32_t idx, float4 p) {
         v1 = axis_val(idx >> 2, p.z, p.w);
     }
     return make_float2(v0.x + v1.x, v0.y + v1.y);
+}
+
+// lut_entry(even + g, p) for g in {0, 1}: the LUT builders' index pattern
+// (lane half g, unrolled even offset).  16-PSK picks between the two unit
+// values of the even offset, which fold to constants when it is known.
+template <int CB>
+__device__ __forceinline__ float2 lut_entry_g(uint32_t even, int g, float4 p) {
+    if (CB == RPFQ_CB_PSK16) {
+        const float2 ue = psk16_unit(even), uo = psk16_unit(even + 1);
+        const float2 u = g ? uo : ue;
+        return make_float2(p.x * u.x, p.x * u.y);
+    }
+    return lut_entry<CB>(even + (uint32_t)g, p);
 }
 
 // De-rotation after quantization (quant_i.py:433-434); built without
@@ -305,8 +333,8 @@ __device__ __forceinline__ void build_lut(uint32_t* lut, const float4* params, i
             u = active ? t[idx] : make_float2(0.0f, 0.0f);
             w = active ? t[16 + idx] : make_float2(0.0f, 0.0f);
         } else {
-            u = lut_entry<CB>(idx, pu);
-            w = lut_entry<CB>(idx, pw);
+            u = lut_entry_g<CB>(2 * j, g, pu);
+            w = lut_entry_g<CB>(2 * j, g, pw);
         }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);

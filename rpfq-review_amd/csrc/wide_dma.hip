@@ -52,8 +52,11 @@ template <int BM> constexpr int dma_stages_at() { return kDmaLutPair; }
 template <int BM> constexpr int dma_codes_at() { return kDmaLutPair + kDmaStages * dma_stage<BM>(); }
 template <int BM> constexpr int dma_lut1_at() { return dma_codes_at<BM>() + 2 * kDmaCodes <= 65536 ? 65536 : 131072; }
 template <int BM> constexpr int dma_bias_at() { return dma_lut1_at<BM>() + kDmaLutPair; }
-template <int BM> constexpr int dma_lds() { return dma_bias_at<BM>() + kDmaBias; }  // 74752 B (BM = 128)
-static_assert(dma_lds<128>() == 74752, "two workgroups per CU");
+// per-row scales of the next tile, staged by DMA: [wave][32 rows][pu | pw] float4 pairs
+constexpr int kDmaParams = 4 * 1024;
+template <int BM> constexpr int dma_params_at() { return dma_bias_at<BM>() + kDmaBias; }
+template <int BM> constexpr int dma_lds() { return dma_params_at<BM>() + kDmaParams; }  // 78848 B (BM = 128)
+static_assert(2 * dma_lds<128>() <= 160 * 1024, "two workgroups per CU");
 static_assert(4 * 64 * kTRow <= kDmaStages * dma_stage<128>(), "epilogue half tile fits the stages");
 static_assert(4 * 128 * kTRow <= kDmaStages * dma_stage<256>(), "epilogue half tile fits the stages");
 
@@ -70,12 +73,14 @@ __device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, ui
 // LUT of one output row in the wave-pair layout: entry e (0..15 U, 16..31 W)
 // of row slot `slot` at lut_pair[64 e + slot]; lane group g writes the even
 // or odd indices.  Same values as build_lut.
+// staged: the row's (pu, pw) at staged[0..1] (LDS) instead of the blob.
 template <int CB>
 __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, const float4* params, int64_t n,
-                                               int nblk, int blk, const RotParams& rot, int g) {
+                                               int nblk, int blk, const RotParams& rot, int g,
+                                               const float4* staged = nullptr) {
     float4 pu = make_float4(0, 0, 0, 0), pw = make_float4(0, 0, 0, 0);
     if constexpr (CB != RPFQ_CB_TABLE) {
-        const float4* p = params + (n * nblk + blk) * 2;
+        const float4* p = staged ? staged : params + (n * nblk + blk) * 2;
         pu = p[0];
         pw = p[1];
     }
@@ -88,8 +93,8 @@ __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, con
             u = t[idx];
             w = t[16 + idx];
         } else {
-            u = lut_entry<CB>(idx, pu);
-            w = lut_entry<CB>(idx, pw);
+            u = lut_entry_g<CB>(2 * j, g, pu);
+            w = lut_entry_g<CB>(2 * j, g, pw);
         }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);
@@ -120,7 +125,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // address of entry 0, whose byte 1 is zero (base is a multiple of 64 KB).
     uint32_t* lut_pair = reinterpret_cast<uint32_t*>(smem + (wave < 2 ? 0 : dma_lut1_at<BM>()));
     const int slot = 32 * (wave & 1) + r;
-    float* bias_s = reinterpret_cast<float*>(smem + dma_bias_at<BM>());  // [wave][re 32 | im 32]
+    float* bias_s = reinterpret_cast<float*>(smem + dma_bias_at<BM>()) + wave * 64;  // [wave][re 32 | im 32]
     const uint32_t lut_slot = lds_addr(lut_pair + slot);
 
     // Activation DMA: wave w fills rows RPW w .. RPW w + RPW - 1 of a stage
@@ -179,6 +184,19 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         xw = reinterpret_cast<const char*>(a.x) + (m0_t + RPW * wave) * ldx * 2;
         cw_src = reinterpret_cast<const char*>(a.codes + (int64_t)(ntw_t < a.NT ? ntw_t : a.NT - 1) * a.KS * 64);
     };
+    // Per-row scales (one scale block per row) of a tile are DMA'd into LDS
+    // together with its first codes and activations (before the previous
+    // tile's epilogue), so the tile start builds its LUT from LDS without a
+    // global load whose wait would drain the activation prefetch.
+    const float4* pstage = reinterpret_cast<const float4*>(smem + dma_params_at<BM>() + wave * 1024);
+    const bool staged = CB != RPFQ_CB_TABLE && a.nblk == 1;
+    auto issue_params = [&](int vb_t) {  // this wave's 32 rows of tile vb_t; lane l: row l / 2, half l % 2
+        if (!staged) return;
+        const int t = xcd_tile(vb_t, total);
+        const int ntw_t = (t - (t / a.tiles_n) * a.tiles_n) * 4 + wave;
+        const int nt = ntw_t < a.NT ? ntw_t : a.NT - 1;
+        dma_dwordx4(a.params + (int64_t)nt * 64, (uint32_t)lane * 16u, lds_addr(pstage));
+    };
     for (int vb = blockIdx.x; vb < total; vb += gridDim.x) {
     const int tile = xcd_tile(vb, total);
     const int mt = tile / a.tiles_n, ntl = tile - mt * a.tiles_n;
@@ -200,15 +218,25 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     if (vb == (int)blockIdx.x) {  // later tiles had these requested before the previous epilogue
         issue_codes(0, 0);
         issue_x(0, 2);
+        issue_params(vb);
     }
-    issue_x(a.KS > 1 ? 1 : 0, 0);
-    // the LUT and bias are written while the loads are in flight
-    int cur_blk = 0;
-    build_lut_slot<CB>(lut_pair, slot, a.params, (int64_t)ntw_ld * 32 + r, a.nblk, 0, a.rot, g);
-    {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue
+    {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue;
+        // loaded before the next k-step's DMA, so its wait covers only loads this tile needs now
         const int64_t nn = (int64_t)ntw * 32 + r;
         const bool ok = a.bias && active && nn < a.N;
-        bias_s[wave * 64 + g * 32 + r] = ok ? a.bias[g * (int64_t)a.N + nn] : 0.0f;
+        bias_s[g * 32 + r] = ok ? a.bias[g * (int64_t)a.N + nn] : 0.0f;
+    }
+    issue_x(a.KS > 1 ? 1 : 0, 0);
+    int cur_blk = 0;
+    if (staged) {
+        // staged scales and bias landed (every load but the newest k-step's)
+        if (RPW == 32)
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        build_lut_slot<CB>(lut_pair, slot, a.params, 0, a.nblk, 0, a.rot, g, pstage + 2 * r);
+    } else {
+        build_lut_slot<CB>(lut_pair, slot, a.params, (int64_t)ntw_ld * 32 + r, a.nblk, 0, a.rot, g);
     }
     // codes and stage 2 landed (at most the newest k-step's loads in flight), LUT written
     if (RPW == 32)
@@ -332,6 +360,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         tile_src(vb + (int)gridDim.x);
         issue_codes(0, 0);
         issue_x(0, 2);
+        issue_params(vb + (int)gridDim.x);
     }
     // Epilogue.  The accumulators hold the transposed tile: lane (r, g) of
     // subtile i has, for x row 32 i + r, outputs n = 32 ntw + 8 q + 4 g + t at
@@ -343,8 +372,8 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     float bre[16], bim[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float4 b0 = *reinterpret_cast<const float4*>(bias_s + wave * 64 + 8 * q + 4 * g);
-        const float4 b1 = *reinterpret_cast<const float4*>(bias_s + wave * 64 + 32 + 8 * q + 4 * g);
+        const float4 b0 = *reinterpret_cast<const float4*>(bias_s + 8 * q + 4 * g);
+        const float4 b1 = *reinterpret_cast<const float4*>(bias_s + 32 + 8 * q + 4 * g);
         bre[4 * q] = b0.x; bre[4 * q + 1] = b0.y; bre[4 * q + 2] = b0.z; bre[4 * q + 3] = b0.w;
         bim[4 * q] = b1.x; bim[4 * q + 1] = b1.y; bim[4 * q + 2] = b1.z; bim[4 * q + 3] = b1.w;
     }

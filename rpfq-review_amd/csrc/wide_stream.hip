@@ -79,8 +79,8 @@ __device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, con
             u = reinterpret_cast<const float2*>(p)[idx];
             w = reinterpret_cast<const float2*>(p)[16 + idx];
         } else {
-            u = lut_entry<CB>(idx, pu);
-            w = lut_entry<CB>(idx, pw);
+            u = lut_entry_g<CB>((uint32_t)(2 * (j0 + jj)), g, pu);
+            w = lut_entry_g<CB>((uint32_t)(2 * (j0 + jj)), g, pw);
         }
         if (rot.rotate) {
             u = derotate(u, rot.cu, rot.su);

@@ -12,7 +12,9 @@ import threading
 
 import torch
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "librpfq.so")
+# RPFQ_LIBRARY names another build of the library to load (e.g. an A/B build).
+_LIB_PATH = os.environ.get("RPFQ_LIBRARY") or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "librpfq.so")
 
 RPFQ_OK = 0
 ERRORS = {
