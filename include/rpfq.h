@@ -166,7 +166,10 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  * reference does (stage sums, de-rotation) and rounded to fp16; each fused
  * coefficient (A11 = Wre + Ure, A12 = Wim - Uim, A21 = Wim + Uim,
  * A22 = -Wre + Ure) is one correctly rounded fp16 add of those; the MFMA
- * accumulates in float32.  flags: the RPFQ_FLAG_* bits above.
+ * accumulates in float32.  The RPFQ_KERNEL_GEMV launches (M <= 8) never
+ * round the fused coefficients: the fp16 U and W values meet x in separate
+ * MFMA products, so their sums are exact in the float32 accumulator.
+ * flags: the RPFQ_FLAG_* bits above.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                      const void* x, int x_dtype, int64_t M, const float* bias,
@@ -176,6 +179,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
 #define RPFQ_KERNEL_STREAM 0  /* weight streaming, 16-row chunks of x */
 #define RPFQ_KERNEL_DMA 1     /* 128-row tiles, activations staged by LDS DMA */
 #define RPFQ_KERNEL_TILED 2   /* 32/64/128-row tiles staged through registers */
+#define RPFQ_KERNEL_GEMV 3    /* weight streaming for M <= 8, U and W as separate MFMA operands */
 
 /*
  * *kernel := the RPFQ_KERNEL_* that rpfq_wide_linear runs for this layer, M,

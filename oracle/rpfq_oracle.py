@@ -31,6 +31,10 @@ Parity status per function (how each one is pinned; see tests/test_oracle.py):
                                pair class incl. ties and subnormals;
                                recompose_fp16 by its error bound against the
                                reference A_q and by sign/permutation identities.
+* ``recompose_split_fp16``  -- build-defined operand of the column-split
+                               kernel: its fp16 rounding equals recompose_fp16
+                               bit for bit; error bound against A_q; W = 0
+                               case exact.
 * ``linear_forward``        -- golden outputs of the reference layer.
 * ``wide_parts(..., "table")`` -- the per-row value tables of the packed
                                next_v1 form: the golden next_v1 A_q of the
@@ -438,11 +442,26 @@ def recompose_fp16(u_re, u_im, w_re, w_im):
     ).astype(F32)
 
 
-def wide_weight(planes, codebook: str = "axis", rotation=None, fp16: bool = False):
+def recompose_split_fp16(u_re, u_im, w_re, w_im):
+    """Fused weight as the column-split streaming kernel (RPFQ_KERNEL_GEMV)
+    contracts it: U and W rounded to fp16 and each coefficient their exact
+    sum in the reference's recombination order (quant_i.py:534-537), float64
+    (the kernel multiplies the fp16 parts separately and sums in float32
+    accumulators).  Build-defined; its round-to-fp16 is recompose_fp16 bit
+    for bit (both are the correctly rounded fp16 sum of the same operands)."""
+    ur, ui, wr, wi = (np.asarray(v, F32).astype(np.float16).astype(np.float64) for v in (u_re, u_im, w_re, w_im))
+    return np.concatenate(
+        [np.concatenate([wr + ur, wi - ui], axis=1), np.concatenate([wi + ui, -wr + ur], axis=1)], axis=0)
+
+
+def wide_weight(planes, codebook: str = "axis", rotation=None, fp16=False):
     """Fused real [2N, 2K] weight of the widely-linear layer: the reference's
     float32 A_q (quant_i.py:534-544), or with fp16=True the fp16 operand the
-    MFMA sees (recompose_fp16)."""
+    MFMA sees (recompose_fp16), or with fp16="split" the exact sums of the
+    fp16 parts the column-split kernel contracts (recompose_split_fp16)."""
     parts = wide_parts(planes, codebook, rotation)
+    if fp16 == "split":
+        return recompose_split_fp16(*parts)
     return recompose_fp16(*parts) if fp16 else recompose(*parts)
 
 

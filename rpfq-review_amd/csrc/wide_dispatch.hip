@@ -57,7 +57,7 @@ static bool stream_pays(const WideArgs& a) {
 // kernel-choice flags (the GELU bit already moved into a.act).
 static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
     if ((flags & RPFQ_FLAG_STREAM) || (!(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)) && stream_pays(a)))
-        return RPFQ_KERNEL_STREAM;
+        return gemv_pays(a) ? RPFQ_KERNEL_GEMV : RPFQ_KERNEL_STREAM;
     flags &= ~RPFQ_FLAG_NO_STREAM;
     // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
     // spill in its k-loop, so they take the register-staged kernel)
@@ -69,7 +69,7 @@ static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
 template <int CB>
 static hipError_t wide_cb(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s) {
     const int k = choose_kernel(a, xdt, ydt, flags);
-    if (k == RPFQ_KERNEL_STREAM) return launch_wide_stream<CB>(a, xdt, ydt, s);
+    if (k == RPFQ_KERNEL_STREAM || k == RPFQ_KERNEL_GEMV) return launch_wide_stream<CB>(a, xdt, ydt, s);
     if (k == RPFQ_KERNEL_DMA) return launch_wide_dma<CB>(a, ydt, s);
     flags &= ~RPFQ_FLAG_NO_STREAM;
     const int bm = (flags & RPFQ_FLAG_TILE_M128) ? 128 : a.M <= 32 ? 32 : a.M <= 64 ? 64 : 128;

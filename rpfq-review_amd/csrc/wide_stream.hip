@@ -223,22 +223,26 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kerne
             }
         }
     };
+    // Whole groups of SK_PF k-steps with a uniform guard around the compute
+    // and each ring slot reloaded after its k-step is consumed: the slots keep
+    // their registers across iterations (no copies, whose waits would drain
+    // every load in flight), and each wait is for the oldest loads only.
     for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
 #pragma unroll
         for (int i = 0; i < SK_PF; ++i) {
             const int ks = ks0 + i;
-            if (ks >= ke) break;
-            const Step cur = ring[i];
-            load_step(ks + SK_PF, ring[i]);  // past the end: reloads the last k-step, unused
-            if (PB) {  // per-(row, block) scales: new LUT at each block start
-                const int nb = ks / a.block_ks;
-                if (nb != blk) {
-                    blk = nb;
-                    const float4* p = a.params + (((int64_t)tile * 32 + R) * a.nblk + nb) * 2;
-                    build_lut_sk<CB>(lut, p, a.rot, R, g);
+            if (ks < ke) {
+                if (PB) {  // per-(row, block) scales: new LUT at each block start
+                    const int nb = ks / a.block_ks;
+                    if (nb != blk) {
+                        blk = nb;
+                        const float4* p = a.params + (((int64_t)tile * 32 + R) * a.nblk + nb) * 2;
+                        build_lut_sk<CB>(lut, p, a.rot, R, g);
+                    }
                 }
+                compute(ks, ring[i]);
             }
-            compute(ks, cur);
+            load_step(ks + SK_PF, ring[i]);  // past the end: reloads the last k-step, unused
         }
     }
 
@@ -310,6 +314,246 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kerne
     }
 }
 
+// ---------------------------------------------------------------------------
+// widely-linear layer for M <= 8: weight streaming with re / im as B columns
+// ---------------------------------------------------------------------------
+// The same code stream and LUT as above, but the fused coefficients A11 ..
+// A22 are never formed: the U and W values of a complex column take separate
+// k slots of the A operand, [Ure, Uim, Wre, Wim], and the real and the
+// imaginary output of x row m are the B columns 2m and 2m + 1:
+//   column 2m:     [ xr, -xi,  xr, xi ]  Ure xr - Uim xi + Wre xr + Wim xi = Re(U x + W conj(x))
+//   column 2m + 1: [ xi,  xr, -xi, xr ]  Ure xi + Uim xr - Wre xi + Wim xr = Im(U x + W conj(x))
+// so a code byte costs two address permutes and two LUT reads, and the sums
+// U + W run on the matrix pipe (products of fp16 values are exact in the
+// float32 accumulator, where the fused kernels round U + W to fp16 first).
+// The B operands depend on x only and are shared by the H row groups.
+//   * lane (r16, q) holds the code dwords t = 0, 1 of rows 16 h + r16 as the
+//     kernel above (complex columns cq + 8 t + e, cq = 16 (q & 1) + 4 (q >> 1),
+//     e = 0..3); MFMA j = 0..3 takes bytes 2 (j & 1) and 2 (j & 1) + 1 of
+//     dword t = j >> 1, columns c0 and c0 + 1: A = [U(c0), W(c0), U(c0+1),
+//     W(c0+1)].
+//   * lane (col = r16, q) of B reads x row min(col / 2, M - 1), columns
+//     cq + 8 t .. cq + 8 t + 3, as L1 = re, L2 = im for an even col and
+//     swapped for an odd one, so each (L1, L2) pair of a column is one
+//     permute with a uniform selector and the two sign patterns are per-lane
+//     XOR masks.
+//   * H = 2: one packed 32-row tile per workgroup; H = 4: two consecutive
+//     tiles (the last one clamped when NT is odd), their LUTs 8 KB apart.
+//   * NW = 2 or 4 waves split K and share the LUT (each builds its share),
+//     wave 0 adding the partial sums through LDS in a fixed order.
+#ifndef RPFQ_GV_OCC
+#define RPFQ_GV_OCC 4
+#endif
+constexpr int GV_XPF = 2;  // prefetch distance of the activations (L2-resident) in k-steps
+static_assert(SK_PF % GV_XPF == 0, "the activation ring must divide the code ring");
+constexpr int gv_lds(int h, int nw) { return (h / 2) * kSkLut + (nw - 1) * h * 4 * 64 * 4; }
+
+template <int XDT>
+__device__ __forceinline__ uint32_t raw2_f16(uint32_t v) {
+    if (XDT != RPFQ_BF16) return v;
+    return pack_h2(bf16_to_f32(v & 0xffffu), bf16_to_f32(v >> 16));
+}
+
+template <int XDT, int YDT, int CB, bool KT, int NW, int H>
+__global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(WideArgs a) {
+    static_assert(H == 2 || H == 4, "16-row groups per workgroup");
+    constexpr int TPG = H / 2;  // packed 32-row tiles per workgroup
+    extern __shared__ __align__(16) char smem[];
+    uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
+    const int lane = threadIdx.x & 63;
+    const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, q = lane >> 4;
+    const int R = lane & 31, g = lane >> 5;
+    const int KS = a.KS, K = a.K;
+    const int M = (int)a.M;  // 1 .. 8 (host-checked)
+    const int chunk = (KS + NW - 1) / NW;
+    const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
+    const int tile0 = (int)blockIdx.x * TPG;
+
+    // codes of tile tile0 + t (t < TPG), clamped to the last packed tile
+    const uint2* ctile[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; ++t)
+        ctile[t] = reinterpret_cast<const uint2*>(a.codes) + (int64_t)min(tile0 + t, a.NT - 1) * KS * 128;
+    const int coff = r16 * 4 + q;
+    // B lane: x row m, part p (0 re, 1 im); L1 = part p, L2 = the other part
+    const int p = r16 & 1;
+    const int xrow = min(r16 >> 1, M - 1) * 2 * K;
+    const int cq = 16 * (q & 1) + 4 * (q >> 1);
+    const int off1 = xrow + (p ? K : 0) + cq, off2 = xrow + (p ? 0 : K) + cq;
+    const uint32_t m0 = p ? 0u : 0x80000000u, m1 = p ? 0x00008000u : 0u;
+
+    uint2 cring[SK_PF][H];
+    uint2 xring[GV_XPF][4];  // [t][L1, L2]: t = 0 at 0, 1; t = 1 at 2, 3
+    auto clamp_ks = [&](int ks) { return ks < ke ? ks : (ke > 0 ? ke - 1 : 0); };  // past the range: unused
+    auto load_codes = [&](int ks, uint2* c) {
+        const int kc = clamp_ks(ks);
+#pragma unroll
+        for (int h = 0; h < H; ++h) c[h] = ctile[h >> 1][kc * 128 + coff + 64 * (h & 1)];
+    };
+    auto load_x = [&](int ks, uint2* xv) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int col = 32 * clamp_ks(ks) + 8 * t;
+            const bool in = !KT || col + cq < K;  // K' tail: the row's first columns, zeroed at use
+            xv[2 * t] = load4_raw<XDT>(a.x, in ? off1 + col : xrow);
+            xv[2 * t + 1] = load4_raw<XDT>(a.x, in ? off2 + col : xrow);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < SK_PF; ++i) load_codes(kb + i, cring[i]);
+#pragma unroll
+    for (int i = 0; i < GV_XPF; ++i) load_x(kb + i, xring[i]);
+
+    {  // the waves build the TPG LUTs in equal shares of their 8 entry pairs
+        constexpr int per = 8 * TPG / NW, nj = per < 8 ? per : 8;
+#pragma unroll
+        for (int f = 0; f < per; f += nj) {
+            const int f0 = wave * per + f, region = f0 >> 3;
+            const int tile = min(tile0 + region, a.NT - 1);
+            const float4* pp = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
+            build_lut_sk<CB, nj>(lut + region * (kSkLut / 4), pp, a.rot, R, g, f0 & 7);
+        }
+    }
+    if (NW > 1) {  // LUT written before any wave reads it; the loads stay in flight
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+    const uint32_t slot0 = (uint32_t)(16 * (q & 1) + r16) * 4;
+
+    // two accumulators per row group when H = 2 (MFMAs j even / odd), so
+    // that four independent chains interleave as with H = 4
+    constexpr int NA = H == 2 ? 2 : 1;
+    floatx4 acc[H * NA];
+#pragma unroll
+    for (int h = 0; h < H * NA; ++h) acc[h] = floatx4{0, 0, 0, 0};
+    auto compute = [&](int ks, const uint2* c, const uint2* xv) {
+        // L1 / L2 dword j: columns c0, c0 + 1 of MFMA j
+        const uint32_t l1[4] = {xv[0].x, xv[0].y, xv[2].x, xv[2].y};
+        const uint32_t l2[4] = {xv[1].x, xv[1].y, xv[3].x, xv[3].y};
+        half8 bx[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t u1 = raw2_f16<XDT>(l1[j]), u2 = raw2_f16<XDT>(l2[j]);
+            const uint32_t p0 = __builtin_amdgcn_perm(u2, u1, 0x05040100u);
+            const uint32_t p1 = __builtin_amdgcn_perm(u2, u1, 0x07060302u);
+            uint4 b = make_uint4(p0 ^ m0, p0 ^ m1, p1 ^ m0, p1 ^ m1);
+            if (KT && 32 * ks + cq + 8 * (j >> 1) >= K) b = make_uint4(0, 0, 0, 0);
+            bx[j] = as_half8(b);
+        }
+        // index nibbles of every row group, then the MFMAs j-major so that
+        // consecutive ones accumulate into different row groups
+        uint32_t pu[H][2], pw[H][2];
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            pu[h][0] = c[h].x & 0x0f0f0f0fu;
+            pw[h][0] = (c[h].x >> 4) & 0x0f0f0f0fu;
+            pu[h][1] = c[h].y & 0x0f0f0f0fu;
+            pw[h][1] = (c[h].y >> 4) & 0x0f0f0f0fu;
+        }
+        auto reads = [&](int j, uint32_t (&av)[H][4]) {
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const uint32_t slot = slot0 + 128 * (h & 1);
+                const int rg = (h >> 1) * (kSkLut / 4);  // LUT of the h-th tile, in dwords
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t sel = 0x03020000u | ((4u + 2 * (j & 1) + e) << 8);
+                    av[h][2 * e] = *((lds_u32_t)__builtin_amdgcn_perm(pu[h][j >> 1], slot, sel) + rg);
+                    av[h][2 * e + 1] = *((lds_u32_t)__builtin_amdgcn_perm(pw[h][j >> 1], slot, sel) + rg + 16 * 64);
+                }
+            }
+        };
+        // LUT reads of MFMA j + 1 are issued before the MFMAs of j, so each
+        // group of MFMAs waits only for reads issued a group earlier
+        uint32_t av[2][H][4];
+        reads(0, av[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j < 3) reads(j + 1, av[(j + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                acc[h * NA + (j % NA)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    as_half8(make_uint4(av[j & 1][h][0], av[j & 1][h][1], av[j & 1][h][2], av[j & 1][h][3])), bx[j],
+                    acc[h * NA + (j % NA)], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // (the k-step loop of the kernel above)
+    for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
+#pragma unroll
+        for (int i = 0; i < SK_PF; ++i) {
+            const int ks = ks0 + i;
+            if (ks < ke) compute(ks, cring[i], xring[i % GV_XPF]);
+            // the slots just consumed take k-step ks + SK_PF (ks + GV_XPF)
+            load_codes(ks + SK_PF, cring[i]);
+            load_x(ks + GV_XPF, xring[i % GV_XPF]);
+        }
+    }
+
+    if (NA == 2) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[h] = acc[h * NA] + acc[h * NA + 1];
+    }
+    if (NW > 1) {  // waves 1 .. NW-1 hand their partial sums to wave 0
+        float* red = reinterpret_cast<float*>(smem + TPG * kSkLut);
+        if (wave > 0) {
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) red[(((wave - 1) * H + h) * 4 + v) * 64 + lane] = acc[h][v];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < NW - 1; ++w)
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[h][v] += red[((w * H + h) * 4 + v) * 64 + lane];
+    }
+
+    // Epilogue: lane (col = r16, q) holds part p of x row m = col / 2 for the
+    // outputs n = 32 tile0 + 16 h + 4 q + v; rows past M and outputs past N'
+    // store nothing.
+    const int m = r16 >> 1;
+    if (m >= M) return;
+    const int64_t ldy = 2 * (int64_t)a.N;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        const int64_t n0 = (int64_t)tile0 * 32 + 16 * h + 4 * q;
+        if (n0 >= a.N) continue;
+        const int64_t base = m * ldy + (p ? a.N : 0) + n0;
+        const float* bias = a.bias ? a.bias + (p ? a.N : 0) : nullptr;
+        float v4[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) v4[v] = acc[h][v] + ((bias && n0 + v < a.N) ? bias[n0 + v] : 0.0f);
+        if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
+            uint2 o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
+            if (a.res) o = add_res4<YDT>(o, a.res, base);
+            if (a.act) o = make_uint2(gelu2_y(o.x, true), gelu2_y(o.y, true));
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = o;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (n0 + v < a.N)
+                    store1<YDT>(a.y, base + v, with_res<YDT>(act_y<YDT>(v4[v], a.act), a.res, base + v));
+        }
+    }
+}
+
+template <int XDT, int YDT, int CB, bool KT, int NW, int H>
+static hipError_t wide_gv_go(WideArgs& a, hipStream_t s) {
+    const int64_t groups = (a.NT + H / 2 - 1) / (H / 2);
+    hipLaunchKernelGGL((wide_linear_gemv_kernel<XDT, YDT, CB, KT, NW, H>), dim3((unsigned)groups),
+                       dim3(64 * NW), gv_lds(H, NW), s, a);
+    return hipGetLastError();
+}
+
 template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
 static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, PB, KT, NW>), dim3((unsigned)sk_groups(a)),
@@ -323,20 +567,22 @@ static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
 // alone fill the SIMDs; ViT-B/16 batch-1 forward 0.834 -> 0.772 ms, and 2
 // waves already from 128 groups measured slower); a long stream of tiles
 // runs one wave each.
-#ifndef RPFQ_SK_SPLIT_TILES
-#define RPFQ_SK_SPLIT_TILES 4096
-#endif
-#ifndef RPFQ_SK_NW2_GROUPS
-#define RPFQ_SK_NW2_GROUPS 400
-#endif
+template <int XDT, int YDT, int CB, bool KT>
+static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
+    if (a.NT >= kSkSplitTiles) return wide_gv_go<XDT, YDT, CB, KT, 2, 4>(a, s);
+    if (a.NT >= kSkNw2Groups) return wide_gv_go<XDT, YDT, CB, KT, 2, 2>(a, s);
+    return wide_gv_go<XDT, YDT, CB, KT, 4, 2>(a, s);
+}
+
 template <int XDT, int YDT, int CB>
 static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
     const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
+    if (gemv_pays(a)) return kt ? wide_gv<XDT, YDT, CB, true>(a, s) : wide_gv<XDT, YDT, CB, false>(a, s);
     if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, true, false, 1>(a, s);
     const int64_t groups = sk_groups(a);
-    if (groups >= RPFQ_SK_NW2_GROUPS && groups < RPFQ_SK_SPLIT_TILES)
+    if (groups >= kSkNw2Groups && groups < kSkSplitTiles)
         return kt ? wide_sk_go<XDT, YDT, CB, false, true, 2>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 2>(a, s);
-    if (groups < RPFQ_SK_SPLIT_TILES)
+    if (groups < kSkSplitTiles)
         return kt ? wide_sk_go<XDT, YDT, CB, false, true, 4>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 4>(a, s);
     return kt ? wide_sk_go<XDT, YDT, CB, false, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, false, false, 1>(a, s);
 }

@@ -236,8 +236,8 @@ class PackedWide:
         return y.reshape(*lead, self.out_features)
 
     def kernel_for(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype, flags: int = 0) -> int:
-        """The kernel linear() runs for m rows (N.KERNEL_STREAM / _DMA /
-        _TILED; rpfq_wide_linear_kernel, no GPU work)."""
+        """The kernel linear() runs for m rows (N.KERNEL_STREAM / _GEMV /
+        _DMA / _TILED; rpfq_wide_linear_kernel, no GPU work)."""
         out = ctypes.c_int32(-1)
         N.check("rpfq_wide_linear_kernel", N.load().rpfq_wide_linear_kernel(
             ctypes.byref(self.desc), int(m), N.dtype_code(x_dtype), N.dtype_code(y_dtype), int(flags),

@@ -551,7 +551,7 @@ class QATLinearComplexPhase(nn.Linear):
                 x = ops.act_quant(x, self.act_quantizer.num_bits)
             bias = None if self.bias is None else self.bias.detach()
             m = x.numel() // x.shape[-1]
-            if m and pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) == N.KERNEL_STREAM:
+            if m and pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) in N.STREAM_KERNELS:
                 return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))

@@ -243,10 +243,12 @@ int main(void) {
 
 
 def test_wide_linear_kernel_choice():
-    """rpfq_wide_linear_kernel (no GPU work): the streaming kernel for a few
-    rows and for small one-tile-deep launches, the DMA kernel for large fp16
-    launches, the register-staged kernel for float32 x, bf16 output with
-    GELU, or RPFQ_FLAG_TILE_M128; the flags force their kernels."""
+    """rpfq_wide_linear_kernel (no GPU work): the streaming kernels for a few
+    rows and for small one-tile-deep launches (the column-split one for
+    M <= 8 on few tiles of short K' or many tiles of long K'), the DMA kernel
+    for large fp16 launches, the register-staged kernel for float32 x, bf16
+    output with GELU, or RPFQ_FLAG_TILE_M128; the flags force their
+    kernels."""
     L, N = lib()
     d = _desc(N, n=1536, k=384)  # ViT-B fc1
 
@@ -254,7 +256,8 @@ def test_wide_linear_kernel_choice():
         out = ctypes.c_int32(-1)
         assert L.rpfq_wide_linear_kernel(ctypes.byref(d), m, xdt, ydt, flags, ctypes.byref(out)) == 0
         return out.value
-    assert kernel(1) == N.KERNEL_STREAM and kernel(16) == N.KERNEL_STREAM
+    assert kernel(1) == N.KERNEL_GEMV and kernel(8) == N.KERNEL_GEMV and kernel(9) == N.KERNEL_STREAM
+    assert kernel(16) == N.KERNEL_STREAM
     assert kernel(197) == N.KERNEL_STREAM  # one image: 624 (chunk, tile) groups vs one 128-row tile deep
     assert kernel(50432) == N.KERNEL_DMA
     assert kernel(50432, flags=N.FLAG_GELU) == N.KERNEL_DMA
@@ -263,6 +266,14 @@ def test_wide_linear_kernel_choice():
     assert kernel(300, flags=N.FLAG_TILE_M128) == N.KERNEL_TILED
     assert kernel(197, flags=N.FLAG_NO_STREAM) == N.KERNEL_DMA
     assert kernel(50432, flags=N.FLAG_STREAM) == N.KERNEL_STREAM
+    assert kernel(8, flags=N.FLAG_STREAM) == N.KERNEL_GEMV
+    d_long = _desc(N, n=384, k=1536)  # ViT-B fc2: 12 tiles of 48 k-steps
+    d_many = _desc(N, n=131072, k=1536)  # 4096 tiles
+    d_many_short = _desc(N, n=131072, k=384)
+    for dd, want in ((d_long, N.KERNEL_STREAM), (d_many, N.KERNEL_GEMV), (d_many_short, N.KERNEL_STREAM)):
+        out = ctypes.c_int32(-1)
+        assert L.rpfq_wide_linear_kernel(ctypes.byref(dd), 1, 1, 1, 0, ctypes.byref(out)) == 0
+        assert out.value == want, (dd.n_complex, dd.k_complex, out.value)
     out = ctypes.c_int32(-1)
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 0, None) == 1
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 0, 1, 1, 0, ctypes.byref(out)) == 2

@@ -231,15 +231,24 @@ def build_packed(r, case):
     return pw, oplanes, a_ref, codebook, rotation
 
 
-def check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp=0.0):
+def operand(pw, m, xdt=torch.float16, ydt=torch.float32, flags=0):
+    """The MFMA operand of the launch: "split" on the column-split kernel
+    (fp16 U and W products summed in float32, oracle.recompose_split_fp16),
+    else True (fused fp16 coefficients, oracle.recompose_fp16)."""
+    ops, N = qm()
+    return "split" if pw.kernel_for(m, xdt, ydt, flags) == N.KERNEL_GEMV else True
+
+
+def check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp=0.0, fp16=True):
     """y from the HIP kernel vs the oracle on the same operands.
-    (a) tight: the exact product with the fp16 coefficients the MFMA sees
-        (oracle.recompose_fp16), float32 accumulation error only;
+    (a) tight: the exact product with the operand the MFMA sees (fp16: see
+        operand()), float32 accumulation error only;
     (b) against the reference's float32 A_q: the fp16 fusing bound
-        |A16 - A_q| <= (2u + u^2) (|W| + |U|), u = 2^-11, per coefficient."""
+        |A16 - A_q| <= (2u + u^2) (|W| + |U|), u = 2^-11, per coefficient
+        (the split operand is within u (|W| + |U|))."""
     bias = np.zeros(0) if bias is None else bias
     b = bias if bias.size else 0.0
-    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=fp16).astype(np.float64)
     a = O.wide_weight(oplanes, codebook, rotation).astype(np.float64)
     mag = O.wide_magnitude(oplanes, codebook, rotation)
     ax = np.abs(xf)
@@ -277,7 +286,7 @@ def test_wide_linear(case, m, flags):
     bias = r.standard_normal(2 * case[0]).astype(np.float32)
     y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32, flags=flags).cpu().numpy()
     xf = x.float().numpy().astype(np.float64)
-    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation, fp16=operand(pw, m, flags=flags))
 
 
 @pytest.mark.parametrize("m", [77, 300])
@@ -455,10 +464,11 @@ def test_wide_linear_streaming(case, m):
     bias = r.standard_normal(2 * case[0]).astype(np.float32)
     y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float32).cpu().numpy()
     xf = x.float().numpy().astype(np.float64)
-    check_against_oracle(y, xf, bias, oplanes, codebook, rotation)
+    mode = operand(pw, m)
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation, fp16=mode)
     # fp16 outputs through the 8-byte store path
     y16 = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.float16).float().cpu().numpy()
-    check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
+    check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11, fp16=mode)
 
 
 @pytest.mark.parametrize("m", [17, 45, 197, 300])
@@ -479,31 +489,41 @@ def test_wide_linear_stream_chunks(case, m):
     check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
-@pytest.mark.parametrize("m", [3, 12])
+@pytest.mark.parametrize("m,k_c", [(3, 640), (12, 640), (3, 320), (8, 320)],
+                         ids=["m3-fused", "m12-fused", "m3-gemv", "m8-gemv"])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
                                      (torch.float16, torch.bfloat16), (torch.float32, torch.float16)])
-def test_wide_linear_streaming_dtypes(xdt, ydt, m):
-    r = rng(800 + m)
-    case = (160, 640, "axis", 2, 0, None)
+def test_wide_linear_streaming_dtypes(xdt, ydt, m, k_c):
+    """Both streaming kernels (K' = 640: the fused one, 20 k-steps on 5
+    tiles; K' = 320 at M <= 8: the column-split one) with float32 and bf16
+    activations (converted to fp16 on load) and every output dtype."""
+    ops, N = qm()
+    r = rng(800 + m + k_c)
+    case = (160, k_c, "axis", 2, 0, None)
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    mode = operand(pw, m, xdt, ydt)
+    assert (mode == "split") == (k_c == 320)
     x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(xdt)
     y = pw.linear(x.to(DEV), None, out_dtype=ydt).float().cpu().numpy()
     xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
     out_ulp = {torch.float32: 1e-6, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
-    check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
+    check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp, fp16=mode)
 
 
 @pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640), (3, 16500, 200),
-                                       (4, 3000, 2048), (2, 131104, 64), (12, 131072, 96), (1, 131200, 200)])
+                                       (4, 3000, 2048), (2, 131104, 64), (12, 131072, 96), (1, 131200, 200),
+                                       (2, 131104, 640), (5, 131072, 648)])
 def test_wide_linear_streaming_persistent(m, n_c, k_c):
-    """Large N' on the streaming kernel's three forms: split K over 2 waves
-    per tile for 400 .. 4095 workgroups (66000 x 96 at M = 8: 2063 groups;
+    """Large N' on the streaming kernels' forms: split K over 2 waves per
+    tile for 400 .. 4095 workgroups (66000 x 96 at M = 8: 2063 tiles;
     70000 x 64: 2188; 16500 x 640: 516; 16500 x 200: 516 with a K' tail),
-    over 4 waves below 400 (3000 x 2048: 94 groups, 64 k-steps), and one
-    wave per tile from 4096 workgroups (the 131,072+ row cases), with K'
-    tails and K' beyond 16 k-steps.  The streaming kernel and the tiled
-    kernel (RPFQ_FLAG_NO_STREAM) contract the same fp16 operands, so float32
-    outputs agree to accumulation order."""
+    over 4 waves below 400 (3000 x 2048: 94 tiles, 64 k-steps), one wave per
+    tile from 4096 tiles (131,072+ rows at short K'), and the column-split
+    kernel's 64-row workgroups of 2 waves from 4096 tiles at >= 20 k-steps
+    (131104 x 640: an odd tile count, the last workgroup's second tile
+    clamped; 131072 x 648: a K' tail).  Each launch against the exact product
+    of the operand it contracts (float32 outputs, float32 accumulation
+    order), and the tiled kernel (RPFQ_FLAG_NO_STREAM) likewise."""
     ops, N = qm()
     r = rng(900 + m)
     planes_np, packed, sre, sim, kinds, cb, nblk = make_wide(r, n_c, k_c)
@@ -513,12 +533,18 @@ def test_wide_linear_streaming_persistent(m, n_c, k_c):
     bias = tdev(r.standard_normal(2 * n_c).astype(np.float32))
     y0 = pw.linear(x, bias, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
     y1 = pw.linear(x, bias, out_dtype=torch.float32, flags=N.FLAG_NO_STREAM).cpu().numpy().astype(np.float64)
-    a16 = pw.decode(round_fp16=True).cpu().numpy().astype(np.float64)
     xf = x.float().cpu().numpy().astype(np.float64)
-    scale = np.abs(xf) @ np.abs(a16).T + np.abs(bias.cpu().numpy())
-    assert np.all(np.abs(y0 - y1) <= 2e-6 * scale + 1e-6)
-    # and the exact product of the decoded fp16 operands
-    assert np.all(np.abs(y0 - (xf @ a16.T + bias.cpu().numpy())) <= 1e-5 * scale + 1e-5)
+    b = bias.cpu().numpy().astype(np.float64)
+    a16 = pw.decode(round_fp16=True).cpu().numpy().astype(np.float64)
+    scale = np.abs(xf) @ np.abs(a16).T + np.abs(b)
+    assert np.all(np.abs(y1 - (xf @ a16.T + b)) <= 1e-5 * scale + 1e-5)
+    if operand(pw, m) == "split":
+        del a16
+        oplanes = oracle_planes(planes_np, sre, sim, kinds, k_c, 0)
+        a_op = O.wide_weight(oplanes, "axis", None, fp16="split")
+    else:
+        a_op = a16
+    assert np.all(np.abs(y0 - (xf @ a_op.T + b)) <= 1e-5 * scale + 1e-5)
 
 
 # ---------------------------------------------------------------------------

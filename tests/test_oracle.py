@@ -379,3 +379,29 @@ def test_recompose_fp16_bound_and_identities(codebook, rot):
     assert np.array_equal(only_u[:n, k:], -only_u[n:, :k])
     # exact where fp16 represents both terms and their sum (W = 0: coefficient = fp16(U))
     assert np.array_equal(only_u[:n, :k], u_re.astype(np.float16).astype(np.float64))
+
+
+@pytest.mark.parametrize("codebook,rot", [("axis", None), ("sign", None), ("psk16", None),
+                                          ("axis", ((0.95533645, 0.29552022), (0.98006660, -0.19866933)))])
+def test_recompose_split_fp16(codebook, rot):
+    """The column-split operand: its correctly rounded fp16 value is the
+    fused operand bit for bit (fp16_add is pinned by exact rationals), it is
+    within u (|U| + |W|) of the reference A_q (one fp16 rounding per part, no
+    rounding of the sum), and with W = 0 it is fp16(U) exactly."""
+    rotation = None if rot is None else tuple((F32(c), F32(s)) for c, s in rot)
+    planes = _wide_case(13, codebook=codebook)
+    a = O.wide_weight(planes, codebook, rotation).astype(np.float64)
+    a16 = O.wide_weight(planes, codebook, rotation, fp16=True).astype(np.float64)
+    asp = O.wide_weight(planes, codebook, rotation, fp16="split")
+    assert asp.dtype == np.float64
+    assert np.array_equal(asp.astype(np.float16).astype(np.float64), a16)
+    mag = O.wide_magnitude(planes, codebook, rotation)
+    u = 2.0 ** -11
+    assert np.all(np.abs(asp - a) <= u * mag + 2.0 ** -25)
+    assert not np.array_equal(asp, a16)  # the sums are not all fp16 numbers
+    u_re, u_im, w_re, w_im = O.wide_parts(planes, codebook, rotation)
+    z = np.zeros_like(u_re)
+    n, k = u_re.shape
+    only_u = O.recompose_split_fp16(u_re, u_im, z, z)
+    assert np.array_equal(only_u[:n, :k], u_re.astype(np.float16).astype(np.float64))
+    assert np.array_equal(only_u[:n, k:], -u_im.astype(np.float16).astype(np.float64))
