@@ -39,7 +39,7 @@ CONFIGS = {
 }
 
 
-def build_model(cfg_name: str, act_quant: bool = False):
+def build_model(cfg_name: str, act_quant: bool = False, dtype=None):
     import torch
     import quant_models as qm
     from quant_models import _native as N
@@ -51,7 +51,7 @@ def build_model(cfg_name: str, act_quant: bool = False):
                             quant_method_w="complex_phase_v2", enable_act_quant=act_quant, enable_rotation=False)
     cb = N.CB_PSK16 if codebook == "psk16" else N.CB_AXIS
     load_synthetic_codes(model, seed, cb)
-    prepare_inference(model, "cuda", torch.float16)
+    prepare_inference(model, "cuda", dtype or torch.float16)
     return model
 
 
@@ -325,7 +325,7 @@ def stream_layer(k_c: int, n_c: int, seed: int, copies: int = 1):
     return [ops.PackedWide(n_c, k_c, N.CB_AXIS, 2, 0, big[i]) for i in range(copies)]
 
 
-def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, seed: int = 5):
+def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, seed: int = 5, dtype=None):
     """Batch-M weight streaming of one layer shape.
     mode "stacked": one launch with N' stacked to >= gib GiB of codes (the
     kernel's streaming rate at this K'); mode "rotate": >= gib GiB of distinct
@@ -345,9 +345,14 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
         layers = stream_layer(k_c, n_c, seed, copies)
     n_layer = layers[0].n_complex
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
-    x = torch.randn(m, 2 * k_c, device=dev, generator=g).to(torch.float16)
+    dt = dtype or torch.float16
+    from quant_models import _native as N
+    kname = {N.KERNEL_STREAM: "rpfq::wide_linear_skinny_kernel", N.KERNEL_GEMV: "rpfq::wide_linear_gemv_kernel",
+             N.KERNEL_DMA: "rpfq::wide_linear_dma_kernel", N.KERNEL_TILED: "rpfq::wide_linear_kernel"}[
+        layers[0].kernel_for(m, dt, dt)]
+    x = torch.randn(m, 2 * k_c, device=dev, generator=g).to(dt)
     bias = torch.randn(2 * n_layer, device=dev, generator=g)
-    y = torch.empty(m, 2 * n_layer, dtype=torch.float16, device=dev)
+    y = torch.empty(m, 2 * n_layer, dtype=dt, device=dev)
 
     def run_all():
         for pw in layers:
@@ -384,7 +389,8 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
     del layers
     torch.cuda.empty_cache()
     gbs = nbytes / (ms / 1e3) / 1e9
-    return {"k_complex": k_c, "n_complex": n_layer, "m": m, "mode": mode, "launches": (1 if mode == "stacked"
+    return {"k_complex": k_c, "n_complex": n_layer, "m": m, "mode": mode, "kernel": kname,
+            "launches": (1 if mode == "stacked"
             else int(code_bytes // (k_c * n_layer))), "code_gib": round(code_bytes / (1 << 30), 3),
             "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
@@ -530,6 +536,8 @@ def main() -> int:
                     help="comma-separated subset of the sweep's layer shapes (e.g. vit_b.fc1)")
     ap.add_argument("--no-stream-line", action="store_true",
                     help="leave the batch-1 streaming summary out of the bench line")
+    ap.add_argument("--dtype", default="fp16", choices=["fp16", "bf16"],
+                    help="activation dtype of the model forward (and of the batch-1 streaming line)")
     ap.add_argument("--act-quant", action="store_true",
                     help="build the model with 4-bit activation quantization (the reference layer's default)")
     ap.add_argument("--graph", action="store_true",
@@ -575,6 +583,7 @@ def main() -> int:
     import torch
     from quant_models import ops
 
+    act_dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     name, batch, img, codebook, seed, desc = CONFIGS[args.config]
     batch = args.batch or batch
     batch1 = None
@@ -582,12 +591,13 @@ def main() -> int:
         # batch-1 weight streaming (HBM roof) at the ViT-B fc1 shape; runs before
         # and outside the timed region of the model forward
         k_c, n_c = STREAM_SHAPES["vit_b.fc1"]
-        batch1 = {"kernel": "rpfq::wide_linear_skinny_kernel (M = 1)", "bound": "hbm", "peak": PEAK_HBM_GBS,
-                  "unit": "GB/s", "stacked": stream_case(k_c, n_c, 1, "stacked", 1.0, 10),
-                  "rotate": stream_case(k_c, n_c, 1, "rotate", 1.0, 5)}
-    model = build_model(args.config, args.act_quant)
+        batch1 = {"kernel": "streaming kernels at M = 1 (per case: the one rpfq_wide_linear_kernel reports)",
+                  "bound": "hbm", "peak": PEAK_HBM_GBS,
+                  "unit": "GB/s", "stacked": stream_case(k_c, n_c, 1, "stacked", 1.0, 10, dtype=act_dtype),
+                  "rotate": stream_case(k_c, n_c, 1, "rotate", 1.0, 5, dtype=act_dtype)}
+    model = build_model(args.config, args.act_quant, act_dtype)
     g = torch.Generator(device="cuda").manual_seed(seed)
-    x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(torch.float16)
+    x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(act_dtype)
 
     graph = None
     with torch.no_grad():
@@ -655,7 +665,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": args.dtype,
         "data": "synthetic (N(0,1) images; random-init weights quantized by the reference axis rule, "
                 "synthetic per-row scales)",
         "config": {"workload": f"{args.config}: {desc} forward, bs{batch}, {img}x{img}"
@@ -669,7 +679,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": None if achieved_tflops is None else round(achieved_tflops / PEAK_F16_TFLOPS, 4),
             "traffic": None,
-            "kernel": "rpfq::wide_linear_dma_kernel (fp16 x, K' % 32 == 0, M >= 128, launches over one tile "
+            "kernel": "rpfq::wide_linear_dma_kernel (fp16 / bf16 x, K' % 32 == 0, M >= 128, launches over one tile "
                       "deep; small launches rpfq::wide_linear_skinny_kernel, else rpfq::wide_linear_kernel): "
                       "all packed-layer launches in the timed region (none under --graph)",
             "launches": len(launches),

@@ -103,7 +103,7 @@ hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t
 // Widely-linear GEMM launchers, one translation unit per codebook (CB):
 // wide_dma.hip (fp16 x, LDS DMA, M >= 128), wide_stream.hip (weight
 // streaming), wide_tiled.hip (register-staged tiles, bm = 32, 64 or 128).
-template <int CB> hipError_t launch_wide_dma(WideArgs& a, int ydt, hipStream_t s);
+template <int CB> hipError_t launch_wide_dma(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int ydt, hipStream_t s);
 // workgroups of the streaming kernel: one per (16-row chunk, 32-row tile)

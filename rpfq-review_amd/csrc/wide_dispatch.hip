@@ -61,7 +61,8 @@ static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
     flags &= ~RPFQ_FLAG_NO_STREAM;
     // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
     // spill in its k-loop, so they take the register-staged kernel)
-    if (xdt == RPFQ_F16 && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M && !(a.act && ydt == RPFQ_BF16))
+    if ((xdt == RPFQ_F16 || xdt == RPFQ_BF16) && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M &&
+        !(a.act && ydt == RPFQ_BF16))
         return RPFQ_KERNEL_DMA;
     return RPFQ_KERNEL_TILED;
 }
@@ -70,7 +71,7 @@ template <int CB>
 static hipError_t wide_cb(WideArgs& a, int xdt, int ydt, int flags, hipStream_t s) {
     const int k = choose_kernel(a, xdt, ydt, flags);
     if (k == RPFQ_KERNEL_STREAM || k == RPFQ_KERNEL_GEMV) return launch_wide_stream<CB>(a, xdt, ydt, s);
-    if (k == RPFQ_KERNEL_DMA) return launch_wide_dma<CB>(a, ydt, s);
+    if (k == RPFQ_KERNEL_DMA) return launch_wide_dma<CB>(a, xdt, ydt, s);
     flags &= ~RPFQ_FLAG_NO_STREAM;
     const int bm = (flags & RPFQ_FLAG_TILE_M128) ? 128 : a.M <= 32 ? 32 : a.M <= 64 ? 64 : 128;
     return launch_wide_tiled<CB>(a, bm, xdt, ydt, s);

@@ -1,4 +1,4 @@
-// Widely-linear GEMM for fp16 activations staged by LDS DMA (large M).
+// Widely-linear GEMM for fp16 or bf16 activations staged by LDS DMA (large M).
 // Compiled once per codebook (RPFQ_CB_SEL).
 #include "rpfq_device.h"
 
@@ -9,7 +9,7 @@
 namespace rpfq {
 
 // ---------------------------------------------------------------------------
-// widely-linear GEMM, fp16 activations staged by LDS DMA (large M)
+// widely-linear GEMM, fp16 / bf16 activations staged by LDS DMA (large M)
 // ---------------------------------------------------------------------------
 // Workgroup = 4 waves, tile = 128 rows of x times 128 complex output rows;
 // wave w owns complex rows 32w..32w+31 (both their real and imaginary
@@ -105,9 +105,33 @@ __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, con
     }
 }
 
+// bf16 activations: the DMA stages raw bf16 and each wave rewrites the rows
+// it loaded as fp16 in place once they land (v_cvt_pk_f16_f32 of the exact
+// float32 value: exact for |x| in [2^-14, 65504], rounded in the fp16
+// subnormal range, +-inf beyond; the conversion every other kernel applies
+// on load), mid-k-step for the next stage, before the barrier that
+// publishes it.  Costs ~20% of the kernel at ViT-B/16 bs256 (the LDS
+// traffic of the rewrite; converting each MFMA operand in registers instead,
+// 4 times over, costs ~35%).
+template <int XDT, int NROWS>
+__device__ __forceinline__ void stage_to_f16(uint32_t rows, int lane) {
+    if constexpr (XDT == RPFQ_BF16) {
+#pragma unroll
+        for (int j = 0; j < NROWS * 128 / 1024; ++j) {  // NROWS rows of 128 B: 16-B chunks, 64 lanes
+            const uint32_t addr = rows + (uint32_t)(j * 64 + lane) * 16u;
+            const u32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const u32x4*>(addr);
+            u32x4 o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = pack_h2(bf16_to_f32(v[t] & 0xffffu), bf16_to_f32(v[t] >> 16));
+            *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(addr) = o;
+        }
+    }
+}
+
 // ACT (compile time, = WideArgs::act): the fused GELU's code stays out of
 // the plain instantiation, whose k-loop runs at the edge of the register file.
-template <int BM, int YDT, int CB, int ACT>
+// XDT: RPFQ_F16 or RPFQ_BF16 (converted in LDS, above).
+template <int BM, int XDT, int YDT, int CB, int ACT>
 __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int MB = BM / 32;
@@ -243,6 +267,10 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
     else
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    if constexpr (XDT == RPFQ_BF16) {
+        stage_to_f16<XDT, RPW>(lds_stages + 2 * kDmaStage, lane);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
@@ -297,6 +325,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         half8 ax_c[MB], b_re, b_im;
         read_sub(0, U, W, ax_c);
         decode(U, W, b_re, b_im);
+
         // Substep pipeline, fenced so the scheduler keeps it: (1) LUT
         // addresses and the 12 LDS reads of substep s+1; (2) 4 MFMAs of
         // substep s, covering the LDS latency; (3) the decode of s+1 next to
@@ -323,6 +352,23 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 for (int i = 0; i < MB; ++i) ax_c[i] = ax_n[i];
             }
             __builtin_amdgcn_sched_barrier(0);
+            if constexpr (XDT == RPFQ_BF16) {
+                // mid-step: the activations of ks + 1 (requested two k-steps
+                // ago; only this step's codes and activations are younger)
+                // have landed; this wave's rows go to fp16 beside the MFMAs
+                if (s == 1 && ks + 1 < a.KS) {
+                    if (ks + 2 < a.KS) {
+                        if (RPW == 32)
+                            asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+                        else
+                            asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+                    } else {
+                        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+                    }
+                    stage_to_f16<XDT, RPW>(lds_stages + (st == 2 ? 0 : st + 1) * kDmaStage, lane);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (ks + 1 < a.KS) {
             const int nb = (ks + 1) / a.block_ks;
@@ -532,37 +578,42 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     }
 }
 
-template <int BM, int YDT, int CB, int ACT>
+template <int BM, int XDT, int YDT, int CB, int ACT>
 static hipError_t wide_dma_act(WideArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
     constexpr int lds = dma_lds<BM>();
-    const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_linear_dma_kernel<BM, YDT, CB, ACT>),
-                                           lds, attr_done);
+    const hipError_t e = set_lds_attr_once(
+        reinterpret_cast<const void*>(&wide_linear_dma_kernel<BM, XDT, YDT, CB, ACT>), lds, attr_done);
     if (e != hipSuccess) return e;
     a.tiles_m = (int)((a.M + BM - 1) / BM);
     a.tiles_n = (int)((a.NT + 3) / 4);
     const int total = a.tiles_m * a.tiles_n;
     const int slots = (BM == 128 ? 2 : 1) * device_cus();  // workgroups resident per CU
     const int grid = total < slots ? total : slots;
-    hipLaunchKernelGGL((wide_linear_dma_kernel<BM, YDT, CB, ACT>), dim3(grid), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((wide_linear_dma_kernel<BM, XDT, YDT, CB, ACT>), dim3(grid), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
-template <int BM, int YDT, int CB>
+template <int BM, int XDT, int YDT, int CB>
 static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
-    if constexpr (YDT == RPFQ_BF16) return wide_dma_act<BM, YDT, CB, 0>(a, s);  // GELU: not routed here
-    else return a.act ? wide_dma_act<BM, YDT, CB, 1>(a, s) : wide_dma_act<BM, YDT, CB, 0>(a, s);
+    if constexpr (YDT == RPFQ_BF16) return wide_dma_act<BM, XDT, YDT, CB, 0>(a, s);  // GELU: not routed here
+    else return a.act ? wide_dma_act<BM, XDT, YDT, CB, 1>(a, s) : wide_dma_act<BM, XDT, YDT, CB, 0>(a, s);
 }
 
-template <int CB>
-hipError_t launch_wide_dma(WideArgs& a, int ydt, hipStream_t s) {
+template <int XDT, int CB>
+static hipError_t wide_dma_y(WideArgs& a, int ydt, hipStream_t s) {
     switch (ydt) {
-        case RPFQ_F32: return wide_dma_go<128, RPFQ_F32, CB>(a, s);
-        case RPFQ_F16: return wide_dma_go<128, RPFQ_F16, CB>(a, s);
-        default: return wide_dma_go<128, RPFQ_BF16, CB>(a, s);
+        case RPFQ_F32: return wide_dma_go<128, XDT, RPFQ_F32, CB>(a, s);
+        case RPFQ_F16: return wide_dma_go<128, XDT, RPFQ_F16, CB>(a, s);
+        default: return wide_dma_go<128, XDT, RPFQ_BF16, CB>(a, s);
     }
 }
 
-template hipError_t launch_wide_dma<RPFQ_CB_SEL>(WideArgs&, int, hipStream_t);
+template <int CB>
+hipError_t launch_wide_dma(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+    return xdt == RPFQ_BF16 ? wide_dma_y<RPFQ_BF16, CB>(a, ydt, s) : wide_dma_y<RPFQ_F16, CB>(a, ydt, s);
+}
+
+template hipError_t launch_wide_dma<RPFQ_CB_SEL>(WideArgs&, int, int, hipStream_t);
 
 }  // namespace rpfq

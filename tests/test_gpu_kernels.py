@@ -386,6 +386,27 @@ def test_wide_linear_model_shapes(case, m, flags):
     check_against_oracle(y16, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", [REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[4], REAL_SHAPES[6]],
+                         ids=["fc1", "fc2", "l-fc2", "l-fc2-psk16"])
+def test_wide_linear_dma_bf16(case, ydt):
+    """bf16 activations on the LDS-DMA kernel (converted to fp16 in LDS after
+    each stage lands) at the model layer shapes, M = 300 (RPFQ_FLAG_NO_STREAM;
+    the last m-tile shifted back), against the oracle on the fp16-converted
+    activations."""
+    ops, N = qm()
+    r = rng(1700 + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    m = 300
+    assert pw.kernel_for(m, torch.bfloat16, ydt, N.FLAG_NO_STREAM) == N.KERNEL_DMA
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.bfloat16)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=ydt, flags=N.FLAG_NO_STREAM).float().cpu().numpy()
+    xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
+    out_ulp = {torch.float32: 1e-6, torch.bfloat16: 2.0 ** -7}[ydt]
+    check_against_oracle(y, xf, bias, oplanes, codebook, rotation, out_ulp)
+
+
 @pytest.mark.parametrize("case", [REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[1], REAL_SHAPES[0]],
                          ids=["fc1", "fc2", "proj", "qkv"])
 def test_wide_linear_full_batch_rows(case):
