@@ -354,6 +354,148 @@ __device__ __forceinline__ uint32_t raw2_f16(uint32_t v) {
     return pack_h2(bf16_to_f32(v & 0xffffu), bf16_to_f32(v >> 16));
 }
 
+// Lane constants of the column-split kernels.
+struct GvLane {
+    int r16, q, R, g;
+    int coff;             // uint2 index of the lane's codes in a 16-row block
+    int p, xrow, cq;      // B lane: part p of x row xrow / 2K, columns cq + 8 t ..
+    int off1, off2;       // element offsets of L1 (part p) and L2 (the other part)
+    uint32_t m0, m1;      // sign masks of the B dwords (re / im column)
+    uint32_t slot0;       // LUT slot of the lane's row in byte 0 of an address
+};
+__device__ __forceinline__ GvLane gv_lane(int lane, int M, int K) {
+    GvLane l;
+    l.r16 = lane & 15;
+    l.q = lane >> 4;
+    l.R = lane & 31;
+    l.g = lane >> 5;
+    l.coff = l.r16 * 4 + l.q;
+    l.p = l.r16 & 1;
+    l.xrow = min(l.r16 >> 1, M - 1) * 2 * K;
+    l.cq = 16 * (l.q & 1) + 4 * (l.q >> 1);
+    l.off1 = l.xrow + (l.p ? K : 0) + l.cq;
+    l.off2 = l.xrow + (l.p ? 0 : K) + l.cq;
+    l.m0 = l.p ? 0u : 0x80000000u;
+    l.m1 = l.p ? 0x00008000u : 0u;
+    l.slot0 = (uint32_t)(16 * (l.q & 1) + l.r16) * 4;
+    return l;
+}
+
+// Activations of k-step ks (raw 16-bit or fp16-converted float32), [t][L1, L2].
+template <int XDT, bool KT>
+__device__ __forceinline__ void gv_load_x(const WideArgs& a, const GvLane& l, int ks, uint2* xv) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int col = 32 * ks + 8 * t;
+        const bool in = !KT || col + l.cq < a.K;  // K' tail: the row's first columns, zeroed at use
+        xv[2 * t] = load4_raw<XDT>(a.x, in ? l.off1 + col : l.xrow);
+        xv[2 * t + 1] = load4_raw<XDT>(a.x, in ? l.off2 + col : l.xrow);
+    }
+}
+
+// One k-step: B operands from the activations, LUT reads of the H row
+// groups' U and W values, 4 x H MFMAs (acc[h * NA + j % NA]).
+template <int XDT, bool KT, int H, int NA>
+__device__ __forceinline__ void gv_kstep(floatx4* acc, const GvLane& l, int ks, int K, const uint2* c,
+                                         const uint2* xv) {
+    // L1 / L2 dword j: columns c0, c0 + 1 of MFMA j
+    const uint32_t l1[4] = {xv[0].x, xv[0].y, xv[2].x, xv[2].y};
+    const uint32_t l2[4] = {xv[1].x, xv[1].y, xv[3].x, xv[3].y};
+    half8 bx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t u1 = raw2_f16<XDT>(l1[j]), u2 = raw2_f16<XDT>(l2[j]);
+        const uint32_t p0 = __builtin_amdgcn_perm(u2, u1, 0x05040100u);
+        const uint32_t p1 = __builtin_amdgcn_perm(u2, u1, 0x07060302u);
+        uint4 b = make_uint4(p0 ^ l.m0, p0 ^ l.m1, p1 ^ l.m0, p1 ^ l.m1);
+        if (KT && 32 * ks + l.cq + 8 * (j >> 1) >= K) b = make_uint4(0, 0, 0, 0);
+        bx[j] = as_half8(b);
+    }
+    // index nibbles of every row group, then the MFMAs j-major so that
+    // consecutive ones accumulate into different row groups
+    uint32_t pu[H][2], pw[H][2];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        pu[h][0] = c[h].x & 0x0f0f0f0fu;
+        pw[h][0] = (c[h].x >> 4) & 0x0f0f0f0fu;
+        pu[h][1] = c[h].y & 0x0f0f0f0fu;
+        pw[h][1] = (c[h].y >> 4) & 0x0f0f0f0fu;
+    }
+    auto reads = [&](int j, uint32_t (&av)[H][4]) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const uint32_t slot = l.slot0 + 128 * (h & 1);
+            const int rg = (h >> 1) * (kSkLut / 4);  // LUT of the h-th tile, in dwords
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t sel = 0x03020000u | ((4u + 2 * (j & 1) + e) << 8);
+                av[h][2 * e] = *((lds_u32_t)__builtin_amdgcn_perm(pu[h][j >> 1], slot, sel) + rg);
+                av[h][2 * e + 1] = *((lds_u32_t)__builtin_amdgcn_perm(pw[h][j >> 1], slot, sel) + rg + 16 * 64);
+            }
+        }
+    };
+    // LUT reads of MFMA j + 1 are issued before the MFMAs of j, so each
+    // group of MFMAs waits only for reads issued a group earlier
+    uint32_t av[2][H][4];
+    reads(0, av[0]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < 3) reads(j + 1, av[(j + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+            acc[h * NA + (j % NA)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                as_half8(make_uint4(av[j & 1][h][0], av[j & 1][h][1], av[j & 1][h][2], av[j & 1][h][3])), bx[j],
+                acc[h * NA + (j % NA)], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Epilogue: lane (col = r16, q) holds part p of x row m = col / 2 for the
+// outputs n = 32 tile0 + 16 h + 4 q + v; rows past M and outputs past N'
+// store nothing.
+template <int YDT, int H>
+__device__ __forceinline__ void gv_store(const WideArgs& a, const GvLane& l, const floatx4* acc, int tile0, int M) {
+    const int m = l.r16 >> 1;
+    if (m >= M) return;
+    const int64_t ldy = 2 * (int64_t)a.N;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        const int64_t n0 = (int64_t)tile0 * 32 + 16 * h + 4 * l.q;
+        if (n0 >= a.N) continue;
+        const int64_t base = m * ldy + (l.p ? a.N : 0) + n0;
+        const float* bias = a.bias ? a.bias + (l.p ? a.N : 0) : nullptr;
+        float v4[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) v4[v] = acc[h][v] + ((bias && n0 + v < a.N) ? bias[n0 + v] : 0.0f);
+        if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
+            uint2 o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
+            if (a.res) o = add_res4<YDT>(o, a.res, base);
+            if (a.act) o = make_uint2(gelu2_y(o.x, true), gelu2_y(o.y, true));
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = o;
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (n0 + v < a.N)
+                    store1<YDT>(a.y, base + v, with_res<YDT>(act_y<YDT>(v4[v], a.act), a.res, base + v));
+        }
+    }
+}
+
+// LUTs of the TPG tiles from tile0 on, each wave of NW building its share
+// of the 8 entry pairs per tile (clamped to the last packed tile).
+template <int CB, int TPG, int NW>
+__device__ __forceinline__ void gv_build_luts(uint32_t* lut, const WideArgs& a, int tile0, int wave, int R, int g) {
+    constexpr int per = 8 * TPG / NW, nj = per < 8 ? per : 8;
+#pragma unroll
+    for (int f = 0; f < per; f += nj) {
+        const int f0 = wave * per + f, region = f0 >> 3;
+        const int tile = min(tile0 + region, a.NT - 1);
+        const float4* pp = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
+        build_lut_sk<CB, nj>(lut + region * (kSkLut / 4), pp, a.rot, R, g, f0 & 7);
+    }
+}
+
 template <int XDT, int YDT, int CB, bool KT, int NW, int H>
 __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(WideArgs a) {
     static_assert(H == 2 || H == 4, "16-row groups per workgroup");
@@ -362,10 +504,9 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
     const int lane = threadIdx.x & 63;
     const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r16 = lane & 15, q = lane >> 4;
-    const int R = lane & 31, g = lane >> 5;
-    const int KS = a.KS, K = a.K;
+    const int KS = a.KS;
     const int M = (int)a.M;  // 1 .. 8 (host-checked)
+    const GvLane l = gv_lane(lane, M, a.K);
     const int chunk = (KS + NW - 1) / NW;
     const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
     const int tile0 = (int)blockIdx.x * TPG;
@@ -375,52 +516,24 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
 #pragma unroll
     for (int t = 0; t < TPG; ++t)
         ctile[t] = reinterpret_cast<const uint2*>(a.codes) + (int64_t)min(tile0 + t, a.NT - 1) * KS * 128;
-    const int coff = r16 * 4 + q;
-    // B lane: x row m, part p (0 re, 1 im); L1 = part p, L2 = the other part
-    const int p = r16 & 1;
-    const int xrow = min(r16 >> 1, M - 1) * 2 * K;
-    const int cq = 16 * (q & 1) + 4 * (q >> 1);
-    const int off1 = xrow + (p ? K : 0) + cq, off2 = xrow + (p ? 0 : K) + cq;
-    const uint32_t m0 = p ? 0u : 0x80000000u, m1 = p ? 0x00008000u : 0u;
-
     uint2 cring[SK_PF][H];
-    uint2 xring[GV_XPF][4];  // [t][L1, L2]: t = 0 at 0, 1; t = 1 at 2, 3
+    uint2 xring[GV_XPF][4];
     auto clamp_ks = [&](int ks) { return ks < ke ? ks : (ke > 0 ? ke - 1 : 0); };  // past the range: unused
     auto load_codes = [&](int ks, uint2* c) {
         const int kc = clamp_ks(ks);
 #pragma unroll
-        for (int h = 0; h < H; ++h) c[h] = ctile[h >> 1][kc * 128 + coff + 64 * (h & 1)];
-    };
-    auto load_x = [&](int ks, uint2* xv) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int col = 32 * clamp_ks(ks) + 8 * t;
-            const bool in = !KT || col + cq < K;  // K' tail: the row's first columns, zeroed at use
-            xv[2 * t] = load4_raw<XDT>(a.x, in ? off1 + col : xrow);
-            xv[2 * t + 1] = load4_raw<XDT>(a.x, in ? off2 + col : xrow);
-        }
+        for (int h = 0; h < H; ++h) c[h] = ctile[h >> 1][kc * 128 + l.coff + 64 * (h & 1)];
     };
 #pragma unroll
     for (int i = 0; i < SK_PF; ++i) load_codes(kb + i, cring[i]);
 #pragma unroll
-    for (int i = 0; i < GV_XPF; ++i) load_x(kb + i, xring[i]);
-
-    {  // the waves build the TPG LUTs in equal shares of their 8 entry pairs
-        constexpr int per = 8 * TPG / NW, nj = per < 8 ? per : 8;
-#pragma unroll
-        for (int f = 0; f < per; f += nj) {
-            const int f0 = wave * per + f, region = f0 >> 3;
-            const int tile = min(tile0 + region, a.NT - 1);
-            const float4* pp = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
-            build_lut_sk<CB, nj>(lut + region * (kSkLut / 4), pp, a.rot, R, g, f0 & 7);
-        }
-    }
+    for (int i = 0; i < GV_XPF; ++i) gv_load_x<XDT, KT>(a, l, clamp_ks(kb + i), xring[i]);
+    gv_build_luts<CB, TPG, NW>(lut, a, tile0, wave, l.R, l.g);
     if (NW > 1) {  // LUT written before any wave reads it; the loads stay in flight
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     }
-    const uint32_t slot0 = (uint32_t)(16 * (q & 1) + r16) * 4;
 
     // two accumulators per row group when H = 2 (MFMAs j even / odd), so
     // that four independent chains interleave as with H = 4
@@ -428,68 +541,15 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
     floatx4 acc[H * NA];
 #pragma unroll
     for (int h = 0; h < H * NA; ++h) acc[h] = floatx4{0, 0, 0, 0};
-    auto compute = [&](int ks, const uint2* c, const uint2* xv) {
-        // L1 / L2 dword j: columns c0, c0 + 1 of MFMA j
-        const uint32_t l1[4] = {xv[0].x, xv[0].y, xv[2].x, xv[2].y};
-        const uint32_t l2[4] = {xv[1].x, xv[1].y, xv[3].x, xv[3].y};
-        half8 bx[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t u1 = raw2_f16<XDT>(l1[j]), u2 = raw2_f16<XDT>(l2[j]);
-            const uint32_t p0 = __builtin_amdgcn_perm(u2, u1, 0x05040100u);
-            const uint32_t p1 = __builtin_amdgcn_perm(u2, u1, 0x07060302u);
-            uint4 b = make_uint4(p0 ^ m0, p0 ^ m1, p1 ^ m0, p1 ^ m1);
-            if (KT && 32 * ks + cq + 8 * (j >> 1) >= K) b = make_uint4(0, 0, 0, 0);
-            bx[j] = as_half8(b);
-        }
-        // index nibbles of every row group, then the MFMAs j-major so that
-        // consecutive ones accumulate into different row groups
-        uint32_t pu[H][2], pw[H][2];
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-            pu[h][0] = c[h].x & 0x0f0f0f0fu;
-            pw[h][0] = (c[h].x >> 4) & 0x0f0f0f0fu;
-            pu[h][1] = c[h].y & 0x0f0f0f0fu;
-            pw[h][1] = (c[h].y >> 4) & 0x0f0f0f0fu;
-        }
-        auto reads = [&](int j, uint32_t (&av)[H][4]) {
-#pragma unroll
-            for (int h = 0; h < H; ++h) {
-                const uint32_t slot = slot0 + 128 * (h & 1);
-                const int rg = (h >> 1) * (kSkLut / 4);  // LUT of the h-th tile, in dwords
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t sel = 0x03020000u | ((4u + 2 * (j & 1) + e) << 8);
-                    av[h][2 * e] = *((lds_u32_t)__builtin_amdgcn_perm(pu[h][j >> 1], slot, sel) + rg);
-                    av[h][2 * e + 1] = *((lds_u32_t)__builtin_amdgcn_perm(pw[h][j >> 1], slot, sel) + rg + 16 * 64);
-                }
-            }
-        };
-        // LUT reads of MFMA j + 1 are issued before the MFMAs of j, so each
-        // group of MFMAs waits only for reads issued a group earlier
-        uint32_t av[2][H][4];
-        reads(0, av[0]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (j < 3) reads(j + 1, av[(j + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int h = 0; h < H; ++h)
-                acc[h * NA + (j % NA)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    as_half8(make_uint4(av[j & 1][h][0], av[j & 1][h][1], av[j & 1][h][2], av[j & 1][h][3])), bx[j],
-                    acc[h * NA + (j % NA)], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
     // (the k-step loop of the kernel above)
     for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
 #pragma unroll
         for (int i = 0; i < SK_PF; ++i) {
             const int ks = ks0 + i;
-            if (ks < ke) compute(ks, cring[i], xring[i % GV_XPF]);
+            if (ks < ke) gv_kstep<XDT, KT, H, NA>(acc, l, ks, a.K, cring[i], xring[i % GV_XPF]);
             // the slots just consumed take k-step ks + SK_PF (ks + GV_XPF)
             load_codes(ks + SK_PF, cring[i]);
-            load_x(ks + GV_XPF, xring[i % GV_XPF]);
+            gv_load_x<XDT, KT>(a, l, clamp_ks(ks + GV_XPF), xring[i % GV_XPF]);
         }
     }
 
@@ -516,34 +576,7 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[h][v] += red[((w * H + h) * 4 + v) * 64 + lane];
     }
-
-    // Epilogue: lane (col = r16, q) holds part p of x row m = col / 2 for the
-    // outputs n = 32 tile0 + 16 h + 4 q + v; rows past M and outputs past N'
-    // store nothing.
-    const int m = r16 >> 1;
-    if (m >= M) return;
-    const int64_t ldy = 2 * (int64_t)a.N;
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-        const int64_t n0 = (int64_t)tile0 * 32 + 16 * h + 4 * q;
-        if (n0 >= a.N) continue;
-        const int64_t base = m * ldy + (p ? a.N : 0) + n0;
-        const float* bias = a.bias ? a.bias + (p ? a.N : 0) : nullptr;
-        float v4[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) v4[v] = acc[h][v] + ((bias && n0 + v < a.N) ? bias[n0 + v] : 0.0f);
-        if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
-            uint2 o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
-            if (a.res) o = add_res4<YDT>(o, a.res, base);
-            if (a.act) o = make_uint2(gelu2_y(o.x, true), gelu2_y(o.y, true));
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = o;
-        } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                if (n0 + v < a.N)
-                    store1<YDT>(a.y, base + v, with_res<YDT>(act_y<YDT>(v4[v], a.act), a.res, base + v));
-        }
-    }
+    gv_store<YDT, H>(a, l, acc, tile0, M);
 }
 
 template <int XDT, int YDT, int CB, bool KT, int NW, int H>
@@ -566,7 +599,7 @@ static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
 // 2 from there (less LUT building and reduction per k-step once the groups
 // alone fill the SIMDs; ViT-B/16 batch-1 forward 0.834 -> 0.772 ms, and 2
 // waves already from 128 groups measured slower); a long stream of tiles
-// runs one wave each.
+// runs one wave each (the column-split kernel: 2 waves per 64 rows).
 template <int XDT, int YDT, int CB, bool KT>
 static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
     if (a.NT >= kSkSplitTiles) return wide_gv_go<XDT, YDT, CB, KT, 2, 4>(a, s);
