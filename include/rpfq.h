@@ -238,6 +238,22 @@ int rpfq_layer_norm_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, 
                               const float* beta, float eps, int bits, void* y, int y_dtype, void* stream);
 
 /*
+ * The exact GELU (approximate = 'none') of each element of x [M, C] in
+ * float32 followed by the activation fake quantization of rpfq_act_quant,
+ * in one pass over the rows: the float32 GELU is quantized per row and per
+ * half (C/2 columns each; C % 16 == 0), only the quantized value rounded to
+ * y_dtype, as the reference quantizes fc2's float32 input; y is
+ * bit-identical to torch's GELU with float32 output followed by
+ * rpfq_act_quant with y_dtype output.  bits: 2 .. 16.  x and y 16-byte
+ * aligned, C up to 4096; y may equal x.  The fc2 input of a block with
+ * activation quantization on:
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:550-553 (act, fc2)
+ *   with RPFQ-ViT-main/quant_models/quant_i.py:546-551 inside fc2.
+ */
+int rpfq_gelu_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, int bits, void* y, int y_dtype,
+                        void* stream);
+
+/*
  * Activation fake quantization of a [M, in_features] feature block laid out
  * [re | im]: per row and per half, scale = qmax * (1 / max(max|x|, 1e-5)),
  * y = clamp(round_half_even(x * scale), -2^(bits-1), 2^(bits-1)-1) / scale,

@@ -235,6 +235,17 @@ int rpfq_layer_norm_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, 
                       "rpfq_layer_norm_act_quant");
 }
 
+int rpfq_gelu_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, int bits, void* y, int y_dtype,
+                        void* stream) {
+    int rc = check_ln(x, x_dtype, M, C, nullptr, nullptr, 0.0f, y, y_dtype);
+    if (rc) return rc;
+    if (C % 16 != 0) return fail(RPFQ_ERR_SHAPE, "C=%lld: each half must be a multiple of 8", (long long)C);
+    if (bits < 2 || bits > 16) return fail(RPFQ_ERR_BITS, "bits=%d unsupported (2..16)", bits);
+    return hip_status(rpfq::launch_gelu_act_quant(x, x_dtype, M, C, bits, y, y_dtype,
+                                                  reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_gelu_act_quant");
+}
+
 int rpfq_act_quant(const void* x, int x_dtype, int64_t M, int64_t in_features, int bits, void* y, int y_dtype,
                    void* stream) {
     if (!x || !y) return fail(RPFQ_ERR_NULL, "x/y must not be NULL");

@@ -464,9 +464,13 @@ __device__ __forceinline__ float group_max(float v) {
 // reference quantizes its float32 LayerNorm output, and rounds only the
 // quantized value to y's dtype: bit-identical to LN with float32 output
 // followed by AQ with y's dtype as output.
+// GE + AQ: the exact GELU of each element in float32 (gelu_f, torch's
+// formula), quantized without rounding to y's dtype in between -- as the
+// reference quantizes fc2's float32 input -- then rounded to y's dtype:
+// bit-identical to GELU with float32 output followed by AQ.
 // Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
 // the two halves.
-template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ>
+template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ, bool GE = false>
 __global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict__ x, int64_t M, int C,
                                                          const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float eps, int bits,
@@ -530,6 +534,15 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict_
                 for (int e = 0; e < 8; ++e) {
                     v[j][e] = (v[j][e] - mean) * rstd * gk[e] + bk[e];
                 }
+            }
+        }
+    }
+    if (GE) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            if (sub + TPR * j < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[j][e] = gelu_f(v[j][e]);
             }
         }
     }
@@ -700,6 +713,9 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
     else if (mode == 2)
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true>), grid, dim3(256), 0, s, x, M, C, gamma,
                            beta, eps, bits, y);
+    else if (mode == 4)
+        hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true, true>), grid, dim3(256), 0, s, x, M, C,
+                           gamma, beta, eps, bits, y);
     else
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, true>), grid, dim3(256), 0, s, x, M, C, gamma,
                            beta, eps, bits, y);
@@ -711,7 +727,8 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
 // lanes whenever that smallest choice would launch fewer than 256
 // workgroups (a batch-1 forward: 197 rows), so the launch spreads over the
 // CUs and each lane's chain of loads and reductions is shorter.
-// mode: 1 LayerNorm, 2 activation quantization, 3 both.
+// mode: 1 LayerNorm, 2 activation quantization, 3 both, 4 GELU + activation
+// quantization.
 template <int XDT, int YDT>
 static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
                         int mode, int bits, void* y, hipStream_t s) {
@@ -748,6 +765,11 @@ static hipError_t row_op(const void* x, int xdt, int64_t M, int64_t C, const flo
 hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
                              float eps, int bits, void* y, int ydt, hipStream_t s) {
     return row_op(x, xdt, M, C, gamma, beta, eps, bits > 0 ? 3 : 1, bits, y, ydt, s);
+}
+
+hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,
+                                 hipStream_t s) {
+    return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 4, bits, y, ydt, s);
 }
 
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, float* out,

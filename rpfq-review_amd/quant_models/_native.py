@@ -53,6 +53,7 @@ EXPORTED = (
     "rpfq_wide_linear_kernel",
     "rpfq_layer_norm",
     "rpfq_layer_norm_act_quant",
+    "rpfq_gelu_act_quant",
     "rpfq_quantize_workspace_bytes",
     "rpfq_quantize_wide",
     "rpfq_quantize_wide_noalloc",
@@ -131,6 +132,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_wide_linear_kernel.argtypes = [dp, i64, i32, i32, i32, ctypes.POINTER(i32)]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
+        lib.rpfq_gelu_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         qp = ctypes.POINTER(QuantDesc)
         lib.rpfq_quantize_workspace_bytes.argtypes = [qp]
         lib.rpfq_quantize_workspace_bytes.restype = sz

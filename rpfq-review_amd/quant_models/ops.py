@@ -96,6 +96,23 @@ def act_quant(x: torch.Tensor, num_bits: int, out_dtype: torch.dtype | None = No
     return y.reshape(*lead, f)
 
 
+def gelu_act_quant(x: torch.Tensor, num_bits: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """act_quant(F.gelu(x)) with the exact GELU in float32 and no rounding to
+    x's dtype in between (rpfq_gelu_act_quant: bit-identical to
+    act_quant(F.gelu(x.float()), num_bits, out_dtype)); [..., C] rows, C %
+    16 == 0, C <= 4096."""
+    N.require_device(x)
+    c = x.shape[-1]
+    x2 = _aligned_rows(x.reshape(-1, c))
+    y = torch.empty(x2.shape, dtype=out_dtype or x.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return y.reshape(x.shape)
+    N.check("rpfq_gelu_act_quant", N.load().rpfq_gelu_act_quant(
+        x2.data_ptr(), N.dtype_code(x2.dtype), x2.shape[0], c, int(num_bits), y.data_ptr(), N.dtype_code(y.dtype),
+        N.stream_of(x2)))
+    return y.reshape(x.shape)
+
+
 def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None, eps: float,
                out_dtype: torch.dtype | None = None, act_bits: int = 0) -> torch.Tensor:
     """nn.LayerNorm over the last dimension on the device (rpfq_layer_norm):

@@ -556,16 +556,17 @@ class QATLinearComplexPhase(nn.Linear):
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
 
-    def forward_residual(self, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        """residual + self(x).  On the packed HIP path the add is fused into
-        the kernel's store (bit-identical to the unfused add in x's dtype);
+    def forward_residual(self, x: torch.Tensor, residual: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
+        """residual + self(x); x already activation-quantized for this layer
+        if prequantized.  On the packed HIP path the add is fused into the
+        kernel's store (bit-identical to the unfused add in x's dtype);
         elsewhere it is the plain sum."""
         if x.is_cuda and not self.training and self.use_packed:
             from . import ops
 
             pw = self.packed(x.device)
-            if self.act_quantizer is not None:
+            if self.act_quantizer is not None and not prequantized:
                 x = ops.act_quant(x, self.act_quantizer.num_bits)
             bias = None if self.bias is None else self.bias.detach()
             return pw.linear(x, bias, out_dtype=x.dtype, residual=residual)
-        return residual + self.forward(x)
+        return residual + (self.forward_prequantized(x) if prequantized else self.forward(x))

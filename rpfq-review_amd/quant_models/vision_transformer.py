@@ -135,9 +135,22 @@ class Mlp(nn.Module):
     def forward_residual(self, x, residual, prequantized: bool = False):
         """residual + self(x) with the add fused into fc2 and an exact GELU
         into fc1's store when fc1 is a phase-quantized Linear (eval mode); x
-        already activation-quantized for fc1 if prequantized."""
+        already activation-quantized for fc1 if prequantized.  When fc2
+        quantizes its input, the GELU and that quantization run as one pass
+        over fc1's output instead (rpfq_gelu_act_quant, float32 GELU
+        quantized without rounding in between)."""
+        gelu_exact = type(self.act) is nn.GELU and self.act.approximate == "none"
+        if FUSE_GELU and FUSE_ACT_QUANT and gelu_exact and type(self.norm) is nn.Identity:
+            bits_of = getattr(self.fc2, "packed_act_bits", None)
+            bits = bits_of(x) if bits_of is not None else 0
+            c = self.fc2.in_features
+            if bits and c % 16 == 0 and c <= 4096:
+                from . import ops
+
+                h = ops.gelu_act_quant(call_layer(self.fc1, x, prequantized), bits)
+                return self.fc2.forward_residual(h, residual, prequantized=True)
         fc1_gelu = getattr(self.fc1, "forward_gelu", None)
-        if FUSE_GELU and fc1_gelu is not None and type(self.act) is nn.GELU and self.act.approximate == "none":
+        if FUSE_GELU and fc1_gelu is not None and gelu_exact:
             h = fc1_gelu(x, prequantized)
         else:
             h = self.act(call_layer(self.fc1, x, prequantized))

@@ -143,6 +143,19 @@ def test_layer_norm_act_quant_argument_errors():
     assert L.rpfq_layer_norm_act_quant(p, 1, 4, 64, None, None, -1.0, 4, p, 1, None) == 6
 
 
+def test_gelu_act_quant_argument_errors():
+    L, _ = lib()
+    p = ctypes.c_void_p(256)
+    assert L.rpfq_gelu_act_quant(None, 1, 4, 64, 4, p, 1, None) == 1
+    assert L.rpfq_gelu_act_quant(p, 1, 4, 40, 4, p, 1, None) == 2      # C/2 % 8
+    assert L.rpfq_gelu_act_quant(p, 1, 4, 8192, 4, p, 1, None) == 2    # C > 4096
+    assert L.rpfq_gelu_act_quant(p, 1, 0, 64, 4, p, 1, None) == 2      # M
+    assert L.rpfq_gelu_act_quant(p, 1, 4, 64, 1, p, 1, None) == 4      # bits
+    assert L.rpfq_gelu_act_quant(p, 1, 4, 64, 17, p, 1, None) == 4
+    assert L.rpfq_gelu_act_quant(p, 3, 4, 64, 4, p, 1, None) == 5
+    assert L.rpfq_gelu_act_quant(ctypes.c_void_p(258), 1, 4, 64, 4, p, 1, None) == 3
+
+
 def test_quantize_wide_argument_errors():
     L, N = lib()
     p = ctypes.c_void_p(256)

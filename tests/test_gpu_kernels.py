@@ -719,6 +719,35 @@ def test_layer_norm_act_quant_bit_exact(m, c, xdt, ydt, bits):
     assert torch.equal(fused.cpu(), ref)
 
 
+@pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 3072), (5, 4096)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)])
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_gelu_act_quant_bit_exact(m, c, xdt, ydt, bits):
+    """rpfq_gelu_act_quant == rpfq_act_quant(torch's exact GELU in float32)
+    rounded to y's dtype, bit for bit (the float32 GELU is quantized as the
+    reference quantizes fc2's float32 input; only the quantized value is
+    rounded), and that quantization is the oracle's; in place too."""
+    import torch.nn.functional as F
+
+    ops, _ = qm()
+    r = rng(1400 + c + bits)
+    x = torch.from_numpy((r.standard_normal((m, c)) * 2).astype(np.float32)).to(xdt).to(DEV)
+    fused = ops.gelu_act_quant(x, bits, out_dtype=ydt)
+    ge = F.gelu(x.float())
+    assert torch.equal(fused, ops.act_quant(ge, bits, out_dtype=ydt))
+    g = ge.cpu().numpy()
+    qr, qi = O.act_quant(g[:, :c // 2], g[:, c // 2:], bits)
+    assert torch.equal(fused.cpu(), torch.from_numpy(np.concatenate([qr, qi], axis=1)).to(ydt))
+    if xdt == ydt:
+        ops_, N = qm()
+        y = x.clone()
+        N.check("rpfq_gelu_act_quant", N.load().rpfq_gelu_act_quant(
+            y.data_ptr(), N.dtype_code(xdt), m, c, bits, y.data_ptr(), N.dtype_code(ydt), N.stream_of(y)))
+        torch.cuda.synchronize()
+        assert torch.equal(y, fused)
+
+
 @pytest.mark.parametrize("k", [8, 384, 1536])
 def test_act_quant_row_kernel_matches_oracle(k):
     """The register-resident act-quant kernel (K' % 8 == 0) is bit-exact with

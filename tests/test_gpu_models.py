@@ -386,11 +386,11 @@ def test_fused_blocks_match_unfused(name):
 def test_fused_act_quant_wiring(name):
     """With activation quantization on, the fused block path feeds qkv / fc1
     (and Swin's patch-merging reduction) from rpfq_layer_norm_act_quant and
-    skips their own quantization pass: the separate act-quant kernel runs
-    only for the other packed layers (proj, fc2, heads), while without the
-    fusion every packed layer runs it.  Each prequantized input holds at
-    most 2^bits distinct values per row and half (a layer fed an unquantized
-    input would hold hundreds)."""
+    fc2 from rpfq_gelu_act_quant, and skips their own quantization pass: the
+    separate act-quant kernel runs only for the other packed layers (proj,
+    heads), while without the fusion every packed layer runs it.  Each
+    prequantized input holds at most 2^bits distinct values per row and half
+    (a layer fed an unquantized input would hold hundreds)."""
     from quant_models import ops
     from quant_models import vision_transformer as vt
     from quant_models.inference import prepare_inference, quant_layers
@@ -403,6 +403,7 @@ def test_fused_act_quant_wiring(name):
     calls, pre = [], []
     act_quant = ops.act_quant
     fwd_pre, fwd_gelu = QATLinearComplexPhase.forward_prequantized, QATLinearComplexPhase.forward_gelu
+    fwd_res = QATLinearComplexPhase.forward_residual
 
     def counting(*args, **kw):
         calls.append(1)
@@ -416,11 +417,17 @@ def test_fused_act_quant_wiring(name):
         if prequantized:
             pre.append(h.reshape(-1, h.shape[-1])[:64].float().cpu())
         return fwd_gelu(self, h, prequantized)
+
+    def recording_res(self, h, residual, prequantized=False):  # proj, fc2 of the fused block
+        if prequantized:
+            pre.append(h.reshape(-1, h.shape[-1])[:64].float().cpu())
+        return fwd_res(self, h, residual, prequantized)
     saved = vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT
     try:
         ops.act_quant = counting
         QATLinearComplexPhase.forward_prequantized = recording
         QATLinearComplexPhase.forward_gelu = recording_gelu
+        QATLinearComplexPhase.forward_residual = recording_res
         with torch.no_grad():
             vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = True, True
             y_f = model(x)
@@ -437,12 +444,13 @@ def test_fused_act_quant_wiring(name):
         ops.act_quant = act_quant
         QATLinearComplexPhase.forward_prequantized = fwd_pre
         QATLinearComplexPhase.forward_gelu = fwd_gelu
+        QATLinearComplexPhase.forward_residual = fwd_res
         vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = saved
     assert n_unfused == n_module == n_layers, (n_unfused, n_module, n_layers)
     blocks = sum(1 for m in model.modules() if hasattr(m, "mlp") and hasattr(m, "norm2"))
     merges = sum(1 for m in model.modules() if type(m).__name__ == "PatchMerging")
-    assert n_fused == n_layers - 2 * blocks - merges, (n_fused, n_layers, blocks, merges)
-    assert len(pre) == 2 * blocks + merges
+    assert n_fused == n_layers - 3 * blocks - merges, (n_fused, n_layers, blocks, merges)
+    assert len(pre) == 3 * blocks + merges
     for h in pre:
         half = h.shape[1] // 2
         for part in (h[:, :half], h[:, half:]):
