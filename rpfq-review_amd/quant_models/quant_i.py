@@ -538,14 +538,12 @@ class QATLinearComplexPhase(nn.Linear):
     def forward_gelu(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         """F.gelu(self(x)) (exact erf GELU); x already activation-quantized
         for this layer if prequantized.  On the packed HIP path the GELU runs
-        in the kernel's store (within 1 ulp of the unfused op) where that
-        measured cheaper than torch's separate GELU pass: on the streaming
-        kernels, and for bf16 outputs, whose GELU launches take the
-        register-staged kernel (ViT-B fc1 at M = 50,432: 474 vs 483 us,
-        ViT-L 676 vs 735 us; ViT-B/16 bs256 bf16 forward +1%).  On the
-        LDS-DMA kernel the float32 erf of the per-tile epilogue costs what the
-        separate pass does (ViT-B/16 bs256 fp16 forward: 18.03k images/s
-        fused vs 18.33k separate)."""
+        in the kernel's store (within 1 ulp of the unfused op) where the
+        launch takes a streaming kernel.  On the tiled kernels the float32
+        erf of the per-tile epilogue costs what torch's separate GELU pass
+        does (ViT-B/16 bs256 forward, fp16 on the LDS-DMA kernel: 18.03k
+        images/s fused vs 18.33k separate; bf16 on the register-staged
+        kernel: the same GEMM + GELU time per forward)."""
         if x.is_cuda and not self.training and self.use_packed:
             from . import _native as N
             from . import ops
@@ -556,7 +554,7 @@ class QATLinearComplexPhase(nn.Linear):
             bias = None if self.bias is None else self.bias.detach()
             m = x.numel() // x.shape[-1]
             kern = pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) if m else None
-            if kern in N.STREAM_KERNELS or (kern == N.KERNEL_TILED and x.dtype == torch.bfloat16):
+            if kern in N.STREAM_KERNELS:
                 return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
