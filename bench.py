@@ -525,6 +525,8 @@ def main() -> int:
     ap.add_argument("--layer-report", default=None, help="write per-shape kernel timings (JSON) here")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (counter calibration) and exit")
+    ap.add_argument("--read-probe-mib", type=int, default=0,
+                    help="only time torch's read (int64 sum) and copy of this many MiB (HBM reference rates) and exit")
     ap.add_argument("--stream-sweep", action="store_true",
                     help="only run the batch-M weight-streaming sweep (M in {1,4,16}, ViT-B/L layer shapes, "
                          ">= --stream-gib GiB of codes per timed pass) and exit")
@@ -562,6 +564,25 @@ def main() -> int:
             return 2
         stream_sweep(tuple(int(v) for v in args.stream_ms.split(",")), tuple(args.stream_modes.split(",")),
                      args.stream_gib, max(1, args.steps), args.stream_out, shapes)
+        return 0
+    if args.read_probe_mib:
+        import torch
+        n = args.read_probe_mib << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        out = {"read_probe_bytes": n}
+        for name, fn, nbytes in (("int64_sum_read", lambda: src.view(torch.int64).sum(), n),
+                                 ("copy_read_write", lambda: dst.copy_(src), 2 * n)):
+            fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out[name + "_gbs"] = round(nbytes / (e0.elapsed_time(e1) / args.steps / 1e3) / 1e9, 1)
+        print(json.dumps(out))
         return 0
     if args.copy_probe_mib:
         import torch
