@@ -101,8 +101,8 @@ int device_cus();
 hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t>& done);
 
 // Widely-linear GEMM launchers, one translation unit per codebook (CB):
-// wide_dma.hip (fp16 x, LDS DMA, M >= 128), wide_stream.hip (weight
-// streaming), wide_tiled.hip (register-staged tiles, bm = 32, 64 or 128).
+// wide_dma.hip (fp16 / bf16 x, LDS DMA, M >= 128), wide_stream.hip (weight
+// streaming, row-chunked and column-split), wide_tiled.hip (register-staged tiles, bm = 32, 64 or 128).
 template <int CB> hipError_t launch_wide_dma(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int ydt, hipStream_t s);
