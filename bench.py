@@ -234,7 +234,7 @@ def bench_config1(steps: int, warmup: int, cpu: bool, budget_s: float) -> int:
                                "complex, per-output-channel scales", "m": m, "k": k, "n": n},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_F16_TFLOPS, 4), "traffic": None,
-                     "kernel": "rpfq::phase_linear_kernel<64, F32, F32, false> (one launch per step; float32 x "
+                     "kernel": "rpfq::phase_linear_kernel<32, F32, F32, false> (one launch per step; float32 x "
                                "runs two fp16 MFMA passes, hi and lo, so the MFMA executes 2x the algorithmic "
                                "flops)",
                      "algorithmic_bytes": nbytes, "algorithmic_gbs": round(nbytes / (ms / 1e3) / 1e9, 1)},

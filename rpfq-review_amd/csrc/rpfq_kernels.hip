@@ -75,14 +75,28 @@ __device__ __forceinline__ uint2 tern_entry(uint32_t nib) {
     return e;
 }
 
+// Workgroup = 4 waves, tile = BM rows of x times 128 output columns; wave w
+// owns columns 32w..32w+31 for all BM rows.  BM = 32 (the launcher's
+// choice): four workgroups per CU with per-row scales, so config 1's 1,200
+// tiles fill more of the 1,024 slots per round than 600 tiles of 64 rows on
+// 512 (measured 8% faster).  Per k-step of 32 columns the
+// x tile goes global -> registers -> (fp16, or fp16 hi + lo for float32 x)
+// -> LDS; the raw loads of k-step ks + 2 are issued before the MFMAs of ks
+// and converted only when k-step ks + 1 is written to LDS, so every load has
+// two k-steps of MFMAs to land (two register sets, two LDS stages).  Loads
+// are unconditional (rows past M read row M - 1, k-steps past the end read
+// the last one) so the loop body is straight-line and the wait counts exact;
+// rows and columns past the edges are never stored.
 template <int BM, int XDT, int YDT, bool PERBLOCK>
-__global__ void __launch_bounds__(256) phase_linear_kernel(PhaseArgs a) {
+__global__ void __launch_bounds__(256, PERBLOCK ? 2 : 4) phase_linear_kernel(PhaseArgs a) {
     constexpr bool SPLIT = (XDT == RPFQ_F32);
     constexpr int MB = BM / 32;
     constexpr int XROW = SPLIT ? 272 : 144;  // bytes per LDS row (+16 pad)
     constexpr int XSTAGE = BM * XROW;
     constexpr int CPT = BM / 32;             // 16-byte chunks per thread per plane pair
+    constexpr int RAW = SPLIT ? 8 : 4;       // dwords of one raw chunk (8 floats or 8 halves)
     __shared__ __align__(16) char smem[2 * XSTAGE];
+    __shared__ uint2 codes_lds[2][128];  // per stage: the k-step's 8 code bytes of each output column
     __shared__ uint2 tern[16];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -92,61 +106,78 @@ __global__ void __launch_bounds__(256) phase_linear_kernel(PhaseArgs a) {
     const int64_t m0 = (int64_t)mt * BM;
     const int64_t n = (int64_t)ntl * 128 + wave * 32 + r;
     const bool n_ok = n < a.N;
-    const int64_t KS = a.K / 32;
+    const int64_t n_ld = n_ok ? n : a.N - 1;
+    const int KS = (int)(a.K / 32);
     const int64_t kb = a.K / 4;
 
     if (tid < 16) tern[tid] = tern_entry(tid);
 
-    uint4 xh[CPT], xl[CPT];
-    uint2 creg = make_uint2(0, 0);
-
-    auto load_x = [&](int64_t ks) {
+    // chunk j of this thread: row, plane and 8-column group of a k-step
+    constexpr int ESZ = SPLIT ? 4 : 2;  // bytes per element of x
+    const char* src[CPT];
+    int soff[CPT];
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            int c = tid + 256 * j;
-            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
-            int64_t m = m0 + row;
-            const void* plane = part ? a.xi : a.xr;
-            int64_t off = m * a.K + ks * 32 + sub * 8;
-            if (m < a.M) {
-                if (SPLIT) {
-                    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(plane) + off);
-                    float4 u = p[0], v = p[1];
-                    split2(u.x, u.y, xh[j].x, xl[j].x);
-                    split2(u.z, u.w, xh[j].y, xl[j].y);
-                    split2(v.x, v.y, xh[j].z, xl[j].z);
-                    split2(v.z, v.w, xh[j].w, xl[j].w);
-                } else {
-                    xh[j] = load8_f16<XDT>(plane, off);
-                }
-            } else {
-                xh[j] = make_uint4(0, 0, 0, 0);
-                xl[j] = make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto store_x = [&](int stage) {
-        char* xs = smem + stage * XSTAGE;
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            int c = tid + 256 * j;
-            int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
-            *reinterpret_cast<uint4*>(xs + row * XROW + part * 64 + sub * 16) = xh[j];
-            if (SPLIT) *reinterpret_cast<uint4*>(xs + row * XROW + 128 + part * 64 + sub * 16) = xl[j];
-        }
-    };
-    auto load_codes = [&](int64_t ks) {
-        creg = n_ok ? *reinterpret_cast<const uint2*>(a.codes + n * kb + ks * 8) : make_uint2(0, 0);
-    };
-
-    floatx16 c1[MB], c2[MB], c3[MB], c4[MB], tre[MB], tim[MB];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        c1[i] = c2[i] = c3[i] = c4[i] = floatx16{0};
-        tre[i] = tim[i] = floatx16{0};
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 256 * j;
+        const int row = c >> 3, part = (c >> 2) & 1, sub = c & 3;
+        const int64_t m = m0 + row < a.M ? m0 + row : a.M - 1;
+        src[j] = reinterpret_cast<const char*>(part ? a.xi : a.xr) + (m * a.K + sub * 8) * ESZ;
+        soff[j] = row * XROW + part * 64 + sub * 16;
     }
 
-    auto flush = [&](int64_t blk) {
+    // one k-step in flight: the raw x chunks and the column's 8 code bytes
+    struct Raw {
+        uint32_t x[CPT][RAW];
+        uint2 c;
+    };
+    Raw raw0, raw1;
+    auto load = [&](int ks, Raw& raw) __attribute__((always_inline)) {
+        ks = ks < KS ? ks : KS - 1;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const uint4* p = reinterpret_cast<const uint4*>(src[j] + ks * 32 * ESZ);
+            const uint4 u = p[0];
+            raw.x[j][0] = u.x; raw.x[j][1] = u.y; raw.x[j][2] = u.z; raw.x[j][3] = u.w;
+            if (SPLIT) {
+                const uint4 v = p[1];
+                raw.x[j][4] = v.x; raw.x[j][5] = v.y; raw.x[j][6] = v.z; raw.x[j][7] = v.w;
+            }
+        }
+        raw.c = *reinterpret_cast<const uint2*>(a.codes + n_ld * kb + ks * 8);
+    };
+    auto store = [&](int stage, const Raw& raw) __attribute__((always_inline)) {
+        char* xs = smem + stage * XSTAGE;
+        if (g == 0) codes_lds[stage][wave * 32 + r] = raw.c;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            uint4 h, l;
+            if (SPLIT) {
+                split2(__uint_as_float(raw.x[j][0]), __uint_as_float(raw.x[j][1]), h.x, l.x);
+                split2(__uint_as_float(raw.x[j][2]), __uint_as_float(raw.x[j][3]), h.y, l.y);
+                split2(__uint_as_float(raw.x[j][4]), __uint_as_float(raw.x[j][5]), h.z, l.z);
+                split2(__uint_as_float(raw.x[j][6]), __uint_as_float(raw.x[j][7]), h.w, l.w);
+            } else if (XDT == RPFQ_BF16) {
+                h.x = pack_h2(bf16_to_f32(raw.x[j][0] & 0xffffu), bf16_to_f32(raw.x[j][0] >> 16));
+                h.y = pack_h2(bf16_to_f32(raw.x[j][1] & 0xffffu), bf16_to_f32(raw.x[j][1] >> 16));
+                h.z = pack_h2(bf16_to_f32(raw.x[j][2] & 0xffffu), bf16_to_f32(raw.x[j][2] >> 16));
+                h.w = pack_h2(bf16_to_f32(raw.x[j][3] & 0xffffu), bf16_to_f32(raw.x[j][3] >> 16));
+            } else {
+                h = make_uint4(raw.x[j][0], raw.x[j][1], raw.x[j][2], raw.x[j][3]);
+            }
+            *reinterpret_cast<uint4*>(xs + soff[j]) = h;
+            if (SPLIT) *reinterpret_cast<uint4*>(xs + soff[j] + 128) = l;
+        }
+    };
+
+    floatx16 c1[MB], c2[MB], c3[MB], c4[MB];
+    floatx16 tre[PERBLOCK ? MB : 1], tim[PERBLOCK ? MB : 1];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) c1[i] = c2[i] = c3[i] = c4[i] = floatx16{0};
+#pragma unroll
+    for (int i = 0; i < (PERBLOCK ? MB : 1); ++i) tre[i] = tim[i] = floatx16{0};
+
+    // per-(row, block) scales applied to the four partial sums
+    auto flush = [&](int blk) __attribute__((always_inline)) {
         float sr = 0.0f, si = 0.0f;
         if (n_ok) {
             sr = 1.0f / (float)__builtin_bit_cast(_Float16, a.gre[n * a.nblk + blk]);
@@ -164,38 +195,28 @@ __global__ void __launch_bounds__(256) phase_linear_kernel(PhaseArgs a) {
         }
     };
 
-    load_x(0);
-    load_codes(0);
-    store_x(0);
-    __syncthreads();
-
-    for (int64_t ks = 0; ks < KS; ++ks) {
-        const uint2 cw = creg;
-        const bool more = ks + 1 < KS;
-        if (more) {
-            load_x(ks + 1);
-            load_codes(ks + 1);
-        }
+    auto mfmas = [&](int ks) __attribute__((always_inline)) {
         const char* xs = smem + (ks & 1) * XSTAGE;
+        const uint2 cw = codes_lds[ks & 1][wave * 32 + r];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            uint32_t c16 = ((s ? cw.y : cw.x) >> (16 * g)) & 0xffffu;
-            uint2 t0 = tern[c16 & 15u], t1 = tern[(c16 >> 4) & 15u];
-            uint2 t2 = tern[(c16 >> 8) & 15u], t3 = tern[c16 >> 12];
-            half8 btr = as_half8(make_uint4(t0.x, t1.x, t2.x, t3.x));
-            half8 bti = as_half8(make_uint4(t0.y, t1.y, t2.y, t3.y));
+            const uint32_t c16 = ((s ? cw.y : cw.x) >> (16 * g)) & 0xffffu;
+            const uint2 t0 = tern[c16 & 15u], t1 = tern[(c16 >> 4) & 15u];
+            const uint2 t2 = tern[(c16 >> 8) & 15u], t3 = tern[c16 >> 12];
+            const half8 btr = as_half8(make_uint4(t0.x, t1.x, t2.x, t3.x));
+            const half8 bti = as_half8(make_uint4(t0.y, t1.y, t2.y, t3.y));
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const char* rp = xs + (i * 32 + r) * XROW + (16 * s + 8 * g) * 2;
-                half8 axr = *reinterpret_cast<const half8*>(rp);
-                half8 axi = *reinterpret_cast<const half8*>(rp + 64);
+                const half8 axr = *reinterpret_cast<const half8*>(rp);
+                const half8 axi = *reinterpret_cast<const half8*>(rp + 64);
                 c1[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, btr, c1[i], 0, 0, 0);
                 c2[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, bti, c2[i], 0, 0, 0);
                 c3[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axr, bti, c3[i], 0, 0, 0);
                 c4[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(axi, btr, c4[i], 0, 0, 0);
                 if (SPLIT) {
-                    half8 lxr = *reinterpret_cast<const half8*>(rp + 128);
-                    half8 lxi = *reinterpret_cast<const half8*>(rp + 192);
+                    const half8 lxr = *reinterpret_cast<const half8*>(rp + 128);
+                    const half8 lxi = *reinterpret_cast<const half8*>(rp + 192);
                     c1[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxr, btr, c1[i], 0, 0, 0);
                     c2[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxi, bti, c2[i], 0, 0, 0);
                     c3[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(lxr, bti, c3[i], 0, 0, 0);
@@ -203,22 +224,56 @@ __global__ void __launch_bounds__(256) phase_linear_kernel(PhaseArgs a) {
                 }
             }
         }
-        if (PERBLOCK && (ks + 1) % a.block_ks == 0) flush(ks / a.block_ks);
-        if (more) store_x((ks + 1) & 1);
+        if (PERBLOCK && (ks + 1) % a.block_ks == 0) flush((int)(ks / a.block_ks));
+    };
+
+    // k-step ks: loads of ks + 2 into the free register set, MFMAs of ks,
+    // k-step ks + 1 (loaded one k-step earlier) converted into the other stage
+    auto step = [&](int ks, Raw& rfree, const Raw& rnext) __attribute__((always_inline)) {
+        load(ks + 2, rfree);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+        mfmas(ks);
+        __builtin_amdgcn_sched_barrier(0);  // and the conversion behind them
+        store((ks + 1) & 1, rnext);
         __syncthreads();
+    };
+
+    load(0, raw0);
+    load(1, raw1);
+    store(0, raw0);
+    __syncthreads();
+    int ks = 0;
+    for (; ks + 1 < KS; ks += 2) {
+        step(ks, raw0, raw1);
+        step(ks + 1, raw1, raw0);
     }
-    if (!PERBLOCK) flush(0);
-    else if (KS % a.block_ks != 0) flush(KS / a.block_ks);
+    if (ks < KS) step(ks, raw0, raw1);
 
     if (!n_ok) return;
+    float sr = 0.0f, si = 0.0f;
+    if (PERBLOCK) {
+        if (KS % a.block_ks != 0) flush(KS / a.block_ks);
+    } else {
+        sr = 1.0f / (float)__builtin_bit_cast(_Float16, a.gre[n]);
+        si = 1.0f / (float)__builtin_bit_cast(_Float16, a.gim[n]);
+    }
+    const float xs = a.xsign;
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            int64_t m = m0 + i * 32 + acc_row(v, g);
+            const int64_t m = m0 + i * 32 + acc_row(v, g);
+            float vr, vi;
+            if (PERBLOCK) {
+                vr = tre[i][v];
+                vi = tim[i][v];
+            } else {
+                vr = sr * c1[i][v] + xs * (si * c2[i][v]);
+                vi = si * c3[i][v] - xs * (sr * c4[i][v]);
+            }
             if (m < a.M) {
-                store1<YDT>(a.yr, m * a.N + n, tre[i][v]);
-                store1<YDT>(a.yi, m * a.N + n, tim[i][v]);
+                store1<YDT>(a.yr, m * a.N + n, vr);
+                store1<YDT>(a.yi, m * a.N + n, vi);
             }
         }
     }
@@ -646,8 +701,8 @@ static hipError_t phase_go(PhaseArgs& a, hipStream_t s) {
 
 template <int XDT, int YDT>
 static hipError_t phase_pb(PhaseArgs& a, hipStream_t s) {
-    if (a.nblk > 1) return phase_go<64, XDT, YDT, true>(a, s);
-    return phase_go<64, XDT, YDT, false>(a, s);
+    if (a.nblk > 1) return phase_go<32, XDT, YDT, true>(a, s);
+    return phase_go<32, XDT, YDT, false>(a, s);
 }
 
 template <int XDT>

@@ -110,8 +110,12 @@ def test_act_quant_bit_exact(bits, golden):
 # single plane phase linear (phase_linear.cpp:119-164)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("m,k,n,block,conj", [(1576, 768, 3072, 0, False), (33, 64, 200, 32, True),
-                                              (130, 256, 129, 64, False), (1, 512, 128, 256, True)])
+                                              (130, 256, 129, 64, False), (1, 512, 128, 256, True),
+                                              (77, 160, 300, 0, True), (45, 224, 70, 96, False)])
 def test_phase_linear_f32_split(m, k, n, block, conj):
+    """Config 1 at full size and ragged shapes: M and N off the 64 x 128
+    tile, an odd number of 32-column k-steps (the two-step pipeline's tail),
+    per-block scales with a partial last block."""
     ops, _ = qm()
     r = rng(10 + m)
     xr = r.standard_normal((m, k)).astype(np.float32)
