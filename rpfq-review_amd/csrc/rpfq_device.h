@@ -221,29 +221,62 @@ __device__ __forceinline__ float gelu_f(float x) {
     return g;
 }
 
+// GELU(x) = x Phi(x) for the GEMM stores, ~20 VALU (2 transcendental)
+// against ~40-60 for the erff form above.  The normal tail Q(a) =
+// P(X > a) = erfc(a / sqrt 2) / 2, a = |x|, is written
+//   Q(a) = exp(-a^2 / 2) t S(t),  t = 1 / (1 + p a),
+// with S a degree-7 polynomial fitted here (weighted least squares on the
+// relative error, Lawson reweighting, over a in [0, 14]) to a relative
+// error below 1e-7 in float64; Phi(x) = 1 - Q(a) for x >= 0, Q(a) below.
+// Evaluated in float32 the GELU is within 1e-6 relative of x Phi(x) for
+// x > -5 (1.8e-6 in the far tail), i.e. correctly rounded to fp16 for all
+// but ~0.02% of fp16 inputs; the erff form loses relative accuracy for
+// x < -3 to the cancellation in 1 + erf (0.9% of fp16 inputs round
+// differently from the exact GELU there).
+__device__ __forceinline__ float gelu_fast(float x) {
+    constexpr float p = 0.305f;
+    constexpr float s0 = 0.12163970644663864f, s1 = 0.12246733368920268f, s2 = 0.10341694433614163f,
+                    s3 = 0.1210368392091385f, s4 = -0.038009486079897375f, s5 = 0.1857564848237517f,
+                    s6 = -0.15301350130459096f, s7 = 0.03670572580834201f;
+    const float a = fabsf(x);
+    const float t = __builtin_amdgcn_rcpf(fmaf(p, a, 1.0f));
+    float sp = fmaf(s7, t, s6);
+    sp = fmaf(sp, t, s5);
+    sp = fmaf(sp, t, s4);
+    sp = fmaf(sp, t, s3);
+    sp = fmaf(sp, t, s2);
+    sp = fmaf(sp, t, s1);
+    sp = fmaf(sp, t, s0);
+    const float e = __builtin_amdgcn_exp2f(a * a * -0.72134752044448170f);  // exp(-a^2 / 2)
+    const float q = e * t * sp;
+    float g = x * (x >= 0.0f ? 1.0f - q : q);
+    asm volatile("" : "+v"(g));  // one rounding to y's dtype after the float32 product
+    return g;
+}
+
 template <int YDT>
 __device__ __forceinline__ float act_y(float v, int act) {
     if (!act) return v;
     if (YDT == RPFQ_F16) v = (float)(_Float16)v;
     if (YDT == RPFQ_BF16) v = bf16_to_f32(f32_to_bf16(v));
-    return gelu_f(v);
+    return gelu_fast(v);
 }
 // two packed 16-bit outputs of y's dtype
 __device__ __forceinline__ uint32_t gelu2_y(uint32_t v, bool f16) {
     if (f16) {
         const half2v h = __builtin_bit_cast(half2v, v);
-        const half2v o = {(_Float16)gelu_f((float)h.x), (_Float16)gelu_f((float)h.y)};
+        const half2v o = {(_Float16)gelu_fast((float)h.x), (_Float16)gelu_fast((float)h.y)};
         return __builtin_bit_cast(uint32_t, o);
     }
-    return (uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v & 0xffffu))) |
-           ((uint32_t)f32_to_bf16(gelu_f(bf16_to_f32(v >> 16))) << 16);
+    return (uint32_t)f32_to_bf16(gelu_fast(bf16_to_f32(v & 0xffffu))) |
+           ((uint32_t)f32_to_bf16(gelu_fast(bf16_to_f32(v >> 16))) << 16);
 }
 __device__ __forceinline__ uint4 gelu8_y(uint4 v, bool f16) {
     return make_uint4(gelu2_y(v.x, f16), gelu2_y(v.y, f16), gelu2_y(v.z, f16), gelu2_y(v.w, f16));
 }
 __device__ __forceinline__ uint16_t gelu1_y(uint16_t e, bool f16) {
-    if (f16) return __builtin_bit_cast(uint16_t, (_Float16)gelu_f((float)__builtin_bit_cast(_Float16, e)));
-    return f32_to_bf16(gelu_f(bf16_to_f32(e)));
+    if (f16) return __builtin_bit_cast(uint16_t, (_Float16)gelu_fast((float)__builtin_bit_cast(_Float16, e)));
+    return f32_to_bf16(gelu_fast(bf16_to_f32(e)));
 }
 // The same 8 outputs one at a time in a rolled loop (the 16-bit values shift
 // through the four words), so only one erf body is live: unrolled, the DMA

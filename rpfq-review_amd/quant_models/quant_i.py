@@ -538,12 +538,12 @@ class QATLinearComplexPhase(nn.Linear):
     def forward_gelu(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         """F.gelu(self(x)) (exact erf GELU); x already activation-quantized
         for this layer if prequantized.  On the packed HIP path the GELU runs
-        in the kernel's store (within 1 ulp of the unfused op) where the
-        launch takes a streaming kernel.  On the tiled kernels the float32
-        erf of the per-tile epilogue costs what torch's separate GELU pass
-        does (ViT-B/16 bs256 forward, fp16 on the LDS-DMA kernel: 18.03k
-        images/s fused vs 18.33k separate; bf16 on the register-staged
-        kernel: the same GEMM + GELU time per forward)."""
+        in the kernel's store (within 1 ulp of the exact GELU of the rounded
+        output) where the launch streams, and on the tiled kernels for bf16
+        activations.  ViT-B/16 bs256, same box: bf16 15,510 -> 16,197
+        images/s fused; fp16 17,603 -> 17,912, but fc1's launch grows by
+        ~40% (the GELU's VALU work in the epilogue is not hidden behind the
+        MFMAs), so fp16 tiled launches keep torch's separate GELU pass."""
         if x.is_cuda and not self.training and self.use_packed:
             from . import _native as N
             from . import ops
@@ -554,7 +554,7 @@ class QATLinearComplexPhase(nn.Linear):
             bias = None if self.bias is None else self.bias.detach()
             m = x.numel() // x.shape[-1]
             kern = pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) if m else None
-            if kern in N.STREAM_KERNELS:
+            if kern in N.STREAM_KERNELS or x.dtype == torch.bfloat16:
                 return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
