@@ -210,6 +210,31 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
                               const void* residual, void* y, int y_dtype, int flags, void* stream);
 
 /*
+ * y = layer(LayerNorm(x)) in one launch: the LayerNorm of rpfq_layer_norm
+ * over the layer's 2K' input features (float32 statistics and affine map,
+ * rounded to x_dtype) runs in the streaming kernel's prologue, and the
+ * packed layer of rpfq_wide_linear contracts the normalized rows from LDS;
+ * the normalized x is never written to memory.  Equal to rpfq_layer_norm
+ * (y_dtype = x_dtype) followed by rpfq_wide_linear up to the order of the
+ * statistics' float32 sums.  gamma, beta: float32 [2K'] or NULL (1 / 0),
+ * 16-byte aligned.  flags: 0 or RPFQ_FLAG_GELU.  Only for launches that
+ * rpfq_layer_norm_wide_linear_fusable accepts (a layer at batch 1-2: the
+ * streaming kernel's split-K forms, per-row scales, K' % 32 == 0,
+ * K' <= 384, fp16 / bf16 x, not RPFQ_CB_TABLE); RPFQ_ERR_VALUE otherwise.
+ * Replaces norm1 -> qkv and norm2 -> fc1 of a ViT block
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:520-521, :549-550
+ *   (RPFQ-ViT-main/quant_models/quant_i.py:554 inside the layer).
+ */
+int rpfq_layer_norm_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
+                                const void* x, int x_dtype, int64_t M, const float* gamma, const float* beta,
+                                float eps, const float* bias, void* y, int y_dtype, int flags, void* stream);
+
+/* *fusable = 1 if rpfq_layer_norm_wide_linear accepts this launch, else 0
+ * (no GPU work; no counterpart in the reference). */
+int rpfq_layer_norm_wide_linear_fusable(const rpfq_wide_desc* desc, int64_t M, int x_dtype, int y_dtype,
+                                        int* fusable);
+
+/*
  * LayerNorm over the last dimension (nn.LayerNorm with biased variance):
  *   y = (x - mean) / sqrt(var + eps) * gamma + beta
  * per row of x [M, C], statistics and the affine map in float32, then

@@ -87,6 +87,13 @@ struct WideArgs {
     int vec_store;  // y rows allow 16-byte stores (N % 8 == 0, aligned y)
     int wg_epi;     // DMA epilogue: workgroup-wide full-line stores (else per wave)
     int act;        // 1: exact GELU of the rounded output (no residual), 0: none
+    // LayerNorm of x fused into the streaming kernel's prologue (ln = 1):
+    // the layer contracts LN(x) = (x - mean) / sqrt(var + eps) * gamma + beta
+    // over the 2K' features of each row, rounded to x's dtype.
+    int ln;
+    float ln_eps;
+    const float* ln_gamma;  // [2K'] or NULL (ones)
+    const float* ln_beta;   // [2K'] or NULL (zeros)
 };
 
 // Compute units of the current device (cached per device, thread-safe;
@@ -145,6 +152,15 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
                               const void* x, int xdt, int64_t M, const float* bias, const void* res,
                               void* y, int ydt, int flags, hipStream_t s);
 int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags);  // RPFQ_KERNEL_*
+// LayerNorm fused into the streaming kernel: whether the launch qualifies, and the launch.
+// K' <= 384: the normalized 16-row tile (<= 25 KB) stays in LDS.  ViT-B,
+// DeiT-Ti and Swin-T layers at batch 1 gain (0.775 -> 0.712, 0.598 -> 0.502,
+// 1.024 -> 0.985 ms per forward); ViT-L's K' = 512 lost (1.75 -> 1.96 ms).
+constexpr int kLnMaxK = 384;
+bool layer_norm_wide_fusable(const WideGeom& g, int xdt, int64_t M, int ydt, int codebook);
+hipError_t launch_layer_norm_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
+                                         const void* x, int xdt, int64_t M, const float* gamma, const float* beta,
+                                         float eps, const float* bias, void* y, int ydt, int flags, hipStream_t s);
 hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
                              const float* beta, float eps, int bits, void* y, int ydt, hipStream_t s);
 hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,

@@ -91,15 +91,30 @@ static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
     return a;
 }
 
+// The fused LayerNorm runs in the streaming kernel split over 4 waves (for
+// launches of fewer than kSkSplitTiles workgroups: a layer at batch 1-2), per-row scales,
+// K' % 32 == 0 and K' <= kLnMaxK, fp16 / bf16 x, not the TABLE codebook.
+bool layer_norm_wide_fusable(const WideGeom& g, int xdt, int64_t M, int ydt, int codebook) {
+    const WideArgs a = wide_shape(g, M, 0);
+    return choose_kernel(a, xdt, ydt, 0) == RPFQ_KERNEL_STREAM && sk_groups(a) < kSkSplitTiles && a.nblk == 1 &&
+           a.K % 32 == 0 && a.K <= kLnMaxK && (xdt == RPFQ_F16 || xdt == RPFQ_BF16) && codebook != RPFQ_CB_TABLE;
+}
+
 int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags) {
     return choose_kernel(wide_shape(g, M, flags), xdt, ydt, flags & ~RPFQ_FLAG_GELU);
 }
 
-hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
-                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
-                              hipStream_t s) {
-    WideArgs a = wide_shape(g, M, flags);
-    flags &= ~RPFQ_FLAG_GELU;
+static hipError_t launch_wide(WideArgs& a, const rpfq_wide_desc& d, int xdt, int ydt, int flags, hipStream_t s) {
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN: return wide_cb<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_PSK16: return wide_cb<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_TABLE: return wide_cb<RPFQ_CB_TABLE>(a, xdt, ydt, flags, s);
+        default: return wide_cb<RPFQ_CB_AXIS>(a, xdt, ydt, flags, s);
+    }
+}
+
+static void wide_operands(WideArgs& a, const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
+                          const float* bias, const void* res, void* y) {
     a.x = x;
     a.codes = reinterpret_cast<const uint4*>(packed);
     a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
@@ -111,12 +126,31 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     // whole 128-column tiles and >= 8 k-steps (ViT-B/L, not DeiT-Ti's K' = 96 / N' = 96 layers):
     // full-line stores pay for the two workgroup barriers per half tile
     a.wg_epi = (g.N % 128 == 0) && (g.KS >= 8);
+}
+
+hipError_t launch_layer_norm_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
+                                         const void* x, int xdt, int64_t M, const float* gamma, const float* beta,
+                                         float eps, const float* bias, void* y, int ydt, int flags, hipStream_t s) {
+    WideArgs a = wide_shape(g, M, flags);
+    wide_operands(a, d, g, packed, x, bias, nullptr, y);
+    a.ln = 1;
+    a.ln_eps = eps;
+    a.ln_gamma = gamma;
+    a.ln_beta = beta;
     switch (d.codebook) {
-        case RPFQ_CB_SIGN: return wide_cb<RPFQ_CB_SIGN>(a, xdt, ydt, flags, s);
-        case RPFQ_CB_PSK16: return wide_cb<RPFQ_CB_PSK16>(a, xdt, ydt, flags, s);
-        case RPFQ_CB_TABLE: return wide_cb<RPFQ_CB_TABLE>(a, xdt, ydt, flags, s);
-        default: return wide_cb<RPFQ_CB_AXIS>(a, xdt, ydt, flags, s);
+        case RPFQ_CB_SIGN: return launch_wide_stream<RPFQ_CB_SIGN>(a, xdt, ydt, s);
+        case RPFQ_CB_PSK16: return launch_wide_stream<RPFQ_CB_PSK16>(a, xdt, ydt, s);
+        default: return launch_wide_stream<RPFQ_CB_AXIS>(a, xdt, ydt, s);
     }
+}
+
+hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
+                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
+                              hipStream_t s) {
+    WideArgs a = wide_shape(g, M, flags);
+    flags &= ~RPFQ_FLAG_GELU;
+    wide_operands(a, d, g, packed, x, bias, res, y);
+    return launch_wide(a, d, xdt, ydt, flags, s);
 }
 
 }  // namespace rpfq

@@ -94,6 +94,46 @@ __device__ __forceinline__ void build_lut_sk(uint32_t* lut, const float4* p, con
     }
 }
 
+// The same LUT (or the NJ-index share from j0 on) from the row's
+// parameters already in registers (not TABLE).
+template <int CB, int NJ = 8>
+__device__ __forceinline__ void build_lut_sk_regs(uint32_t* lut, float4 pu, float4 pw, const RotParams& rot, int R,
+                                                  int g, int j0 = 0) {
+    const int s0 = 32 * (R >> 4) + (R & 15);
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+        const uint32_t idx = (uint32_t)(g + 2 * (j0 + jj));
+        float2 u = lut_entry_g<CB>((uint32_t)(2 * (j0 + jj)), g, pu);
+        float2 w = lut_entry_g<CB>((uint32_t)(2 * (j0 + jj)), g, pw);
+        if (rot.rotate) {
+            u = derotate(u, rot.cu, rot.su);
+            w = derotate(w, rot.cw, rot.sw);
+        }
+        const uint32_t hu = cvt_pk(u.x, u.y), hw = cvt_pk(w.x, w.y);
+        lut[idx * 64 + s0] = hu;
+        lut[idx * 64 + s0 + 16] = hu;
+        lut[(16 + idx) * 64 + s0] = hw;
+        lut[(16 + idx) * 64 + s0 + 16] = hw;
+    }
+}
+
+// 8 activations of a 16-B chunk (fp16 or bf16) as float32.
+template <int XDT>
+__device__ __forceinline__ void chunk_f32(uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (XDT == RPFQ_BF16) {
+            f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+            f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        } else {
+            const half2v h = __builtin_bit_cast(half2v, w[i]);
+            f[2 * i] = (float)h.x;
+            f[2 * i + 1] = (float)h.y;
+        }
+    }
+}
+
 // 4 consecutive activations at element offset `off`: the raw 16-bit values
 // (fp16, bf16; converted at use so the load stays in flight) or, for
 // float32, 4 fp16 converted on load.
@@ -119,8 +159,15 @@ __device__ __forceinline__ uint2 raw4_f16(uint2 v) {
 #ifndef RPFQ_SK_OCC
 #define RPFQ_SK_OCC 4  // waves per SIMD the register budget is sized for
 #endif
-template <int XDT, int YDT, int CB, bool PB, bool KT, int NW>
-__global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
+// LN (NW = 4, per-row scales, K' % 32 == 0, K' <= kLnMaxK, fp16 / bf16
+// x, not TABLE): the workgroup first normalizes its 16 rows of x
+// (nn.LayerNorm over the 2K' features, float32, two passes, rounded to x's
+// dtype as the separate LayerNorm kernel rounds its output) into an LDS tile
+// [16][2K' + 4] fp16, which the k-steps then read instead of x.  Wave w
+// normalizes rows 16 w / NW ..; lane (row, part) holds chunks part + LPR j
+// of its row in registers.  Rows past M are zero rows (never stored).
+template <int XDT, int YDT, int CB, bool PB, bool KT, int NW, bool LN = false>
+__global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
     const int lane = threadIdx.x & 63;
@@ -152,6 +199,7 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kerne
         const uint2* cp = ctile + kc * 128;
         st.c[0] = cp[coff];
         st.c[1] = cp[coff + 64];
+        if (LN) return;  // activations from the normalized LDS tile
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if (KT) {
@@ -166,19 +214,122 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kerne
             }
         }
     };
+    // LN tile: rows of xsb bytes after the LUT and the split-K partials,
+    // then gamma and beta as float32 [2K'] each
+    const int C2 = 2 * K, nch = C2 / 8;
+    const int xsb = 2 * C2 + 8;  // the 8-B pad puts consecutive rows 2 banks apart
+    char* xtile = smem + sk_lds(NW);
+    float* gs = reinterpret_cast<float*>(xtile + 16 * xsb);
+    float* bs = gs + C2;
+    constexpr int RW = 16 / NW, LPR = 64 / RW;  // (LN) rows per wave, lanes per row
+    constexpr int CPL = LN ? (2 * kLnMaxK / 8 + LPR - 1) / LPR : 1;
+    constexpr int GBI = LN ? (2 * kLnMaxK / 4 + 64 * NW - 1) / (64 * NW) : 1;
+    const int lrow = lane % RW, part = lane / RW, lnrow = wave * RW + lrow;
+    uint4 lnv[CPL];
+    float4 gv[GBI], bv[GBI];
+    float4 prm[2];
+    if (LN) {  // requested before the code ring: their waits leave the codes in flight
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = part + LPR * j;
+            lnv[j] = (c < nch && lnrow < M)
+                         ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xc) + lnrow * C2 + 8 * c)
+                         : make_uint4(0, 0, 0, 0);
+        }
+        const int tid = (int)threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < GBI; ++i) {
+            const int f = tid + 64 * NW * i;  // float4 index
+            const bool ok = 4 * f < C2;
+            gv[i] = (ok && a.ln_gamma) ? reinterpret_cast<const float4*>(a.ln_gamma)[f] : make_float4(1, 1, 1, 1);
+            bv[i] = (ok && a.ln_beta) ? reinterpret_cast<const float4*>(a.ln_beta)[f] : make_float4(0, 0, 0, 0);
+        }
+        const float4* pp = a.params + ((int64_t)tile * 32 + R) * 2;
+        prm[0] = pp[0];
+        prm[1] = pp[1];
+    }
+
     Step ring[SK_PF];
 #pragma unroll
     for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
 
     int blk = 0;
-    {  // split K: each wave builds 1 / NW of the shared LUT
+    if (LN) {
+        const int tid = (int)threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < GBI; ++i) {
+            const int f = tid + 64 * NW * i;
+            if (4 * f < C2) {
+                reinterpret_cast<float4*>(gs)[f] = gv[i];
+                reinterpret_cast<float4*>(bs)[f] = bv[i];
+            }
+        }
+        // statistics of this lane's row (the LayerNorm kernel's two passes)
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (part + LPR * j < nch) {
+                float f[8];
+                chunk_f32<XDT>(lnv[j], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum += f[e];
+            }
+        }
+#pragma unroll
+        for (int o = RW; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+        const float mean = sum / (float)C2;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (part + LPR * j < nch) {
+                float f[8];
+                chunk_f32<XDT>(lnv[j], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = f[e] - mean;
+                    s2 += d * d;
+                }
+            }
+        }
+#pragma unroll
+        for (int o = RW; o < 64; o <<= 1) s2 += __shfl_xor(s2, o, 64);
+        const float rstd = 1.0f / sqrtf(s2 / (float)C2 + a.ln_eps);
+        build_lut_sk_regs<CB, 8 / NW>(lut, prm[0], prm[1], a.rot, R, g, (8 / NW) * wave);  // this wave's share
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // gamma / beta in LDS
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = part + LPR * j;
+            if (c < nch) {
+                float f[8];
+                chunk_f32<XDT>(lnv[j], f);
+                const float4 g0 = reinterpret_cast<const float4*>(gs + 8 * c)[0], g1 = reinterpret_cast<const float4*>(gs + 8 * c)[1];
+                const float4 b0 = reinterpret_cast<const float4*>(bs + 8 * c)[0], b1 = reinterpret_cast<const float4*>(bs + 8 * c)[1];
+                const float gk[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                const float bk[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float y0 = (f[2 * i] - mean) * rstd * gk[2 * i] + bk[2 * i];
+                    float y1 = (f[2 * i + 1] - mean) * rstd * gk[2 * i + 1] + bk[2 * i + 1];
+                    if (XDT == RPFQ_BF16) {  // rounded to x's dtype, then exactly to fp16 for the MFMA
+                        y0 = bf16_to_f32(f32_to_bf16(y0));
+                        y1 = bf16_to_f32(f32_to_bf16(y1));
+                    }
+                    o[i] = lnrow < M ? cvt_pk(y0, y1) : 0u;
+                }
+                *reinterpret_cast<uint4*>(xtile + lnrow * xsb + 16 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    } else {  // split K: each wave builds 1 / NW of the shared LUT
         const float4* p = a.params + ((int64_t)tile * 32 + R) * (CB == RPFQ_CB_TABLE ? 16 : a.nblk * 2);
         if (NW == 1)
             build_lut_sk<CB>(lut, p, a.rot, R, g);
         else
             build_lut_sk<CB, 8 / NW>(lut, p, a.rot, R, g, (8 / NW) * wave);
     }
-    if (NW > 1) {  // LUT written before any wave reads it; the code loads stay in flight
+    if (NW > 1) {  // LUT (and the LN tile) written before any wave reads it; the code loads stay in flight
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -192,7 +343,15 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_SK_OCC) wide_linear_skinny_kerne
         half8 bx[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const uint2 re = raw4_f16<XDT>(st.xr[t]), im = raw4_f16<XDT>(st.xi[t]);
+            uint2 re, im;
+            if (LN) {  // row r16 of the normalized tile (fp16)
+                const char* rp = xtile + r16 * xsb + (32 * ks + xcol + 8 * t) * 2;
+                re = *reinterpret_cast<const uint2*>(rp);
+                im = *reinterpret_cast<const uint2*>(rp + 2 * K);
+            } else {
+                re = raw4_f16<XDT>(st.xr[t]);
+                im = raw4_f16<XDT>(st.xi[t]);
+            }
             uint4 b = make_uint4(__builtin_amdgcn_perm(im.x, re.x, 0x05040100u),
                                  __builtin_amdgcn_perm(im.x, re.x, 0x07060302u),
                                  __builtin_amdgcn_perm(im.y, re.y, 0x05040100u),
@@ -594,6 +753,14 @@ static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int XDT, int YDT, int CB, int NW>
+static hipError_t wide_sk_ln_go(WideArgs& a, hipStream_t s) {
+    const int lds = sk_lds(NW) + 16 * (4 * a.K + 8) + 2 * (2 * a.K) * (int)sizeof(float);
+    hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, false, false, NW, true>), dim3((unsigned)sk_groups(a)),
+                       dim3(64 * NW), lds, s, a);
+    return hipGetLastError();
+}
+
 // Split K when the launch has too few workgroups to give every SIMD a few
 // waves (a single layer at batch 1): over 4 waves below 400 workgroups, over
 // 2 from there (less LUT building and reduction per k-step once the groups
@@ -609,6 +776,15 @@ static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
 
 template <int XDT, int YDT, int CB>
 static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
+    // Fused LayerNorm (qualified on the host, layer_norm_wide_fusable): K
+    // split over 4 waves at any group count, so each wave normalizes 4 of
+    // the chunk's 16 rows (ViT-B/16 batch-1 forward 0.775 -> 0.712 ms; over
+    // 2 waves from 400 groups, as without the LayerNorm, 0.781 ms: the
+    // prologue's per-wave work sits on every workgroup's critical path).
+    if (a.ln) {
+        if constexpr (CB != RPFQ_CB_TABLE && XDT != RPFQ_F32) return wide_sk_ln_go<XDT, YDT, CB, 4>(a, s);
+        return hipErrorInvalidValue;
+    }
     const bool pb = a.nblk > 1, kt = a.K % 32 != 0;
     if (gemv_pays(a)) return kt ? wide_gv<XDT, YDT, CB, true>(a, s) : wide_gv<XDT, YDT, CB, false>(a, s);
     if (pb) return kt ? wide_sk_go<XDT, YDT, CB, true, true, 1>(a, s) : wide_sk_go<XDT, YDT, CB, true, false, 1>(a, s);

@@ -204,8 +204,8 @@ class PackedWide:
         _native.FLAG_NO_STREAM or _native.FLAG_STREAM.  residual ([..., 2N'] of out_dtype): y =
         residual + layer(x), fused into the kernel's store and rounded as the
         unfused add would round it (rpfq_wide_linear_residual).  gelu: y =
-        F.gelu(layer(x)) (exact erf GELU in the store, equal to the unfused
-        op; not with a residual)."""
+        GELU(layer(x)) in the store (within 1 ulp of out_dtype of the exact
+        GELU of the rounded output; not with a residual)."""
         N.require_device(x, bias, residual)
         if gelu:
             if residual is not None:
@@ -250,6 +250,43 @@ class PackedWide:
                 nbytes += m * self.out_features * y.element_size()
             rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex), nbytes,
                 (m, self.n_complex, self.k_complex))
+        return y.reshape(*lead, self.out_features)
+
+    def ln_fusable(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype | None = None) -> bool:
+        """Whether layer_norm_linear() fuses the LayerNorm for m rows
+        (rpfq_layer_norm_wide_linear_fusable, no GPU work)."""
+        out = ctypes.c_int32(0)
+        N.check("rpfq_layer_norm_wide_linear_fusable", N.load().rpfq_layer_norm_wide_linear_fusable(
+            ctypes.byref(self.desc), int(m), N.dtype_code(x_dtype), N.dtype_code(y_dtype or x_dtype),
+            ctypes.byref(out)))
+        return bool(out.value)
+
+    def layer_norm_linear(self, x: torch.Tensor, ln_weight: torch.Tensor | None, ln_bias: torch.Tensor | None,
+                          eps: float, bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                          gelu: bool = False) -> torch.Tensor:
+        """self.linear(layer_norm(x, ln_weight, ln_bias, eps), bias) in one
+        launch (rpfq_layer_norm_wide_linear): the LayerNorm over the 2K' input
+        features runs in the streaming kernel's prologue, its output rounded
+        to x's dtype as layer_norm() rounds it.  Only where ln_fusable();
+        gelu as in linear()."""
+        N.require_device(x, ln_weight, ln_bias, bias)
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        x2 = _aligned_rows(x.reshape(-1, self.in_features))
+        m = x2.shape[0]
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
+        if m == 0:
+            return y.reshape(*lead, self.out_features)
+        w = None if ln_weight is None else ln_weight.detach().float().contiguous()
+        b = None if ln_bias is None else ln_bias.detach().float().contiguous()
+        if bias is not None:
+            bias = bias.contiguous().float()
+        N.check("rpfq_layer_norm_wide_linear", N.load().rpfq_layer_norm_wide_linear(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(), N.dtype_code(x2.dtype),
+            m, N.ptr(w), N.ptr(b), float(eps), N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype),
+            N.FLAG_GELU if gelu else 0, N.stream_of(x2)))
         return y.reshape(*lead, self.out_features)
 
     def kernel_for(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype, flags: int = 0) -> int:

@@ -559,6 +559,21 @@ class QATLinearComplexPhase(nn.Linear):
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
 
+    def forward_layer_norm(self, x: torch.Tensor, ln_weight, ln_bias, eps: float, gelu: bool = False):
+        """self(layer_norm(x)) (and its exact GELU if gelu) with the LayerNorm
+        fused into the packed layer's launch (rpfq_layer_norm_wide_linear), or
+        None where that launch does not apply (training, host tensors,
+        activation quantization on, stage groups, a launch the fused kernel
+        does not take: see PackedWide.ln_fusable)."""
+        if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None:
+            return None
+        pw = self.packed(x.device)
+        m = x.numel() // x.shape[-1]
+        if not hasattr(pw, "ln_fusable") or m == 0 or not pw.ln_fusable(m, x.dtype):
+            return None
+        bias = None if self.bias is None else self.bias.detach()
+        return pw.layer_norm_linear(x, ln_weight, ln_bias, eps, bias, out_dtype=x.dtype, gelu=gelu)
+
     def forward_residual(self, x: torch.Tensor, residual: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         """residual + self(x); x already activation-quantized for this layer
         if prequantized.  On the packed HIP path the add is fused into the

@@ -132,9 +132,12 @@ class SwinTransformerBlock(nn.Module):
         hn, q = norm_quant_fwd(self.norm1, x, self.attn.qkv)
         x = x + self._attn(hn, q)
         x = x.reshape(b, -1, c)
-        if _fused(self, x):  # the MLP residual add fused into fc2's store
-            hn, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
-            x = self.mlp.forward_residual(hn, x, q)
+        if _fused(self, x):  # the MLP residual add fused into fc2's store (norm2 into fc1 where it streams)
+            y = self.mlp.forward_norm_residual(self.norm2, x)
+            if y is None:
+                hn, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
+                y = self.mlp.forward_residual(hn, x, q)
+            x = y
         else:
             x = x + self.mlp(self.norm2(x))
         return x.reshape(b, h, w, c)

@@ -28,6 +28,10 @@ FUSE_ACT_QUANT = os.environ.get("RPFQ_FUSE_AQ", "1") != "0"
 # Within the fused path, the MLP's exact GELU runs in fc1's store when fc1 is
 # a packed phase-quantized Linear (rpfq_wide_linear with RPFQ_FLAG_GELU).
 FUSE_GELU = os.environ.get("RPFQ_FUSE_GELU", "1") != "0"
+# LayerNorm in the following packed layer's launch (norm1 -> qkv, norm2 ->
+# fc1) where that layer streams: a block at batch 1-2.  RPFQ_FUSE_LN=0 keeps
+# the LayerNorm kernel.
+FUSE_LN = os.environ.get("RPFQ_FUSE_LN", "1") != "0"
 
 
 def _fused(module: nn.Module, x: torch.Tensor) -> bool:
@@ -72,6 +76,18 @@ def norm_quant_fwd(norm: nn.Module, x: torch.Tensor, layer: nn.Module):
 
     w, b = _ln_params(norm)
     return ops.layer_norm(x, w, b, norm.eps, act_bits=bits), True
+
+
+def norm_layer_fwd(norm: nn.Module, x: torch.Tensor, layer: nn.Module, gelu: bool = False):
+    """layer(norm(x)) (GELU'd if gelu) in one packed-layer launch with the
+    LayerNorm in its prologue, or None where that does not apply (the
+    caller then runs norm and layer separately)."""
+    fwd = getattr(layer, "forward_layer_norm", None)
+    if not (FUSE_LN and fwd is not None and _fused(norm, x) and type(norm) is nn.LayerNorm
+            and len(norm.normalized_shape) == 1):
+        return None
+    w, b = _ln_params(norm)
+    return fwd(x, w, b, norm.eps, gelu)
 
 
 def call_layer(layer: nn.Module, h: torch.Tensor, prequantized: bool) -> torch.Tensor:
@@ -154,7 +170,20 @@ class Mlp(nn.Module):
             h = fc1_gelu(x, prequantized)
         else:
             h = self.act(call_layer(self.fc1, x, prequantized))
+        return self.forward_hidden_residual(h, residual)
+
+    def forward_hidden_residual(self, h, residual):
+        """residual + fc2(h) for h = act(fc1(x)) already computed."""
         return linear_residual(self.fc2, self.norm(self.drop1(h)), residual)
+
+    def forward_norm_residual(self, norm, x):
+        """x + self(norm(x)) with norm fused into fc1's launch (and the exact
+        GELU into its store), or None where that does not apply."""
+        gelu = FUSE_GELU and type(self.act) is nn.GELU and self.act.approximate == "none"
+        h = norm_layer_fwd(norm, x, self.fc1, gelu)
+        if h is None:
+            return None
+        return self.forward_hidden_residual(h if gelu else self.act(h), x)
 
 
 class Attention(nn.Module):
@@ -171,8 +200,12 @@ class Attention(nn.Module):
         self.proj_drop = nn.Dropout(proj_drop)
 
     def _mix(self, x, prequantized: bool = False):
-        b, n, c = x.shape
-        qkv = call_layer(self.qkv, x, prequantized).reshape(b, n, 3, self.num_heads, self.head_dim)
+        return self._attend(call_layer(self.qkv, x, prequantized))
+
+    def _attend(self, qkv):
+        b, n, c3 = qkv.shape
+        c = c3 // 3
+        qkv = qkv.reshape(b, n, 3, self.num_heads, self.head_dim)
         qkv = qkv.permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)
         x = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
@@ -185,6 +218,14 @@ class Attention(nn.Module):
         """residual + self(x) with the add fused into proj (eval mode); x
         already activation-quantized for qkv if prequantized."""
         return linear_residual(self.proj, self._mix(x, prequantized), residual)
+
+    def forward_norm_residual(self, norm, x):
+        """x + self(norm(x)) with norm fused into qkv's launch, or None where
+        that does not apply."""
+        qkv = norm_layer_fwd(norm, x, self.qkv)
+        if qkv is None:
+            return None
+        return linear_residual(self.proj, self._attend(qkv), x)
 
 
 class Block(nn.Module):
@@ -202,10 +243,16 @@ class Block(nn.Module):
         if _fused(self, x) and isinstance(self.ls1, nn.Identity) and isinstance(self.ls2, nn.Identity):
             # audit_rpfq_vit_ios_parity.py:520-556 with the residual adds in
             # the proj / fc2 stores and LayerNorm on the device kernel
-            h, q = norm_quant_fwd(self.norm1, x, self.attn.qkv)
-            x = self.attn.forward_residual(h, x, q)
-            h, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
-            return self.mlp.forward_residual(h, x, q)
+            y = self.attn.forward_norm_residual(self.norm1, x)
+            if y is None:
+                h, q = norm_quant_fwd(self.norm1, x, self.attn.qkv)
+                y = self.attn.forward_residual(h, x, q)
+            x = y
+            y = self.mlp.forward_norm_residual(self.norm2, x)
+            if y is None:
+                h, q = norm_quant_fwd(self.norm2, x, self.mlp.fc1)
+                y = self.mlp.forward_residual(h, x, q)
+            return y
         x = x + self.ls1(self.attn(self.norm1(x)))
         x = x + self.ls2(self.mlp(self.norm2(x)))
         return x

@@ -255,6 +255,52 @@ int main(void) {
     assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stdout, out.stderr)
 
 
+def test_layer_norm_wide_linear_fusable_and_errors():
+    """rpfq_layer_norm_wide_linear_fusable (no GPU work): the LayerNorm fuses
+    into the streaming kernel's split-K forms only -- ViT-B qkv / fc1 / proj
+    at one image (197 rows), not at 50,432 rows (DMA kernel), not for M <= 8
+    on the column-split kernel, not for K' > 384, float32 x, per-block scales
+    or the TABLE codebook; rpfq_layer_norm_wide_linear validates its
+    arguments on the host and refuses launches the query refuses."""
+    L, N = lib()
+
+    def fusable(d, m, xdt=1, ydt=1):
+        out = ctypes.c_int32(-1)
+        assert L.rpfq_layer_norm_wide_linear_fusable(ctypes.byref(d), m, xdt, ydt, ctypes.byref(out)) == 0
+        return out.value
+    for n, k in ((1152, 384), (1536, 384), (384, 384), (288, 96)):
+        assert fusable(_desc(N, n=n, k=k), 197) == 1, (n, k)
+        assert fusable(_desc(N, n=n, k=k), 197, xdt=2, ydt=2) == 1, (n, k)
+    fc1 = _desc(N, n=1536, k=384)
+    assert fusable(fc1, 50432) == 0
+    assert fusable(fc1, 1) == 0          # column-split kernel
+    assert fusable(fc1, 197, xdt=0) == 0  # float32 x
+    assert fusable(_desc(N, n=1536, k=512), 197) == 0       # K' > 384 (ViT-L: measured slower fused)
+    assert fusable(_desc(N, n=1536, k=384, block=128), 197) == 0
+    assert fusable(_desc(N, n=1536, k=384, cb=N.CB_TABLE, stages=1), 197) == 0
+    out = ctypes.c_int32(-1)
+    assert L.rpfq_layer_norm_wide_linear_fusable(ctypes.byref(fc1), 197, 1, 1, None) == 1
+    assert L.rpfq_layer_norm_wide_linear_fusable(ctypes.byref(fc1), 0, 1, 1, ctypes.byref(out)) == 2
+    assert L.rpfq_layer_norm_wide_linear_fusable(ctypes.byref(fc1), 197, 7, 1, ctypes.byref(out)) == 5
+    # launches: argument errors before any GPU work
+    nbytes = L.rpfq_wide_packed_bytes(ctypes.byref(fc1))
+    fake = 1 << 20  # an aligned non-NULL address; never dereferenced on these paths
+
+    def call(d=fc1, packed=fake, nb=nbytes, x=fake, xdt=1, m=197, g=None, b=None, eps=1e-6, y=fake, ydt=1,
+             flags=0):
+        return L.rpfq_layer_norm_wide_linear(ctypes.byref(d), packed, nb, x, xdt, m, g, b, ctypes.c_float(eps),
+                                             None, y, ydt, flags, None)
+    assert call(packed=None) == 1 and call(x=None) == 1 and call(y=None) == 1
+    assert call(xdt=9) == 5
+    assert call(m=0) == 2
+    assert call(flags=N.FLAG_NO_STREAM) == 6
+    assert call(eps=-1.0) == 6
+    assert call(nb=nbytes - 1) == 2
+    assert call(x=fake + 8) == 3 and call(g=fake + 4) == 3
+    assert call(m=50432) == 6  # not fusable: use rpfq_layer_norm + rpfq_wide_linear
+    assert b"rpfq_layer_norm" in L.rpfq_last_error()
+
+
 def test_wide_linear_kernel_choice():
     """rpfq_wide_linear_kernel (no GPU work): the streaming kernels for a few
     rows and for small one-tile-deep launches (the column-split one for

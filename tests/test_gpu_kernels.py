@@ -720,6 +720,69 @@ def test_layer_norm(m, c, xdt, ydt):
     assert np.abs(y0 - ref0).max() <= 2e-5 * (np.abs(ref0).max() + 1)
 
 
+# LayerNorm fused into the streaming kernel (rpfq_layer_norm_wide_linear):
+# ViT-B/16 qkv / fc1 / proj (K' = 384, the largest fused K'), DeiT-Ti qkv
+# with rotation, a 16-PSK layer, a sign-codebook layer
+LN_CASES = [
+    (1152, 384, "axis", 2, 0, None),
+    (1536, 384, "axis", 2, 0, None),
+    (384, 384, "axis", 2, 0, None),
+    (288, 96, "axis", 2, 0, ((0.8, 0.6), (0.6, -0.8))),
+    (1024, 384, "psk16", 1, 0, None),
+    (200, 64, "sign", 2, 0, None),
+]
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [9, 45, 197])
+@pytest.mark.parametrize("case", LN_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}" for c in LN_CASES])
+def test_layer_norm_wide_linear(case, m, xdt):
+    """One launch of LayerNorm + packed layer against the two launches it
+    replaces (rpfq_layer_norm with x's dtype, then rpfq_wide_linear on the
+    same streaming kernel): the normalized rows differ only where the float32
+    statistics, summed in another order, move a value across a rounding
+    boundary of x's dtype, by one ulp u_x, so |y - y_sep| <= u_x |h| |A16| +
+    float32 accumulation; the separate path itself against the oracle.  Also
+    without the affine parameters and with the GELU in the store."""
+    ops, N = qm()
+    r = rng(1900 + m + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    assert pw.ln_fusable(m, xdt), (case, m)
+    c2 = 2 * case[1]
+    x = torch.from_numpy((r.standard_normal((m, c2)) * 3 + 1).astype(np.float32)).to(xdt).to(DEV)
+    g = tdev(r.standard_normal(c2).astype(np.float32))
+    b = tdev(r.standard_normal(c2).astype(np.float32))
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    u_x = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[xdt]
+    a16 = np.abs(O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64))
+    for gg, bb in ((g, b), (None, None)):
+        y = pw.layer_norm_linear(x, gg, bb, 1e-6, bias, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+        h = ops.layer_norm(x, gg, bb, 1e-6)
+        y_sep = pw.linear(h, bias, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+        hf = h.float().cpu().numpy().astype(np.float64)
+        scale = np.abs(hf) @ a16.T + np.abs(bias.cpu().numpy())
+        assert np.all(np.abs(y - y_sep) <= u_x * (np.abs(hf) @ a16.T) + 2e-6 * scale + 1e-5), (case, m)
+        check_against_oracle(y_sep, hf, bias.cpu().numpy().astype(np.float64), oplanes, codebook, rotation)
+    yg = pw.layer_norm_linear(x, g, b, 1e-6, bias, out_dtype=torch.float16, gelu=True).float().cpu().numpy()
+    h = ops.layer_norm(x, g, b, 1e-6)
+    yg_sep = pw.linear(h, bias, out_dtype=torch.float16, gelu=True).float().cpu().numpy()
+    hf = h.float().cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(yg - yg_sep) <= 1.2 * u_x * (np.abs(hf) @ a16.T) + 2.0 ** -9 * np.abs(yg_sep) + 1e-4)
+
+
+def test_layer_norm_wide_linear_refuses_unfusable():
+    """Launches outside the fused kernel's forms raise (the caller runs the
+    LayerNorm and the layer separately)."""
+    ops, N = qm()
+    r = rng(1950)
+    pw, *_ = build_packed(r, LN_CASES[1])
+    x = torch.zeros(300, 768, dtype=torch.float16, device=DEV)
+    assert not pw.ln_fusable(50432, torch.float16)
+    assert not pw.ln_fusable(4, torch.float16)  # column-split kernel
+    with pytest.raises(N.RPFQError, match="RPFQ_ERR_VALUE"):
+        pw.layer_norm_linear(x.float(), None, None, 1e-6)
+
+
 @pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 1024), (5, 3072)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
                                      (torch.bfloat16, torch.bfloat16)])

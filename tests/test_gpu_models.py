@@ -376,7 +376,7 @@ def test_fused_blocks_match_unfused(name):
     finally:
         vt.FUSED_BLOCKS = saved
     err = (y_f - y_u).abs().max()
-    tol = LOGIT_TOL[dt]
+    tol = LOGIT_TOL["fp16"]
     assert err <= tol * y_u.abs().max() + tol / 10, (err, y_u.abs().max())
     top = y_u.topk(2, dim=1).values
     confident = (top[:, 0] - top[:, 1]) > 4 * err
@@ -486,12 +486,19 @@ def test_fused_gelu_wiring(name, dt, batch):
     fused = []
     linear = ops.PackedWide.linear
 
+    ln_linear = ops.PackedWide.layer_norm_linear
+
     def counting(self, *args, **kw):
         fused.append(bool(kw.get("gelu", False)))
         return linear(self, *args, **kw)
+
+    def counting_ln(self, *args, **kw):  # fc1 with norm2 fused into its launch (one image)
+        fused.append(bool(kw.get("gelu", False)))
+        return ln_linear(self, *args, **kw)
     saved = vt.FUSED_BLOCKS, vt.FUSE_GELU
     try:
         ops.PackedWide.linear = counting
+        ops.PackedWide.layer_norm_linear = counting_ln
         with torch.no_grad():
             vt.FUSED_BLOCKS, vt.FUSE_GELU = True, True
             y_f = model(x)
@@ -500,10 +507,69 @@ def test_fused_gelu_wiring(name, dt, batch):
             y_u = model(x)
     finally:
         ops.PackedWide.linear = linear
+        ops.PackedWide.layer_norm_linear = ln_linear
         vt.FUSED_BLOCKS, vt.FUSE_GELU = saved
     assert n_fused >= 2, n_fused
     assert torch.isfinite(y_f).all()
     y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
+    err = (y_f - y_u).abs().max()
+    tol = LOGIT_TOL[dt]
+    assert err <= tol * y_u.abs().max() + tol / 10, (err, y_u.abs().max())
+    top = y_u.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
+
+
+@pytest.mark.parametrize("name,dt", [("rpfq_vit_base_patch16_224_q", "fp16"), ("rpfq_vit_base_patch16_224_q", "bf16"),
+                                     ("rpfq_deit_tiny_patch16_224_q", "fp16"),
+                                     ("rpfq_swin_tiny_patch4_window7_224_q", "fp16")])
+def test_fused_layer_norm_wiring(name, dt):
+    """At one image the blocks run norm1 -> qkv and norm2 -> fc1 as single
+    launches (rpfq_layer_norm_wide_linear; Swin: norm2 -> fc1 where fc1
+    streams): counted, and the logits within LOGIT_TOL * max|logit| +
+    LOGIT_TOL / 10 of the same model with the fusion off, identical top-1 on
+    margin-confident samples.  A LayerNorm skipped or applied twice moves
+    them by orders of magnitude more."""
+    import quant_models as qm
+    from quant_models import ops
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(9)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    load_synthetic_codes(model, 9)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, torch.nn.LayerNorm):
+                mod.weight.normal_(1.0, 0.1)
+                mod.bias.normal_(0.0, 0.1)
+    act = torch.bfloat16 if dt == "bf16" else torch.float16
+    prepare_inference(model, DEV, act)
+    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(13)).to(DEV, act)
+    calls = []
+    fused_call = ops.PackedWide.layer_norm_linear
+
+    def counting(self, *args, **kw):
+        calls.append(1)
+        return fused_call(self, *args, **kw)
+    saved = vt.FUSE_LN
+    try:
+        ops.PackedWide.layer_norm_linear = counting
+        with torch.no_grad():
+            vt.FUSE_LN = True
+            y_f = model(x)
+            n_fused = len(calls)
+            vt.FUSE_LN = False
+            y_u = model(x)
+    finally:
+        ops.PackedWide.layer_norm_linear = fused_call
+        vt.FUSE_LN = saved
+    blocks = sum(1 for m in model.modules() if type(m).__name__ in ("Block", "SwinTransformerBlock"))
+    assert n_fused >= (2 * blocks if "swin" not in name else 2), (n_fused, blocks)
+    assert len(calls) == n_fused  # nothing fused with the switch off
+    y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
+    assert torch.isfinite(y_f).all()
     err = (y_f - y_u).abs().max()
     tol = LOGIT_TOL[dt]
     assert err <= tol * y_u.abs().max() + tol / 10, (err, y_u.abs().max())
