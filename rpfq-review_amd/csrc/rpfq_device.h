@@ -207,21 +207,21 @@ __device__ __forceinline__ uint2 add_res4(uint2 v, const void* res, int64_t off)
     return make_uint2(add2_y(v.x, r.x, f16), add2_y(v.y, r.y, f16));
 }
 
-// Fused activation of the stored output (WideArgs::act = 1): exact GELU
-// (approximate = 'none') of the value already rounded to y's dtype, computed
-// in float32 by the formula of torch's GELU kernel for 16-bit and float32
-// tensors, x * 0.5 * (1 + erf(x * sqrt(1/2))), and rounded to y's dtype by
-// the store.  The empty asm keeps that float32 rounding: without it the
-// backend may fold the last multiply and the fp16 conversion into one
-// v_fma_mixlo_f16 (a single rounding), which changes the result where the
-// exact value lies near an fp16 rounding tie, and differently per kernel.
+// Exact GELU (approximate = 'none') in float32 by the formula of torch's
+// GELU kernel, x * 0.5 * (1 + erf(x * sqrt(1/2))): the GELU + act-quant row
+// kernel, whose quantized values are bit-exact with torch's GELU followed by
+// the reference's act quant.  The empty asm keeps the float32 result: without
+// it the backend may fold the last multiply and a following fp16 conversion
+// into one v_fma_mixlo_f16 (a single rounding).
 __device__ __forceinline__ float gelu_f(float x) {
     float g = x * 0.5f * (1.0f + erff(x * 0.707106781186547524f));
     asm volatile("" : "+v"(g));
     return g;
 }
 
-// GELU(x) = x Phi(x) for the GEMM stores, ~20 VALU (2 transcendental)
+// Fused activation of the GEMM stores (WideArgs::act = 1), applied to the
+// output already rounded to y's dtype and rounded again by the store:
+// GELU(x) = x Phi(x), ~20 VALU (2 transcendental)
 // against ~40-60 for the erff form above.  The normal tail Q(a) =
 // P(X > a) = erfc(a / sqrt 2) / 2, a = |x|, is written
 //   Q(a) = exp(-a^2 / 2) t S(t),  t = 1 / (1 + p a),

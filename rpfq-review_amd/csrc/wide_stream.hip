@@ -249,6 +249,38 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
         prm[1] = pp[1];
     }
 
+    // The epilogue's bias and residual (wave 0, rows < M).  With split K (a
+    // layer at batch 1-2, latency-bound) they are requested before the code
+    // ring, so their latency overlaps the k-loop instead of following it
+    // (ViT-B/16 batch-1 forward -1%); one wave per tile (many tiles, where
+    // occupancy hides the epilogue) loads them at the end, keeping the
+    // registers.  The residual read stays before this lane's own store of the
+    // same elements, so y may alias it.
+    const int64_t ldy = 2 * (int64_t)a.N;
+    const bool epi = (NW == 1 || wave == 0) && m_ok;
+    float eb[2][2][4];  // [h][re / im][v]
+    uint2 er[2][2];     // [h][re / im]: 4 residual values of the vector store
+    auto fetch_epi = [&]() {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t n0 = (int64_t)tile * 32 + 16 * h + 4 * q;
+            const int64_t base = (m0 + r16) * ldy + n0;
+            const bool vec = a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const bool ok = epi && a.bias && n0 + v < a.N;
+                eb[h][0][v] = ok ? a.bias[n0 + v] : 0.0f;
+                eb[h][1][v] = ok ? a.bias[a.N + n0 + v] : 0.0f;
+            }
+            const bool rv = epi && vec && a.res;
+            er[h][0] = rv ? *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.res) + base)
+                          : make_uint2(0, 0);
+            er[h][1] = rv ? *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.res) + base + a.N)
+                          : make_uint2(0, 0);
+        }
+    };
+    if (NW > 1) fetch_epi();
+
     Step ring[SK_PF];
 #pragma unroll
     for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
@@ -435,25 +467,23 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
     // Epilogue: lane (m = r16, q) holds outputs n = 32 tile + 16 h + 4 q + v
     // of x row m; rows past M and outputs past N' store nothing.
     if (!m_ok) return;
-    const int64_t ldy = 2 * (int64_t)a.N;
+    if (NW == 1) fetch_epi();
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int64_t n0 = (int64_t)tile * 32 + 16 * h + 4 * q;
         float vr[4], vi[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int64_t n = n0 + v;
-            const bool ok = n < a.N;
-            vr[v] = acc_re[h][v] + ((a.bias && ok) ? a.bias[n] : 0.0f);
-            vi[v] = acc_im[h][v] + ((a.bias && ok) ? a.bias[a.N + n] : 0.0f);
+            vr[v] = acc_re[h][v] + eb[h][0][v];
+            vi[v] = acc_im[h][v] + eb[h][1][v];
         }
         const int64_t base = (m0 + r16) * ldy + n0;
         if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
             uint2 hr = make_uint2(cvt_pk(vr[0], vr[1]), cvt_pk(vr[2], vr[3]));
             uint2 hi = make_uint2(cvt_pk(vi[0], vi[1]), cvt_pk(vi[2], vi[3]));
             if (a.res) {
-                hr = add_res4<YDT>(hr, a.res, base);
-                hi = add_res4<YDT>(hi, a.res, base + a.N);
+                hr = make_uint2(add2_y(hr.x, er[h][0].x, true), add2_y(hr.y, er[h][0].y, true));
+                hi = make_uint2(add2_y(hi.x, er[h][1].x, true), add2_y(hi.y, er[h][1].y, true));
             }
             if (a.act) {
                 hr = make_uint2(gelu2_y(hr.x, true), gelu2_y(hr.y, true));
