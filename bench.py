@@ -437,6 +437,61 @@ def layer_probe(n_c: int, k_c: int, m: int, steps: int) -> int:
     return 0
 
 
+GRAD_SHAPES = (("qkv", 1152, 384), ("proj", 384, 384), ("fc1", 1536, 384), ("fc2", 384, 1536))
+
+
+def grad_x_bench(m: int, steps: int) -> int:
+    """Input gradient of the ViT-B/16 q2 layers at m rows (default bs256 x
+    197 tokens) on the packed blob (rpfq_wide_linear_grad_x) against the
+    dense library GEMM on the decoded weight (torch.matmul, hipBLASLt):
+    fp16 grad_y into fp16 grad_x, and float32 grad_y into float32 grad_x
+    (the float32 QAT backward: packed fp16 MFMA operands after the per-row
+    scaling vs the float32 library GEMM).  HIP events over `steps` calls on
+    the current stream; prints one JSON line."""
+    import torch
+
+    def timed(fn):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    rows = {}
+    g = torch.Generator(device="cuda").manual_seed(3)
+    for name, n_c, k_c in GRAD_SHAPES:
+        pw = stream_layer(k_c, n_c, 1)[0]
+        pw.adjoint()
+        a16 = pw.decode(round_fp16=True)
+        flops = 2 * m * 2 * n_c * 2 * k_c
+        row = {"n_complex": n_c, "k_complex": k_c}
+        for tag, dt in (("fp16", torch.float16), ("f32", torch.float32)):
+            gy = torch.randn(m, 2 * n_c, device="cuda", generator=g).to(dt)
+            a = a16.to(dt)
+            us_packed = timed(lambda: pw.grad_x(gy, dt))
+            us_dense = timed(lambda: torch.matmul(gy, a))
+            row[tag] = {"packed_us": round(us_packed, 1), "packed_tflops": round(flops / us_packed / 1e6, 1),
+                        "frac": round(flops / us_packed / 1e6 / 2500.0, 4), "dense_library_us": round(us_dense, 1)}
+            del gy, a
+        rows[name] = row
+        print(f"# grad_x {name}: {row}", file=sys.stderr, flush=True)
+        del pw, a16
+        torch.cuda.empty_cache()
+    tot = {t: sum(r[t]["packed_us"] for r in rows.values()) for t in ("fp16", "f32")}
+    dense = {t: sum(r[t]["dense_library_us"] for r in rows.values()) for t in ("fp16", "f32")}
+    flops = sum(2 * m * 2 * n * 2 * k for _, n, k in GRAD_SHAPES)
+    print(json.dumps({"metric": "grad_x TFLOP/s, ViT-B/16 q2 layer shapes (one block)", "m": m, "steps": steps,
+                      "value": round(flops / tot["fp16"] / 1e6, 1), "unit": "TFLOP/s",
+                      "roofline": {"bound": "mfma", "peak": 2500.0, "frac": round(flops / tot["fp16"] / 1e6 / 2500.0, 4),
+                                   "kernel": "rpfq::wide_grad_x_kernel"},
+                      "block_us": tot, "dense_library_block_us": dense, "layers": rows}))
+    return 0
+
+
 def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: bool, modes=("hip", "torch")):
     """Quantization-aware training steps of the configured model (float32,
     rotation at the family default, SGD): forward with every Linear
@@ -547,12 +602,16 @@ def main() -> int:
     ap.add_argument("--layer-probe", default=None, metavar="NC,KC",
                     help="time one q2 layer of N' x K' complex (random codes) on 50,432 fp16 rows instead "
                          "(--steps launches; for counter runs)")
+    ap.add_argument("--grad-x", action="store_true",
+                    help="time the packed input gradient (rpfq_wide_linear_grad_x) on the ViT-B layer shapes")
     ap.add_argument("--train", action="store_true",
                     help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
     ap.add_argument("--train-modes", default="hip,torch")
     args = ap.parse_args()
     if args.layer_probe:
         return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
+    if args.grad_x:
+        return grad_x_bench(args.batch * 197 if args.batch else 50432, args.steps)
     if args.train:
         return train_bench(args.config, args.batch or 64, args.steps, args.warmup, args.act_quant,
                            tuple(args.train_modes.split(",")))

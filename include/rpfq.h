@@ -209,6 +209,44 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
                               const void* x, int x_dtype, int64_t M, const float* bias,
                               const void* residual, void* y, int y_dtype, int flags, void* stream);
 
+/* Bytes of the adjoint code tiles that rpfq_wide_pack_adjoint writes for
+ * `desc` (0 if the descriptor is invalid). */
+size_t rpfq_wide_adjoint_bytes(const rpfq_wide_desc* desc);
+
+/*
+ * Adjoint code tiles of a packed layer: its codes with rows and columns
+ * exchanged, for rpfq_wide_linear_grad_x (the per-row parameters stay in
+ * the packed blob).  Run once per packed blob; both buffers 256-byte aligned.
+ * No counterpart in the reference: it is this library's layout of the
+ * codes for contractions over N'.
+ */
+int rpfq_wide_pack_adjoint(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, void* adjoint,
+                           size_t adjoint_bytes, void* stream);
+
+/*
+ * Input gradient of rpfq_wide_linear: grad_x = grad_y A, where A [2N', 2K']
+ * is the real matrix of y = U x + W conj(x) made of the fused fp16
+ * coefficients that rpfq_wide_linear feeds its MFMAs (A11 = Wre + Ure,
+ * A12 = Wim - Uim, A21 = Wim + Uim, A22 = -Wre + Ure, bit for bit):
+ *   gx_re = gy_re A11 + gy_im A21,   gx_im = gy_re A12 + gy_im A22.
+ * grad_y: [M, 2N'] of grad_y_dtype (16-byte aligned when N' % 8 == 0);
+ * grad_x: [M, 2K'] of grad_x_dtype.  packed / adjoint: the layer's blob and
+ * its rpfq_wide_pack_adjoint tiles.  The products run on fp16 MFMA
+ * operands with float32 accumulation; float32 and bf16 grad_y rows are
+ * scaled by a power of two per row (largest magnitude in [2^14, 2^15))
+ * before the fp16 rounding and unscaled exactly after, so each grad_y
+ * element carries one fp16 rounding (relative 2^-11) unless it is below
+ * 2^-24 of its row's largest.  The bias gradient is the column sum of
+ * grad_y and is left to the caller.
+ * Replaces grad_x = einsum('blo, oi -> bli', grad_output, w_quant) of
+ *   RPFQ-ViT-main/quant_models/kernel.py:585 (the reference operator's
+ *   backward), i.e. the input gradient of F.linear(x, A_q, bias) at
+ *   quant_i.py:554 under the straight-through estimator (quant_i.py:128-130).
+ */
+int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* adjoint,
+                            size_t adjoint_bytes, const void* grad_y, int grad_y_dtype, int64_t M, void* grad_x,
+                            int grad_x_dtype, void* stream);
+
 /*
  * y = layer(LayerNorm(x)) in one launch: the LayerNorm of rpfq_layer_norm
  * over the layer's 2K' input features (float32 statistics and affine map,

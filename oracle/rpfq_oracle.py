@@ -25,6 +25,10 @@ Parity status per function (how each one is pinned; see tests/test_oracle.py):
 * ``phase_linear``          -- compiled reference (oracle/_ref) and brute force.
 * ``wide_linear``           -- compiled reference (oracle/_ref); equals
                                ``x @ A_q.T + b`` in float64 (golden A_q).
+* ``wide_linear_grad_x``    -- the adjoint identity <gy, wide_linear(x)> =
+                               <wide_linear_grad_x(gy), x> against the pinned
+                               forward, and torch autograd of F.linear on the
+                               same A_q (an independent library routine).
 * ``fp16_add`` / ``recompose_fp16`` -- build-defined fp16 operand (no
                                reference counterpart): fp16_add pinned by exact
                                rational arithmetic (fractions) on every fp16
@@ -484,6 +488,15 @@ def wide_linear(x, planes, bias=None, codebook: str = "axis", rotation=None, fp1
     if bias is not None:
         y = y + np.asarray(bias, np.float64)
     return y
+
+
+def wide_linear_grad_x(gy, planes, codebook: str = "axis", rotation=None, fp16_weight: bool = False):
+    """Input gradient of wide_linear: gx = gy @ A_q in float64, the
+    reference operator's backward grad_x = einsum('blo, oi -> bli',
+    grad_output, w_quant) (kernel.py:585) with w_quant the fused A_q
+    (quant_i.py:534-544); fp16_weight=True uses the MFMA operand."""
+    a = wide_weight(planes, codebook, rotation, fp16=fp16_weight).astype(np.float64)
+    return np.asarray(gy, np.float64) @ a
 
 
 def rotate_for_quant(re, im, c, s):

@@ -96,6 +96,30 @@ struct WideArgs {
     const float* ln_beta;   // [2K'] or NULL (zeros)
 };
 
+// ---------------------------------------------------------------------------
+// Adjoint code tiles (rpfq_wide_pack_adjoint), the packed layer's codes with
+// rows and columns exchanged, for contractions over N' (grad_x):
+//  codesT: [KS][NT][32 columns][32 bytes]: byte b of (complex column k,
+//          row step t) holds the code byte of row n' = 32 t + 8 s + 4 g + e
+//          (g = b / 16, s = (b / 4) & 3, e = b & 3) and column k, so MFMA
+//          lane group g of the lane owning column k streams its 16 rows of
+//          a row step with one 128-bit load.
+// ---------------------------------------------------------------------------
+inline size_t wide_adjoint_bytes(const WideGeom& g) { return (size_t)g.NT * g.KS * 1024; }
+
+// Launch arguments of the grad_x kernel: gx [M, 2K'] = gy [M, 2N'] A.
+struct AdjArgs {
+    const void* gy;
+    int64_t M;
+    int K, N, NT, KS, nblk, block_ks;
+    const uint4* codes_t;  // adjoint code tiles
+    const float4* params;  // the packed layer's per-row parameters
+    RotParams rot;
+    void* gx;
+    int tiles_m, tiles_k;
+    int vec_store;  // gx rows allow 16-byte stores (K' % 8 == 0, aligned gx)
+};
+
 // Compute units of the current device (cached per device, thread-safe;
 // 256 on MI355X), rounded down to a multiple of 4 so a persistent grid of
 // 2 workgroups per CU stays a multiple of 8 (XCD-local tile order).
@@ -178,5 +202,11 @@ size_t quant_scratch_bytes();
 hipError_t quant_scratch_ptr(void** out);
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               float* a, int round_fp16, hipStream_t s);
+// adjoint code tiles (rpfq_kernels.hip) and the grad_x kernel (wide_adjoint.hip, one per codebook)
+hipError_t launch_wide_pack_adjoint(const WideGeom& g, const void* packed, void* adjoint, hipStream_t s);
+template <int CB> hipError_t launch_wide_grad_x(AdjArgs& a, int gdt, int xdt, hipStream_t s);
+hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
+                                     const void* adjoint, const void* gy, int gdt, int64_t M, void* gx, int xdt,
+                                     hipStream_t s);
 
 }  // namespace rpfq

@@ -369,6 +369,31 @@ __global__ void wide_pack_params_kernel(PackArgs a) {
     dst[0] = make_float4(p[0], p[1], p[2], p[3]);
     dst[1] = make_float4(p[4], p[5], p[6], p[7]);
 }
+// Adjoint code tiles: one workgroup per 32 x 32 block of codes.  The block
+// of (row tile t, k-step ks) is staged in LDS as it lies ([row][byte]), and
+// thread i writes dword i & 7 of column i >> 3 of the transposed block
+// (ks, t): its byte e of that dword is code (row 8 s + 4 g + e, column
+// k = i >> 3) with s = (i & 7) & 3, g = (i & 7) >> 2, taken from byte
+// 16 g' + 4 s' + e' of the row (k = 8 s' + 4 g' + e').
+__global__ void __launch_bounds__(256) wide_pack_adjoint_kernel(const uint32_t* __restrict__ codes,
+                                                                uint32_t* __restrict__ codes_t, int64_t NT,
+                                                                int64_t KS) {
+    __shared__ uint32_t blk[256];
+    const int64_t b = blockIdx.x;  // source block index t * KS + ks
+    const int64_t t = b / KS, ks = b - t * KS;
+    const int i = threadIdx.x;
+    blk[i] = codes[b * 256 + i];
+    __syncthreads();
+    const int k = i >> 3, d = i & 7;
+    const int src_b = 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3);  // byte of column k in a row
+    const int row0 = 8 * (d & 3) + 4 * (d >> 2);
+    const uint8_t* bytes = reinterpret_cast<const uint8_t*>(blk);
+    uint32_t out = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out |= (uint32_t)bytes[(row0 + e) * 32 + src_b] << (8 * e);
+    codes_t[(ks * NT + t) * 256 + i] = out;
+}
+
 // Fused weight A_q [2N, 2K] from the native blob (same decode as the GEMM).
 template <int CB>
 __global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const float4* __restrict__ params,
@@ -864,6 +889,14 @@ hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const
 hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,
                                  hipStream_t s) {
     return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 4, bits, y, ydt, s);
+}
+
+hipError_t launch_wide_pack_adjoint(const WideGeom& g, const void* packed, void* adjoint, hipStream_t s) {
+    const int64_t blocks = g.NT * g.KS;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(wide_pack_adjoint_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                       reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<uint32_t*>(adjoint), g.NT, g.KS);
+    return hipGetLastError();
 }
 
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, float* out,

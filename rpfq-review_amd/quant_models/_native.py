@@ -50,6 +50,9 @@ EXPORTED = (
     "rpfq_wide_decode",
     "rpfq_act_quant",
     "rpfq_wide_linear_residual",
+    "rpfq_wide_adjoint_bytes",
+    "rpfq_wide_pack_adjoint",
+    "rpfq_wide_linear_grad_x",
     "rpfq_layer_norm_wide_linear",
     "rpfq_layer_norm_wide_linear_fusable",
     "rpfq_wide_linear_kernel",
@@ -132,6 +135,10 @@ def load() -> ctypes.CDLL:
         lib.rpfq_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         lib.rpfq_wide_linear_residual.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, i32, i32, vp]
         lib.rpfq_wide_linear_kernel.argtypes = [dp, i64, i32, i32, i32, ctypes.POINTER(i32)]
+        lib.rpfq_wide_adjoint_bytes.argtypes = [dp]
+        lib.rpfq_wide_adjoint_bytes.restype = sz
+        lib.rpfq_wide_pack_adjoint.argtypes = [dp, vp, sz, vp, sz, vp]
+        lib.rpfq_wide_linear_grad_x.argtypes = [dp, vp, sz, vp, sz, vp, i32, i64, vp, i32, vp]
         lib.rpfq_layer_norm_wide_linear.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, ctypes.c_float, vp, vp, i32,
                                                     i32, vp]
         lib.rpfq_layer_norm_wide_linear_fusable.argtypes = [dp, i64, i32, i32, ctypes.POINTER(i32)]
@@ -144,7 +151,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_quantize_wide.argtypes = [qp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.rpfq_quantize_wide_noalloc.argtypes = [qp, vp, vp, vp, vp, vp, vp]
         for name in EXPORTED[2:]:
-            if name not in ("rpfq_wide_packed_bytes", "rpfq_quantize_workspace_bytes"):
+            if name not in ("rpfq_wide_packed_bytes", "rpfq_wide_adjoint_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32
         _lib = lib
         return lib

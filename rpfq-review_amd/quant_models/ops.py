@@ -157,6 +157,7 @@ class PackedWide:
     blob: torch.Tensor
     rotation: tuple | None = None
     desc: N.WideDesc = field(init=False, repr=False)
+    _adjoint: torch.Tensor | None = field(default=None, init=False, repr=False, compare=False)
 
     def __post_init__(self):
         self.desc = make_desc(self.n_complex, self.k_complex, self.codebook, self.stages, self.block,
@@ -316,6 +317,42 @@ class PackedWide:
             N.dtype_code(x.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(y.dtype), int(flags),
             N.stream_of(x)))
 
+    def adjoint(self) -> torch.Tensor:
+        """The adjoint code tiles of this blob (rpfq_wide_pack_adjoint),
+        built on first use and kept with the layer."""
+        if self._adjoint is None:
+            lib = N.load()
+            nbytes = lib.rpfq_wide_adjoint_bytes(ctypes.byref(self.desc))
+            if nbytes == 0:
+                N.check("rpfq_wide_adjoint_bytes", 2)
+            adj = torch.empty(nbytes, dtype=torch.uint8, device=self.blob.device)
+            N.check("rpfq_wide_pack_adjoint", lib.rpfq_wide_pack_adjoint(
+                ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), adj.data_ptr(), nbytes,
+                N.stream_of(self.blob)))
+            self._adjoint = adj
+        return self._adjoint
+
+    def grad_x(self, grad_y: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Input gradient of linear(): grad_y [..., 2N'] -> grad_y A
+        [..., 2K'] with A the fused fp16 coefficients linear() contracts
+        with (rpfq_wide_linear_grad_x; the backward of F.linear's input,
+        RPFQ-ViT-main/quant_models/kernel.py:585)."""
+        N.require_device(grad_y)
+        if grad_y.shape[-1] != self.out_features:
+            raise ValueError(f"expected last dim {self.out_features}, got {grad_y.shape[-1]}")
+        lead = grad_y.shape[:-1]
+        g2 = _aligned_rows(grad_y.reshape(-1, self.out_features))
+        m = g2.shape[0]
+        out_dtype = out_dtype or grad_y.dtype
+        gx = torch.empty(m, self.in_features, dtype=out_dtype, device=grad_y.device)
+        if m == 0:
+            return gx.reshape(*lead, self.in_features)
+        adj = self.adjoint()
+        N.check("rpfq_wide_linear_grad_x", N.load().rpfq_wide_linear_grad_x(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), adj.data_ptr(), adj.numel(),
+            g2.data_ptr(), N.dtype_code(g2.dtype), m, gx.data_ptr(), N.dtype_code(out_dtype), N.stream_of(g2)))
+        return gx.reshape(*lead, self.in_features)
+
     def decode(self, round_fp16: bool = False) -> torch.Tensor:
         """Fused float32 weight A_q [2N', 2K'] (quant_i.py:534-544 layout)."""
         a = torch.empty(self.out_features, self.in_features, dtype=torch.float32, device=self.blob.device)
@@ -389,6 +426,14 @@ class PackedStages:
         for g in self.groups[1:]:
             y = g.linear(x, None, y.dtype, flags, residual=y)
         return y
+
+    def grad_x(self, grad_y: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Input gradient over all stage groups: the sum of the groups'
+        grad_x, each in float32, rounded once to out_dtype."""
+        gx = self.groups[0].grad_x(grad_y, torch.float32)
+        for g in self.groups[1:]:
+            gx += g.grad_x(grad_y, torch.float32)
+        return gx.to(out_dtype or grad_y.dtype)
 
     def decode(self, round_fp16: bool = False) -> torch.Tensor:
         """Sum of the groups' fused weights (float32)."""

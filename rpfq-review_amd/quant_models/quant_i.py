@@ -379,6 +379,30 @@ class _HipActQuantSTE(torch.autograd.Function):
         return grad, None
 
 
+class _PackedLinearFn(torch.autograd.Function):
+    """Eval-mode packed layer under autograd: the forward runs
+    rpfq_wide_linear; the backward gives the input the gradient through the
+    packed weight on the device (rpfq_wide_linear_grad_x, the reference
+    operator's grad_x = grad_output @ w_quant, kernel.py:585) and the bias
+    its column sum (:588).  The packed weight is frozen (it is not a
+    parameter), so it receives no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, bias, pw):
+        ctx.pw = pw
+        ctx.x_dtype = x.dtype
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return pw.linear(x, None if bias is None else bias.detach(), out_dtype=x.dtype)
+
+    @staticmethod
+    def backward(ctx, grad):
+        gx = ctx.pw.grad_x(grad, out_dtype=ctx.x_dtype) if ctx.needs_input_grad[0] else None
+        gb = None
+        if ctx.needs_input_grad[1]:
+            gb = grad.reshape(-1, grad.shape[-1]).float().sum(0).to(ctx.bias_dtype)
+        return gx, gb, None
+
+
 class QATLinearComplexPhase(nn.Linear):
     """Complex-structured quantized linear layer (quant_i.py:475-554).
 
@@ -508,10 +532,18 @@ class QATLinearComplexPhase(nn.Linear):
                 vs.append((p.data_ptr(), p._version))
         return tuple(vs)
 
+    def _records_grad(self, x: torch.Tensor) -> bool:
+        """Autograd records this call: x or the bias needs a gradient."""
+        return torch.is_grad_enabled() and (x.requires_grad or (self.bias is not None and self.bias.requires_grad))
+
     def _packed_forward(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         from . import ops
 
         pw = self.packed(x.device)
+        if self._records_grad(x):
+            if self.act_quantizer is not None and not prequantized:
+                x = _HipActQuantSTE.apply(x, self.act_quantizer.num_bits)
+            return _PackedLinearFn.apply(x, self.bias, pw)
         if self.act_quantizer is not None and not prequantized:
             x = ops.act_quant(x, self.act_quantizer.num_bits)
         bias = None if self.bias is None else self.bias.detach()
@@ -544,7 +576,7 @@ class QATLinearComplexPhase(nn.Linear):
         images/s fused; fp16 17,603 -> 17,912, but fc1's launch grows by
         ~40% (the GELU's VALU work in the epilogue is not hidden behind the
         MFMAs), so fp16 tiled launches keep torch's separate GELU pass."""
-        if x.is_cuda and not self.training and self.use_packed:
+        if x.is_cuda and not self.training and self.use_packed and not self._records_grad(x):
             from . import _native as N
             from . import ops
 
@@ -565,7 +597,8 @@ class QATLinearComplexPhase(nn.Linear):
         None where that launch does not apply (training, host tensors,
         activation quantization on, stage groups, a launch the fused kernel
         does not take: see PackedWide.ln_fusable)."""
-        if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None:
+        if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None \
+                or self._records_grad(x):
             return None
         pw = self.packed(x.device)
         m = x.numel() // x.shape[-1]
@@ -579,7 +612,7 @@ class QATLinearComplexPhase(nn.Linear):
         if prequantized.  On the packed HIP path the add is fused into the
         kernel's store (bit-identical to the unfused add in x's dtype);
         elsewhere it is the plain sum."""
-        if x.is_cuda and not self.training and self.use_packed:
+        if x.is_cuda and not self.training and self.use_packed and not self._records_grad(x):
             from . import ops
 
             pw = self.packed(x.device)

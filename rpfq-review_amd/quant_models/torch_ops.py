@@ -14,8 +14,11 @@ contract is registered here, running the HIP kernels of librpfq.so:
   the gradient through A_q).  No global rotation (a module-level parameter in
   the reference, handled by QATLinearComplexPhase).
 * ``torch.ops.rpfq.wide_linear(x, packed, n_complex, k_complex, codebook,
-  stages, block, rotation, bias)``: inference on a packed blob
-  (rpfq_wide_linear), y = U x + W conj(x) + bias on [re | im] features.
+  stages, block, rotation, bias)``: a packed blob (rpfq_wide_linear),
+  y = U x + W conj(x) + bias on [re | im] features; backward: the input
+  gradient on the same blob (rpfq_wide_linear_grad_x, after relaying its
+  codes out with rpfq_wide_pack_adjoint per call) and the bias gradient as
+  the column sum (the reference operator's backward, kernel.py:585-588).
 * ``torch.ops.rpfq.act_quant(x, num_bits)``: ActivationQuantSTE's forward
   (quant_i.py:438-455) on [..., 2K'] features.
 
@@ -109,6 +112,31 @@ def wide_linear(x: torch.Tensor, packed: torch.Tensor, n_complex: int, k_complex
 @wide_linear.register_fake
 def _(x, packed, n_complex, k_complex, codebook, stages, block, rotation, bias):
     return x.new_empty(tuple(x.shape[:-1]) + (2 * n_complex,))
+
+
+def _wide_setup(ctx, inputs, output):
+    x, packed, n_complex, k_complex, codebook, stages, block, rotation, bias = inputs
+    ctx.layer = (n_complex, k_complex, codebook, stages, block, rotation)
+    ctx.x_dtype = x.dtype
+    ctx.bias_dtype = None if bias is None else bias.dtype
+    ctx.save_for_backward(packed)
+
+
+def _wide_backward(ctx, grad):
+    from . import ops
+
+    (packed,) = ctx.saved_tensors
+    n_complex, k_complex, codebook, stages, block, rotation = ctx.layer
+    rot = None if rotation is None else ((rotation[0], rotation[1]), (rotation[2], rotation[3]))
+    pw = ops.PackedWide(n_complex, k_complex, codebook, stages, block, packed, rot)
+    grad_x = pw.grad_x(grad, out_dtype=ctx.x_dtype) if ctx.needs_input_grad[0] else None
+    grad_b = None
+    if ctx.bias_dtype is not None and ctx.needs_input_grad[8]:
+        grad_b = grad.reshape(-1, grad.shape[-1]).float().sum(0).to(ctx.bias_dtype)
+    return grad_x, None, None, None, None, None, None, None, grad_b
+
+
+wide_linear.register_autograd(_wide_backward, setup_context=_wide_setup)
 
 
 @torch.library.custom_op("rpfq::act_quant", mutates_args=())

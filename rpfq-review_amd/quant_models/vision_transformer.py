@@ -35,7 +35,11 @@ FUSE_LN = os.environ.get("RPFQ_FUSE_LN", "1") != "0"
 
 
 def _fused(module: nn.Module, x: torch.Tensor) -> bool:
-    return FUSED_BLOCKS and x.is_cuda and not module.training
+    """Whether the fused inference kernels run: eval-mode device tensors that
+    no gradient has to flow through (with autograd recording, the blocks run
+    module by module: torch's LayerNorm and GELU, the packed layers with
+    their input gradient on the device)."""
+    return FUSED_BLOCKS and x.is_cuda and not module.training and not (torch.is_grad_enabled() and x.requires_grad)
 
 
 def norm_fwd(norm: nn.Module, x: torch.Tensor) -> torch.Tensor:

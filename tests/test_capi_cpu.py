@@ -337,3 +337,35 @@ def test_wide_linear_kernel_choice():
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 0, None) == 1
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 0, 1, 1, 0, ctypes.byref(out)) == 2
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 16, ctypes.byref(out)) == 6
+
+
+def test_wide_grad_x_geometry_and_argument_errors():
+    """rpfq_wide_adjoint_bytes is one 1 KiB tile per (32-row tile, k-step);
+    rpfq_wide_pack_adjoint and rpfq_wide_linear_grad_x validate every
+    argument on the host before any GPU work."""
+    L, N = lib()
+    d = _desc(N, n=50, k=48)
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(d)) == 2 * 2 * 1024
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, n=1536, k=384))) == 48 * 12 * 1024
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, k=12))) == 0  # invalid -> 0
+    fc2 = _desc(N, n=384, k=1536)
+    nbytes = L.rpfq_wide_packed_bytes(ctypes.byref(fc2))
+    abytes = L.rpfq_wide_adjoint_bytes(ctypes.byref(fc2))
+    fake = 1 << 20  # an aligned non-NULL address; never dereferenced on these paths
+
+    def pack(packed=fake, nb=nbytes, adj=fake, ab=abytes):
+        return L.rpfq_wide_pack_adjoint(ctypes.byref(fc2), packed, nb, adj, ab, None)
+    assert pack(packed=None) == 1 and pack(adj=None) == 1
+    assert pack(nb=nbytes - 1) == 2 and pack(ab=abytes - 1) == 2
+    assert pack(adj=fake + 16) == 3
+
+    def grad(packed=fake, nb=nbytes, adj=fake, ab=abytes, gy=fake, gdt=1, m=197, gx=fake, xdt=1):
+        return L.rpfq_wide_linear_grad_x(ctypes.byref(fc2), packed, nb, adj, ab, gy, gdt, m, gx, xdt, None)
+    assert grad(packed=None) == 1 and grad(adj=None) == 1 and grad(gy=None) == 1 and grad(gx=None) == 1
+    assert grad(gdt=7) == 5 and grad(xdt=9) == 5
+    assert grad(m=0) == 2 and grad(m=(1 << 30) + 1) == 2
+    assert grad(nb=nbytes - 1) == 2 and grad(ab=abytes - 1) == 2
+    assert grad(packed=fake + 128) == 3 and grad(gy=fake + 8) == 3  # N' % 8 == 0: 16-byte rows
+    assert grad(gx=fake + 1) == 3
+    assert L.rpfq_wide_linear_grad_x(ctypes.byref(_desc(N, k=12)), fake, nbytes, fake, abytes, fake, 1, 4, fake, 1,
+                                     None) == 3

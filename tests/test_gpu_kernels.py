@@ -849,3 +849,110 @@ def test_act_quant_row_kernel_matches_oracle(k):
         ys = ops.act_quant(tdev(xs), bits).cpu().numpy()
         qr, qi = O.act_quant(xs[:, :k], xs[:, k:], bits)
         assert np.array_equal(ys, np.concatenate([qr, qi], axis=1))
+
+
+# ---------------------------------------------------------------------------
+# input gradient on the packed blob (rpfq_wide_linear_grad_x; the reference
+# operator's backward grad_x = grad_output @ w_quant, kernel.py:585)
+# ---------------------------------------------------------------------------
+def check_grad_x(gx, gyf, oplanes, codebook, rotation, gy_rel=0.0, out_ulp=0.0):
+    """gx from the HIP kernel vs the oracle's gy @ A16 on the forward's fp16
+    operand: float32 accumulation within 1e-5 of sum |gy| |A16|, plus gy_rel
+    of it for the fp16 rounding of a float32 grad_y (2^-11) and out_ulp of
+    |gx| for the rounding of a 16-bit output."""
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    ref = O.wide_linear_grad_x(gyf, oplanes, codebook, rotation, fp16_weight=True)
+    scale = np.abs(gyf) @ np.abs(a16)
+    err = np.abs(gx.astype(np.float64) - ref)
+    assert np.all(err <= (1e-5 + gy_rel) * scale + out_ulp * np.abs(ref) + 1e-35), \
+        float((err / np.maximum(scale, 1e-300)).max())
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[8]],
+                         ids=["96x64", "50x48", "130x512-b256", "table"])
+def test_wide_pack_adjoint_layout(case):
+    """The adjoint tiles hold code byte (row n, column k) in tile
+    (k // 32, n // 32), column k % 32, byte 16 g + 4 s + e where
+    n % 32 = 8 s + 4 g + e -- the forward tiles' byte order with rows and
+    columns exchanged -- bit for bit."""
+    r = rng(400)
+    pw, *_ = build_packed(r, case)
+    nt, ks = -(-case[0] // 32), -(-case[1] // 32)
+    codes = pw.blob[: nt * ks * 1024].cpu().numpy().reshape(nt, ks, 32, 32)
+    b = np.arange(32)
+    perm = 8 * ((b >> 2) & 3) + 4 * (b >> 4) + (b & 3)  # index held by byte b of a tile row
+    full = np.zeros((nt * 32, ks * 32), np.uint8)
+    for t in range(nt):
+        for s in range(ks):
+            full[t * 32:(t + 1) * 32, s * 32 + perm] = codes[t, s]
+    adj = pw.adjoint().cpu().numpy().reshape(ks, nt, 32, 32)
+    want = np.zeros_like(adj)
+    for s in range(ks):
+        for t in range(nt):
+            want[s, t][:, b] = full[t * 32 + perm, s * 32:(s + 1) * 32].T
+    assert np.array_equal(adj, want)
+
+
+@pytest.mark.parametrize("m", [1, 64, 65, 300])
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}{c[3]}-b{c[4]}-r{int(c[5] is not None)}"
+                                             for c in CASES])
+def test_wide_linear_grad_x(case, m):
+    """fp16 grad_y (exact operands) into float32 grad_x, every codebook,
+    N' / K' tails, per-block scales, rotation, 64- and 128-row tiles."""
+    r = rng(500 + m)
+    pw, oplanes, _, codebook, rotation = build_packed(r, case)
+    gy = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32)).to(torch.float16)
+    gx = pw.grad_x(gy.to(DEV), out_dtype=torch.float32).cpu().numpy()
+    assert gx.shape == (m, 2 * case[1])
+    check_grad_x(gx, gy.float().numpy().astype(np.float64), oplanes, codebook, rotation)
+
+
+GRAD_DT = [(torch.float16, torch.float16), (torch.float16, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+           (torch.bfloat16, torch.float32), (torch.float32, torch.float32), (torch.float32, torch.float16)]
+_ULP = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 0.0}
+
+
+@pytest.mark.parametrize("gdt,xdt", GRAD_DT, ids=[f"{str(a)[6:]}-{str(b)[6:]}" for a, b in GRAD_DT])
+@pytest.mark.parametrize("case", [(160, 128, "axis", 2, 0, None), (100, 96, "sign", 2, 0, None)],
+                         ids=["160x128", "100x96"])
+@pytest.mark.parametrize("m", [77, 300])
+def test_wide_linear_grad_x_dtypes(gdt, xdt, case, m):
+    """grad_y fp16 / bf16 / float32 (bf16 values are exact fp16 operands
+    after the per-row power-of-two scaling; float32 ones round once, 2^-11),
+    16-bit outputs within their rounding; N' % 8 != 0 takes element loads."""
+    r = rng(600 + m)
+    pw, oplanes, _, codebook, rotation = build_packed(r, case)
+    gy = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32)).to(gdt)
+    gx = pw.grad_x(gy.to(DEV), out_dtype=xdt).float().cpu().numpy()
+    check_grad_x(gx, gy.float().numpy().astype(np.float64), oplanes, codebook, rotation,
+                 gy_rel=2.0 ** -11 if gdt == torch.float32 else 0.0, out_ulp=_ULP[xdt])
+
+
+@pytest.mark.parametrize("gdt", [torch.float32, torch.bfloat16])
+def test_wide_linear_grad_x_row_scaling(gdt):
+    """Rows far outside fp16's range (1e-9 flushes to zero in fp16, 1e30
+    overflows) and a zero row keep each row's relative accuracy: the per-row
+    power of two is applied before the fp16 rounding and undone exactly."""
+    r = rng(700)
+    case = (160, 128, "axis", 2, 0, None)
+    pw, oplanes, _, codebook, rotation = build_packed(r, case)
+    row_scale = np.array([1.0, 1e-9, 1e30, 1e-30, 0.0, 3e4, 7e-5])[:, None]
+    gy = torch.from_numpy((r.standard_normal((7, 320)) * row_scale).astype(np.float32)).to(gdt)
+    gx = pw.grad_x(gy.to(DEV), out_dtype=torch.float32).cpu().numpy()
+    assert np.all(gx[4] == 0.0)
+    check_grad_x(gx, gy.float().numpy().astype(np.float64), oplanes, codebook, rotation,
+                 gy_rel=2.0 ** -11 if gdt == torch.float32 else 0.0)
+
+
+@pytest.mark.parametrize("n_c,k_c", [(1152, 384), (384, 384), (1536, 384), (384, 1536), (512, 2048)],
+                         ids=["qkv", "proj", "fc1", "fc2", "L-fc2"])
+def test_wide_linear_grad_x_model_shapes(n_c, k_c):
+    """The ViT-B/16 layer shapes (and ViT-L fc2) at M = 2000 and 128, fp16
+    grad_y into fp16 grad_x, every row against the oracle."""
+    r = rng(800)
+    pw, oplanes, _, codebook, rotation = build_packed(r, (n_c, k_c, "axis", 2, 0, None))
+    for m in (2000, 128):
+        gy = torch.from_numpy(r.standard_normal((m, 2 * n_c)).astype(np.float32)).to(torch.float16)
+        gx = pw.grad_x(gy.to(DEV), out_dtype=torch.float16).float().cpu().numpy()
+        check_grad_x(gx, gy.float().numpy().astype(np.float64), oplanes, codebook, rotation,
+                     out_ulp=2.0 ** -11)

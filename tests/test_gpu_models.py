@@ -106,6 +106,79 @@ def test_packed_layer_vs_reference_outputs(golden, method, act, rot):
         assert np.array_equal(dec, golden[f"fwd_aq_{tag}"])
 
 
+@pytest.mark.parametrize("method", ["complex_phase_v1", "complex_phase_v2", "complex_phase_v4",
+                                    "complex_phase_new_v2", "complex_phase_next_v1"])
+@pytest.mark.parametrize("act", [0, 1])
+def test_packed_layer_input_gradient(golden, method, act):
+    """Eval-mode packed layer under autograd, the reference operator's
+    backward (kernel.py:585-588, straight through the act quant,
+    quant_i.py:452-455): x.grad = grad_y A within the fp16 operand bound of
+    the reference's A_q -- grad_y (float32) rounded to fp16 (u = 2^-11) and
+    the fused fp16 coefficients, |A16 - A_q| <= (2u + u^2)(|W| + |U|) --
+    bit-identical to PackedWide.grad_x, and bias.grad = the column sum of
+    grad_y."""
+    layer = _layer(method, act, 0, golden).to(DEV).eval()
+    x = torch.from_numpy(golden["fwd_x"]).to(DEV).requires_grad_(True)
+    y = layer(x)
+    assert y.grad_fn is not None
+    gy = torch.from_numpy(np.random.default_rng(7).standard_normal(tuple(y.shape)).astype(np.float32)).to(DEV)
+    y.backward(gy)
+    a_ref = golden[f"fwd_aq_{method}_a{act}_r0"].astype(np.float64)
+    gyf = gy.cpu().numpy().astype(np.float64)
+    steps = {"complex_phase_v3": 3, "complex_phase_v4": 4}.get(method, 0)
+    if steps:
+        mag = _group_magnitude(golden, steps, 0)
+    else:
+        u_re, u_im, w_re, w_im = (np.abs(v) for v in O.decompose(a_ref))
+        mag = np.block([[w_re + u_re, w_im + u_im], [w_im + u_im, w_re + u_re]])
+    u = 2.0 ** -11
+    ag = np.abs(gyf)
+    bound = u * (ag @ np.abs(a_ref)) + 1.001 * (2 * u + u * u) * (ag @ mag) + 1e-5
+    gx = x.grad.cpu().numpy()
+    assert np.all(np.abs(gx - gyf @ a_ref) <= bound), np.abs(gx - gyf @ a_ref).max()
+    assert torch.equal(x.grad, layer.packed(torch.device(DEV)).grad_x(gy, torch.float32))
+    assert torch.allclose(layer.bias.grad, gy.sum(0), rtol=1e-6, atol=1e-5)
+
+
+def test_model_input_gradient():
+    """Input gradient through a whole eval-mode model on the device (the
+    packed layers' grad_x, torch's LayerNorm, attention and GELU under
+    autograd) against the float32 CPU reference model's autograd on the
+    oracle-decoded weights: relative L2 error <= 1e-2, cosine >= 0.9999;
+    every packed layer's input gradient ran on the device kernel."""
+    from quant_models import ops
+    from quant_models.inference import prepare_inference, quant_layers
+
+    name = "rpfq_deit_tiny_patch16_224_q"
+    model, ref_state = _synthetic_model(name, 5)
+    prepare_inference(model, DEV, torch.float32)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, 3, 224, 224, generator=g)
+    calls = []
+    orig = ops.PackedWide.grad_x
+
+    def counted(self, grad_y, out_dtype=None):
+        calls.append(grad_y.shape)
+        return orig(self, grad_y, out_dtype)
+    ops.PackedWide.grad_x = counted
+    try:
+        xg = x.to(DEV).requires_grad_(True)
+        y = model(xg)
+        gy = torch.randn(y.shape, generator=g)
+        y.backward(gy.to(DEV))
+    finally:
+        ops.PackedWide.grad_x = orig
+    assert len(calls) == len(list(quant_layers(model)))
+    ref = _reference_model_cpu(model, name, ref_state)
+    xc = x.clone().requires_grad_(True)
+    ref(xc).backward(gy)
+    gd, gr = xg.grad.cpu().double(), xc.grad.double()
+    rel = float((gd - gr).norm() / gr.norm())
+    cos = float((gd * gr).sum() / (gd.norm() * gr.norm()))
+    print(f"model input gradient: rel L2 {rel:.2e}, cosine {cos:.6f}")
+    assert rel <= 1e-2 and cos >= 0.9999
+
+
 def test_packed_path_refuses_unsupported_method(golden):
     from quant_models.quant_i import QATLinearComplexPhase
 
@@ -152,6 +225,14 @@ def _reference_forward_cpu(model_gpu, name, x_cpu, state, act_quant=False, **kw)
     """float32 CPU copy of the model whose quantized layers run
     x @ A_q.T + b on the oracle's decoding of exactly the codes the GPU model
     uses, with the oracle's activation quantization first when act_quant."""
+    ref = _reference_model_cpu(model_gpu, name, state, act_quant, **kw)
+    with torch.no_grad():
+        return ref(x_cpu)
+
+
+def _reference_model_cpu(model_gpu, name, state, act_quant=False, **kw):
+    """The float32 CPU reference model of _reference_forward_cpu (its
+    quantized layers are torch ops, so autograd runs through them)."""
     import quant_models as qm
     from quant_models.inference import quant_layers
 
@@ -168,8 +249,7 @@ def _reference_forward_cpu(model_gpu, name, x_cpu, state, act_quant=False, **kw)
             l_c.forward = (lambda xx, a_q=a_q, bias=bias, bits=bits: F.linear(_oracle_act_quant(xx, bits), a_q, bias))
         else:
             l_c.forward = (lambda xx, a_q=a_q, bias=bias: F.linear(xx, a_q, bias))
-    with torch.no_grad():
-        return ref(x_cpu)
+    return ref
 
 
 def _synthetic_model(name, seed, codebook=None, act_quant=False, **kw):

@@ -405,3 +405,29 @@ def test_recompose_split_fp16(codebook, rot):
     only_u = O.recompose_split_fp16(u_re, u_im, z, z)
     assert np.array_equal(only_u[:n, :k], u_re.astype(np.float16).astype(np.float64))
     assert np.array_equal(only_u[:n, k:], -u_im.astype(np.float16).astype(np.float64))
+
+
+@pytest.mark.parametrize("codebook,rot", [("axis", None), ("psk16", None),
+                                          ("axis", ((0.95533645, 0.29552022), (0.98006660, -0.19866933)))])
+@pytest.mark.parametrize("fp16", [False, True])
+def test_wide_linear_grad_x_adjoint_and_autograd(codebook, rot, fp16):
+    """wide_linear_grad_x is the adjoint of the pinned forward,
+    <gy, wide_linear(x)> = <wide_linear_grad_x(gy), x>, and equals torch
+    autograd of F.linear on the same A (N' != K', so a transposed operand
+    cannot pass)."""
+    import torch
+    rotation = None if rot is None else tuple((F32(c), F32(s)) for c, s in rot)
+    planes = _wide_case(14, n=24, k=40, codebook=codebook)
+    rng = np.random.default_rng(15)
+    x = rng.standard_normal((5, 80))
+    gy = rng.standard_normal((5, 48))
+    y = O.wide_linear(x, planes, None, codebook, rotation, fp16_weight=fp16)
+    gx = O.wide_linear_grad_x(gy, planes, codebook, rotation, fp16_weight=fp16)
+    assert gx.shape == x.shape
+    lhs, rhs = float(np.sum(gy * y)), float(np.sum(gx * x))
+    assert abs(lhs - rhs) <= 1e-12 * (np.abs(gy) @ np.abs(O.wide_weight(planes, codebook, rotation, fp16=fp16))
+                                      .astype(np.float64) @ np.abs(x).T).sum()
+    a = torch.from_numpy(O.wide_weight(planes, codebook, rotation, fp16=fp16).astype(np.float64))
+    xt = torch.from_numpy(x).requires_grad_(True)
+    torch.nn.functional.linear(xt, a).backward(torch.from_numpy(gy))
+    assert np.allclose(xt.grad.numpy(), gx, rtol=1e-12, atol=1e-12)

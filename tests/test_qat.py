@@ -291,3 +291,26 @@ def test_rpfq_wide_linear_op_matches_packed(golden):
                                       None, bias)
     assert torch.equal(y_op, pw.linear(x, bias))
     assert torch.equal(torch.ops.rpfq.act_quant(x.float(), 4), ops.act_quant(x.float(), 4))
+
+
+@pytest.mark.gpu
+def test_rpfq_wide_linear_op_backward(golden):
+    """The registered backward of torch.ops.rpfq.wide_linear: the input
+    gradient is PackedWide.grad_x on the same blob (bit for bit) and the
+    bias gradient the column sum of grad_y (kernel.py:585-588)."""
+    import quant_models  # noqa: F401
+    from quant_models import ops
+    from quant_models import packing as P
+
+    lc = P.quantize_layer(torch.from_numpy(golden["w_weight"]), "complex_phase_v2", "complex_phase_v2")
+    pw = ops.pack_layer([p.to(DEV) for p in lc.planes], [s.to(DEV) for s in lc.scale_re],
+                        [s.to(DEV) for s in lc.scale_im], lc.n_complex, lc.k_complex, lc.codebook, lc.stages)
+    x = torch.randn(3, 9, 96, device=DEV).half().requires_grad_(True)
+    bias = torch.randn(64, device=DEV).requires_grad_(True)
+    y = torch.ops.rpfq.wide_linear(x, pw.blob, pw.n_complex, pw.k_complex, pw.codebook, pw.stages, pw.block,
+                                   None, bias)
+    gy = torch.randn(y.shape, device=DEV).half()
+    y.backward(gy)
+    assert x.grad.dtype == torch.float16 and bias.grad.dtype == torch.float32
+    assert torch.equal(x.grad, pw.grad_x(gy, torch.float16))
+    assert torch.allclose(bias.grad, gy.float().reshape(-1, 64).sum(0), rtol=1e-6, atol=1e-5)
