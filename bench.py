@@ -497,7 +497,9 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
     rotation at the family default, SGD): forward with every Linear
     quantized from its float32 master weight, backward with straight-through
     gradients, optimizer step.  'hip' runs the weight quantizer and the act
-    quant as HIP kernels (rpfq_quantize_wide, rpfq_act_quant); 'torch' runs
+    quant as HIP kernels (rpfq_quantize_wide, rpfq_act_quant); 'hip_pgrad'
+    also takes each layer's input gradient on the packed blob of the step's
+    codes (rpfq_wide_linear_grad_x, RPFQ_QAT_PACKED_GRAD=1); 'torch' runs
     the reference formulation in torch ops on the GPU.  Also times the weight
     quantization of all layers alone (no grad).  Prints one JSON line."""
     import torch
@@ -509,7 +511,8 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
     name, _, img, _, seed, desc = CONFIGS[cfg_name]
     out = {}
     for mode in modes:
-        quant_i.HIP_QAT = mode == "hip"
+        quant_i.HIP_QAT = mode in ("hip", "hip_pgrad")
+        quant_i.QAT_PACKED_GRAD = "1" if mode == "hip_pgrad" else "0"
         torch.manual_seed(seed)
         model = qm.create_model(name, img_size=img, quant_method_u="complex_phase_v2",
                                 quant_method_w="complex_phase_v2", enable_act_quant=act_quant).cuda().train()
@@ -538,7 +541,7 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
         with torch.no_grad():
             for _ in range(2):
                 for layer in layers:
-                    if mode == "hip":
+                    if mode != "torch":
                         quant_i._HipWideQuantSTE.apply(layer.weight, layer.quantizer_u.rotation_angle,
                                                        layer.quantizer_w.rotation_angle, layer._hip_qat_spec(probe))
                     else:
@@ -546,7 +549,7 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
             torch.cuda.synchronize()
             tq = time.perf_counter()
             for layer in layers:
-                if mode == "hip":
+                if mode != "torch":
                     quant_i._HipWideQuantSTE.apply(layer.weight, layer.quantizer_u.rotation_angle,
                                                    layer.quantizer_w.rotation_angle, layer._hip_qat_spec(probe))
                 else:
@@ -559,6 +562,7 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
         del model, opt
         torch.cuda.empty_cache()
     quant_i.HIP_QAT = True
+    quant_i.QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "auto")
     first = out[modes[0]]
     print(json.dumps({"metric": f"QAT training images/s {desc}, float32, SGD", "value": first["images_per_s"],
                       "unit": "images/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -606,7 +610,7 @@ def main() -> int:
                     help="time the packed input gradient (rpfq_wide_linear_grad_x) on the ViT-B layer shapes")
     ap.add_argument("--train", action="store_true",
                     help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
-    ap.add_argument("--train-modes", default="hip,torch")
+    ap.add_argument("--train-modes", default="hip,hip_pgrad,torch")
     args = ap.parse_args()
     if args.layer_probe:
         return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)

@@ -173,10 +173,12 @@ class PackedWide:
 
     @classmethod
     def from_planes(cls, planes, scale_re, scale_im, n_complex: int, k_complex: int, codebook: int = N.CB_AXIS,
-                    stages: int = 2, block: int = 0, rotation=None) -> "PackedWide":
+                    stages: int = 2, block: int = 0, rotation=None, sync: bool = True) -> "PackedWide":
         """planes: packed code planes (u_s0[, u_s1], w_s0[, w_s1] or u, w for
         PSK16) as uint8 device tensors; scale_re/scale_im: float32 [N', nblk]
-        multipliers per plane."""
+        multipliers per plane.  sync=False skips the final stream
+        synchronization: for sources produced and released on the current
+        stream (the caching allocator reuses their memory in stream order)."""
         dev = planes[0].device
         N.require_device(*planes)
         desc = make_desc(n_complex, k_complex, codebook, stages, block, rotation)
@@ -194,7 +196,8 @@ class PackedWide:
             arr(*[s.data_ptr() for s in sre]), arr(*[s.data_ptr() for s in sim]),
             blob.data_ptr(), nbytes, N.stream_of(blob)))
         # keep the sources alive until the pack kernels have consumed them
-        torch.cuda.current_stream(dev).synchronize()
+        if sync:
+            torch.cuda.current_stream(dev).synchronize()
         return cls(n_complex, k_complex, codebook, stages, block, blob, rotation)
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
@@ -444,13 +447,13 @@ class PackedStages:
 
 
 def pack_layer(planes, scale_re, scale_im, n_complex: int, k_complex: int, codebook: int = N.CB_AXIS,
-               stages: int = 2, block: int = 0, rotation=None):
+               stages: int = 2, block: int = 0, rotation=None, sync: bool = True):
     """PackedWide for stages <= 2, else PackedStages over groups of two
     stages.  planes / scales ordered u_s0..u_s{S-1}, w_s0..w_s{S-1} (AXIS,
     SIGN) as PackedWide.from_planes takes them."""
     if stages <= 2 or codebook in (N.CB_PSK16, N.CB_TABLE):
         return PackedWide.from_planes(planes, scale_re, scale_im, n_complex, k_complex, codebook, stages, block,
-                                      rotation)
+                                      rotation, sync)
     if len(planes) != 2 * stages:
         raise ValueError(f"expected {2 * stages} planes, got {len(planes)}")
     groups = []
@@ -459,7 +462,7 @@ def pack_layer(planes, scale_re, scale_im, n_complex: int, k_complex: int, codeb
         idx = list(range(lo, hi)) + list(range(stages + lo, stages + hi))
         groups.append(PackedWide.from_planes([planes[i] for i in idx], [scale_re[i] for i in idx],
                                              [scale_im[i] for i in idx], n_complex, k_complex, codebook,
-                                             hi - lo, block, rotation))
+                                             hi - lo, block, rotation, sync))
     return PackedStages(groups)
 
 

@@ -261,15 +261,22 @@ def quantize_layer_device(weight: torch.Tensor, method_u: str, method_w: str, ro
         rotation = ((vals[0], vals[1]), (vals[2], vals[3]))
     _, scales, codes = ops.quantize_wide(weight.detach().float(), kind_u, steps_u, kind_w, steps_w, rot=rot,
                                          want_aq=False, want_codes=True)
-    n_c, k_c = weight.shape[0] // 2, weight.shape[1] // 2
+    return quantizer_codes(scales, codes, weight.shape[0] // 2, weight.shape[1] // 2, kind_u, steps_u, rotation)
+
+
+def quantizer_codes(scales: torch.Tensor, codes: torch.Tensor, n_c: int, k_c: int, kind: str, steps: int,
+                    rotation=None) -> LayerCodes:
+    """LayerCodes of rpfq_quantize_wide's outputs (scales [2, 4, 2] per
+    U/W, stage, re/im; code planes [2 steps, N', K'/4]), device tensors
+    kept on the device: per-tensor scales become per-row columns."""
     planes, sre, sim = [], [], []
-    for p, steps in ((0, steps_u), (1, steps_w)):
+    for p in range(2):
         for t in range(steps):
-            planes.append(codes[p * steps_u + t])
+            planes.append(codes[p * steps + t])
             sre.append(scales[p, t, 0].reshape(1, 1).expand(n_c, 1).contiguous())
             sim.append(scales[p, t, 1].reshape(1, 1).expand(n_c, 1).contiguous())
-    cb = N.CB_AXIS if kind_u == "axis" else N.CB_SIGN
-    return LayerCodes(planes, sre, sim, n_c, k_c, cb, steps_u, 0, rotation)
+    cb = N.CB_AXIS if kind == "axis" else N.CB_SIGN
+    return LayerCodes(planes, sre, sim, n_c, k_c, cb, steps, 0, rotation)
 
 
 def synthetic_layer(weight: torch.Tensor, generator: torch.Generator, lo: float = 0.01, hi: float = 0.1,

@@ -303,6 +303,15 @@ HIP_QAT = os.environ.get("RPFQ_HIP_QAT", "1") != "0"
 # ~1 ulp from the host's torch CPU order; no host round trip of the weight)
 DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
 
+# Input gradient of the HIP training forward on the packed blob of the
+# step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
+# A_q: "auto" for 16-bit activations (the reference's AMP precision class:
+# fp16 operands either way), "1" also for float32 (each grad_y element then
+# carries one fp16 rounding, 2^-11 relative, and the fused fp16
+# coefficients; ~3x faster than the float32 library GEMM on MI355X), "0"
+# never.
+QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "auto")
+
 _HIP_KINDS = {
     "complex_phase_v1": ("axis", 1),
     "complex_phase_v2": ("axis", 2),
@@ -362,6 +371,50 @@ class _HipWideQuantSTE(torch.autograd.Function):
         weight, a_q = ctx.saved_tensors
         th_u, th_w = rotation_grad(grad.float(), weight.detach(), a_q)
         return grad, th_u.reshape(1), th_w.reshape(1), None
+
+
+class _GivenWeightSTE(torch.autograd.Function):
+    """_HipWideQuantSTE with the quantization already done: forward returns
+    the given A_q; backward as _HipWideQuantSTE (the weight gets the A_q
+    gradient, the rotation angles rotation_grad)."""
+
+    @staticmethod
+    def forward(ctx, weight, theta_u, theta_w, a_q):
+        ctx.rotated = theta_u is not None
+        if ctx.rotated:
+            ctx.save_for_backward(weight, a_q)
+        return a_q
+
+    @staticmethod
+    def backward(ctx, grad):
+        if not ctx.rotated:
+            return grad, None, None, None
+        weight, a_q = ctx.saved_tensors
+        th_u, th_w = rotation_grad(grad.float(), weight.detach(), a_q)
+        return grad, th_u.reshape(1), th_w.reshape(1), None
+
+
+class _LinearPackedGradX(torch.autograd.Function):
+    """F.linear(x, a_q, bias) whose input gradient runs on the packed blob
+    of the same codes (grad_y A16, rpfq_wide_linear_grad_x) while the weight
+    and bias gradients stay the library GEMM and column sum (kernel.py:
+    581-588)."""
+
+    @staticmethod
+    def forward(ctx, x, a_q, bias, pw):
+        ctx.pw = pw
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(x)
+        return F.linear(x, a_q, bias)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (x,) = ctx.saved_tensors
+        g2 = grad.reshape(-1, grad.shape[-1])
+        gx = ctx.pw.grad_x(grad, out_dtype=x.dtype) if ctx.needs_input_grad[0] else None
+        gw = (g2.t() @ x.reshape(-1, x.shape[-1]).to(g2.dtype)) if ctx.needs_input_grad[1] else None
+        gb = g2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return gx, gw, gb, None
 
 
 class _HipActQuantSTE(torch.autograd.Function):
@@ -449,8 +502,41 @@ class QATLinearComplexPhase(nn.Linear):
             return None
         return ku + kw
 
+    def _packed_grad(self, x: torch.Tensor) -> bool:
+        if QAT_PACKED_GRAD == "0" or not torch.is_grad_enabled():
+            return False
+        return QAT_PACKED_GRAD == "1" or x.dtype in (torch.float16, torch.bfloat16) or torch.is_autocast_enabled()
+
+    def _qat_forward_packed_grad(self, x: torch.Tensor, spec) -> torch.Tensor:
+        """The HIP training forward with the input gradient on the packed
+        blob of this step's codes (QAT_PACKED_GRAD)."""
+        from . import ops
+
+        qu, qw = self.quantizer_u, self.quantizer_w
+        rot, rotation = None, None
+        if qu.rotation_angle is not None:
+            th = torch.cat((qu.rotation_angle.detach().float().reshape(1), qw.rotation_angle.detach().float().reshape(1)))
+            rot = torch.stack((torch.cos(th[0]), torch.sin(th[0]), torch.cos(th[1]), torch.sin(th[1])))
+            v = rot.tolist()
+            rotation = ((v[0], v[1]), (v[2], v[3]))
+        a_q, scales, codes = ops.quantize_wide(self.weight.detach(), *spec, rot=rot, want_codes=True)
+        q_weight = _GivenWeightSTE.apply(self.weight, qu.rotation_angle, qw.rotation_angle, a_q)
+        lc = P.quantizer_codes(scales, codes, self.out_features // 2, self.in_features // 2, spec[0], spec[1],
+                               rotation)
+        pw = ops.pack_layer(lc.planes, lc.scale_re, lc.scale_im, lc.n_complex, lc.k_complex, lc.codebook, lc.stages,
+                            0, rotation, sync=False)
+        if self.act_quantizer is not None:
+            if x.dtype == torch.float32:
+                x = _HipActQuantSTE.apply(x, self.act_quantizer.num_bits)
+            else:
+                h = self.in_features // 2
+                x = torch.cat(self.act_quantizer(x[..., :h], x[..., h:]), dim=-1)
+        return _LinearPackedGradX.apply(x, q_weight, self.bias, pw)
+
     def _qat_forward(self, x: torch.Tensor) -> torch.Tensor:
         spec = self._hip_qat_spec(x)
+        if spec is not None and spec[0] == spec[2] and spec[1] == spec[3] and self._packed_grad(x):
+            return self._qat_forward_packed_grad(x, spec)
         if spec is not None:
             q_weight = _HipWideQuantSTE.apply(self.weight, self.quantizer_u.rotation_angle,
                                               self.quantizer_w.rotation_angle, spec)

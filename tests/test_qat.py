@@ -233,6 +233,64 @@ def test_hip_training_step_matches_torch_formulation(method, act, rot):
             assert torch.allclose(a, b, rtol=1e-3, atol=1e-4 * float(b.abs().max()))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("method,act,rot", [("complex_phase_v2", 1, 1), ("complex_phase_new_v2", 0, 0),
+                                            ("complex_phase_v4", 1, 0)])
+def test_hip_training_packed_grad_x(method, act, rot):
+    """The training forward with the input gradient on the packed blob of
+    the step's own codes (RPFQ_QAT_PACKED_GRAD): the output, weight, bias and
+    rotation gradients equal the library path's (the same F.linear, STE and
+    weight GEMM); x.grad is within the fp16 operand bound of grad_y A_q --
+    grad_y rounded once to fp16 (u = 2^-11) and the fused fp16 coefficients,
+    (2u + u^2)(|W| + |U|) -- of the library path's."""
+    from quant_models import quant_i
+    from quant_models.quant_i import QATLinearComplexPhase
+
+    torch.manual_seed(5)
+    layer = QATLinearComplexPhase(quant_method_u=method, quant_method_w=method, enable_act_quant=bool(act),
+                                  act_num_bits=4, enable_rotation=bool(rot), in_features=192, out_features=128)
+    with torch.no_grad():
+        layer.bias.normal_(0.0, 0.1)
+        if rot:
+            layer.quantizer_u.rotation_angle.fill_(0.25)
+            layer.quantizer_w.rotation_angle.fill_(-0.6)
+    layer = layer.to(DEV).train()
+    x = torch.randn(3, 37, 192, device=DEV)
+    gy = torch.randn(3, 37, 128, device=DEV)
+    res = {}
+    saved = quant_i.QAT_PACKED_GRAD
+    try:
+        for mode in ("0", "1"):
+            quant_i.QAT_PACKED_GRAD = mode
+            layer.zero_grad(set_to_none=True)
+            xg = x.clone().requires_grad_(True)
+            y = layer(xg)
+            y.backward(gy)
+            grads = [xg.grad, layer.weight.grad, layer.bias.grad]
+            if rot:
+                grads += [layer.quantizer_u.rotation_angle.grad, layer.quantizer_w.rotation_angle.grad]
+            res[mode] = (y.detach(), [g.detach().clone() for g in grads])
+    finally:
+        quant_i.QAT_PACKED_GRAD = saved
+    (y0, g0), (y1, g1) = res["0"], res["1"]
+    assert torch.equal(y0, y1)
+    for a, b in zip(g1[1:], g0[1:]):
+        assert torch.allclose(a, b, rtol=1e-5, atol=1e-6 * float(b.abs().max()))
+    with torch.no_grad():
+        a_q = layer.cpu().quantized_weight().double().numpy()
+    u_re, u_im, w_re, w_im = (np.abs(v) for v in O.decompose(a_q))
+    mag = np.block([[w_re + u_re, w_im + u_im], [w_im + u_im, w_re + u_re]])
+    u = 2.0 ** -11
+    ag = np.abs(gy.cpu().double().numpy().reshape(-1, 128))
+    # v4 runs as two stage groups, each fused on its own: their magnitudes
+    # add, up to twice the residual group's beyond |W| + |U| of the sum
+    fuse = 3.0 if method == "complex_phase_v4" else 1.001
+    bound = u * (ag @ np.abs(a_q)) + fuse * (2 * u + u * u) * (ag @ mag) + 1e-4
+    diff = (g1[0] - g0[0]).cpu().double().numpy().reshape(-1, 192)
+    assert np.all(np.abs(diff) <= bound), float(np.abs(diff).max())
+    assert not torch.equal(g1[0], g0[0])  # the packed path ran
+
+
 # ---------------------------------------------------------------------------
 # torch.ops.rpfq.* (the reference's operator contract, kernel.py:599-605)
 # ---------------------------------------------------------------------------
