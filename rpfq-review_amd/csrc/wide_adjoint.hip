@@ -15,16 +15,21 @@
 
 namespace rpfq {
 
-constexpr int kAdjLutRow = 40;                          // dwords per LUT row: 16 U + 16 W entries + pad
-constexpr int kAdjLutWave = 32 * kAdjLutRow;            // dwords of one 32-row LUT
-constexpr int kAdjLutStage = 4 * kAdjLutWave * 4;       // bytes per stage (room for one LUT per wave)
+constexpr int kAdjLutRow = 40;                // dwords per LUT row: 16 U + 16 W entries + pad
+constexpr int kAdjLutWave = 32 * kAdjLutRow;  // dwords of one 32-row LUT
 
+// LDS bytes per LUT stage: one table per workgroup (per-row scales) or one
+// per wave (per-block scales).
+__host__ __device__ constexpr int adj_lut_stage(bool per_wave) { return (per_wave ? 4 : 1) * kAdjLutWave * 4; }
+
+// LDS layout: per-row exponents [BM] int, then the gy stages and LUT stages,
+// which the epilogue's transpose tile reuses (4 waves x BM rows x kTRow).
 template <int BM>
-constexpr int adj_lds_bytes() {
-    return 2 * BM * kXRow + 2 * kAdjLutStage + BM * 4;  // gy stages, LUT stages, per-row exponents
+constexpr int adj_lds_bytes(bool per_wave) {
+    return BM * 4 + (2 * BM * kXRow + 2 * adj_lut_stage(per_wave) > 4 * BM * kTRow
+                         ? 2 * BM * kXRow + 2 * adj_lut_stage(per_wave)
+                         : 4 * BM * kTRow);
 }
-static_assert(4 * 128 * kTRow <= 2 * 128 * kXRow + 2 * kAdjLutStage, "epilogue tile fits below the exponents");
-static_assert(4 * 64 * kTRow <= 2 * 64 * kXRow + 2 * kAdjLutStage, "epilogue tile fits below the exponents");
 
 // gx [M, 2K'] = gy [M, 2N'] A with A the layer's fused fp16 coefficients
 // (the forward's MFMA operands):
@@ -66,8 +71,10 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     const int ktw_ld = active ? ktw : a.KS - 1;
     const int64_t ldg = 2 * (int64_t)a.N;
     const bool per_wave = a.nblk > 1;
-    char* const lut_base = smem + 2 * XSTAGE;
-    int* const row_exp = reinterpret_cast<int*>(smem + 2 * XSTAGE + 2 * kAdjLutStage);
+    int* const row_exp = reinterpret_cast<int*>(smem);
+    char* const base = smem + BM * 4;
+    char* const lut_base = base + 2 * XSTAGE;
+    const int lut_stage = adj_lut_stage(per_wave);
     const bool gvec = (a.N % 8) == 0;
 
     constexpr int RAW = (GDT == RPFQ_F32) ? 4 : 2;
@@ -136,7 +143,7 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
         }
     };
     auto store_g = [&](int stage, const uint4 (&xraw)[CPT][RAW], uint32_t xok) {
-        char* xs = smem + stage * XSTAGE;
+        char* xs = base + stage * XSTAGE;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int c = tid + 256 * j;
@@ -268,7 +275,7 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
         }
     };
     auto build = [&](int stage, const float4 p0, const float4 p1) {
-        uint32_t* lut = reinterpret_cast<uint32_t*>(lut_base + stage * kAdjLutStage) +
+        uint32_t* lut = reinterpret_cast<uint32_t*>(lut_base + stage * lut_stage) +
                         (per_wave ? wave * kAdjLutWave : 0) + lrow * kAdjLutRow;
         auto put = [&](int j, float2 u, float2 w) {
             if (a.rot.rotate) {
@@ -319,8 +326,8 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
             fill_codes = load_codes(np);
             load_params(np, fp0, fp1);
         }
-        const char* xs = smem + (ns & 1) * XSTAGE;
-        const uint32_t* lut = reinterpret_cast<const uint32_t*>(lut_base + (ns & 1) * kAdjLutStage) +
+        const char* xs = base + (ns & 1) * XSTAGE;
+        const uint32_t* lut = reinterpret_cast<const uint32_t*>(lut_base + (ns & 1) * lut_stage) +
                               (per_wave ? wave * kAdjLutWave : 0);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -390,8 +397,8 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     }
     // 16-bit outputs: transpose the wave's [BM x 64] tile through LDS (the
     // staging buffers are free after the final barrier; the per-row
-    // exponents lie past them) and write 16-byte chunks.
-    uint16_t* tt = reinterpret_cast<uint16_t*>(smem + wave * (BM * kTRow));
+    // exponents lie before them) and write 16-byte chunks.
+    uint16_t* tt = reinterpret_cast<uint16_t*>(base + wave * (BM * kTRow));
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
 #pragma unroll
@@ -437,10 +444,10 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
 template <int BM, int GDT, int XDT, int CB>
 static hipError_t grad_go(AdjArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
-    constexpr int lds = adj_lds_bytes<BM>();
-    const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_grad_x_kernel<BM, GDT, XDT, CB>), lds,
-                                           attr_done);
+    const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_grad_x_kernel<BM, GDT, XDT, CB>),
+                                           adj_lds_bytes<BM>(true), attr_done);
     if (e != hipSuccess) return e;
+    const int lds = adj_lds_bytes<BM>(a.nblk > 1);
     a.tiles_m = (int)((a.M + BM - 1) / BM);
     a.tiles_k = (a.KS + 3) / 4;
     hipLaunchKernelGGL((wide_grad_x_kernel<BM, GDT, XDT, CB>), dim3(a.tiles_m * a.tiles_k), dim3(256), lds, s, a);

@@ -6,8 +6,13 @@ Tensor? bias) -> Tensor`` (RPFQ-ViT-main/quant_models/kernel.py:599-605,
 CompositeExplicitAutograd).  The same ``(x, weight-or-packed, bias) -> y``
 contract is registered here, running the HIP kernels of librpfq.so:
 
-* ``torch.ops.rpfq.qat_linear(x, weight, bias, method_u, method_w, act_bits)``:
-  the reference layer's training forward (quant_i.py:513-554) with the weight
+* ``torch.ops.rpfq.qat_linear(x, weight, bias, method_u="complex_phase_v2",
+  method_w="complex_phase_v2", act_bits=8)``: called as ``(x, weight, bias)``
+  it takes the reference operator's configuration -- two residual axis
+  stages for U and W and 8-bit activations (kernel.py:416-445, :504-505) --
+  in quant_i.py's float32 arithmetic (the Triton operator splits U / W to
+  bf16 first).  It is the reference layer's training forward
+  (quant_i.py:513-554) with the weight
   quantized on the GPU (rpfq_quantize_wide) and float32 activations
   fake-quantized by the act-quant kernel, ``F.linear`` on the float32 A_q;
   backward straight-through (the weight receives the A_q gradient, the input
@@ -57,8 +62,9 @@ def _act(x: torch.Tensor, act_bits: int) -> torch.Tensor:
 
 
 @torch.library.custom_op("rpfq::qat_linear", mutates_args=())
-def qat_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], method_u: str,
-               method_w: str, act_bits: int) -> torch.Tensor:
+def qat_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+               method_u: str = "complex_phase_v2", method_w: str = "complex_phase_v2",
+               act_bits: int = 8) -> torch.Tensor:
     from . import ops
 
     N.require_device(x, weight, bias)
@@ -67,7 +73,7 @@ def qat_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tenso
 
 
 @qat_linear.register_fake
-def _(x, weight, bias, method_u, method_w, act_bits):
+def _(x, weight, bias, method_u="complex_phase_v2", method_w="complex_phase_v2", act_bits=8):
     return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))
 
 

@@ -301,6 +301,8 @@ def test_rpfq_ops_registered_with_fake_shapes():
     with FakeTensorMode():
         x, w, b = torch.empty(3, 5, 96), torch.empty(64, 96), torch.empty(64)
         assert torch.ops.rpfq.qat_linear(x, w, b, "complex_phase_v2", "complex_phase_v2", 4).shape == (3, 5, 64)
+        # the reference operator's own (x, weight, bias) call (kernel.py:599-605)
+        assert torch.ops.rpfq.qat_linear(x, w, b).shape == (3, 5, 64)
         blob = torch.empty(4096, dtype=torch.uint8)
         assert torch.ops.rpfq.wide_linear(x, blob, 32, 48, 0, 2, 0, None, b).shape == (3, 5, 64)
         assert torch.ops.rpfq.act_quant(x, 4).shape == (3, 5, 96)
