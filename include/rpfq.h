@@ -267,8 +267,35 @@ int rpfq_layer_norm_wide_linear(const rpfq_wide_desc* desc, const void* packed, 
                                 const void* x, int x_dtype, int64_t M, const float* gamma, const float* beta,
                                 float eps, const float* bias, void* y, int y_dtype, int flags, void* stream);
 
-/* *fusable = 1 if rpfq_layer_norm_wide_linear accepts this launch, else 0
- * (no GPU work; no counterpart in the reference). */
+/*
+ * y = layer(act_quant(x)) or, with layer_norm = 1, layer(act_quant(LayerNorm(x)))
+ * in one launch, with an optional residual added in the store: the
+ * activation fake quantization of rpfq_act_quant (per row and half, scale =
+ * qmax * (1 / max(max|v|, 1e-5)), v_q = clamp(rint(v scale), qmin, qmax) /
+ * scale, bits 2 .. 16), applied to x or to the float32 LayerNorm output as
+ * rpfq_layer_norm_act_quant applies it, rounded to x_dtype, runs in the
+ * streaming kernel's prologue, and the packed layer contracts the quantized
+ * rows from LDS.  The prepared rows are bit-identical to those of
+ * rpfq_act_quant / rpfq_layer_norm_act_quant (same lane order of the
+ * statistics), so y is bit-identical to that kernel followed by
+ * rpfq_wide_linear (or rpfq_wide_linear_residual) on the same launch.
+ * gamma, beta, eps: as rpfq_layer_norm_wide_linear (ignored when
+ * layer_norm = 0); residual: [M, 2N'] of y_dtype or NULL, 16-byte aligned,
+ * may equal y; flags: 0 or RPFQ_FLAG_GELU (not with a residual).  Only for
+ * launches that rpfq_layer_norm_wide_linear_fusable accepts; RPFQ_ERR_VALUE
+ * otherwise.
+ * Replaces the act quant of the layer's input and the contraction,
+ *   RPFQ-ViT-main/quant_models/quant_i.py:546-554 (ActivationQuantSTE then
+ *   F.linear), after norm1 / norm2 (audit_rpfq_vit_ios_parity.py:520, :549)
+ *   when layer_norm = 1; the Triton analogue kernel.py:449-521.
+ */
+int rpfq_act_quant_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                               int x_dtype, int64_t M, int bits, int layer_norm, const float* gamma, const float* beta,
+                               float eps, const float* bias, const void* residual, void* y, int y_dtype, int flags,
+                               void* stream);
+
+/* *fusable = 1 if rpfq_layer_norm_wide_linear (and rpfq_act_quant_wide_linear)
+ * accepts this launch, else 0 (no GPU work; no counterpart in the reference). */
 int rpfq_layer_norm_wide_linear_fusable(const rpfq_wide_desc* desc, int64_t M, int x_dtype, int y_dtype,
                                         int* fusable);
 

@@ -232,6 +232,38 @@ int rpfq_layer_norm_wide_linear(const rpfq_wide_desc* desc, const void* packed, 
                       "rpfq_layer_norm_wide_linear");
 }
 
+int rpfq_act_quant_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                               int x_dtype, int64_t M, int bits, int layer_norm, const float* gamma, const float* beta,
+                               float eps, const float* bias, const void* residual, void* y, int y_dtype, int flags,
+                               void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!packed || !x || !y) return fail(RPFQ_ERR_NULL, "packed/x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0 || M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld out of range", (long long)M);
+    if (bits < 2 || bits > 16) return fail(RPFQ_ERR_BITS, "bits=%d unsupported (2..16)", bits);
+    if (flags & ~RPFQ_FLAG_GELU) return fail(RPFQ_ERR_VALUE, "flags=%d: only RPFQ_FLAG_GELU is allowed", flags);
+    if ((flags & RPFQ_FLAG_GELU) && residual)
+        return fail(RPFQ_ERR_VALUE, "the GELU and the residual add cannot be fused together");
+    if (layer_norm && !(eps >= 0.0f)) return fail(RPFQ_ERR_VALUE, "eps must be >= 0");
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(gamma, 16) || !aligned(beta, 16) || !aligned(residual, 16))
+        return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x, gamma, beta and residual 16-byte aligned");
+    if (!rpfq::layer_norm_wide_fusable(g, x_dtype, M, y_dtype, desc->codebook))
+        return fail(RPFQ_ERR_VALUE,
+                    "M=%lld K'=%lld: the act-quant prologue needs a streaming split-K launch, per-row scales, "
+                    "K' %% 32 == 0, K' <= %d, fp16 / bf16 x and a non-table codebook "
+                    "(use rpfq_layer_norm_act_quant / rpfq_act_quant + rpfq_wide_linear)",
+                    (long long)M, (long long)desc->k_complex, rpfq::kLnMaxK);
+    return hip_status(rpfq::launch_act_quant_wide_linear(*desc, g, packed, x, x_dtype, M, bits, layer_norm ? 1 : 0,
+                                                         gamma, beta, eps, bias, residual, y, y_dtype, flags,
+                                                         reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_act_quant_wide_linear");
+}
+
 int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
                               int x_dtype, int64_t M, const float* bias, const void* residual, void* y,
                               int y_dtype, int flags, void* stream) {

@@ -94,6 +94,10 @@ struct WideArgs {
     float ln_eps;
     const float* ln_gamma;  // [2K'] or NULL (ones)
     const float* ln_beta;   // [2K'] or NULL (zeros)
+    // Activation fake quantization of x (after the LayerNorm when ln = 1) in
+    // the same prologue: bits 2 .. 16, 0 = none (rpfq_act_quant's arithmetic
+    // per row and half, rounded to x's dtype).
+    int aq_bits;
 };
 
 // ---------------------------------------------------------------------------
@@ -185,6 +189,12 @@ bool layer_norm_wide_fusable(const WideGeom& g, int xdt, int64_t M, int ydt, int
 hipError_t launch_layer_norm_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                                          const void* x, int xdt, int64_t M, const float* gamma, const float* beta,
                                          float eps, const float* bias, void* y, int ydt, int flags, hipStream_t s);
+// The same row prologue with the act quant (layer_norm = 0: act quant of x
+// alone) and an optional residual added in the store.
+hipError_t launch_act_quant_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
+                                        const void* x, int xdt, int64_t M, int bits, int layer_norm,
+                                        const float* gamma, const float* beta, float eps, const float* bias,
+                                        const void* res, void* y, int ydt, int flags, hipStream_t s);
 hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
                              const float* beta, float eps, int bits, void* y, int ydt, hipStream_t s);
 hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,

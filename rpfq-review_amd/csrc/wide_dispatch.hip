@@ -144,6 +144,24 @@ hipError_t launch_layer_norm_wide_linear(const rpfq_wide_desc& d, const WideGeom
     }
 }
 
+hipError_t launch_act_quant_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
+                                        const void* x, int xdt, int64_t M, int bits, int layer_norm,
+                                        const float* gamma, const float* beta, float eps, const float* bias,
+                                        const void* res, void* y, int ydt, int flags, hipStream_t s) {
+    WideArgs a = wide_shape(g, M, flags);
+    wide_operands(a, d, g, packed, x, bias, res, y);
+    a.ln = layer_norm ? 1 : 0;
+    a.ln_eps = eps;
+    a.ln_gamma = gamma;
+    a.ln_beta = beta;
+    a.aq_bits = bits;
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN: return launch_wide_stream<RPFQ_CB_SIGN>(a, xdt, ydt, s);
+        case RPFQ_CB_PSK16: return launch_wide_stream<RPFQ_CB_PSK16>(a, xdt, ydt, s);
+        default: return launch_wide_stream<RPFQ_CB_AXIS>(a, xdt, ydt, s);
+    }
+}
+
 hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                                      const void* adjoint, const void* gy, int gdt, int64_t M, void* gx, int xdt,
                                      hipStream_t s) {

@@ -159,13 +159,13 @@ __device__ __forceinline__ uint2 raw4_f16(uint2 v) {
 #ifndef RPFQ_SK_OCC
 #define RPFQ_SK_OCC 4  // waves per SIMD the register budget is sized for
 #endif
-// LN (NW = 4, per-row scales, K' % 32 == 0, K' <= kLnMaxK, fp16 / bf16
-// x, not TABLE): the workgroup first normalizes its 16 rows of x
-// (nn.LayerNorm over the 2K' features, float32, two passes, rounded to x's
-// dtype as the separate LayerNorm kernel rounds its output) into an LDS tile
-// [16][2K' + 4] fp16, which the k-steps then read instead of x.  Wave w
-// normalizes rows 16 w / NW ..; lane (row, part) holds chunks part + LPR j
-// of its row in registers.  Rows past M are zero rows (never stored).
+// LN, the row prologue (NW = 4, per-row scales, K' % 32 == 0, K' <=
+// kLnMaxK, fp16 / bf16 x, not TABLE): the workgroup first prepares its 16
+// rows of x -- nn.LayerNorm over the 2K' features (a.ln; float32, two
+// passes) and / or the activation fake quantization of each half
+// (a.aq_bits), rounded to x's dtype as the separate row kernels round their
+// output -- into an LDS tile [16][2K' + 4] fp16, which the k-steps then read
+// instead of x.  Rows past M are zero rows (never stored).
 template <int XDT, int YDT, int CB, bool PB, bool KT, int NW, bool LN = false>
 __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_skinny_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
@@ -214,35 +214,44 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
             }
         }
     };
-    // LN tile: rows of xsb bytes after the LUT and the split-K partials,
-    // then gamma and beta as float32 [2K'] each
+    // Row prologue tile (LN): rows of xsb bytes after the LUT and the
+    // split-K partials.  Wave w prepares rows RW w .. RW w + RW - 1 of the
+    // chunk, each with all 64 lanes, lane l holding chunks l + 64 j: the
+    // LayerNorm / act-quant row kernel's lane order at 64 lanes per row (its
+    // choice for every launch this kernel fuses), so the statistics, the
+    // per-half maxima and every value after them are bit-identical to
+    // rpfq_layer_norm / rpfq_layer_norm_act_quant / rpfq_act_quant.
     const int C2 = 2 * K, nch = C2 / 8;
     const int xsb = 2 * C2 + 8;  // the 8-B pad puts consecutive rows 2 banks apart
     char* xtile = smem + sk_lds(NW);
-    float* gs = reinterpret_cast<float*>(xtile + 16 * xsb);
-    float* bs = gs + C2;
-    constexpr int RW = 16 / NW, LPR = 64 / RW;  // (LN) rows per wave, lanes per row
-    constexpr int CPL = LN ? (2 * kLnMaxK / 8 + LPR - 1) / LPR : 1;
-    constexpr int GBI = LN ? (2 * kLnMaxK / 4 + 64 * NW - 1) / (64 * NW) : 1;
-    const int lrow = lane % RW, part = lane / RW, lnrow = wave * RW + lrow;
-    uint4 lnv[CPL];
-    float4 gv[GBI], bv[GBI];
+    constexpr int RW = 16 / NW;                                  // (LN) rows per wave
+    constexpr int NCP = LN ? (2 * kLnMaxK / 8 + 63) / 64 : 1;    // chunks per lane and row
+    uint4 lnv[RW][NCP];
+    float4 gv[NCP][2], bv[NCP][2];
     float4 prm[2];
     if (LN) {  // requested before the code ring: their waits leave the codes in flight
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = part + LPR * j;
-            lnv[j] = (c < nch && lnrow < M)
-                         ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xc) + lnrow * C2 + 8 * c)
-                         : make_uint4(0, 0, 0, 0);
-        }
-        const int tid = (int)threadIdx.x;
+        for (int i = 0; i < RW; ++i) {
+            const int row = wave * RW + i;
 #pragma unroll
-        for (int i = 0; i < GBI; ++i) {
-            const int f = tid + 64 * NW * i;  // float4 index
-            const bool ok = 4 * f < C2;
-            gv[i] = (ok && a.ln_gamma) ? reinterpret_cast<const float4*>(a.ln_gamma)[f] : make_float4(1, 1, 1, 1);
-            bv[i] = (ok && a.ln_beta) ? reinterpret_cast<const float4*>(a.ln_beta)[f] : make_float4(0, 0, 0, 0);
+            for (int j = 0; j < NCP; ++j) {
+                const int c = lane + 64 * j;
+                lnv[i][j] = (c < nch && row < M)
+                                ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xc) + row * C2 + 8 * c)
+                                : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NCP; ++j) {
+            const int c = lane + 64 * j;
+            const bool ok = a.ln && c < nch;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                gv[j][t] = (ok && a.ln_gamma) ? reinterpret_cast<const float4*>(a.ln_gamma)[2 * c + t]
+                                              : make_float4(1, 1, 1, 1);
+                bv[j][t] = (ok && a.ln_beta) ? reinterpret_cast<const float4*>(a.ln_beta)[2 * c + t]
+                                             : make_float4(0, 0, 0, 0);
+            }
         }
         const float4* pp = a.params + ((int64_t)tile * 32 + R) * 2;
         prm[0] = pp[0];
@@ -287,71 +296,159 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
 
     int blk = 0;
     if (LN) {
-        const int tid = (int)threadIdx.x;
+        // y = LayerNorm(x) (a.ln) or x, float32, per row i of the wave; the
+        // RW rows' reductions interleave so their shuffle chains overlap
+        float mean[RW], rstd[RW];
 #pragma unroll
-        for (int i = 0; i < GBI; ++i) {
-            const int f = tid + 64 * NW * i;
-            if (4 * f < C2) {
-                reinterpret_cast<float4*>(gs)[f] = gv[i];
-                reinterpret_cast<float4*>(bs)[f] = bv[i];
-            }
+        for (int i = 0; i < RW; ++i) {
+            mean[i] = 0.0f;
+            rstd[i] = 1.0f;
         }
-        // statistics of this lane's row (the LayerNorm kernel's two passes)
-        float sum = 0.0f;
+        if (a.ln) {
+            float sum[RW], s2[RW];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            if (part + LPR * j < nch) {
-                float f[8];
-                chunk_f32<XDT>(lnv[j], f);
+            for (int i = 0; i < RW; ++i) {
+                sum[i] = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sum += f[e];
-            }
-        }
+                for (int j = 0; j < NCP; ++j) {
+                    if (lane + 64 * j < nch) {
+                        float f[8];
+                        chunk_f32<XDT>(lnv[i][j], f);
 #pragma unroll
-        for (int o = RW; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
-        const float mean = sum / (float)C2;
-        float s2 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            if (part + LPR * j < nch) {
-                float f[8];
-                chunk_f32<XDT>(lnv[j], f);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float d = f[e] - mean;
-                    s2 += d * d;
+                        for (int e = 0; e < 8; ++e) sum[i] += f[e];
+                    }
                 }
             }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+                for (int i = 0; i < RW; ++i) sum[i] += __shfl_xor(sum[i], o, 64);
+            }
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                mean[i] = sum[i] / (float)C2;
+                s2[i] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NCP; ++j) {
+                    if (lane + 64 * j < nch) {
+                        float f[8];
+                        chunk_f32<XDT>(lnv[i][j], f);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float d = f[e] - mean[i];
+                            s2[i] += d * d;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+                for (int i = 0; i < RW; ++i) s2[i] += __shfl_xor(s2[i], o, 64);
+            }
+#pragma unroll
+            for (int i = 0; i < RW; ++i) rstd[i] = 1.0f / sqrtf(s2[i] / (float)C2 + a.ln_eps);
         }
-#pragma unroll
-        for (int o = RW; o < 64; o <<= 1) s2 += __shfl_xor(s2, o, 64);
-        const float rstd = 1.0f / sqrtf(s2 / (float)C2 + a.ln_eps);
         build_lut_sk_regs<CB, 8 / NW>(lut, prm[0], prm[1], a.rot, R, g, (8 / NW) * wave);  // this wave's share
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // gamma / beta in LDS
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
+        auto value = [&](int i, int j, float* y) {
+            chunk_f32<XDT>(lnv[i][j], y);
+            if (a.ln) {
+                const float gk[8] = {gv[j][0].x, gv[j][0].y, gv[j][0].z, gv[j][0].w,
+                                     gv[j][1].x, gv[j][1].y, gv[j][1].z, gv[j][1].w};
+                const float bk[8] = {bv[j][0].x, bv[j][0].y, bv[j][0].z, bv[j][0].w,
+                                     bv[j][1].x, bv[j][1].y, bv[j][1].z, bv[j][1].w};
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = part + LPR * j;
-            if (c < nch) {
-                float f[8];
-                chunk_f32<XDT>(lnv[j], f);
-                const float4 g0 = reinterpret_cast<const float4*>(gs + 8 * c)[0], g1 = reinterpret_cast<const float4*>(gs + 8 * c)[1];
-                const float4 b0 = reinterpret_cast<const float4*>(bs + 8 * c)[0], b1 = reinterpret_cast<const float4*>(bs + 8 * c)[1];
-                const float gk[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-                const float bk[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+                for (int e = 0; e < 8; ++e) y[e] = (y[e] - mean[i]) * rstd[i] * gk[e] + bk[e];
+            }
+        };
+        // activation fake quantization (a.aq_bits): per row and half, scale
+        // = qmax * (1 / max(max|y|, 1e-5)), y_q = clamp(rint(y scale)) / scale;
+        // for <= 4 bits the quotients of the 16 levels are divided once per
+        // row (lane l < 32: level (l & 15) - 8 of half l >> 4) and fetched
+        // with ds_bpermute, which every lane takes part in (lanes past the
+        // row's chunks hold zeros and store nothing)
+        const int bits = a.aq_bits;
+        const float qmax = (float)((1 << (bits - 1)) - 1), qmin = -(float)(1 << (bits - 1));
+        const int half_ch = nch >> 1;
+        float sc0[RW], sc1[RW];
+        int tvb[RW];
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            sc0[i] = sc1[i] = 1.0f;
+            tvb[i] = 0;
+        }
+        if (bits) {
+            float m0[RW], m1[RW];
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                m0[i] = m1[i] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NCP; ++j) {
+                    const int c = lane + 64 * j;
+                    if (c < nch) {
+                        float y[8];
+                        value(i, j, y);
+                        float mx = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(y[e]));
+                        if (c < half_ch) m0[i] = fmaxf(m0[i], mx); else m1[i] = fmaxf(m1[i], mx);
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+                for (int i = 0; i < RW; ++i) {
+                    m0[i] = fmaxf(m0[i], __shfl_xor(m0[i], o, 64));
+                    m1[i] = fmaxf(m1[i], __shfl_xor(m1[i], o, 64));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                // torch evaluates `float(qmax) / tensor` as reciprocal(tensor) * qmax
+                sc0[i] = (1.0f / fmaxf(m0[i], 1e-5f)) * qmax;
+                sc1[i] = (1.0f / fmaxf(m1[i], 1e-5f)) * qmax;
+                tvb[i] = __float_as_int((float)((lane & 15) - 8) / ((lane & 16) ? sc1[i] : sc0[i]));
+            }
+        }
+        const bool table = bits > 0 && bits <= 4;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int row = wave * RW + i;
+#pragma unroll
+            for (int j = 0; j < NCP; ++j) {
+                const int c = lane + 64 * j;
+                float y[8];
+                value(i, j, y);
+                if (bits) {
+                    const bool hi = c >= half_ch;
+                    const float sc = hi ? sc1[i] : sc0[i];
+                    float qv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) qv[e] = fminf(fmaxf(rintf(y[e] * sc), qmin), qmax);
+                    if (table) {
+                        int d[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            d[e] = __builtin_amdgcn_ds_bpermute(((hi ? 16 : 0) + (int)qv[e] + 8) << 2, tvb[i]);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) y[e] = copysignf(__int_as_float(d[e]), qv[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) y[e] = qv[e] / sc;
+                    }
+                }
                 uint32_t o[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float y0 = (f[2 * i] - mean) * rstd * gk[2 * i] + bk[2 * i];
-                    float y1 = (f[2 * i + 1] - mean) * rstd * gk[2 * i + 1] + bk[2 * i + 1];
+                for (int t = 0; t < 4; ++t) {
+                    float y0 = y[2 * t], y1 = y[2 * t + 1];
                     if (XDT == RPFQ_BF16) {  // rounded to x's dtype, then exactly to fp16 for the MFMA
                         y0 = bf16_to_f32(f32_to_bf16(y0));
                         y1 = bf16_to_f32(f32_to_bf16(y1));
                     }
-                    o[i] = lnrow < M ? cvt_pk(y0, y1) : 0u;
+                    o[t] = row < M ? cvt_pk(y0, y1) : 0u;
                 }
-                *reinterpret_cast<uint4*>(xtile + lnrow * xsb + 16 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+                if (c < nch) *reinterpret_cast<uint4*>(xtile + row * xsb + 16 * c) = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
     } else {  // split K: each wave builds 1 / NW of the shared LUT
@@ -785,7 +882,7 @@ static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
 
 template <int XDT, int YDT, int CB, int NW>
 static hipError_t wide_sk_ln_go(WideArgs& a, hipStream_t s) {
-    const int lds = sk_lds(NW) + 16 * (4 * a.K + 8) + 2 * (2 * a.K) * (int)sizeof(float);
+    const int lds = sk_lds(NW) + 16 * (4 * a.K + 8);
     hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, false, false, NW, true>), dim3((unsigned)sk_groups(a)),
                        dim3(64 * NW), lds, s, a);
     return hipGetLastError();
@@ -806,12 +903,13 @@ static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
 
 template <int XDT, int YDT, int CB>
 static hipError_t wide_sk(WideArgs& a, hipStream_t s) {
-    // Fused LayerNorm (qualified on the host, layer_norm_wide_fusable): K
-    // split over 4 waves at any group count, so each wave normalizes 4 of
-    // the chunk's 16 rows (ViT-B/16 batch-1 forward 0.775 -> 0.712 ms; over
-    // 2 waves from 400 groups, as without the LayerNorm, 0.781 ms: the
-    // prologue's per-wave work sits on every workgroup's critical path).
-    if (a.ln) {
+    // Fused row prologue, LayerNorm and / or act quant (qualified on the
+    // host, layer_norm_wide_fusable): K split over 4 waves at any group
+    // count, so each wave prepares 4 of the chunk's 16 rows (ViT-B/16
+    // batch-1 forward 0.775 -> 0.712 ms with the LayerNorm; over 2 waves from
+    // 400 groups, as without it, 0.781 ms: the prologue's per-wave work sits
+    // on every workgroup's critical path).
+    if (a.ln || a.aq_bits) {
         if constexpr (CB != RPFQ_CB_TABLE && XDT != RPFQ_F32) return wide_sk_ln_go<XDT, YDT, CB, 4>(a, s);
         return hipErrorInvalidValue;
     }

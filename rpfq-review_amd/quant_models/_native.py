@@ -55,6 +55,7 @@ EXPORTED = (
     "rpfq_wide_linear_grad_x",
     "rpfq_layer_norm_wide_linear",
     "rpfq_layer_norm_wide_linear_fusable",
+    "rpfq_act_quant_wide_linear",
     "rpfq_wide_linear_kernel",
     "rpfq_layer_norm",
     "rpfq_layer_norm_act_quant",
@@ -142,6 +143,8 @@ def load() -> ctypes.CDLL:
         lib.rpfq_layer_norm_wide_linear.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, ctypes.c_float, vp, vp, i32,
                                                     i32, vp]
         lib.rpfq_layer_norm_wide_linear_fusable.argtypes = [dp, i64, i32, i32, ctypes.POINTER(i32)]
+        lib.rpfq_act_quant_wide_linear.argtypes = [dp, vp, sz, vp, i32, i64, i32, i32, vp, vp, ctypes.c_float, vp,
+                                                   vp, vp, i32, i32, vp]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
         lib.rpfq_gelu_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]

@@ -293,6 +293,45 @@ class PackedWide:
             N.FLAG_GELU if gelu else 0, N.stream_of(x2)))
         return y.reshape(*lead, self.out_features)
 
+    def act_quant_linear(self, x: torch.Tensor, bits: int, bias: torch.Tensor | None = None,
+                         out_dtype: torch.dtype | None = None, gelu: bool = False,
+                         residual: torch.Tensor | None = None, layer_norm=None) -> torch.Tensor:
+        """self.linear(act_quant(x, bits), bias) -- or of act_quant(layer_norm(x))
+        with layer_norm = (ln_weight, ln_bias, eps) -- in one launch
+        (rpfq_act_quant_wide_linear): the streaming kernel's prologue quantizes
+        the rows as act_quant() / layer_norm(act_bits=bits) does, bit for bit.
+        residual ([..., 2N'] of out_dtype): added in the store.  Only where
+        ln_fusable(); gelu as in linear() (not with a residual)."""
+        N.require_device(x, bias, residual)
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
+        lead = x.shape[:-1]
+        x2 = _aligned_rows(x.reshape(-1, self.in_features))
+        m = x2.shape[0]
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
+        r2 = None
+        if residual is not None:
+            if residual.shape[:-1] != lead or residual.shape[-1] != self.out_features:
+                raise ValueError(f"residual must have shape {tuple(lead) + (self.out_features,)}")
+            r2 = _aligned_rows(residual.to(out_dtype).reshape(-1, self.out_features))
+        if m == 0:
+            return y.reshape(*lead, self.out_features)
+        w = b = None
+        eps = 0.0
+        if layer_norm is not None:
+            ln_w, ln_b, eps = layer_norm
+            N.require_device(ln_w, ln_b)
+            w = None if ln_w is None else ln_w.detach().float().contiguous()
+            b = None if ln_b is None else ln_b.detach().float().contiguous()
+        if bias is not None:
+            bias = bias.contiguous().float()
+        N.check("rpfq_act_quant_wide_linear", N.load().rpfq_act_quant_wide_linear(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(), N.dtype_code(x2.dtype),
+            m, int(bits), int(layer_norm is not None), N.ptr(w), N.ptr(b), float(eps), N.ptr(bias), N.ptr(r2),
+            y.data_ptr(), N.dtype_code(out_dtype), N.FLAG_GELU if gelu else 0, N.stream_of(x2)))
+        return y.reshape(*lead, self.out_features)
+
     def kernel_for(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype, flags: int = 0) -> int:
         """The kernel linear() runs for m rows (N.KERNEL_STREAM / _GEMV /
         _DMA / _TILED; rpfq_wide_linear_kernel, no GPU work)."""

@@ -303,6 +303,10 @@ HIP_QAT = os.environ.get("RPFQ_HIP_QAT", "1") != "0"
 # ~1 ulp from the host's torch CPU order; no host round trip of the weight)
 DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
 
+# Eval-mode act quant in the packed layer's own launch (the streaming
+# kernel's row prologue, rpfq_act_quant_wide_linear) where that launch
+# qualifies; RPFQ_FUSE_AQ_PROLOGUE=0 runs the separate act-quant pass.
+FUSE_AQ_PROLOGUE = os.environ.get("RPFQ_FUSE_AQ_PROLOGUE", "1") != "0"
 # Input gradient of the HIP training forward on the packed blob of the
 # step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
 # A_q: "auto" for 16-bit activations (the reference's AMP precision class:
@@ -630,10 +634,19 @@ class QATLinearComplexPhase(nn.Linear):
             if self.act_quantizer is not None and not prequantized:
                 x = _HipActQuantSTE.apply(x, self.act_quantizer.num_bits)
             return _PackedLinearFn.apply(x, self.bias, pw)
-        if self.act_quantizer is not None and not prequantized:
-            x = ops.act_quant(x, self.act_quantizer.num_bits)
         bias = None if self.bias is None else self.bias.detach()
+        if self.act_quantizer is not None and not prequantized:
+            if self._aq_fusable(pw, x):  # act quant in the layer's own launch
+                return pw.act_quant_linear(x, self.act_quantizer.num_bits, bias, out_dtype=x.dtype)
+            x = ops.act_quant(x, self.act_quantizer.num_bits)
         return pw.linear(x, bias, out_dtype=x.dtype)
+
+    @staticmethod
+    def _aq_fusable(pw, x: torch.Tensor) -> bool:
+        """The streaming kernel's row prologue takes this launch
+        (rpfq_act_quant_wide_linear: a layer at batch 1-2, K' <= 384)."""
+        m = x.numel() // x.shape[-1] if x.dim() else 0
+        return FUSE_AQ_PROLOGUE and hasattr(pw, "ln_fusable") and m > 0 and pw.ln_fusable(m, x.dtype)
 
     def packed_act_bits(self, x: torch.Tensor) -> int:
         """Bits of the activation quantization the packed path would apply to
@@ -667,9 +680,11 @@ class QATLinearComplexPhase(nn.Linear):
             from . import ops
 
             pw = self.packed(x.device)
-            if self.act_quantizer is not None and not prequantized:
-                x = ops.act_quant(x, self.act_quantizer.num_bits)
             bias = None if self.bias is None else self.bias.detach()
+            if self.act_quantizer is not None and not prequantized:
+                if self._aq_fusable(pw, x):  # act quant, layer and GELU in one launch
+                    return pw.act_quant_linear(x, self.act_quantizer.num_bits, bias, out_dtype=x.dtype, gelu=True)
+                x = ops.act_quant(x, self.act_quantizer.num_bits)
             m = x.numel() // x.shape[-1]
             kern = pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) if m else None
             if kern in N.STREAM_KERNELS or x.dtype == torch.bfloat16:
@@ -680,9 +695,14 @@ class QATLinearComplexPhase(nn.Linear):
     def forward_layer_norm(self, x: torch.Tensor, ln_weight, ln_bias, eps: float, gelu: bool = False):
         """self(layer_norm(x)) (and its exact GELU if gelu) with the LayerNorm
         fused into the packed layer's launch (rpfq_layer_norm_wide_linear), or
-        None where that launch does not apply (training, host tensors,
-        activation quantization on, stage groups, a launch the fused kernel
-        does not take: see PackedWide.ln_fusable)."""
+        None where that launch does not apply (training, autograd, host
+        tensors, activation quantization on, stage groups, a launch the fused
+        kernel does not take: see PackedWide.ln_fusable).  With activation
+        quantization the LayerNorm + act quant row kernel runs first instead:
+        in the prologue of every one of qkv's 36 (fc1's 48) tiles it measured
+        slower at one ViT-B/16 image (qkv 15.5 vs 5.2 + 9.5 us, fc1 19.3 vs
+        5.2 + 12.0 us); the act quant alone pays in the prologue (proj 9.3 vs
+        4.7 + 9.2 us), see _packed_forward / forward_residual."""
         if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None \
                 or self._records_grad(x):
             return None
@@ -702,8 +722,11 @@ class QATLinearComplexPhase(nn.Linear):
             from . import ops
 
             pw = self.packed(x.device)
-            if self.act_quantizer is not None and not prequantized:
-                x = ops.act_quant(x, self.act_quantizer.num_bits)
             bias = None if self.bias is None else self.bias.detach()
+            if self.act_quantizer is not None and not prequantized:
+                if self._aq_fusable(pw, x):  # act quant, layer and residual add in one launch
+                    return pw.act_quant_linear(x, self.act_quantizer.num_bits, bias, out_dtype=x.dtype,
+                                               residual=residual)
+                x = ops.act_quant(x, self.act_quantizer.num_bits)
             return pw.linear(x, bias, out_dtype=x.dtype, residual=residual)
         return residual + (self.forward_prequantized(x) if prequantized else self.forward(x))

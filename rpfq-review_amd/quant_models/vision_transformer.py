@@ -160,15 +160,12 @@ class Mlp(nn.Module):
         over fc1's output instead (rpfq_gelu_act_quant, float32 GELU
         quantized without rounding in between)."""
         gelu_exact = type(self.act) is nn.GELU and self.act.approximate == "none"
-        if FUSE_GELU and FUSE_ACT_QUANT and gelu_exact and type(self.norm) is nn.Identity:
-            bits_of = getattr(self.fc2, "packed_act_bits", None)
-            bits = bits_of(x) if bits_of is not None else 0
-            c = self.fc2.in_features
-            if bits and c % 16 == 0 and c <= 4096:
-                from . import ops
+        bits = self._gelu_act_quant_bits(x)
+        if bits:
+            from . import ops
 
-                h = ops.gelu_act_quant(call_layer(self.fc1, x, prequantized), bits)
-                return self.fc2.forward_residual(h, residual, prequantized=True)
+            h = ops.gelu_act_quant(call_layer(self.fc1, x, prequantized), bits)
+            return self.fc2.forward_residual(h, residual, prequantized=True)
         fc1_gelu = getattr(self.fc1, "forward_gelu", None)
         if FUSE_GELU and fc1_gelu is not None and gelu_exact:
             h = fc1_gelu(x, prequantized)
@@ -176,13 +173,35 @@ class Mlp(nn.Module):
             h = self.act(call_layer(self.fc1, x, prequantized))
         return self.forward_hidden_residual(h, residual)
 
+    def _gelu_act_quant_bits(self, x) -> int:
+        """Bits of fc2's activation quantization when the exact GELU and that
+        quantization run as one pass over fc1's output (rpfq_gelu_act_quant,
+        bit-exact with torch's GELU followed by the act quant), else 0."""
+        gelu_exact = type(self.act) is nn.GELU and self.act.approximate == "none"
+        if not (FUSE_GELU and FUSE_ACT_QUANT and gelu_exact and type(self.norm) is nn.Identity):
+            return 0
+        bits_of = getattr(self.fc2, "packed_act_bits", None)
+        bits = bits_of(x) if bits_of is not None else 0
+        c = self.fc2.in_features
+        return bits if bits and c % 16 == 0 and c <= 4096 else 0
+
     def forward_hidden_residual(self, h, residual):
         """residual + fc2(h) for h = act(fc1(x)) already computed."""
         return linear_residual(self.fc2, self.norm(self.drop1(h)), residual)
 
     def forward_norm_residual(self, norm, x):
-        """x + self(norm(x)) with norm fused into fc1's launch (and the exact
-        GELU into its store), or None where that does not apply."""
+        """x + self(norm(x)) with norm (and fc1's act quant) fused into fc1's
+        launch and the GELU into its store -- or, when fc2 quantizes its
+        input, the GELU and that act quant in one pass after fc1 -- or None
+        where that does not apply."""
+        bits = self._gelu_act_quant_bits(x)
+        if bits:
+            h = norm_layer_fwd(norm, x, self.fc1, False)
+            if h is None:
+                return None
+            from . import ops
+
+            return self.fc2.forward_residual(ops.gelu_act_quant(h, bits), x, prequantized=True)
         gelu = FUSE_GELU and type(self.act) is nn.GELU and self.act.approximate == "none"
         h = norm_layer_fwd(norm, x, self.fc1, gelu)
         if h is None:

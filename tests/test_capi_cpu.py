@@ -369,3 +369,30 @@ def test_wide_grad_x_geometry_and_argument_errors():
     assert grad(gx=fake + 1) == 3
     assert L.rpfq_wide_linear_grad_x(ctypes.byref(_desc(N, k=12)), fake, nbytes, fake, abytes, fake, 1, 4, fake, 1,
                                      None) == 3
+
+
+def test_act_quant_wide_linear_argument_errors():
+    """rpfq_act_quant_wide_linear validates on the host before any GPU work:
+    NULLs, dtypes, M, bits, flags (GELU not with a residual), eps, sizes,
+    alignment, and launches outside the row prologue's forms."""
+    L, N = lib()
+    fc1 = _desc(N, n=1536, k=384)
+    nbytes = L.rpfq_wide_packed_bytes(ctypes.byref(fc1))
+    fake = 1 << 20  # an aligned non-NULL address; never dereferenced on these paths
+
+    def call(packed=fake, nb=nbytes, x=fake, xdt=1, m=197, bits=4, ln=1, g=None, b=None, eps=1e-6, res=None,
+             y=fake, ydt=1, flags=0):
+        return L.rpfq_act_quant_wide_linear(ctypes.byref(fc1), packed, nb, x, xdt, m, bits, ln, g, b,
+                                            ctypes.c_float(eps), None, res, y, ydt, flags, None)
+    assert call(packed=None) == 1 and call(x=None) == 1 and call(y=None) == 1
+    assert call(xdt=9) == 5
+    assert call(m=0) == 2
+    assert call(bits=1) == 4 and call(bits=17) == 4
+    assert call(flags=N.FLAG_NO_STREAM) == 6
+    assert call(flags=N.FLAG_GELU, res=fake) == 6
+    assert call(eps=-1.0) == 6
+    assert call(nb=nbytes - 1) == 2
+    assert call(x=fake + 8) == 3 and call(res=fake + 4) == 3
+    assert call(m=50432) == 6  # not on the streaming split-K kernel
+    assert b"rpfq_act_quant" in L.rpfq_last_error()
+    assert call(xdt=0) == 6  # float32 x

@@ -770,6 +770,66 @@ def test_layer_norm_wide_linear(case, m, xdt):
     assert np.all(np.abs(yg - yg_sep) <= 1.2 * u_x * (np.abs(hf) @ a16.T) + 2.0 ** -9 * np.abs(yg_sep) + 1e-4)
 
 
+AQ_CASES = [LN_CASES[0], LN_CASES[2], LN_CASES[3], LN_CASES[4], LN_CASES[5]]
+
+
+@pytest.mark.parametrize("layer_norm", [False, True], ids=["aq", "ln-aq"])
+@pytest.mark.parametrize("bits", [4, 8, 2])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [9, 197])
+@pytest.mark.parametrize("case", AQ_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}" for c in AQ_CASES])
+def test_act_quant_wide_linear(case, m, xdt, bits, layer_norm):
+    """The act quant (after the LayerNorm when layer_norm) in the streaming
+    kernel's row prologue (rpfq_act_quant_wide_linear): the quantized rows are
+    bit-identical to rpfq_act_quant / rpfq_layer_norm_act_quant's, so the
+    output is the oracle's product on those rows within float32 accumulation
+    only (a single element quantized differently moves its row by a whole
+    quantization step and fails the bound); with a residual, the fp16 output
+    within its two roundings of the oracle's sum."""
+    ops, N = qm()
+    r = rng(2100 + m + case[0] + case[1] + bits)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    assert pw.ln_fusable(m, xdt), (case, m)
+    c2 = 2 * case[1]
+    x = torch.from_numpy((r.standard_normal((m, c2)) * 3 + 1).astype(np.float32)).to(xdt).to(DEV)
+    g = tdev(r.standard_normal(c2).astype(np.float32))
+    b = tdev(r.standard_normal(c2).astype(np.float32))
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    if layer_norm:
+        h = ops.layer_norm(x, g, b, 1e-6, act_bits=bits)
+        ln = (g, b, 1e-6)
+    else:
+        h = ops.act_quant(x, bits)
+        ln = None
+    hf = h.float().cpu().numpy().astype(np.float64)
+    y = pw.act_quant_linear(x, bits, bias, out_dtype=torch.float32, layer_norm=ln).cpu().numpy()
+    check_against_oracle(y, hf, bias.cpu().numpy().astype(np.float64), oplanes, codebook, rotation)
+    res = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32)).to(torch.float16).to(DEV)
+    yr = pw.act_quant_linear(x, bits, bias, out_dtype=torch.float16, residual=res,
+                             layer_norm=ln).float().cpu().numpy()
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    lay = hf @ a16.T + bias.cpu().numpy()
+    ref = lay + res.float().cpu().numpy()
+    scale = np.abs(hf) @ np.abs(a16).T + np.abs(bias.cpu().numpy())
+    u = 2.0 ** -11
+    assert np.all(np.abs(yr - ref) <= 1e-5 * scale + u * np.abs(lay) + 1.001 * u * np.abs(ref) + 1e-5)
+
+
+def test_act_quant_wide_linear_refuses():
+    """Launches outside the row prologue's forms and bad arguments raise."""
+    ops, N = qm()
+    r = rng(2190)
+    pw, *_ = build_packed(r, LN_CASES[1])
+    x = torch.zeros(300, 768, dtype=torch.float16, device=DEV)
+    with pytest.raises(N.RPFQError, match="RPFQ_ERR_VALUE"):
+        pw.act_quant_linear(torch.zeros(50432, 768, dtype=torch.float16, device=DEV), 4)
+    with pytest.raises(N.RPFQError, match="RPFQ_ERR_BITS"):
+        pw.act_quant_linear(x[:197], 1)
+    with pytest.raises(N.RPFQError, match="RPFQ_ERR_VALUE"):
+        pw.act_quant_linear(x[:197], 4, gelu=True, residual=torch.zeros(197, 3072, dtype=torch.float16,
+                                                                      device=DEV))
+
+
 def test_layer_norm_wide_linear_refuses_unfusable():
     """Launches outside the fused kernel's forms raise (the caller runs the
     LayerNorm and the layer separately)."""

@@ -472,11 +472,13 @@ def test_fused_act_quant_wiring(name):
     heads), while without the fusion every packed layer runs it.  Each
     prequantized input holds at most 2^bits distinct values per row and half
     (a layer fed an unquantized input would hold hundreds)."""
-    from quant_models import ops
+    from quant_models import ops, quant_i
     from quant_models import vision_transformer as vt
     from quant_models.inference import prepare_inference, quant_layers
     from quant_models.quant_i import QATLinearComplexPhase
 
+    # (the act quant inside a streaming layer's own launch has its own test:
+    # test_fused_act_quant_prologue)
     model, _ = _synthetic_model(name, 4, act_quant=True)
     prepare_inference(model, DEV, torch.float16)
     n_layers = sum(1 for _ in quant_layers(model))
@@ -503,8 +505,9 @@ def test_fused_act_quant_wiring(name):
         if prequantized:
             pre.append(h.reshape(-1, h.shape[-1])[:64].float().cpu())
         return fwd_res(self, h, residual, prequantized)
-    saved = vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT
+    saved = vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT, quant_i.FUSE_AQ_PROLOGUE
     try:
+        quant_i.FUSE_AQ_PROLOGUE = False
         ops.act_quant = counting
         QATLinearComplexPhase.forward_prequantized = recording
         QATLinearComplexPhase.forward_gelu = recording_gelu
@@ -526,7 +529,7 @@ def test_fused_act_quant_wiring(name):
         QATLinearComplexPhase.forward_prequantized = fwd_pre
         QATLinearComplexPhase.forward_gelu = fwd_gelu
         QATLinearComplexPhase.forward_residual = fwd_res
-        vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT = saved
+        vt.FUSED_BLOCKS, vt.FUSE_ACT_QUANT, quant_i.FUSE_AQ_PROLOGUE = saved
     assert n_unfused == n_module == n_layers, (n_unfused, n_module, n_layers)
     blocks = sum(1 for m in model.modules() if hasattr(m, "mlp") and hasattr(m, "norm2"))
     merges = sum(1 for m in model.modules() if type(m).__name__ == "PatchMerging")
@@ -539,6 +542,56 @@ def test_fused_act_quant_wiring(name):
             assert levels <= 16, levels
     for y in (y_f, y_u, y_m):
         assert torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+@pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_deit_tiny_patch16_224_q",
+                                  "rpfq_swin_tiny_patch4_window7_224_q"])
+def test_fused_act_quant_prologue(name, dt):
+    """At one image with activation quantization on, the act quant of a
+    streaming layer whose input comes unquantized (proj) runs in the layer's
+    own launch (rpfq_act_quant_wide_linear): counted (ViT / DeiT: one per
+    block), and the logits within LOGIT_TOL * max|logit| + LOGIT_TOL / 10 of
+    the same model running the separate act-quant kernel, identical top-1 on
+    margin-confident samples (the quantized rows are the same bits; only the
+    layer's split-K summation order differs)."""
+    from quant_models import ops, quant_i
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import prepare_inference
+
+    model, _ = _synthetic_model(name, 14, act_quant=True)
+    act = torch.bfloat16 if dt == "bf16" else torch.float16
+    prepare_inference(model, DEV, act)
+    x = torch.randn(1, 3, 224, 224, generator=torch.Generator().manual_seed(15)).to(DEV, act)
+    calls = []
+    fused_call = ops.PackedWide.act_quant_linear
+
+    def counting(self, *args, **kw):
+        calls.append(1)
+        return fused_call(self, *args, **kw)
+    saved = vt.FUSE_LN, quant_i.FUSE_AQ_PROLOGUE
+    try:
+        ops.PackedWide.act_quant_linear = counting
+        with torch.no_grad():
+            y_f = model(x)
+            n_fused = len(calls)
+            vt.FUSE_LN, quant_i.FUSE_AQ_PROLOGUE = False, False
+            y_u = model(x)
+    finally:
+        ops.PackedWide.act_quant_linear = fused_call
+        vt.FUSE_LN, quant_i.FUSE_AQ_PROLOGUE = saved
+    blocks = sum(1 for m in model.modules() if type(m).__name__ in ("Block", "SwinTransformerBlock"))
+    assert n_fused >= (blocks if "swin" not in name else 1), (n_fused, blocks)
+    assert len(calls) == n_fused  # nothing fused with the switches off
+    y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
+    err = float((y_f - y_u).abs().max())
+    tol = LOGIT_TOL[dt]
+    print(f"{name} {dt}: act-quant prologue fused vs separate max|dlogit| {err:.4g} "
+          f"(max|logit| {float(y_u.abs().max()):.3g}), {n_fused} fused launches")
+    assert err <= tol * float(y_u.abs().max()) + tol / 10
+    top = y_u.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
 
 
 @pytest.mark.parametrize("dt,batch", [("fp16", 1), ("bf16", 2)], ids=["fp16-bs1", "bf16-bs2"])
