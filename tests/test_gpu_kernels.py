@@ -867,7 +867,7 @@ def test_layer_norm_act_quant_bit_exact(m, c, xdt, ydt, bits):
     assert torch.equal(fused.cpu(), ref)
 
 
-@pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 3072), (5, 4096)])
+@pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 3072), (5, 4096), (1100, 3072), (1030, 768)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
                                      (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)])
 @pytest.mark.parametrize("bits", [2, 4, 8])
@@ -894,6 +894,65 @@ def test_gelu_act_quant_bit_exact(m, c, xdt, ydt, bits):
             y.data_ptr(), N.dtype_code(xdt), m, c, bits, y.data_ptr(), N.dtype_code(ydt), N.stream_of(y)))
         torch.cuda.synchronize()
         assert torch.equal(y, fused)
+
+
+def _gelu_boundary_rows(bits, c, r):
+    """float32 rows whose GELU * scale crowds the act quant's rounding
+    boundaries k + 1/2: one anchor element fixes the half's maximum (7.0,
+    exactly its own GELU in float32; or 0.3, a maximum from the small
+    positive range), the rest sits within +-3e-4 of the x whose exact GELU *
+    scale is a boundary, on both sides.  Boundaries of the positive branch
+    and, for the small anchor, of the negative one (x < -0.75)."""
+    from scipy.optimize import brentq
+    from scipy.special import ndtr
+
+    def gelu(t):
+        return t * ndtr(t)
+    qmax = 2 ** (bits - 1) - 1
+    rows = []
+    half = c // 2
+    for anchor in (7.0, 0.3):
+        amax = gelu(anchor)
+        sc = qmax / amax
+        if anchor == 7.0:
+            targets = [((k + 0.5) / sc, 0.0, 10.0) for k in range(0, min(qmax, 6))]
+        else:
+            targets = [(-(k + 0.5) / sc, -8.0, -0.7518) for k in range(0, 5) if (k + 0.5) / sc < 0.16]
+        for tgt, lo, hi in targets:
+            x0 = brentq(lambda t: gelu(t) - tgt, lo, hi, xtol=1e-15)
+            xs = x0 + 2e-7 * max(1.0, abs(x0)) * np.arange(-(half // 2), half - half // 2)
+            row_half = xs.astype(np.float32)
+            row_half[r.integers(0, half)] = anchor
+            other = r.standard_normal(half).astype(np.float32) * 0.05
+            other[r.integers(0, half)] = anchor
+            rows.append(np.concatenate([row_half, other]))
+            rows.append(np.concatenate([other, row_half]))
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("c", [768, 3072])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("big", [False, True], ids=["block", "lanes64"])
+def test_gelu_act_quant_near_boundaries(c, bits, big):
+    """GELU + act quant against torch's GELU followed by the act quant, bit
+    for bit, on rows built to crowd the rounding boundaries (any GELU that
+    is not torch's float32 erf form, bit for bit, moves some of these
+    elements a level); both kernel forms (a workgroup per row for few rows,
+    64 lanes per row for many)."""
+    import torch.nn.functional as F
+
+    ops, _ = qm()
+    r = rng(1500 + c + bits)
+    rows = _gelu_boundary_rows(bits, c, r)
+    if big:  # past the workgroup-per-row form's row limit
+        rows = np.concatenate([rows] * (1100 // len(rows) + 1))
+    x = torch.from_numpy(rows).to(DEV)
+    fused = ops.gelu_act_quant(x, bits, out_dtype=torch.float32)
+    ref = ops.act_quant(F.gelu(x), bits, out_dtype=torch.float32)
+    assert torch.equal(fused, ref)
+    g = F.gelu(x).cpu().numpy()
+    qr, qi = O.act_quant(g[:, :c // 2], g[:, c // 2:], bits)
+    assert torch.equal(fused.cpu(), torch.from_numpy(np.concatenate([qr, qi], axis=1)))
 
 
 @pytest.mark.parametrize("k", [8, 384, 1536])
