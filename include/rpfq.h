@@ -209,16 +209,17 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
                               const void* x, int x_dtype, int64_t M, const float* bias,
                               const void* residual, void* y, int y_dtype, int flags, void* stream);
 
-/* Bytes of the adjoint code tiles that rpfq_wide_pack_adjoint writes for
- * `desc` (0 if the descriptor is invalid). */
+/* Bytes of the adjoint blob that rpfq_wide_pack_adjoint writes for `desc`
+ * (0 if the descriptor is invalid). */
 size_t rpfq_wide_adjoint_bytes(const rpfq_wide_desc* desc);
 
 /*
- * Adjoint code tiles of a packed layer: its codes with rows and columns
- * exchanged, for rpfq_wide_linear_grad_x (the per-row parameters stay in
- * the packed blob).  Run once per packed blob; both buffers 256-byte aligned.
- * No counterpart in the reference: it is this library's layout of the
- * codes for contractions over N'.
+ * Adjoint blob of a packed layer, for rpfq_wide_linear_grad_x: its codes
+ * with rows and columns exchanged, and each row's U / W value tables as the
+ * fp16 (re, im) pairs the kernels contract (de-rotated; every codebook).
+ * Run once per packed blob (and again after the blob or the descriptor's
+ * rotation changes); both buffers 256-byte aligned.  No counterpart in the
+ * reference: it is this library's layout for contractions over N'.
  */
 int rpfq_wide_pack_adjoint(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, void* adjoint,
                            size_t adjoint_bytes, void* stream);
@@ -230,8 +231,8 @@ int rpfq_wide_pack_adjoint(const rpfq_wide_desc* desc, const void* packed, size_
  * A12 = Wim - Uim, A21 = Wim + Uim, A22 = -Wre + Ure, bit for bit):
  *   gx_re = gy_re A11 + gy_im A21,   gx_im = gy_re A12 + gy_im A22.
  * grad_y: [M, 2N'] of grad_y_dtype (16-byte aligned when N' % 8 == 0);
- * grad_x: [M, 2K'] of grad_x_dtype.  packed / adjoint: the layer's blob and
- * its rpfq_wide_pack_adjoint tiles.  The products run on fp16 MFMA
+ * grad_x: [M, 2K'] of grad_x_dtype.  adjoint: the layer's
+ * rpfq_wide_pack_adjoint blob.  The products run on fp16 MFMA
  * operands with float32 accumulation; float32 and bf16 grad_y rows are
  * scaled by a power of two per row (largest magnitude in [2^14, 2^15))
  * before the fp16 rounding and unscaled exactly after, so each grad_y
@@ -243,9 +244,8 @@ int rpfq_wide_pack_adjoint(const rpfq_wide_desc* desc, const void* packed, size_
  *   backward), i.e. the input gradient of F.linear(x, A_q, bias) at
  *   quant_i.py:554 under the straight-through estimator (quant_i.py:128-130).
  */
-int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* adjoint,
-                            size_t adjoint_bytes, const void* grad_y, int grad_y_dtype, int64_t M, void* grad_x,
-                            int grad_x_dtype, void* stream);
+int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* adjoint, size_t adjoint_bytes, const void* grad_y,
+                            int grad_y_dtype, int64_t M, void* grad_x, int grad_x_dtype, void* stream);
 
 /*
  * y = layer(LayerNorm(x)) in one launch: the LayerNorm of rpfq_layer_norm

@@ -305,28 +305,23 @@ int rpfq_wide_pack_adjoint(const rpfq_wide_desc* desc, const void* packed, size_
     if (!aligned(packed, 256) || !aligned(adjoint, 256))
         return fail(RPFQ_ERR_ALIGN, "packed and adjoint must be 256-byte aligned");
     if (g.NT * g.KS > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "layer too large for the adjoint relayout");
-    return hip_status(rpfq::launch_wide_pack_adjoint(g, packed, adjoint, reinterpret_cast<hipStream_t>(stream)),
+    return hip_status(rpfq::launch_wide_pack_adjoint(*desc, g, packed, adjoint, reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_pack_adjoint");
 }
 
-int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* adjoint,
-                            size_t adjoint_bytes, const void* grad_y, int grad_y_dtype, int64_t M, void* grad_x,
-                            int grad_x_dtype, void* stream) {
+int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* adjoint, size_t adjoint_bytes, const void* grad_y,
+                            int grad_y_dtype, int64_t M, void* grad_x, int grad_x_dtype, void* stream) {
     int rc = check_desc(desc);
     if (rc) return rc;
-    if (!packed || !adjoint || !grad_y || !grad_x)
-        return fail(RPFQ_ERR_NULL, "packed/adjoint/grad_y/grad_x must not be NULL");
+    if (!adjoint || !grad_y || !grad_x) return fail(RPFQ_ERR_NULL, "adjoint/grad_y/grad_x must not be NULL");
     if (!dtype_ok(grad_y_dtype) || !dtype_ok(grad_x_dtype))
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype grad_y=%d grad_x=%d", grad_y_dtype, grad_x_dtype);
     if (M <= 0 || M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld out of range", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if (packed_bytes < g.total_bytes)
-        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (adjoint_bytes < rpfq::wide_adjoint_bytes(g))
         return fail(RPFQ_ERR_SHAPE, "adjoint buffer holds %zu bytes, need %zu", adjoint_bytes,
                     rpfq::wide_adjoint_bytes(g));
-    if (!aligned(packed, 256) || !aligned(adjoint, 256))
-        return fail(RPFQ_ERR_ALIGN, "packed and adjoint must be 256-byte aligned");
+    if (!aligned(adjoint, 256)) return fail(RPFQ_ERR_ALIGN, "adjoint must be 256-byte aligned");
     const size_t esize = grad_y_dtype == RPFQ_F32 ? 4 : 2;
     if (g.N % 8 == 0 && !aligned(grad_y, 16))
         return fail(RPFQ_ERR_ALIGN, "grad_y must be 16-byte aligned");
@@ -334,8 +329,8 @@ int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* packed, size
         return fail(RPFQ_ERR_ALIGN, "grad_y / grad_x must be aligned to their element size");
     const int64_t tiles = ((M + 127) / 128) * ((g.KS + 3) / 4);
     if (tiles > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld: too many tiles", (long long)M);
-    return hip_status(rpfq::launch_wide_linear_grad_x(*desc, g, packed, adjoint, grad_y, grad_y_dtype, M, grad_x,
-                                                      grad_x_dtype, reinterpret_cast<hipStream_t>(stream)),
+    return hip_status(rpfq::launch_wide_linear_grad_x(*desc, g, adjoint, grad_y, grad_y_dtype, M, grad_x, grad_x_dtype,
+                                                      reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear_grad_x");
 }
 

@@ -101,15 +101,22 @@ struct WideArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Adjoint code tiles (rpfq_wide_pack_adjoint), the packed layer's codes with
-// rows and columns exchanged, for contractions over N' (grad_x):
+// Adjoint blob (rpfq_wide_pack_adjoint), the packed layer arranged for
+// contractions over N' (grad_x):
 //  codesT: [KS][NT][32 columns][32 bytes]: byte b of (complex column k,
 //          row step t) holds the code byte of row n' = 32 t + 8 s + 4 g + e
 //          (g = b / 16, s = (b / 4) & 3, e = b & 3) and column k, so MFMA
 //          lane group g of the lane owning column k streams its 16 rows of
 //          a row step with one 128-bit load.
+//  lutT:   at wide_adjoint_codes_bytes: [NT*32 rows][nblk][32] fp16 (re, im)
+//          pairs, entries 0..15 U(index), 16..31 W(index) of the row (and
+//          scale block), de-rotated and rounded to fp16 -- the tables the
+//          forward kernels build in LDS.  Padded rows 0.
 // ---------------------------------------------------------------------------
-inline size_t wide_adjoint_bytes(const WideGeom& g) { return (size_t)g.NT * g.KS * 1024; }
+inline size_t wide_adjoint_codes_bytes(const WideGeom& g) { return (size_t)g.NT * g.KS * 1024; }
+inline size_t wide_adjoint_bytes(const WideGeom& g) {
+    return wide_adjoint_codes_bytes(g) + (size_t)g.NT * 32 * g.nblk * 128;
+}
 
 // Launch arguments of the grad_x kernel: gx [M, 2K'] = gy [M, 2N'] A.
 struct AdjArgs {
@@ -117,7 +124,7 @@ struct AdjArgs {
     int64_t M;
     int K, N, NT, KS, nblk, block_ks;
     const uint4* codes_t;  // adjoint code tiles
-    const float4* params;  // the packed layer's per-row parameters
+    const uint4* lut_t;    // adjoint U / W tables, 8 uint4 per (row, block)
     RotParams rot;
     void* gx;
     int tiles_m, tiles_k;
@@ -212,11 +219,11 @@ size_t quant_scratch_bytes();
 hipError_t quant_scratch_ptr(void** out);
 hipError_t launch_wide_decode(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                               float* a, int round_fp16, hipStream_t s);
-// adjoint code tiles (rpfq_kernels.hip) and the grad_x kernel (wide_adjoint.hip, one per codebook)
-hipError_t launch_wide_pack_adjoint(const WideGeom& g, const void* packed, void* adjoint, hipStream_t s);
-template <int CB> hipError_t launch_wide_grad_x(AdjArgs& a, int gdt, int xdt, hipStream_t s);
-hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
-                                     const void* adjoint, const void* gy, int gdt, int64_t M, void* gx, int xdt,
-                                     hipStream_t s);
+// adjoint blob (rpfq_kernels.hip) and the grad_x kernel (wide_adjoint.hip)
+hipError_t launch_wide_pack_adjoint(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, void* adjoint,
+                                    hipStream_t s);
+hipError_t launch_wide_grad_x(AdjArgs& a, int gdt, int xdt, hipStream_t s);
+hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* adjoint,
+                                     const void* gy, int gdt, int64_t M, void* gx, int xdt, hipStream_t s);
 
 }  // namespace rpfq

@@ -394,6 +394,34 @@ __global__ void __launch_bounds__(256) wide_pack_adjoint_kernel(const uint32_t* 
     codes_t[(ks * NT + t) * 256 + i] = out;
 }
 
+// Adjoint U / W tables: thread (row, block, index) writes entry `index` of U
+// and of W as the GEMM kernels' LUT builders compute it (same entry
+// function, de-rotation and fp16 rounding).
+template <int CB>
+__global__ void wide_adjoint_lut_kernel(const float4* __restrict__ params, int64_t rows, int64_t nblk, RotParams rot,
+                                        uint32_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nblk * 16) return;
+    const uint32_t idx = (uint32_t)(i & 15);
+    const int64_t rb = i >> 4;  // row * nblk + block
+    float2 u, w;
+    if constexpr (CB == RPFQ_CB_TABLE) {
+        const float2* t = reinterpret_cast<const float2*>(params) + rb * 32;  // nblk = 1
+        u = t[idx];
+        w = t[16 + idx];
+    } else {
+        const float4* p = params + rb * 2;
+        u = lut_entry<CB>(idx, p[0]);
+        w = lut_entry<CB>(idx, p[1]);
+    }
+    if (rot.rotate) {
+        u = derotate(u, rot.cu, rot.su);
+        w = derotate(w, rot.cw, rot.sw);
+    }
+    out[rb * 32 + idx] = cvt_pk(u.x, u.y);
+    out[rb * 32 + 16 + idx] = cvt_pk(w.x, w.y);
+}
+
 // Fused weight A_q [2N, 2K] from the native blob (same decode as the GEMM).
 template <int CB>
 __global__ void wide_decode_kernel(const uint8_t* __restrict__ codes, const float4* __restrict__ params,
@@ -989,11 +1017,31 @@ hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, i
     return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 4, bits, y, ydt, s);
 }
 
-hipError_t launch_wide_pack_adjoint(const WideGeom& g, const void* packed, void* adjoint, hipStream_t s) {
+template <int CB>
+static void launch_adjoint_lut(const WideGeom& g, const float4* params, const RotParams& rot, uint32_t* out,
+                               hipStream_t s) {
+    const int64_t total = g.NT * 32 * g.nblk * 16;
+    hipLaunchKernelGGL(wide_adjoint_lut_kernel<CB>, dim3(grid1d(total, 256)), dim3(256), 0, s, params,
+                       g.NT * 32, g.nblk, rot, out);
+}
+
+hipError_t launch_wide_pack_adjoint(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, void* adjoint,
+                                    hipStream_t s) {
     const int64_t blocks = g.NT * g.KS;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(wide_pack_adjoint_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
                        reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<uint32_t*>(adjoint), g.NT, g.KS);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const float4* params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
+    uint32_t* lut = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(adjoint) + wide_adjoint_codes_bytes(g));
+    const RotParams rot = rot_of(d);
+    switch (d.codebook) {
+        case RPFQ_CB_SIGN: launch_adjoint_lut<RPFQ_CB_SIGN>(g, params, rot, lut, s); break;
+        case RPFQ_CB_PSK16: launch_adjoint_lut<RPFQ_CB_PSK16>(g, params, rot, lut, s); break;
+        case RPFQ_CB_TABLE: launch_adjoint_lut<RPFQ_CB_TABLE>(g, params, rot, lut, s); break;
+        default: launch_adjoint_lut<RPFQ_CB_AXIS>(g, params, rot, lut, s); break;
+    }
     return hipGetLastError();
 }
 

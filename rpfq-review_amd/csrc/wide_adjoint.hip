@@ -4,14 +4,10 @@
 // reference's Triton autograd).  Register-staged tiles like
 // wide_linear_kernel, with the roles of the two code dimensions exchanged:
 // the output columns are the layer's K' inputs and the k-loop runs over row
-// steps of 32 layer rows, whose codes come from the adjoint code tiles and
-// whose U / W values are rebuilt into LDS every row step.  Compiled once per
-// codebook (RPFQ_CB_SEL).
+// steps of 32 layer rows, whose codes and U / W tables come from the adjoint
+// blob (rpfq_wide_pack_adjoint).  Codebook-independent: the tables hold
+// every codebook's entries as fp16 pairs.
 #include "rpfq_device.h"
-
-#ifndef RPFQ_CB_SEL
-#error "compile once per codebook with -DRPFQ_CB_SEL=<RPFQ_CB_*>"
-#endif
 
 namespace rpfq {
 
@@ -44,15 +40,16 @@ constexpr int adj_lds_bytes(bool per_wave) {
 //     epilogue, so the fp16 operands neither overflow nor flush;
 //   * codes: one 128-bit load per lane from the adjoint tiles: lane group g
 //     gets rows 8 s + 4 g + e of its column, e = 0..3, s = substep;
-//   * U / W: the 32 rows' 16 + 16 entries as fp16 (re, im) pairs in an LDS
-//     table [row][entry] (row stride 40 dwords: the two lane groups, 4 rows
-//     apart, hit disjoint banks), built from the per-row parameters one row
-//     step ahead; one table per workgroup with per-row scales, one per wave
-//     with per-(row, block) scales (a wave's 32 columns lie in one block);
+//   * U / W: the 32 rows' 16 + 16 entries as fp16 (re, im) pairs, copied
+//     from the adjoint blob's tables (4 KB per row step, one 16-B load per
+//     thread, prefetched a step ahead) into an LDS table [row][entry] (row
+//     stride 40 dwords: the two lane groups, 4 rows apart, hit disjoint
+//     banks); one table per workgroup with per-row scales, one per wave with
+//     per-(row, block) scales (a wave's 32 columns lie in one block);
 //   * coefficients (A11, A21) = U + W and (A12, A22) = (Wim - Uim, Ure - Wre),
 //     one v_pk_add_f16 each: the same correctly rounded fp16 adds as the
 //     forward's, so A is bit for bit the forward's operand.
-template <int BM, int GDT, int XDT, int CB>
+template <int BM, int GDT, int XDT>
 __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int MB = BM / 32;
@@ -81,7 +78,7 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     uint4 xbufA[CPT][RAW], xbufB[CPT][RAW];
     uint32_t okA = 0, okB = 0;
     uint4 cA = make_uint4(0, 0, 0, 0), cB = make_uint4(0, 0, 0, 0);
-    float4 pA0, pA1, pB0, pB1;  // LUT parameters of the row step waiting in each buffer
+    uint4 pA, pB;  // (shared table) this thread's 16 B of the row step's table waiting in each buffer
 
     // chunk c = tid + 256 j: gy row c >> 2, complex columns 8 (c & 3) .. +7 of the row step
     auto load_g = [&](int ns, uint4 (&xraw)[CPT][RAW], uint32_t& xok) {
@@ -255,46 +252,27 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     auto load_codes = [&](int ns) -> uint4 {
         return a.codes_t[(((int64_t)ktw_ld * a.NT + ns) * 32 + r) * 2 + g];
     };
-    // LUT jobs.  Shared table (per-row scales): thread tid fills entries
-    // 2 (tid & 7) + {0, 1} of U and W in row tid >> 3.  Per-wave tables
-    // (per-(row, block) scales): lane fills entries 8 (lane & 1) + 0..7 of U
-    // and W in row lane >> 1 for the wave's block.
-    const int lrow = per_wave ? (lane >> 1) : (tid >> 3);
-    const int lj0 = per_wave ? 8 * (lane & 1) : 2 * (tid & 7);
+    // Table copies.  Shared table (per-row scales): thread tid copies dwords
+    // 4 (tid & 7) .. + 3 of row tid >> 3, prefetched with the row step's
+    // other loads.  Per-wave tables (per-(row, block) scales): lane copies
+    // dwords 16 (lane & 1) .. + 15 of row lane >> 1 for the wave's block,
+    // loaded when the table is staged.
     const int64_t lblk = per_wave ? ktw_ld / a.block_ks : 0;
-    auto load_params = [&](int ns, float4& p0, float4& p1) {
-        const int64_t n = (int64_t)ns * 32 + lrow;
-        if constexpr (CB == RPFQ_CB_TABLE) {  // entries lj0, lj0 + 1 of U (p0) and W (p1)
-            const float4* t = reinterpret_cast<const float4*>(reinterpret_cast<const float2*>(a.params) + n * 32);
-            p0 = t[lj0 >> 1];
-            p1 = t[(16 + lj0) >> 1];
-        } else {
-            const float4* p = a.params + (n * a.nblk + lblk) * 2;
-            p0 = p[0];
-            p1 = p[1];
-        }
+    auto load_lut = [&](int ns) -> uint4 {
+        if (per_wave) return make_uint4(0, 0, 0, 0);
+        return a.lut_t[((int64_t)ns * 32 + (tid >> 3)) * 8 + (tid & 7)];
     };
-    auto build = [&](int stage, const float4 p0, const float4 p1) {
-        uint32_t* lut = reinterpret_cast<uint32_t*>(lut_base + stage * lut_stage) +
-                        (per_wave ? wave * kAdjLutWave : 0) + lrow * kAdjLutRow;
-        auto put = [&](int j, float2 u, float2 w) {
-            if (a.rot.rotate) {
-                u = derotate(u, a.rot.cu, a.rot.su);
-                w = derotate(w, a.rot.cw, a.rot.sw);
-            }
-            lut[j] = cvt_pk(u.x, u.y);
-            lut[16 + j] = cvt_pk(w.x, w.y);
-        };
-        if constexpr (CB == RPFQ_CB_TABLE) {
-            put(lj0, make_float2(p0.x, p0.y), make_float2(p1.x, p1.y));
-            put(lj0 + 1, make_float2(p0.z, p0.w), make_float2(p1.z, p1.w));
-        } else if (per_wave) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) put(lj0 + j, lut_entry<CB>(lj0 + j, p0), lut_entry<CB>(lj0 + j, p1));
-        } else {
-            put(lj0, lut_entry<CB>(lj0, p0), lut_entry<CB>(lj0, p1));
-            put(lj0 + 1, lut_entry<CB>(lj0 + 1, p0), lut_entry<CB>(lj0 + 1, p1));
+    auto build = [&](int ns, int stage, const uint4 v) {
+        uint32_t* lut = reinterpret_cast<uint32_t*>(lut_base + stage * lut_stage);
+        if (!per_wave) {
+            *reinterpret_cast<uint4*>(lut + (tid >> 3) * kAdjLutRow + 4 * (tid & 7)) = v;
+            return;
         }
+        const int row = lane >> 1, h = lane & 1;
+        const uint4* src = a.lut_t + (((int64_t)ns * 32 + row) * a.nblk + lblk) * 8 + 4 * h;
+        uint4* dst = reinterpret_cast<uint4*>(lut + wave * kAdjLutWave + row * kAdjLutRow + 16 * h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = src[i];
     };
 
     floatx16 acc_re[MB], acc_im[MB];
@@ -302,29 +280,28 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
     // prologue: row step 0 staged (gy and LUT), row step 1 waiting in registers
-    load_params(0, pA0, pA1);
+    pA = load_lut(0);
     load_g(0, xbufA, okA);
     cA = load_codes(0);
     {
         const int n1 = a.NT > 1 ? 1 : 0;
         load_g(n1, xbufB, okB);
         cB = load_codes(n1);
-        load_params(n1, pB0, pB1);
+        pB = load_lut(n1);
     }
-    build(0, pA0, pA1);
+    build(0, 0, pA);
     store_g(0, xbufA, okA);
     __syncthreads();
 
     // One row step: prefetch row step ns+2 into `fill`, run the MFMAs of ns,
     // stage row step ns+1 (waiting in `next`) into the other LDS buffers.
-    auto step = [&](int ns, const uint4 cw, uint4 (&next)[CPT][RAW], uint32_t next_ok, const float4 np0,
-                    const float4 np1, uint4 (&fill)[CPT][RAW], uint32_t& fill_ok, uint4& fill_codes, float4& fp0,
-                    float4& fp1) {
+    auto step = [&](int ns, const uint4 cw, uint4 (&next)[CPT][RAW], uint32_t next_ok, const uint4 nlut,
+                    uint4 (&fill)[CPT][RAW], uint32_t& fill_ok, uint4& fill_codes, uint4& flut) {
         {
             const int np = ns + 2 < a.NT ? ns + 2 : a.NT - 1;
             load_g(np, fill, fill_ok);
             fill_codes = load_codes(np);
-            load_params(np, fp0, fp1);
+            flut = load_lut(np);
         }
         const char* xs = base + (ns & 1) * XSTAGE;
         const uint32_t* lut = reinterpret_cast<const uint32_t*>(lut_base + (ns & 1) * lut_stage) +
@@ -361,16 +338,16 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
         }
         if (ns + 1 < a.NT) {
             store_g((ns + 1) & 1, next, next_ok);
-            build((ns + 1) & 1, np0, np1);
+            build(ns + 1, (ns + 1) & 1, nlut);
         }
         __syncthreads();
     };
     for (int ns = 0; ns < a.NT; ns += 2) {
         const uint4 c0 = cA;
-        step(ns, c0, xbufB, okB, pB0, pB1, xbufA, okA, cA, pA0, pA1);
+        step(ns, c0, xbufB, okB, pB, xbufA, okA, cA, pA);
         if (ns + 1 < a.NT) {
             const uint4 c1 = cB;
-            step(ns + 1, c1, xbufA, okA, pA0, pA1, xbufB, okB, cB, pB0, pB1);
+            step(ns + 1, c1, xbufA, okA, pA, xbufB, okB, cB, pB);
         }
     }
 
@@ -441,43 +418,40 @@ __global__ void __launch_bounds__(256, 2) wide_grad_x_kernel(AdjArgs a) {
     }
 }
 
-template <int BM, int GDT, int XDT, int CB>
+template <int BM, int GDT, int XDT>
 static hipError_t grad_go(AdjArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
-    const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_grad_x_kernel<BM, GDT, XDT, CB>),
+    const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_grad_x_kernel<BM, GDT, XDT>),
                                            adj_lds_bytes<BM>(true), attr_done);
     if (e != hipSuccess) return e;
     const int lds = adj_lds_bytes<BM>(a.nblk > 1);
     a.tiles_m = (int)((a.M + BM - 1) / BM);
     a.tiles_k = (a.KS + 3) / 4;
-    hipLaunchKernelGGL((wide_grad_x_kernel<BM, GDT, XDT, CB>), dim3(a.tiles_m * a.tiles_k), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((wide_grad_x_kernel<BM, GDT, XDT>), dim3(a.tiles_m * a.tiles_k), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
-template <int BM, int GDT, int CB>
+template <int BM, int GDT>
 static hipError_t grad_x_dt(AdjArgs& a, int xdt, hipStream_t s) {
     switch (xdt) {
-        case RPFQ_F32: return grad_go<BM, GDT, RPFQ_F32, CB>(a, s);
-        case RPFQ_F16: return grad_go<BM, GDT, RPFQ_F16, CB>(a, s);
-        default: return grad_go<BM, GDT, RPFQ_BF16, CB>(a, s);
+        case RPFQ_F32: return grad_go<BM, GDT, RPFQ_F32>(a, s);
+        case RPFQ_F16: return grad_go<BM, GDT, RPFQ_F16>(a, s);
+        default: return grad_go<BM, GDT, RPFQ_BF16>(a, s);
     }
 }
 
-template <int BM, int CB>
+template <int BM>
 static hipError_t grad_g16(AdjArgs& a, int gdt, int xdt, hipStream_t s) {
-    if (gdt == RPFQ_F16) return grad_x_dt<BM, RPFQ_F16, CB>(a, xdt, s);
-    return grad_x_dt<BM, RPFQ_BF16, CB>(a, xdt, s);
+    if (gdt == RPFQ_F16) return grad_x_dt<BM, RPFQ_F16>(a, xdt, s);
+    return grad_x_dt<BM, RPFQ_BF16>(a, xdt, s);
 }
 
-template <int CB>
 hipError_t launch_wide_grad_x(AdjArgs& a, int gdt, int xdt, hipStream_t s) {
     // float32 gy takes 64-row tiles: at 128 rows its raw prefetch buffers
     // (8 x 16 B per chunk) push the k-loop past 256 VGPRs and spill
-    if (gdt == RPFQ_F32) return grad_x_dt<64, RPFQ_F32, CB>(a, xdt, s);
-    if (a.M <= 64) return grad_g16<64, CB>(a, gdt, xdt, s);
-    return grad_g16<128, CB>(a, gdt, xdt, s);
+    if (gdt == RPFQ_F32) return grad_x_dt<64, RPFQ_F32>(a, xdt, s);
+    if (a.M <= 64) return grad_g16<64>(a, gdt, xdt, s);
+    return grad_g16<128>(a, gdt, xdt, s);
 }
-
-template hipError_t launch_wide_grad_x<RPFQ_CB_SEL>(AdjArgs&, int, int, hipStream_t);
 
 }  // namespace rpfq

@@ -162,9 +162,8 @@ hipError_t launch_act_quant_wide_linear(const rpfq_wide_desc& d, const WideGeom&
     }
 }
 
-hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
-                                     const void* adjoint, const void* gy, int gdt, int64_t M, void* gx, int xdt,
-                                     hipStream_t s) {
+hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g, const void* adjoint,
+                                     const void* gy, int gdt, int64_t M, void* gx, int xdt, hipStream_t s) {
     AdjArgs a = {};
     a.gy = gy;
     a.M = M;
@@ -175,16 +174,11 @@ hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g,
     a.nblk = (int)g.nblk;
     a.block_ks = (int)g.block_ks;
     a.codes_t = reinterpret_cast<const uint4*>(adjoint);
-    a.params = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed) + g.codes_bytes);
-    a.rot = rot_of(d);
+    a.lut_t = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(adjoint) + wide_adjoint_codes_bytes(g));
     a.gx = gx;
     a.vec_store = (g.K % 8 == 0) && (reinterpret_cast<uintptr_t>(gx) % 16 == 0);
-    switch (d.codebook) {
-        case RPFQ_CB_SIGN: return launch_wide_grad_x<RPFQ_CB_SIGN>(a, gdt, xdt, s);
-        case RPFQ_CB_PSK16: return launch_wide_grad_x<RPFQ_CB_PSK16>(a, gdt, xdt, s);
-        case RPFQ_CB_TABLE: return launch_wide_grad_x<RPFQ_CB_TABLE>(a, gdt, xdt, s);
-        default: return launch_wide_grad_x<RPFQ_CB_AXIS>(a, gdt, xdt, s);
-    }
+    (void)d;
+    return launch_wide_grad_x(a, gdt, xdt, s);
 }
 
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,

@@ -139,7 +139,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_wide_adjoint_bytes.argtypes = [dp]
         lib.rpfq_wide_adjoint_bytes.restype = sz
         lib.rpfq_wide_pack_adjoint.argtypes = [dp, vp, sz, vp, sz, vp]
-        lib.rpfq_wide_linear_grad_x.argtypes = [dp, vp, sz, vp, sz, vp, i32, i64, vp, i32, vp]
+        lib.rpfq_wide_linear_grad_x.argtypes = [dp, vp, sz, vp, i32, i64, vp, i32, vp]
         lib.rpfq_layer_norm_wide_linear.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, ctypes.c_float, vp, vp, i32,
                                                     i32, vp]
         lib.rpfq_layer_norm_wide_linear_fusable.argtypes = [dp, i64, i32, i32, ctypes.POINTER(i32)]

@@ -360,8 +360,9 @@ class PackedWide:
             N.stream_of(x)))
 
     def adjoint(self) -> torch.Tensor:
-        """The adjoint code tiles of this blob (rpfq_wide_pack_adjoint),
-        built on first use and kept with the layer."""
+        """The adjoint blob of this layer (rpfq_wide_pack_adjoint: transposed
+        code tiles and U / W tables), built on first use and kept with the
+        layer."""
         if self._adjoint is None:
             lib = N.load()
             nbytes = lib.rpfq_wide_adjoint_bytes(ctypes.byref(self.desc))
@@ -391,8 +392,8 @@ class PackedWide:
             return gx.reshape(*lead, self.in_features)
         adj = self.adjoint()
         N.check("rpfq_wide_linear_grad_x", N.load().rpfq_wide_linear_grad_x(
-            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), adj.data_ptr(), adj.numel(),
-            g2.data_ptr(), N.dtype_code(g2.dtype), m, gx.data_ptr(), N.dtype_code(out_dtype), N.stream_of(g2)))
+            ctypes.byref(self.desc), adj.data_ptr(), adj.numel(), g2.data_ptr(), N.dtype_code(g2.dtype), m,
+            gx.data_ptr(), N.dtype_code(out_dtype), N.stream_of(g2)))
         return gx.reshape(*lead, self.in_features)
 
     def decode(self, round_fp16: bool = False) -> torch.Tensor:

@@ -340,13 +340,15 @@ def test_wide_linear_kernel_choice():
 
 
 def test_wide_grad_x_geometry_and_argument_errors():
-    """rpfq_wide_adjoint_bytes is one 1 KiB tile per (32-row tile, k-step);
-    rpfq_wide_pack_adjoint and rpfq_wide_linear_grad_x validate every
+    """rpfq_wide_adjoint_bytes is one 1 KiB code tile per (32-row tile,
+    k-step) plus a 128-B U / W table per (row, scale block) of the padded
+    rows; rpfq_wide_pack_adjoint and rpfq_wide_linear_grad_x validate every
     argument on the host before any GPU work."""
     L, N = lib()
     d = _desc(N, n=50, k=48)
-    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(d)) == 2 * 2 * 1024
-    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, n=1536, k=384))) == 48 * 12 * 1024
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(d)) == 2 * 2 * 1024 + 64 * 128
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, n=1536, k=384))) == 48 * 12 * 1024 + 1536 * 128
+    assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, n=64, k=512, block=256))) == 2 * 16 * 1024 + 64 * 2 * 128
     assert L.rpfq_wide_adjoint_bytes(ctypes.byref(_desc(N, k=12))) == 0  # invalid -> 0
     fc2 = _desc(N, n=384, k=1536)
     nbytes = L.rpfq_wide_packed_bytes(ctypes.byref(fc2))
@@ -359,16 +361,15 @@ def test_wide_grad_x_geometry_and_argument_errors():
     assert pack(nb=nbytes - 1) == 2 and pack(ab=abytes - 1) == 2
     assert pack(adj=fake + 16) == 3
 
-    def grad(packed=fake, nb=nbytes, adj=fake, ab=abytes, gy=fake, gdt=1, m=197, gx=fake, xdt=1):
-        return L.rpfq_wide_linear_grad_x(ctypes.byref(fc2), packed, nb, adj, ab, gy, gdt, m, gx, xdt, None)
-    assert grad(packed=None) == 1 and grad(adj=None) == 1 and grad(gy=None) == 1 and grad(gx=None) == 1
+    def grad(adj=fake, ab=abytes, gy=fake, gdt=1, m=197, gx=fake, xdt=1):
+        return L.rpfq_wide_linear_grad_x(ctypes.byref(fc2), adj, ab, gy, gdt, m, gx, xdt, None)
+    assert grad(adj=None) == 1 and grad(gy=None) == 1 and grad(gx=None) == 1
     assert grad(gdt=7) == 5 and grad(xdt=9) == 5
     assert grad(m=0) == 2 and grad(m=(1 << 30) + 1) == 2
-    assert grad(nb=nbytes - 1) == 2 and grad(ab=abytes - 1) == 2
-    assert grad(packed=fake + 128) == 3 and grad(gy=fake + 8) == 3  # N' % 8 == 0: 16-byte rows
+    assert grad(ab=abytes - 1) == 2
+    assert grad(adj=fake + 128) == 3 and grad(gy=fake + 8) == 3  # N' % 8 == 0: 16-byte rows
     assert grad(gx=fake + 1) == 3
-    assert L.rpfq_wide_linear_grad_x(ctypes.byref(_desc(N, k=12)), fake, nbytes, fake, abytes, fake, 1, 4, fake, 1,
-                                     None) == 3
+    assert L.rpfq_wide_linear_grad_x(ctypes.byref(_desc(N, k=12)), fake, abytes, fake, 1, 4, fake, 1, None) == 3
 
 
 def test_act_quant_wide_linear_argument_errors():

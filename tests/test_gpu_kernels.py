@@ -987,16 +987,19 @@ def check_grad_x(gx, gyf, oplanes, codebook, rotation, gy_rel=0.0, out_ulp=0.0):
         float((err / np.maximum(scale, 1e-300)).max())
 
 
-@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[8]],
-                         ids=["96x64", "50x48", "130x512-b256", "table"])
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[6], CASES[7], CASES[8]],
+                         ids=["96x64", "50x48", "130x512-b256", "psk16", "rot", "table"])
 def test_wide_pack_adjoint_layout(case):
-    """The adjoint tiles hold code byte (row n, column k) in tile
-    (k // 32, n // 32), column k % 32, byte 16 g + 4 s + e where
-    n % 32 = 8 s + 4 g + e -- the forward tiles' byte order with rows and
-    columns exchanged -- bit for bit."""
+    """The adjoint blob: code byte (row n, column k) in tile (k // 32,
+    n // 32), column k % 32, byte 16 g + 4 s + e where n % 32 = 8 s + 4 g + e
+    -- the forward tiles' byte order with rows and columns exchanged -- bit
+    for bit; and the U / W tables after the codes: entry (row n, block of k,
+    index of (n, k)) is the fp16 rounding of the oracle's de-rotated U and W
+    of element (n, k), for every element of the layer."""
     r = rng(400)
-    pw, *_ = build_packed(r, case)
-    nt, ks = -(-case[0] // 32), -(-case[1] // 32)
+    pw, oplanes, _, codebook, rotation = build_packed(r, case)
+    n_c, k_c, block = case[0], case[1], case[4]
+    nt, ks = -(-n_c // 32), -(-k_c // 32)
     codes = pw.blob[: nt * ks * 1024].cpu().numpy().reshape(nt, ks, 32, 32)
     b = np.arange(32)
     perm = 8 * ((b >> 2) & 3) + 4 * (b >> 4) + (b & 3)  # index held by byte b of a tile row
@@ -1004,12 +1007,26 @@ def test_wide_pack_adjoint_layout(case):
     for t in range(nt):
         for s in range(ks):
             full[t * 32:(t + 1) * 32, s * 32 + perm] = codes[t, s]
-    adj = pw.adjoint().cpu().numpy().reshape(ks, nt, 32, 32)
-    want = np.zeros_like(adj)
+    adj = pw.adjoint().cpu().numpy()
+    assert adj.size == pw.adjoint().numel()
+    tiles = adj[: nt * ks * 1024].reshape(ks, nt, 32, 32)
+    want = np.zeros_like(tiles)
     for s in range(ks):
         for t in range(nt):
             want[s, t][:, b] = full[t * 32 + perm, s * 32:(s + 1) * 32].T
-    assert np.array_equal(adj, want)
+    assert np.array_equal(tiles, want)
+    nblk = 1 if block == 0 else -(-k_c // block)
+    lut = adj[nt * ks * 1024:].view(np.float16).reshape(nt * 32, nblk, 32, 2)
+    u_re, u_im, w_re, w_im = (np.asarray(v, np.float32).astype(np.float16)
+                              for v in O.wide_parts(oplanes, codebook, rotation))
+    n_idx, k_idx = np.meshgrid(np.arange(n_c), np.arange(k_c), indexing="ij")
+    blk = k_idx // block if block else np.zeros_like(k_idx)
+    cb = full[:n_c, :k_c].astype(np.int64)
+    got_u = lut[n_idx, blk, cb & 15]
+    got_w = lut[n_idx, blk, 16 + (cb >> 4)]
+    for got, re, im in ((got_u, u_re, u_im), (got_w, w_re, w_im)):
+        assert np.array_equal(got[..., 0].view(np.uint16), re.view(np.uint16))
+        assert np.array_equal(got[..., 1].view(np.uint16), im.view(np.uint16))
 
 
 @pytest.mark.parametrize("m", [1, 64, 65, 300])
