@@ -492,9 +492,12 @@ def grad_x_bench(m: int, steps: int) -> int:
     return 0
 
 
-def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: bool, modes=("hip", "torch")):
+def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: bool, modes=("hip", "torch"),
+                amp: bool = False):
     """Quantization-aware training steps of the configured model (float32,
-    rotation at the family default, SGD): forward with every Linear
+    or with amp the forward under fp16 autocast and a gradient scaler as the
+    reference trainer's --amp runs it; rotation at the family default, SGD):
+    forward with every Linear
     quantized from its float32 master weight, backward with straight-through
     gradients, optimizer step.  'hip' runs the weight quantizer and the act
     quant as HIP kernels (rpfq_quantize_wide, rpfq_act_quant); 'hip_pgrad'
@@ -521,11 +524,20 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
         x = torch.randn(batch, 3, img, img, device="cuda", generator=g)
         labels = torch.randint(0, 1000, (batch,), device="cuda", generator=g)
 
+        scaler = torch.amp.GradScaler("cuda") if amp else None
+
         def step():
             opt.zero_grad(set_to_none=True)
-            loss = F.cross_entropy(model(x), labels)
-            loss.backward()
-            opt.step()
+            if scaler is None:
+                loss = F.cross_entropy(model(x), labels)
+                loss.backward()
+                opt.step()
+                return loss
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = F.cross_entropy(model(x), labels)
+            scaler.scale(loss).backward()
+            scaler.step(opt)
+            scaler.update()
             return loss
 
         for _ in range(warmup):
@@ -562,12 +574,14 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
         del model, opt
         torch.cuda.empty_cache()
     quant_i.HIP_QAT = True
-    quant_i.QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "auto")
+    quant_i.QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "0")
     first = out[modes[0]]
-    print(json.dumps({"metric": f"QAT training images/s {desc}, float32, SGD", "value": first["images_per_s"],
+    prec = "fp16 autocast" if amp else "float32"
+    print(json.dumps({"metric": f"QAT training images/s {desc}, {prec}, SGD", "value": first["images_per_s"],
                       "unit": "images/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
                       "ms_per_step": first["ms_per_step"], "higher_is_better": True, "data": "synthetic",
-                      "config": {"workload": cfg_name, "batch": batch, "act_quant": act_quant, "mode": modes[0]},
+                      "config": {"workload": cfg_name, "batch": batch, "act_quant": act_quant, "mode": modes[0],
+                                 "amp": amp},
                       "modes": out}))
     return 0
 
@@ -611,6 +625,7 @@ def main() -> int:
     ap.add_argument("--train", action="store_true",
                     help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
     ap.add_argument("--train-modes", default="hip,hip_pgrad,torch")
+    ap.add_argument("--amp", action="store_true", help="with --train: fp16 autocast forward and a gradient scaler")
     args = ap.parse_args()
     if args.layer_probe:
         return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
@@ -618,7 +633,7 @@ def main() -> int:
         return grad_x_bench(args.batch * 197 if args.batch else 50432, args.steps)
     if args.train:
         return train_bench(args.config, args.batch or 64, args.steps, args.warmup, args.act_quant,
-                           tuple(args.train_modes.split(",")))
+                           tuple(args.train_modes.split(",")), amp=args.amp)
     if args.stream_sweep:
         shapes = None if not args.stream_shapes else set(args.stream_shapes.split(","))
         if shapes and not shapes <= set(STREAM_SHAPES):

@@ -309,12 +309,14 @@ DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
 FUSE_AQ_PROLOGUE = os.environ.get("RPFQ_FUSE_AQ_PROLOGUE", "1") != "0"
 # Input gradient of the HIP training forward on the packed blob of the
 # step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
-# A_q: "auto" for 16-bit activations (the reference's AMP precision class:
-# fp16 operands either way), "1" also for float32 (each grad_y element then
-# carries one fp16 rounding, 2^-11 relative, and the fused fp16
-# coefficients; ~3x faster than the float32 library GEMM on MI355X), "0"
-# never.
-QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "auto")
+# A_q: "1" on (each grad_y element of a float32 step then carries one fp16
+# rounding, 2^-11 relative, and the fused fp16 coefficients replace A_q),
+# "0" (default) off.  Measured on ViT-B/16 bs64, MI355X: float32 steps gain
+# 2-5% (the kernel is ~3x faster than the float32 library GEMM); fp16
+# autocast steps lose 20% (2,042 -> 1,626 images/s: the per-step repack and
+# a host read of each rotated layer's angles cost more than the kernel,
+# which is slower than the library's fp16 GEMM on the decoded weight).
+QAT_PACKED_GRAD = os.environ.get("RPFQ_QAT_PACKED_GRAD", "0")
 
 _HIP_KINDS = {
     "complex_phase_v1": ("axis", 1),
@@ -506,10 +508,9 @@ class QATLinearComplexPhase(nn.Linear):
             return None
         return ku + kw
 
-    def _packed_grad(self, x: torch.Tensor) -> bool:
-        if QAT_PACKED_GRAD == "0" or not torch.is_grad_enabled():
-            return False
-        return QAT_PACKED_GRAD == "1" or x.dtype in (torch.float16, torch.bfloat16) or torch.is_autocast_enabled()
+    @staticmethod
+    def _packed_grad() -> bool:
+        return QAT_PACKED_GRAD == "1" and torch.is_grad_enabled()
 
     def _qat_forward_packed_grad(self, x: torch.Tensor, spec) -> torch.Tensor:
         """The HIP training forward with the input gradient on the packed
@@ -539,7 +540,7 @@ class QATLinearComplexPhase(nn.Linear):
 
     def _qat_forward(self, x: torch.Tensor) -> torch.Tensor:
         spec = self._hip_qat_spec(x)
-        if spec is not None and spec[0] == spec[2] and spec[1] == spec[3] and self._packed_grad(x):
+        if spec is not None and spec[0] == spec[2] and spec[1] == spec[3] and self._packed_grad():
             return self._qat_forward_packed_grad(x, spec)
         if spec is not None:
             q_weight = _HipWideQuantSTE.apply(self.weight, self.quantizer_u.rotation_angle,
