@@ -407,6 +407,7 @@ def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, r
                 rows.append(row)
                 print(json.dumps(row), flush=True)
     if out:
+        os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
         with open(out, "w") as f:
             json.dump(rows, f, indent=1)
     return rows

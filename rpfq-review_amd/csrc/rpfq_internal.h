@@ -152,7 +152,7 @@ template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int
 inline int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
 
 // Streaming launches (M <= 8) that take the column-split kernel: for many
-// tiles (>= 4096, one workgroup per 64 rows) when K' spans >= 14 k-steps,
+// tiles (>= 4096, one workgroup per 64 rows) when K' spans >= 12 k-steps,
 // and for few tiles (split K) when it spans fewer than 20.  Measured per
 // launch at M = 1 / 8 on MI355X: N' stacked to 1 GiB of codes, K' = 1536:
 // 317 / 396 us vs 355 / 460 us (fused kernel); K' = 2048: 303 / 386 vs
@@ -160,16 +160,21 @@ inline int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
 // 446 / 554.  Single ViT layers: K' = 384, N' = 1536: 4.98 / 5.81 vs
 // 5.46 / 5.86 us; K' = 1536, N' = 384: 9.21 / 10.39 vs 8.88 / 9.26 us.
 // (A persistent single-wave form that streams codes across row groups
-// measured 10-40% slower than both.)
+// measured 10-40% slower than both.)  Below 16 k-steps the many-tile form
+// runs one wave per 64 rows instead of two (each wave then walks all of
+// K'): K' = 384 at M = 1 / 4, 1 GiB stacked, 431 / 409 us against 455 / 510
+// (two waves) and 440 / 473 (fused kernel); K' = 512 352 / 386 against
+// 343 / 385; K' = 1536 325 / 348 against 299 / 342, so longer K' keeps two.
 // Streaming workgroups: split K over 4 waves below kSkNw2Groups, over 2 up
-// to kSkSplitTiles, one wave per tile (the column-split kernel: 2 waves per
-// 64 rows) from there.
+// to kSkSplitTiles, one wave per tile (the column-split kernel: 1 or 2
+// waves per 64 rows, above) from there.
 constexpr int64_t kSkNw2Groups = 400, kSkSplitTiles = 4096;
 constexpr int kGemvMaxM = 8;
 inline bool gemv_pays(const WideArgs& a) {
     if (a.M > kGemvMaxM || a.nblk > 1) return false;
-    return a.NT >= kSkSplitTiles ? a.KS >= 14 : a.KS < 20;
+    return a.NT >= kSkSplitTiles ? a.KS >= 12 : a.KS < 20;
 }
+inline bool gemv_single_wave(const WideArgs& a) { return a.NT >= kSkSplitTiles && a.KS < 16; }
 
 // launchers (rpfq_kernels.hip); return hipError_t
 hipError_t launch_unpack(const uint8_t* codes, int bits, int64_t rows, int64_t k,

@@ -893,9 +893,11 @@ static hipError_t wide_sk_ln_go(WideArgs& a, hipStream_t s) {
 // 2 from there (less LUT building and reduction per k-step once the groups
 // alone fill the SIMDs; ViT-B/16 batch-1 forward 0.834 -> 0.772 ms, and 2
 // waves already from 128 groups measured slower); a long stream of tiles
-// runs one wave each (the column-split kernel: 2 waves per 64 rows).
+// runs one wave each (the column-split kernel: 2 waves per 64 rows, or 1
+// below 16 k-steps).
 template <int XDT, int YDT, int CB, bool KT>
 static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
+    if (gemv_single_wave(a)) return wide_gv_go<XDT, YDT, CB, KT, 1, 4>(a, s);
     if (a.NT >= kSkSplitTiles) return wide_gv_go<XDT, YDT, CB, KT, 2, 4>(a, s);
     if (a.NT >= kSkNw2Groups) return wide_gv_go<XDT, YDT, CB, KT, 2, 2>(a, s);
     return wide_gv_go<XDT, YDT, CB, KT, 4, 2>(a, s);

@@ -537,16 +537,18 @@ def test_wide_linear_streaming_dtypes(xdt, ydt, m, k_c):
 
 @pytest.mark.parametrize("m,n_c,k_c", [(8, 66000, 96), (2, 70000, 64), (16, 16500, 640), (3, 16500, 200),
                                        (4, 3000, 2048), (2, 131104, 64), (12, 131072, 96), (1, 131200, 200),
-                                       (2, 131104, 640), (5, 131072, 648)])
+                                       (2, 131104, 640), (5, 131072, 648), (1, 131072, 384), (6, 131104, 416),
+                                       (3, 131072, 456)])
 def test_wide_linear_streaming_persistent(m, n_c, k_c):
     """Large N' on the streaming kernels' forms: split K over 2 waves per
     tile for 400 .. 4095 workgroups (66000 x 96 at M = 8: 2063 tiles;
     70000 x 64: 2188; 16500 x 640: 516; 16500 x 200: 516 with a K' tail),
     over 4 waves below 400 (3000 x 2048: 94 tiles, 64 k-steps), one wave per
     tile from 4096 tiles (131,072+ rows at short K'), and the column-split
-    kernel's 64-row workgroups of 2 waves from 4096 tiles at >= 20 k-steps
+    kernel's 64-row workgroups from 4096 tiles: 2 waves at >= 16 k-steps
     (131104 x 640: an odd tile count, the last workgroup's second tile
-    clamped; 131072 x 648: a K' tail).  Each launch against the exact product
+    clamped; 131072 x 648: a K' tail), 1 wave at 12 .. 15 (131072 x 384;
+    131104 x 416: odd tile count; 131072 x 456: a K' tail).  Each launch against the exact product
     of the operand it contracts (float32 outputs, float32 accumulation
     order), and the tiled kernel (RPFQ_FLAG_NO_STREAM) likewise."""
     ops, N = qm()
