@@ -328,8 +328,10 @@ def test_wide_linear_kernel_choice():
     assert kernel(8, flags=N.FLAG_STREAM) == N.KERNEL_GEMV
     d_long = _desc(N, n=384, k=1536)  # ViT-B fc2: 12 tiles of 48 k-steps
     d_many = _desc(N, n=131072, k=1536)  # 4096 tiles
-    d_many_short = _desc(N, n=131072, k=384)
-    for dd, want in ((d_long, N.KERNEL_STREAM), (d_many, N.KERNEL_GEMV), (d_many_short, N.KERNEL_STREAM)):
+    d_many_mid = _desc(N, n=131072, k=384)  # 12 k-steps: the one-wave column-split form
+    d_many_short = _desc(N, n=131072, k=256)
+    for dd, want in ((d_long, N.KERNEL_STREAM), (d_many, N.KERNEL_GEMV), (d_many_mid, N.KERNEL_GEMV),
+                     (d_many_short, N.KERNEL_STREAM)):
         out = ctypes.c_int32(-1)
         assert L.rpfq_wide_linear_kernel(ctypes.byref(dd), 1, 1, 1, 0, ctypes.byref(out)) == 0
         assert out.value == want, (dd.n_complex, dd.k_complex, out.value)
