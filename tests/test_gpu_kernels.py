@@ -574,6 +574,29 @@ def test_wide_linear_streaming_persistent(m, n_c, k_c):
     assert np.all(np.abs(y0 - (xf @ a_op.T + b)) <= 1e-5 * scale + 1e-5)
 
 
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float32, torch.float16)])
+def test_wide_linear_gemv_one_wave_dtypes(xdt, ydt):
+    """The column-split kernel's one-wave many-tile form (>= 4096 tiles at
+    12-15 k-steps: 131104 x 384, an odd tile count) with float32 and bf16
+    activations (fp16 on load) and each output dtype, against the oracle on
+    the split operand it contracts."""
+    ops, N = qm()
+    r = rng(1300)
+    n_c, k_c, m = 131104, 384, 2
+    planes_np, packed, sre, sim, kinds, cb, nblk = make_wide(r, n_c, k_c)
+    pw = ops.PackedWide.from_planes([tdev(p) for p in packed], [tdev(s) for s in sre], [tdev(s) for s in sim],
+                                    n_c, k_c, cb, 2, 0, None)
+    assert pw.kernel_for(m, xdt, ydt) == N.KERNEL_GEMV
+    x = torch.from_numpy(r.standard_normal((m, 2 * k_c)).astype(np.float32)).to(xdt)
+    bias = r.standard_normal(2 * n_c).astype(np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=ydt).float().cpu().numpy()
+    xf = x.float().to(torch.float16).float().numpy().astype(np.float64)
+    out_ulp = {torch.float32: 1e-6, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
+    check_against_oracle(y, xf, bias, oracle_planes(planes_np, sre, sim, kinds, k_c, 0), "axis", None, out_ulp,
+                         fp16="split")
+
+
 # ---------------------------------------------------------------------------
 # fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
 # followed by the add in y's dtype, on every kernel path
