@@ -441,6 +441,57 @@ def layer_probe(n_c: int, k_c: int, m: int, steps: int) -> int:
 GRAD_SHAPES = (("qkv", 1152, 384), ("proj", 384, 384), ("fc1", 1536, 384), ("fc2", 384, 1536))
 
 
+def vs_library_bench(m: int, steps: int) -> int:
+    """The forward of the ViT-B/16 q2 layer shapes at m rows (default bs256
+    x 197 tokens): the packed kernel (rpfq_wide_linear, fp16 in and out,
+    float32 bias) against the dense library GEMM on the same layer's decoded
+    fp16 coefficients (F.linear with the bias, hipBLASLt), on the same box,
+    alternating (packed, library) twice per shape; HIP events over `steps`
+    calls each; prints one JSON line."""
+    import torch
+    import torch.nn.functional as F
+
+    def timed(fn):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    rows = {}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for name, n_c, k_c in GRAD_SHAPES:
+        pw = stream_layer(k_c, n_c, 1)[0]
+        a16 = pw.decode(round_fp16=True).half()
+        x = torch.randn(m, 2 * k_c, device="cuda", generator=g).half()
+        bias = torch.randn(2 * n_c, device="cuda", generator=g) * 0.1
+        b16 = bias.half()
+        y = torch.empty(m, 2 * n_c, device="cuda", dtype=torch.float16)
+        packed, dense = [], []
+        for _ in range(2):
+            packed.append(timed(lambda: pw.linear_into(x, bias, y)))
+            dense.append(timed(lambda: F.linear(x, a16, b16)))
+        flops = 2 * m * 2 * n_c * 2 * k_c
+        row = {"n_complex": n_c, "k_complex": k_c, "packed_us": round(sum(packed) / 2, 1),
+               "library_us": round(sum(dense) / 2, 1),
+               "packed_tflops": round(flops / (sum(packed) / 2) / 1e6, 1),
+               "library_tflops": round(flops / (sum(dense) / 2) / 1e6, 1)}
+        rows[name] = row
+        print(f"# vs library {name}: {row}", file=sys.stderr, flush=True)
+        del pw, a16, x, y
+        torch.cuda.empty_cache()
+    tot = sum(r["packed_us"] for r in rows.values())
+    lib = sum(r["library_us"] for r in rows.values())
+    print(json.dumps({"metric": "ViT-B/16 q2 layer forward, packed kernel vs dense library GEMM on the decoded weight",
+                      "m": m, "steps": steps, "block_packed_us": round(tot, 1), "block_library_us": round(lib, 1),
+                      "layers": rows}))
+    return 0
+
+
 def grad_x_bench(m: int, steps: int) -> int:
     """Input gradient of the ViT-B/16 q2 layers at m rows (default bs256 x
     197 tokens) on the packed blob (rpfq_wide_linear_grad_x) against the
@@ -621,6 +672,9 @@ def main() -> int:
     ap.add_argument("--layer-probe", default=None, metavar="NC,KC",
                     help="time one q2 layer of N' x K' complex (random codes) on 50,432 fp16 rows instead "
                          "(--steps launches; for counter runs)")
+    ap.add_argument("--vs-library", action="store_true",
+                    help="only time the ViT-B/16 layer forwards on the packed kernel against the dense library GEMM "
+                         "on the decoded weight (same box)")
     ap.add_argument("--grad-x", action="store_true",
                     help="time the packed input gradient (rpfq_wide_linear_grad_x) on the ViT-B layer shapes")
     ap.add_argument("--train", action="store_true",
@@ -632,6 +686,8 @@ def main() -> int:
         return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
     if args.grad_x:
         return grad_x_bench(args.batch * 197 if args.batch else 50432, args.steps)
+    if args.vs_library:
+        return vs_library_bench(args.batch * 197 if args.batch else 50432, args.steps)
     if args.train:
         return train_bench(args.config, args.batch or 64, args.steps, args.warmup, args.act_quant,
                            tuple(args.train_modes.split(",")), amp=args.amp)
