@@ -446,8 +446,9 @@ def vs_library_bench(m: int, steps: int) -> int:
     x 197 tokens): the packed kernel (rpfq_wide_linear, fp16 in and out,
     float32 bias) against the dense library GEMM on the same layer's decoded
     fp16 coefficients (F.linear with the bias, hipBLASLt), on the same box,
-    alternating (packed, library) twice per shape; HIP events over `steps`
-    calls each; prints one JSON line."""
+    alternating (packed, library) per shape; HIP events over `steps`
+    calls each (both warmed first; medians of three alternations); prints
+    one JSON line."""
     import torch
     import torch.nn.functional as F
 
@@ -471,15 +472,17 @@ def vs_library_bench(m: int, steps: int) -> int:
         bias = torch.randn(2 * n_c, device="cuda", generator=g) * 0.1
         b16 = bias.half()
         y = torch.empty(m, 2 * n_c, device="cuda", dtype=torch.float16)
+        for _ in range(steps):  # warm clocks and caches for both before timing
+            pw.linear_into(x, bias, y)
+            F.linear(x, a16, b16)
         packed, dense = [], []
-        for _ in range(2):
+        for _ in range(3):
             packed.append(timed(lambda: pw.linear_into(x, bias, y)))
             dense.append(timed(lambda: F.linear(x, a16, b16)))
+        us_p, us_d = sorted(packed)[1], sorted(dense)[1]  # medians of the three alternations
         flops = 2 * m * 2 * n_c * 2 * k_c
-        row = {"n_complex": n_c, "k_complex": k_c, "packed_us": round(sum(packed) / 2, 1),
-               "library_us": round(sum(dense) / 2, 1),
-               "packed_tflops": round(flops / (sum(packed) / 2) / 1e6, 1),
-               "library_tflops": round(flops / (sum(dense) / 2) / 1e6, 1)}
+        row = {"n_complex": n_c, "k_complex": k_c, "packed_us": round(us_p, 1), "library_us": round(us_d, 1),
+               "packed_tflops": round(flops / us_p / 1e6, 1), "library_tflops": round(flops / us_d / 1e6, 1)}
         rows[name] = row
         print(f"# vs library {name}: {row}", file=sys.stderr, flush=True)
         del pw, a16, x, y
