@@ -799,7 +799,7 @@ AQ_CASES = [LN_CASES[0], LN_CASES[2], LN_CASES[3], LN_CASES[4], LN_CASES[5]]
 
 
 @pytest.mark.parametrize("layer_norm", [False, True], ids=["aq", "ln-aq"])
-@pytest.mark.parametrize("bits", [4, 8, 2])
+@pytest.mark.parametrize("bits", [4, 8, 2, 16])
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [9, 197])
 @pytest.mark.parametrize("case", AQ_CASES, ids=[f"{c[0]}x{c[1]}-{c[2]}" for c in AQ_CASES])
