@@ -327,7 +327,9 @@ int rpfq_wide_linear_grad_x(const rpfq_wide_desc* desc, const void* adjoint, siz
         return fail(RPFQ_ERR_ALIGN, "grad_y must be 16-byte aligned");
     if (!aligned(grad_y, esize) || !aligned(grad_x, grad_x_dtype == RPFQ_F32 ? 4 : 2))
         return fail(RPFQ_ERR_ALIGN, "grad_y / grad_x must be aligned to their element size");
-    const int64_t tiles = ((M + 127) / 128) * ((g.KS + 3) / 4);
+    // the launcher takes 64-row tiles for float32 grad_y and M <= 64, 128 otherwise:
+    // count the smaller tile so the grid size fits an int either way
+    const int64_t tiles = ((M + 63) / 64) * ((g.KS + 3) / 4);
     if (tiles > 0x7fffffffLL) return fail(RPFQ_ERR_SHAPE, "M=%lld: too many tiles", (long long)M);
     return hip_status(rpfq::launch_wide_linear_grad_x(*desc, g, adjoint, grad_y, grad_y_dtype, M, grad_x, grad_x_dtype,
                                                       reinterpret_cast<hipStream_t>(stream)),

@@ -197,6 +197,18 @@ int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, in
 // DeiT-Ti and Swin-T layers at batch 1 gain (0.775 -> 0.712, 0.598 -> 0.502,
 // 1.024 -> 0.985 ms per forward); ViT-L's K' = 512 lost (1.75 -> 1.96 ms).
 constexpr int kLnMaxK = 384;
+// Lanes per row of the LayerNorm row kernel (layer_norm_kernel, modes 1-4)
+// for M rows of C features: the smallest of 8, 16, 32, 64 that keeps every
+// lane at <= 4 chunks of 8 (C <= 2048), and 64 whenever that choice would
+// launch fewer than 256 workgroups (M * lanes < 65,536) or C > 1024.  The
+// fused row prologue of the streaming kernel sums the LayerNorm statistics
+// in the 64-lane order, so it is bit-identical to the row kernel only where
+// this returns 64.
+inline int ln_row_lanes(int64_t M, int64_t C) {
+    const int64_t nch = C / 8;
+    const int tpr = nch <= 32 ? 8 : nch <= 64 ? 16 : nch <= 128 ? 32 : 64;
+    return (nch <= 256 && tpr < 64 && M * tpr < 256 * 256) ? 64 : tpr;
+}
 bool layer_norm_wide_fusable(const WideGeom& g, int xdt, int64_t M, int ydt, int codebook);
 hipError_t launch_layer_norm_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
                                          const void* x, int xdt, int64_t M, const float* gamma, const float* beta,

@@ -479,9 +479,9 @@ __device__ __forceinline__ float load1(const void* base, int64_t off) {
 // One 256-thread workgroup per row; each half [0, K) and [K, 2K) gets its own
 // scale = qmax * (1 / max(max|x|, 1e-5)) and x_hat = clamp(rint(x scale)) / scale,
 // all in float32 (rint = round half to even, as torch.round).
+// x and y may be the same buffer (in-place act quant): neither is __restrict__.
 template <int XDT, int YDT>
-__global__ void __launch_bounds__(256) act_quant_kernel(const void* __restrict__ x, int64_t K, int bits,
-                                                        void* __restrict__ y) {
+__global__ void __launch_bounds__(256) act_quant_kernel(const void* x, int64_t K, int bits, void* y) {
     __shared__ float red[2][4];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -579,7 +579,7 @@ __device__ __forceinline__ float group_max(float v) {
 // Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
 // the two halves.
 template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ, bool GE = false>
-__global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict__ x, int64_t M, int C,
+__global__ void __launch_bounds__(256) layer_norm_kernel(const void* x, int64_t M, int C,  // y may equal x
                                                          const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float eps, int bits,
                                                          void* y) {
@@ -740,7 +740,7 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* __restrict_
 // 16 elements each.  Every output is computed per element and the per-half
 // maxima are exact, so the result is bit-identical to the 64-lane form.
 template <int XDT, int YDT, bool GE>
-__global__ void __launch_bounds__(256) row_aq_block_kernel(const void* __restrict__ x, int C, int bits, void* y) {
+__global__ void __launch_bounds__(256) row_aq_block_kernel(const void* x, int C, int bits, void* y) {  // y may equal x
     __shared__ float red[2][4];
     constexpr int NC = 2;  // C <= 4096: 512 chunks of 8 over 256 lanes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -956,8 +956,7 @@ template <int XDT, int YDT>
 static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
                         int mode, int bits, void* y, hipStream_t s) {
     const int nch = C / 8;
-    const int tpr = nch <= 32 ? 8 : nch <= 64 ? 16 : nch <= 128 ? 32 : 64;
-    if (nch <= 256 && tpr < 64 && M * tpr < 256 * 256)
+    if (nch <= 256 && ln_row_lanes(M, C) == 64)
         return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
     if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
     if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);

@@ -93,11 +93,14 @@ static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
 
 // The fused LayerNorm runs in the streaming kernel split over 4 waves (for
 // launches of fewer than kSkSplitTiles workgroups: a layer at batch 1-2), per-row scales,
-// K' % 32 == 0 and K' <= kLnMaxK, fp16 / bf16 x, not the TABLE codebook.
+// K' % 32 == 0 and K' <= kLnMaxK, fp16 / bf16 x, not the TABLE codebook, and
+// only where the row kernel would also sum the statistics over 64 lanes per
+// row (ln_row_lanes), so the prepared rows stay bit-identical to it.
 bool layer_norm_wide_fusable(const WideGeom& g, int xdt, int64_t M, int ydt, int codebook) {
     const WideArgs a = wide_shape(g, M, 0);
     return choose_kernel(a, xdt, ydt, 0) == RPFQ_KERNEL_STREAM && sk_groups(a) < kSkSplitTiles && a.nblk == 1 &&
-           a.K % 32 == 0 && a.K <= kLnMaxK && (xdt == RPFQ_F16 || xdt == RPFQ_BF16) && codebook != RPFQ_CB_TABLE;
+           a.K % 32 == 0 && a.K <= kLnMaxK && (xdt == RPFQ_F16 || xdt == RPFQ_BF16) && codebook != RPFQ_CB_TABLE &&
+           ln_row_lanes(M, 2 * a.K) == 64;
 }
 
 int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags) {

@@ -462,6 +462,24 @@ class _PackedLinearFn(torch.autograd.Function):
         return gx, gb, None
 
 
+def records_grad(module: nn.Module, x: torch.Tensor) -> bool:
+    """Autograd records a call of `module` on x: grad mode is on and x or
+    one of the module's parameters requires a gradient.  The fused inference
+    kernels (LayerNorm, act quant, GELU, residual stores) have no backward,
+    so every caller that picks them checks this one predicate."""
+    return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters()))
+
+
+def _linear(x: torch.Tensor, q_weight: torch.Tensor, bias):
+    """F.linear(x, A_q, bias) (quant_i.py:554).  Reduced-precision x outside
+    autocast meets A_q and the bias cast to x's dtype, as autocast casts
+    them (autograd flows through the casts)."""
+    if x.dtype != q_weight.dtype and not torch.is_autocast_enabled(x.device.type):
+        q_weight = q_weight.to(x.dtype)
+        bias = None if bias is None else bias.to(x.dtype)
+    return F.linear(x, q_weight, bias)
+
+
 class QATLinearComplexPhase(nn.Linear):
     """Complex-structured quantized linear layer (quant_i.py:475-554).
 
@@ -551,13 +569,13 @@ class QATLinearComplexPhase(nn.Linear):
                 else:  # reduced-precision activations: the reference's per-op rounding
                     h = self.in_features // 2
                     x = torch.cat(self.act_quantizer(x[..., :h], x[..., h:]), dim=-1)
-            return F.linear(x, q_weight, self.bias)
+            return _linear(x, q_weight, self.bias)
         q_weight = self.quantized_weight()
         if self.act_quantizer is not None:
             h = self.in_features // 2
             qr, qi = self.act_quantizer(x[..., :h], x[..., h:])
             x = torch.cat((qr, qi), dim=-1)
-        return F.linear(x, q_weight, self.bias)
+        return _linear(x, q_weight, self.bias)
 
     # -- packed HIP path ------------------------------------------------------
     def load_packed(self, codes: "P.LayerCodes") -> None:
@@ -623,13 +641,31 @@ class QATLinearComplexPhase(nn.Linear):
                 vs.append((p.data_ptr(), p._version))
         return tuple(vs)
 
+    def _weights_need_grad(self) -> bool:
+        """A parameter the packed blob is derived from (the float32 weight,
+        the rotation angles, the learned phase tables) requires a gradient.
+        Codes supplied through load_packed are not derived from them, so such
+        a layer's weights get no gradient from its output."""
+        if self._override is not None:
+            return False
+        return any(p.requires_grad for name, p in self.named_parameters() if name != "bias")
+
     def _records_grad(self, x: torch.Tensor) -> bool:
-        """Autograd records this call: x or the bias needs a gradient."""
-        return torch.is_grad_enabled() and (x.requires_grad or (self.bias is not None and self.bias.requires_grad))
+        """Autograd records this call: x or a parameter needs a gradient
+        (records_grad, shared with the model-level fused-block predicate)."""
+        return records_grad(self, x)
 
     def _packed_forward(self, x: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         from . import ops
 
+        if prequantized and self._records_grad(x):
+            raise RuntimeError("forward_prequantized under autograd: the fused act quant has no gradient")
+        if torch.is_grad_enabled() and self._weights_need_grad():
+            # The reference's forward is the same straight-through formulation
+            # in eval as in training (quant_i.py:513-554), so the weight and
+            # rotation angles get their gradients; the packed blob is a
+            # constant of the weight and could give them none.
+            return self._qat_forward(x)
         pw = self.packed(x.device)
         if self._records_grad(x):
             if self.act_quantizer is not None and not prequantized:
@@ -650,9 +686,11 @@ class QATLinearComplexPhase(nn.Linear):
         return FUSE_AQ_PROLOGUE and hasattr(pw, "ln_fusable") and m > 0 and pw.ln_fusable(m, x.dtype)
 
     def packed_act_bits(self, x: torch.Tensor) -> int:
-        """Bits of the activation quantization the packed path would apply to
-        x (0 if none or if x does not take the packed path)."""
-        if self.act_quantizer is None or not (x.is_cuda and not self.training and self.use_packed):
+        """Bits of the activation quantization the packed inference path would
+        apply to x (0 if none, if x does not take the packed path, or if
+        autograd records the call: the fused kernels have no backward)."""
+        if self.act_quantizer is None or not (x.is_cuda and not self.training and self.use_packed) \
+                or self._records_grad(x):
             return 0
         return self.act_quantizer.num_bits
 

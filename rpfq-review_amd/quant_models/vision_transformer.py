@@ -18,6 +18,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .quant_i import records_grad
+
 # Eval-mode device forward of a block uses the fused kernels: LayerNorm on the
 # HIP kernel and the residual add after attn.proj / mlp.fc2 fused into the
 # packed layer's store.  RPFQ_FUSED=0 keeps the module-by-module forward.
@@ -36,10 +38,14 @@ FUSE_LN = os.environ.get("RPFQ_FUSE_LN", "1") != "0"
 
 def _fused(module: nn.Module, x: torch.Tensor) -> bool:
     """Whether the fused inference kernels run: eval-mode device tensors that
-    no gradient has to flow through (with autograd recording, the blocks run
-    module by module: torch's LayerNorm and GELU, the packed layers with
-    their input gradient on the device)."""
-    return FUSED_BLOCKS and x.is_cuda and not module.training and not (torch.is_grad_enabled() and x.requires_grad)
+    autograd does not record (records_grad: grad mode on and x or a
+    parameter of the module requiring a gradient).  Under autograd the blocks
+    run module by module: torch's LayerNorm and GELU, and each packed layer
+    either the reference formulation (weights requiring gradients) or the
+    packed kernels with the input gradient on the device (frozen weights).
+    Inference therefore runs under torch.no_grad() / torch.inference_mode(),
+    as the reference's validation loop does, or on frozen parameters."""
+    return FUSED_BLOCKS and x.is_cuda and not module.training and not records_grad(module, x)
 
 
 def norm_fwd(norm: nn.Module, x: torch.Tensor) -> torch.Tensor:

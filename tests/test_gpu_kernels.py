@@ -868,6 +868,30 @@ def test_layer_norm_wide_linear_refuses_unfusable():
         pw.layer_norm_linear(x.float(), None, None, 1e-6)
 
 
+def test_ln_fusable_follows_row_kernel_lanes():
+    """The fused prologue sums the LayerNorm statistics over 64 lanes per row;
+    the row kernel takes 32 lanes for C = 768 from M = 2,048 rows (M x 32 >=
+    65,536), so a narrow layer that still streams there (K' = 384, N' = 64)
+    is fusable at M = 2,047 -- LayerNorm + act quant rows bit-identical to
+    rpfq_layer_norm_act_quant, the output within float32 accumulation of the
+    oracle on them -- and refused at M = 2,048."""
+    ops, N = qm()
+    case = (64, 384, "axis", 2, 0, None)
+    r = rng(1960)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    assert not pw.ln_fusable(2048, torch.float16)
+    assert pw.ln_fusable(2047, torch.float16)
+    m, c2 = 2047, 768
+    x = torch.from_numpy((r.standard_normal((m, c2)) * 3 + 1).astype(np.float32)).to(torch.float16).to(DEV)
+    g = tdev(r.standard_normal(c2).astype(np.float32))
+    b = tdev(r.standard_normal(c2).astype(np.float32))
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    h = ops.layer_norm(x, g, b, 1e-6, act_bits=4)
+    hf = h.float().cpu().numpy().astype(np.float64)
+    y = pw.act_quant_linear(x, 4, bias, out_dtype=torch.float32, layer_norm=(g, b, 1e-6)).cpu().numpy()
+    check_against_oracle(y, hf, bias.cpu().numpy().astype(np.float64), oplanes, codebook, rotation)
+
+
 @pytest.mark.parametrize("m,c", [(3, 96), (300, 768), (17, 1024), (5, 3072)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32),
                                      (torch.bfloat16, torch.bfloat16)])

@@ -116,8 +116,13 @@ def test_packed_layer_input_gradient(golden, method, act):
     the reference's A_q -- grad_y (float32) rounded to fp16 (u = 2^-11) and
     the fused fp16 coefficients, |A16 - A_q| <= (2u + u^2)(|W| + |U|) --
     bit-identical to PackedWide.grad_x, and bias.grad = the column sum of
-    grad_y."""
+    grad_y.  The float32 weight is frozen (a layer whose weight requires a
+    gradient runs the reference formulation instead, see
+    test_eval_layer_weight_gradient)."""
     layer = _layer(method, act, 0, golden).to(DEV).eval()
+    for name, p in layer.named_parameters():
+        if name != "bias":
+            p.requires_grad_(False)
     x = torch.from_numpy(golden["fwd_x"]).to(DEV).requires_grad_(True)
     y = layer(x)
     assert y.grad_fn is not None
@@ -138,6 +143,72 @@ def test_packed_layer_input_gradient(golden, method, act):
     assert np.all(np.abs(gx - gyf @ a_ref) <= bound), np.abs(gx - gyf @ a_ref).max()
     assert torch.equal(x.grad, layer.packed(torch.device(DEV)).grad_x(gy, torch.float32))
     assert torch.allclose(layer.bias.grad, gy.sum(0), rtol=1e-6, atol=1e-5)
+
+
+@pytest.mark.parametrize("method", ["complex_phase_v2", "complex_phase_new_v2", "complex_phase_next_v1"])
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("rot", [0, 1])
+def test_eval_layer_weight_gradient(golden, method, act, rot):
+    """An eval-mode layer whose float32 weight (and rotation angles) require
+    gradients, called with grad mode on: the reference's forward is the same
+    straight-through formulation in eval as in training (quant_i.py:513-554),
+    so weight.grad, bias.grad, the rotation angles' and x's gradients are
+    populated and equal the torch formulation's on the CPU (the same layer in
+    eval on host tensors) within float32 GEMM order and scale ulps (1e-4
+    relative); the output agrees within the same bound.  Under no_grad the
+    same layer takes the packed kernels."""
+    if method == "complex_phase_next_v1" and rot:
+        pytest.skip("next_v1 has no global rotation angle")
+    layer = _layer(method, act, rot, golden)
+    ref = _layer(method, act, rot, golden).eval()
+    layer = layer.to(DEV).eval()
+    xs = torch.from_numpy(golden["fwd_x"])
+    gy = torch.from_numpy(np.random.default_rng(9).standard_normal((xs.shape[0], 64)).astype(np.float32))
+    x = xs.to(DEV).requires_grad_(True)
+    y = layer(x)
+    y.backward(gy.to(DEV))
+    xr = xs.clone().requires_grad_(True)
+    yr = ref(xr)
+    yr.backward(gy)
+
+    def close(a, b):
+        a, b = a.detach().cpu().double(), b.detach().double()
+        return float((a - b).abs().max()) <= 1e-4 * float(b.abs().max()) + 1e-6
+
+    assert close(y, yr)
+    assert layer.weight.grad is not None and close(layer.weight.grad, ref.weight.grad)
+    assert close(layer.bias.grad, ref.bias.grad)
+    assert close(x.grad, xr.grad)
+    for (n, p), (_, pr) in zip(layer.named_parameters(), ref.named_parameters()):
+        if pr.grad is not None:
+            assert p.grad is not None and close(p.grad, pr.grad), n
+    with torch.no_grad():
+        y0 = layer(xs.to(DEV))
+    assert layer._packed is not None and y0.shape == y.shape
+
+
+def test_eval_logits_grad_mode_independent():
+    """Eval-mode logits with grad mode on (autograd records: the blocks run
+    module by module, the packed layers with their device input gradient)
+    and off (fused block path) agree within the fused-vs-unfused bound,
+    max-abs <= 1e-2 * max|logit| + 1e-3 (torch's LayerNorm / GELU against
+    the device kernels), with the same top-1 on margin-confident images."""
+    from quant_models.inference import prepare_inference
+
+    model, _ = _synthetic_model("rpfq_deit_tiny_patch16_224_q", 17)
+    prepare_inference(model, DEV, torch.float16)
+    x = torch.randn(8, 3, 224, 224, generator=torch.Generator().manual_seed(19)).to(DEV, torch.float16)
+    with torch.no_grad():
+        y_off = model(x).float().cpu()
+    y_on = model(x)
+    assert y_on.grad_fn is not None
+    y_on = y_on.detach().float().cpu()
+    err = (y_on - y_off).abs().max()
+    tol = LOGIT_TOL["fp16"]
+    assert err <= tol * y_off.abs().max() + tol / 10, (err, y_off.abs().max())
+    top = y_off.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_on.argmax(1) == y_off.argmax(1))[confident].all())
 
 
 def test_model_input_gradient():
