@@ -641,6 +641,52 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
     return 0
 
 
+def time_forward(model, x, steps: int, warmup: int, use_graph: bool):
+    """Warm up, then time `steps` forwards of model(x) between two events
+    (graph replays with use_graph, after checking every replay against the
+    eager forward).  Returns (total ms, per-launch records of the packed
+    layers -- none under a graph --, the graph or None)."""
+    import torch
+    from quant_models import ops
+
+    graph = None
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(x)
+        torch.cuda.synchronize()
+        if use_graph:
+            eager = model(x).clone()
+            graph = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    gout = model(x)
+            torch.cuda.current_stream().wait_stream(s)
+            for _ in range(3):  # every replay, with eager work between, equals the eager forward
+                graph.replay()
+                torch.cuda.synchronize()
+                if not torch.equal(gout, eager):
+                    raise AssertionError("graph replay differs from the eager forward")
+                model(x)
+                torch.cuda.synchronize()
+
+        launches = []
+        ops.set_launch_recorder(lambda e0, e1, fl, by, shape: launches.append((e0, e1, fl, by, shape)))
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            if graph is not None:
+                graph.replay()
+            else:
+                model(x)
+        end.record()
+        torch.cuda.synchronize()
+        ops.set_launch_recorder(None)
+    return start.elapsed_time(end), launches, graph
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -684,6 +730,8 @@ def main() -> int:
                     help="time quantization-aware training steps (HIP quantizer vs torch ops) instead")
     ap.add_argument("--train-modes", default="hip,hip_pgrad,torch")
     ap.add_argument("--amp", action="store_true", help="with --train: fp16 autocast forward and a gradient scaler")
+    ap.add_argument("--no-bf16-line", action="store_true",
+                    help="skip the bf16-activation sub-block of the default (fp16) bench line")
     args = ap.parse_args()
     if args.layer_probe:
         return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
@@ -758,43 +806,7 @@ def main() -> int:
     g = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(batch, 3, img, img, device="cuda", generator=g).to(act_dtype)
 
-    graph = None
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            model(x)
-        torch.cuda.synchronize()
-        if args.graph:
-            eager = model(x).clone()
-            graph = torch.cuda.CUDAGraph()
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                with torch.cuda.graph(graph, stream=s):
-                    gout = model(x)
-            torch.cuda.current_stream().wait_stream(s)
-            for _ in range(3):  # every replay, with eager work between, equals the eager forward
-                graph.replay()
-                torch.cuda.synchronize()
-                if not torch.equal(gout, eager):
-                    raise AssertionError("graph replay differs from the eager forward")
-                model(x)
-                torch.cuda.synchronize()
-
-        launches = []
-        ops.set_launch_recorder(lambda e0, e1, fl, by, shape: launches.append((e0, e1, fl, by, shape)))
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(args.steps):
-            if graph is not None:
-                graph.replay()
-            else:
-                out = model(x)
-        end.record()
-        torch.cuda.synchronize()
-        ops.set_launch_recorder(None)
-
-    total_ms = start.elapsed_time(end)
+    total_ms, launches, graph = time_forward(model, x, args.steps, args.warmup, args.graph)
     ms_step = total_ms / args.steps
     value = batch * args.steps / (total_ms / 1e3)
     kt = sum(e0.elapsed_time(e1) for e0, e1, *_ in launches)
@@ -854,6 +866,26 @@ def main() -> int:
             line["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     if batch1 is not None:
         line["batch1_stream"] = batch1
+    if args.dtype == "fp16" and not args.no_bf16_line and not args.graph:
+        # the configs' stated bf16 activations: the same forward on a bf16 copy
+        # of the model, timed like the headline (after it, outside its region)
+        del model
+        torch.cuda.empty_cache()
+        model_b = build_model(args.config, args.act_quant, torch.bfloat16)
+        xb = x.to(torch.bfloat16)
+        tb, lb, _ = time_forward(model_b, xb, args.steps, args.warmup, False)
+        ktb = sum(e0.elapsed_time(e1) for e0, e1, *_ in lb)
+        kfb = sum(fl for _, _, fl, _, _ in lb)
+        ach_b = kfb / (ktb / 1e3) / 1e12 if ktb > 0 else None
+        line["bf16"] = {"value": round(batch * args.steps / (tb / 1e3), 2), "unit": "images/s",
+                        "ms_per_step": round(tb / args.steps, 4), "steps": args.steps, "warmup": args.warmup,
+                        "dtype": "bf16",
+                        "roofline": {"bound": "mfma", "achieved": None if ach_b is None else round(ach_b, 2),
+                                     "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": None if ach_b is None else round(ach_b / PEAK_F16_TFLOPS, 4),
+                                     "launches": len(lb), "avg_launch_us": round(1e3 * ktb / max(1, len(lb)), 2)}}
+        model = model_b
+        x = xb
     if not args.no_cpu_baseline:
         rows = rows_per_image(model, x[:1])
         line["cpu_baseline"] = cpu_baseline(model, rows, args.cpu_budget)

@@ -396,6 +396,7 @@ MODEL_CASES = [
     ("rpfq_vit_base_patch16_224_q", "axis", 256, 3, "fp16"),    # config 3 at batch 256
     ("rpfq_vit_large_patch16_224_q", "psk16", 2, 2, "fp16"),    # config 5, 16-PSK
     ("rpfq_vit_large_patch16_224_q", "psk16", 512, 2, "fp16"),  # config 5 at batch 512
+    ("rpfq_vit_large_patch16_224_q", "psk16", 1, 1, "fp16"),    # config 5 at batch 1: streaming kernels
     ("rpfq_swin_tiny_patch4_window7_224_q", "axis", 128, 6, "fp16"),  # config 4 at batch 128
     ("rpfq_deit_tiny_patch16_224_q", "axis", 64, 8, "fp16"),    # config 2 at batch 64
     # the configs' stated bf16 activations (bf16 LayerNorm / attention /
@@ -403,6 +404,8 @@ MODEL_CASES = [
     ("rpfq_vit_base_patch16_224_q", "axis", 256, 3, "bf16"),
     ("rpfq_vit_base_patch16_224_q", "axis", 1, 1, "bf16"),
     ("rpfq_vit_large_patch16_224_q", "psk16", 2, 2, "bf16"),
+    ("rpfq_vit_large_patch16_224_q", "psk16", 1, 1, "bf16"),    # config 5 batch sweep {1, 512}, bf16
+    ("rpfq_vit_large_patch16_224_q", "psk16", 512, 2, "bf16"),
     ("rpfq_swin_tiny_patch4_window7_224_q", "axis", 128, 6, "bf16"),
     ("rpfq_deit_tiny_patch16_224_q", "axis", 64, 8, "bf16"),
 ]
