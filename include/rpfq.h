@@ -169,6 +169,11 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  * accumulates in float32.  The RPFQ_KERNEL_GEMV launches (M <= 8) never
  * round the fused coefficients: the fp16 U and W values meet x in separate
  * MFMA products, so their sums are exact in the float32 accumulator.
+ * Input range: x is rounded to fp16 for the MFMA as it stands, which is
+ * exact for fp16 x and for bf16 x in [2^-14, 65504] and 2^-11 relative for
+ * float32 x in that range; larger magnitudes become +-inf and smaller ones
+ * lose relative precision.  rpfq_wide_linear_scaled with the row prescales
+ * of rpfq_row_scales removes that limit for float32 / bf16 x.
  * flags: the RPFQ_FLAG_* bits above.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
@@ -208,6 +213,38 @@ int rpfq_wide_linear_kernel(const rpfq_wide_desc* desc, int64_t M, int x_dtype, 
 int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
                               const void* x, int x_dtype, int64_t M, const float* bias,
                               const void* residual, void* y, int y_dtype, int flags, void* stream);
+
+/*
+ * Per-row prescales of x [M, C] for rpfq_wide_linear_scaled (the forward's
+ * range guard): scale[m] = 2^(14 - floor(log2 max_k |x[m, k]|)), clamped to
+ * [2^-126, 2^126], so the row's largest element times scale[m] lies in
+ * [2^14, 2^15); 1 for rows whose maximum is 0, inf or NaN.  x: any of the
+ * three dtypes, element-aligned (C % 8 == 0 with 16-byte aligned rows reads
+ * 16-byte chunks); scale: float32 [M].  No counterpart in the reference: its
+ * float32 F.linear has float32's range, which this restores around the
+ * kernels' fp16 operands.
+ */
+int rpfq_row_scales(const void* x, int x_dtype, int64_t M, int64_t C, float* scale, void* stream);
+
+/*
+ * rpfq_wide_linear (residual = NULL) or rpfq_wide_linear_residual with the
+ * rows of a float32 / bf16 x prescaled: row m is multiplied by row_scale[m]
+ * before its fp16 rounding and its layer output by 1 / row_scale[m] (exact)
+ * before the bias, the GELU and the residual add.  row_scale: float32 [M],
+ * 16-byte aligned, powers of two in [2^-126, 2^126] (as rpfq_row_scales
+ * writes them), or NULL (no prescale); ignored for fp16 x, which the MFMA
+ * takes exactly.  Power-of-two factors commute with the roundings of the
+ * contraction, so a row inside fp16's range gives the same output as
+ * rpfq_wide_linear, and a row of any float32 / bf16 range keeps that
+ * relative accuracy (2^-11 of sum |x| |A| for float32 x, exact operands for
+ * bf16 x).  Other arguments and flags as rpfq_wide_linear (RPFQ_FLAG_GELU
+ * only without a residual).
+ * Replaces F.linear(x, A_q, bias) of quant_i.py:554 on float32 activations
+ * of any magnitude (the reference layer's dtype).
+ */
+int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                            int x_dtype, int64_t M, const float* row_scale, const float* bias, const void* residual,
+                            void* y, int y_dtype, int flags, void* stream);
 
 /* Bytes of the adjoint blob that rpfq_wide_pack_adjoint writes for `desc`
  * (0 if the descriptor is invalid). */

@@ -173,7 +173,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
     if (!aligned(packed, 256) || !aligned(x, 16))
         return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte and x 16-byte aligned");
     if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
-    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, nullptr, y, y_dtype, flags,
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, nullptr, bias, nullptr, y, y_dtype, flags,
                                                reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear");
 }
@@ -280,11 +280,44 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
     if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(residual, 16))
         return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x and residual 16-byte aligned");
     if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
-    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, bias, residual, y, y_dtype, flags,
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, nullptr, bias, residual, y, y_dtype, flags,
                                                reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear_residual");
 }
 
+
+int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
+                            int x_dtype, int64_t M, const float* row_scale, const float* bias, const void* residual,
+                            void* y, int y_dtype, int flags, void* stream) {
+    int rc = check_desc(desc);
+    if (rc) return rc;
+    if (!packed || !x || !y) return fail(RPFQ_ERR_NULL, "packed/x/y must not be NULL");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype))
+        return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
+    if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
+    rpfq::WideGeom g = rpfq::wide_geom(*desc);
+    if ((rc = check_flags(flags, g, M, residual != nullptr))) return rc;
+    if (packed_bytes < g.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
+    if (!aligned(packed, 256) || !aligned(x, 16) || (residual && !aligned(residual, 16)))
+        return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x and residual 16-byte aligned");
+    if (row_scale && !aligned(row_scale, 16)) return fail(RPFQ_ERR_ALIGN, "row_scale must be 16-byte aligned");
+    if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, row_scale, bias, residual, y, y_dtype,
+                                               flags, reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_linear_scaled");
+}
+
+int rpfq_row_scales(const void* x, int x_dtype, int64_t M, int64_t C, float* scale, void* stream) {
+    if (!x || !scale) return fail(RPFQ_ERR_NULL, "x/scale must not be NULL");
+    if (!dtype_ok(x_dtype)) return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d", x_dtype);
+    if (M <= 0 || C <= 0 || M > (int64_t)1 << 31 || C > (int64_t)1 << 30)
+        return fail(RPFQ_ERR_SHAPE, "M=%lld, C=%lld out of range", (long long)M, (long long)C);
+    if (!aligned(x, x_dtype == RPFQ_F32 ? 4 : 2) || !aligned(scale, 4))
+        return fail(RPFQ_ERR_ALIGN, "x and scale must be aligned to their element size");
+    return hip_status(rpfq::launch_row_scales(x, x_dtype, M, C, scale, reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_row_scales");
+}
 
 size_t rpfq_wide_adjoint_bytes(const rpfq_wide_desc* desc) {
     if (check_desc(desc) != RPFQ_OK) return 0;

@@ -397,6 +397,29 @@ __device__ __forceinline__ void load8_f32(const void* base, int64_t off, float* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// per-row prescale of float32 / bf16 activations (the forward's range guard)
+// ---------------------------------------------------------------------------
+// The MFMA takes activations as fp16, whose normal range is [2^-14, 65504].
+// A float32 / bf16 row whose largest magnitude is mx is multiplied by
+// s = 2^(14 - floor(log2 mx)) before that rounding, so its largest element
+// lands in [2^14, 2^15), and the row's outputs are multiplied by 1/s
+// (exact) before the bias.  Power-of-two factors commute with every
+// rounding that stays inside the formats' ranges (the fp16 conversion, the
+// exact fp16 products, the float32 accumulation), so a row that already
+// fits gives bit for bit the unscaled result, and any other row keeps the
+// relative accuracy of one that fits.  The exponent is clamped to
+// [-126, 126] (max|x| in [2^-112, 2^140) scales exactly); zero, NaN and
+// infinite maxima keep s = 1.
+__device__ __forceinline__ float row_prescale(float mx) {
+    if (!(mx > 0.0f) || !(mx <= 3.40282347e38f)) return 1.0f;
+    int k = 15 - __builtin_amdgcn_frexp_expf(mx);  // frexp: mx = f 2^e, f in [0.5, 1)
+    k = k < -126 ? -126 : (k > 126 ? 126 : k);
+    return __builtin_amdgcn_ldexpf(1.0f, k);
+}
+// 1 / s for a prescale s (a power of two in [2^-126, 2^126]): exact.
+__device__ __forceinline__ float row_unscale(float s) { return 1.0f / s; }
+
 // LDS address-space views and the LDS byte address of a shared pointer.
 typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

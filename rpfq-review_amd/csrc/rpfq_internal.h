@@ -98,6 +98,11 @@ struct WideArgs {
     // the same prologue: bits 2 .. 16, 0 = none (rpfq_act_quant's arithmetic
     // per row and half, rounded to x's dtype).
     int aq_bits;
+    // Per-row prescale of float32 / bf16 x ([M] powers of two, row_prescale
+    // of the row's largest magnitude; NULL: none; unused for fp16 x): row m
+    // is multiplied by xs[m] before its fp16 rounding and its outputs by
+    // 1 / xs[m] before the bias.
+    const float* xs;
 };
 
 // ---------------------------------------------------------------------------
@@ -189,8 +194,10 @@ hipError_t launch_wide_pack(const rpfq_wide_desc& d, const WideGeom& g, const ui
                             void* packed, hipStream_t s);
 // dispatch (wide_dispatch.hip)
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed,
-                              const void* x, int xdt, int64_t M, const float* bias, const void* res,
-                              void* y, int ydt, int flags, hipStream_t s);
+                              const void* x, int xdt, int64_t M, const float* xs, const float* bias,
+                              const void* res, void* y, int ydt, int flags, hipStream_t s);
+// per-row prescales of x [M, C] (rpfq_row_scales; rpfq_kernels.hip)
+hipError_t launch_row_scales(const void* x, int xdt, int64_t M, int64_t C, float* scale, hipStream_t s);
 int wide_linear_kernel_choice(const WideGeom& g, int xdt, int64_t M, int ydt, int flags);  // RPFQ_KERNEL_*
 // LayerNorm fused into the streaming kernel: whether the launch qualifies, and the launch.
 // K' <= 384: the normalized 16-row tile (<= 25 KB) stays in LDS.  ViT-B,

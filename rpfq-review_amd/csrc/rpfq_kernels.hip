@@ -731,6 +731,48 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* x, int64_t 
     }
 }
 // ---------------------------------------------------------------------------
+// per-row prescales (rpfq_row_scales): one wave per row, the row's largest
+// magnitude (exact: max is order-free) through row_prescale
+// ---------------------------------------------------------------------------
+template <int XDT>
+__global__ void __launch_bounds__(256) row_scale_kernel(const void* x, int64_t M, int64_t C, int vec,
+                                                        float* scale) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;  // whole waves leave together
+    const int64_t base = row * C;
+    float mx = 0.0f;
+    if (vec) {  // C % 8 == 0, 16-byte aligned rows: 8 elements per load
+        for (int64_t c = lane; c < C / 8; c += 64) {
+            float v[8];
+            load8_ln<XDT>(x, base + 8 * c, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[e]));
+        }
+    } else {
+        for (int64_t c = lane; c < C; c += 64) mx = fmaxf(mx, fabsf(load1<XDT>(x, base + c)));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) scale[row] = row_prescale(mx);
+}
+
+template <int XDT>
+static hipError_t row_scales_go(const void* x, int64_t M, int64_t C, float* scale, hipStream_t s) {
+    const int vec = C % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    hipLaunchKernelGGL((row_scale_kernel<XDT>), dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, x, M, C, vec, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_scales(const void* x, int xdt, int64_t M, int64_t C, float* scale, hipStream_t s) {
+    switch (xdt) {
+        case RPFQ_F32: return row_scales_go<RPFQ_F32>(x, M, C, scale, s);
+        case RPFQ_F16: return row_scales_go<RPFQ_F16>(x, M, C, scale, s);
+        default: return row_scales_go<RPFQ_BF16>(x, M, C, scale, s);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 // The act-quant and GELU + act-quant row passes (modes 2 and 4 of

@@ -185,11 +185,12 @@ hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g,
 }
 
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
-                              int xdt, int64_t M, const float* bias, const void* res, void* y, int ydt, int flags,
-                              hipStream_t s) {
+                              int xdt, int64_t M, const float* xs, const float* bias, const void* res, void* y,
+                              int ydt, int flags, hipStream_t s) {
     WideArgs a = wide_shape(g, M, flags);
     flags &= ~RPFQ_FLAG_GELU;
     wide_operands(a, d, g, packed, x, bias, res, y);
+    a.xs = xdt == RPFQ_F16 ? nullptr : xs;  // fp16 x is the MFMA operand as it stands
     return launch_wide(a, d, xdt, ydt, flags, s);
 }
 

@@ -55,7 +55,9 @@ template <int BM> constexpr int dma_bias_at() { return dma_lut1_at<BM>() + kDmaL
 // per-row scales of the next tile, staged by DMA: [wave][32 rows][pu | pw] float4 pairs
 constexpr int kDmaParams = 4 * 1024;
 template <int BM> constexpr int dma_params_at() { return dma_bias_at<BM>() + kDmaBias; }
-template <int BM> constexpr int dma_lds() { return dma_params_at<BM>() + kDmaParams; }  // 78848 B (BM = 128)
+// row prescales of bf16 x (WideArgs::xs) of the current and the next tile: [2][BM] floats
+template <int BM> constexpr int dma_xs_at() { return dma_params_at<BM>() + kDmaParams; }
+template <int BM> constexpr int dma_lds() { return dma_xs_at<BM>() + 2 * BM * 4; }  // 79872 B (BM = 128)
 static_assert(2 * dma_lds<128>() <= 160 * 1024, "two workgroups per CU");
 static_assert(4 * 64 * kTRow <= kDmaStages * dma_stage<128>(), "epilogue half tile fits the stages");
 static_assert(4 * 128 * kTRow <= kDmaStages * dma_stage<256>(), "epilogue half tile fits the stages");
@@ -68,6 +70,11 @@ static_assert(4 * 128 * kTRow <= kDmaStages * dma_stage<256>(), "epilogue half t
 // before reading the destination.
 __device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
+}
+
+// LDS DMA of one dword per lane (lane l: 4 B from gbase + voff[l] to lds + 4 l).
+__device__ __forceinline__ void dma_dword(const void* gbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
 }
 
 // LUT of one output row in the wave-pair layout: entry e (0..15 U, 16..31 W)
@@ -112,17 +119,28 @@ __device__ __forceinline__ void build_lut_slot(uint32_t* lut_pair, int slot, con
 // on load), mid-k-step for the next stage, before the barrier that
 // publishes it.  Costs ~20% of the kernel at ViT-B/16 bs256 (the LDS
 // traffic of the rewrite; converting each MFMA operand in registers instead,
-// 4 times over, costs ~35%).
+// 4 times over, costs ~35%).  srow: LDS byte address of the prescales of
+// the NROWS rows (WideArgs::xs), applied before the conversion (exact), or
+// 0 for none (address 0 holds a LUT, never the prescales).
 template <int XDT, int NROWS>
-__device__ __forceinline__ void stage_to_f16(uint32_t rows, int lane) {
+__device__ __forceinline__ void stage_to_f16(uint32_t rows, int lane, uint32_t srow) {
     if constexpr (XDT == RPFQ_BF16) {
 #pragma unroll
         for (int j = 0; j < NROWS * 128 / 1024; ++j) {  // NROWS rows of 128 B: 16-B chunks, 64 lanes
             const uint32_t addr = rows + (uint32_t)(j * 64 + lane) * 16u;
             const u32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const u32x4*>(addr);
             u32x4 o;
+            if (srow) {
+                // chunk j 64 + lane lies in row 8 j + lane / 8
+                const float sc = *reinterpret_cast<__attribute__((address_space(3))) const float*>(
+                    srow + (uint32_t)(8 * j + (lane >> 3)) * 4u);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) o[t] = pack_h2(bf16_to_f32(v[t] & 0xffffu), bf16_to_f32(v[t] >> 16));
+                for (int t = 0; t < 4; ++t)
+                    o[t] = pack_h2(bf16_to_f32(v[t] & 0xffffu) * sc, bf16_to_f32(v[t] >> 16) * sc);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[t] = pack_h2(bf16_to_f32(v[t] & 0xffffu), bf16_to_f32(v[t] >> 16));
+            }
             *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(addr) = o;
         }
     }
@@ -214,6 +232,17 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // global load whose wait would drain the activation prefetch.
     const float4* pstage = reinterpret_cast<const float4*>(smem + dma_params_at<BM>() + wave * 1024);
     const bool staged = CB != RPFQ_CB_TABLE && a.nblk == 1;
+    // bf16 x with row prescales: wave w's RPW rows of a tile, DMA'd with the
+    // tile's first loads into buffer (tile iteration & 1), RPW lanes of 4 B
+    float* xs_lds = reinterpret_cast<float*>(smem + dma_xs_at<BM>());
+    const bool scaled = XDT == RPFQ_BF16 && a.xs != nullptr;
+    auto issue_xs = [&](int vb_t, int buf) {
+        if (!scaled) return;
+        const int t = xcd_tile(vb_t, total);
+        const int64_t m0_t = min((int64_t)(t / a.tiles_n) * BM, a.M - BM);
+        if (lane < RPW) dma_dword(a.xs + m0_t + RPW * wave, (uint32_t)lane * 4u, lds_addr(xs_lds + buf * BM + RPW * wave));
+    };
+    int it = 0;  // tile iteration of this workgroup
     auto issue_params = [&](int vb_t) {  // this wave's 32 rows of tile vb_t; lane l: row l / 2, half l % 2
         if (!staged) return;
         const int t = xcd_tile(vb_t, total);
@@ -239,10 +268,13 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc_re[i] = acc_im[i] = floatx16{0};
 
+    const int xb = it & 1;  // this tile's prescale buffer
+    const uint32_t srow = scaled ? lds_addr(xs_lds + xb * BM + RPW * wave) : 0u;
     if (vb == (int)blockIdx.x) {  // later tiles had these requested before the previous epilogue
         issue_codes(0, 0);
         issue_x(0, 2);
         issue_params(vb);
+        issue_xs(vb, xb);
     }
     {   // bias of this wave's 32 output rows (0 past N or without bias), read in the epilogue;
         // loaded before the next k-step's DMA, so its wait covers only loads this tile needs now
@@ -268,7 +300,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     else
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
     if constexpr (XDT == RPFQ_BF16) {
-        stage_to_f16<XDT, RPW>(lds_stages + 2 * kDmaStage, lane);
+        stage_to_f16<XDT, RPW>(lds_stages + 2 * kDmaStage, lane, srow);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
@@ -365,7 +397,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     } else {
                         asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
                     }
-                    stage_to_f16<XDT, RPW>(lds_stages + (st == 2 ? 0 : st + 1) * kDmaStage, lane);
+                    stage_to_f16<XDT, RPW>(lds_stages + (st == 2 ? 0 : st + 1) * kDmaStage, lane, srow);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -407,6 +439,20 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         issue_codes(0, 0);
         issue_x(0, 2);
         issue_params(vb + (int)gridDim.x);
+        issue_xs(vb + (int)gridDim.x, xb ^ 1);
+    }
+    if constexpr (XDT == RPFQ_BF16) {
+        if (scaled) {  // undo the rows' prescales (exact) before the bias: subtile i, lane r holds x row 32 i + r
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const float inv = row_unscale(xs_lds[xb * BM + 32 * i + r]);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    acc_re[i][v] *= inv;
+                    acc_im[i][v] *= inv;
+                }
+            }
+        }
     }
     // Epilogue.  The accumulators hold the transposed tile: lane (r, g) of
     // subtile i has, for x row 32 i + r, outputs n = 32 ntw + 8 q + 4 g + t at
@@ -575,6 +621,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    ++it;
     }
 }
 

@@ -136,18 +136,18 @@ __device__ __forceinline__ void chunk_f32(uint4 v, float* f) {
 
 // 4 consecutive activations at element offset `off`: the raw 16-bit values
 // (fp16, bf16; converted at use so the load stays in flight) or, for
-// float32, 4 fp16 converted on load.
+// float32, 4 fp16 converted on load after the row's prescale xs (exact).
 template <int XDT>
-__device__ __forceinline__ uint2 load4_raw(const void* base, int64_t off) {
+__device__ __forceinline__ uint2 load4_raw(const void* base, int64_t off, float xs) {
     if (XDT != RPFQ_F32) return *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + off);
     const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
-    return make_uint2(pack_h2(f.x, f.y), pack_h2(f.z, f.w));
+    return make_uint2(pack_h2(f.x * xs, f.y * xs), pack_h2(f.z * xs, f.w * xs));
 }
 template <int XDT>
-__device__ __forceinline__ uint2 raw4_f16(uint2 v) {
+__device__ __forceinline__ uint2 raw4_f16(uint2 v, float xs) {
     if (XDT != RPFQ_BF16) return v;
-    return make_uint2(pack_h2(bf16_to_f32(v.x & 0xffffu), bf16_to_f32(v.x >> 16)),
-                      pack_h2(bf16_to_f32(v.y & 0xffffu), bf16_to_f32(v.y >> 16)));
+    return make_uint2(pack_h2(bf16_to_f32(v.x & 0xffffu) * xs, bf16_to_f32(v.x >> 16) * xs),
+                      pack_h2(bf16_to_f32(v.y & 0xffffu) * xs, bf16_to_f32(v.y >> 16) * xs));
 }
 
 // PB: per-(row, block) scales (the LUT is rebuilt at each block start);
@@ -189,6 +189,9 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
     const int coff = r16 * 4 + q;
     const bool m_ok = r16 < M;
     const int xoff = (m_ok ? r16 : M - 1) * 2 * K + 16 * (q & 1) + 4 * (q >> 1);  // + 32 ks + 8 t
+    // prescale of this lane's x row (float32 / bf16 x with a.xs, else 1); the
+    // row prologue computes its own from the prepared rows (xs_tile below)
+    const float xsl = (XDT != RPFQ_F16 && !LN && a.xs) ? a.xs[m0 + (m_ok ? r16 : M - 1)] : 1.0f;
     const int xcol = 16 * (q & 1) + 4 * (q >> 1);
     struct Step {
         uint2 c[2];          // code dwords (t = 0, 1) of rows r16 and 16 + r16
@@ -205,12 +208,12 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
             if (KT) {
                 const int col = 32 * kc + xcol + 8 * t;
                 const int off = xoff - xcol + (col < K ? col : 0);  // K' tail: in bounds, zeroed at use
-                st.xr[t] = load4_raw<XDT>(xc, off);
-                st.xi[t] = load4_raw<XDT>(xc, off + K);
+                st.xr[t] = load4_raw<XDT>(xc, off, xsl);
+                st.xi[t] = load4_raw<XDT>(xc, off + K, xsl);
             } else {
                 const int64_t xb = 32 * (int64_t)kc + 8 * t;
-                st.xr[t] = load4_raw<XDT>(xc, xb + xoff);
-                st.xi[t] = load4_raw<XDT>(xc, xb + K + xoff);
+                st.xr[t] = load4_raw<XDT>(xc, xb + xoff, xsl);
+                st.xi[t] = load4_raw<XDT>(xc, xb + K + xoff, xsl);
             }
         }
     };
@@ -224,6 +227,8 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
     const int C2 = 2 * K, nch = C2 / 8;
     const int xsb = 2 * C2 + 8;  // the 8-B pad puts consecutive rows 2 banks apart
     char* xtile = smem + sk_lds(NW);
+    // (LN, bf16 x) the prepared rows' prescales, [16] floats after the tile
+    float* xs_tile = reinterpret_cast<float*>(xtile + 16 * xsb);
     constexpr int RW = 16 / NW;                                  // (LN) rows per wave
     constexpr int NCP = LN ? (2 * kLnMaxK / 8 + 63) / 64 : 1;    // chunks per lane and row
     uint4 lnv[RW][NCP];
@@ -412,6 +417,68 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
             }
         }
         const bool table = bits > 0 && bits <= 4;
+        // the prepared value of chunk j of row i: LayerNorm / act quant, and
+        // for bf16 x the rounding to x's dtype (every lane calls it: the
+        // ds_bpermute reads take all lanes)
+        auto prepared = [&](int i, int j, float* y) {
+            const int c = lane + 64 * j;
+            value(i, j, y);
+            if (bits) {
+                const bool hi = c >= half_ch;
+                const float sc = hi ? sc1[i] : sc0[i];
+                float qv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qv[e] = fminf(fmaxf(rintf(y[e] * sc), qmin), qmax);
+                if (table) {
+                    int d[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        d[e] = __builtin_amdgcn_ds_bpermute(((hi ? 16 : 0) + (int)qv[e] + 8) << 2, tvb[i]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y[e] = copysignf(__int_as_float(d[e]), qv[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y[e] = qv[e] / sc;
+                }
+            }
+            if (XDT == RPFQ_BF16) {  // rounded to x's dtype (then exactly to fp16 for the MFMA)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = bf16_to_f32(f32_to_bf16(y[e]));
+            }
+        };
+        // bf16 x: each prepared row takes the range guard's prescale of its
+        // largest magnitude before the fp16 conversion, as rpfq_row_scales
+        // and rpfq_wide_linear_scaled apply it to the row kernel's bf16
+        // output (a first pass for the maxima; fp16 x is rounded directly)
+        float rs[RW];
+#pragma unroll
+        for (int i = 0; i < RW; ++i) rs[i] = 1.0f;
+        if (XDT == RPFQ_BF16) {
+            float mx[RW];
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                mx[i] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NCP; ++j) {
+                    float y[8];
+                    prepared(i, j, y);
+                    if (lane + 64 * j < nch) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) mx[i] = fmaxf(mx[i], fabsf(y[e]));
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+                for (int i = 0; i < RW; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o, 64));
+            }
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                rs[i] = row_prescale(mx[i]);
+                if (lane == 0) xs_tile[wave * RW + i] = rs[i];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int row = wave * RW + i;
@@ -419,35 +486,10 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
             for (int j = 0; j < NCP; ++j) {
                 const int c = lane + 64 * j;
                 float y[8];
-                value(i, j, y);
-                if (bits) {
-                    const bool hi = c >= half_ch;
-                    const float sc = hi ? sc1[i] : sc0[i];
-                    float qv[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) qv[e] = fminf(fmaxf(rintf(y[e] * sc), qmin), qmax);
-                    if (table) {
-                        int d[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            d[e] = __builtin_amdgcn_ds_bpermute(((hi ? 16 : 0) + (int)qv[e] + 8) << 2, tvb[i]);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) y[e] = copysignf(__int_as_float(d[e]), qv[e]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) y[e] = qv[e] / sc;
-                    }
-                }
+                prepared(i, j, y);
                 uint32_t o[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float y0 = y[2 * t], y1 = y[2 * t + 1];
-                    if (XDT == RPFQ_BF16) {  // rounded to x's dtype, then exactly to fp16 for the MFMA
-                        y0 = bf16_to_f32(f32_to_bf16(y0));
-                        y1 = bf16_to_f32(f32_to_bf16(y1));
-                    }
-                    o[t] = row < M ? cvt_pk(y0, y1) : 0u;
-                }
+                for (int t = 0; t < 4; ++t) o[t] = row < M ? cvt_pk(y[2 * t] * rs[i], y[2 * t + 1] * rs[i]) : 0u;
                 if (c < nch) *reinterpret_cast<uint4*>(xtile + row * xsb + 16 * c) = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
@@ -478,8 +520,8 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
                 re = *reinterpret_cast<const uint2*>(rp);
                 im = *reinterpret_cast<const uint2*>(rp + 2 * K);
             } else {
-                re = raw4_f16<XDT>(st.xr[t]);
-                im = raw4_f16<XDT>(st.xi[t]);
+                re = raw4_f16<XDT>(st.xr[t], xsl);
+                im = raw4_f16<XDT>(st.xi[t], xsl);
             }
             uint4 b = make_uint4(__builtin_amdgcn_perm(im.x, re.x, 0x05040100u),
                                  __builtin_amdgcn_perm(im.x, re.x, 0x07060302u),
@@ -565,14 +607,16 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
     // of x row m; rows past M and outputs past N' store nothing.
     if (!m_ok) return;
     if (NW == 1) fetch_epi();
+    // undo the row's prescale (exact; 1 without one) before the bias
+    const float inv = row_unscale((LN && XDT == RPFQ_BF16) ? xs_tile[r16] : xsl);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int64_t n0 = (int64_t)tile * 32 + 16 * h + 4 * q;
         float vr[4], vi[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            vr[v] = acc_re[h][v] + eb[h][0][v];
-            vi[v] = acc_im[h][v] + eb[h][1][v];
+            vr[v] = acc_re[h][v] * inv + eb[h][0][v];
+            vi[v] = acc_im[h][v] * inv + eb[h][1][v];
         }
         const int64_t base = (m0 + r16) * ldy + n0;
         if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
@@ -635,9 +679,9 @@ static_assert(SK_PF % GV_XPF == 0, "the activation ring must divide the code rin
 constexpr int gv_lds(int h, int nw) { return (h / 2) * kSkLut + (nw - 1) * h * 4 * 64 * 4; }
 
 template <int XDT>
-__device__ __forceinline__ uint32_t raw2_f16(uint32_t v) {
+__device__ __forceinline__ uint32_t raw2_f16(uint32_t v, float xs) {
     if (XDT != RPFQ_BF16) return v;
-    return pack_h2(bf16_to_f32(v & 0xffffu), bf16_to_f32(v >> 16));
+    return pack_h2(bf16_to_f32(v & 0xffffu) * xs, bf16_to_f32(v >> 16) * xs);
 }
 
 // Lane constants of the column-split kernels.
@@ -648,6 +692,7 @@ struct GvLane {
     int off1, off2;       // element offsets of L1 (part p) and L2 (the other part)
     uint32_t m0, m1;      // sign masks of the B dwords (re / im column)
     uint32_t slot0;       // LUT slot of the lane's row in byte 0 of an address
+    float xs;             // prescale of the lane's x row (float32 / bf16 x with a.xs, else 1)
 };
 __device__ __forceinline__ GvLane gv_lane(int lane, int M, int K) {
     GvLane l;
@@ -664,6 +709,7 @@ __device__ __forceinline__ GvLane gv_lane(int lane, int M, int K) {
     l.m0 = l.p ? 0u : 0x80000000u;
     l.m1 = l.p ? 0x00008000u : 0u;
     l.slot0 = (uint32_t)(16 * (l.q & 1) + l.r16) * 4;
+    l.xs = 1.0f;
     return l;
 }
 
@@ -674,8 +720,8 @@ __device__ __forceinline__ void gv_load_x(const WideArgs& a, const GvLane& l, in
     for (int t = 0; t < 2; ++t) {
         const int col = 32 * ks + 8 * t;
         const bool in = !KT || col + l.cq < a.K;  // K' tail: the row's first columns, zeroed at use
-        xv[2 * t] = load4_raw<XDT>(a.x, in ? l.off1 + col : l.xrow);
-        xv[2 * t + 1] = load4_raw<XDT>(a.x, in ? l.off2 + col : l.xrow);
+        xv[2 * t] = load4_raw<XDT>(a.x, in ? l.off1 + col : l.xrow, l.xs);
+        xv[2 * t + 1] = load4_raw<XDT>(a.x, in ? l.off2 + col : l.xrow, l.xs);
     }
 }
 
@@ -690,7 +736,7 @@ __device__ __forceinline__ void gv_kstep(floatx4* acc, const GvLane& l, int ks, 
     half8 bx[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t u1 = raw2_f16<XDT>(l1[j]), u2 = raw2_f16<XDT>(l2[j]);
+        const uint32_t u1 = raw2_f16<XDT>(l1[j], l.xs), u2 = raw2_f16<XDT>(l2[j], l.xs);
         const uint32_t p0 = __builtin_amdgcn_perm(u2, u1, 0x05040100u);
         const uint32_t p1 = __builtin_amdgcn_perm(u2, u1, 0x07060302u);
         uint4 b = make_uint4(p0 ^ l.m0, p0 ^ l.m1, p1 ^ l.m0, p1 ^ l.m1);
@@ -752,8 +798,9 @@ __device__ __forceinline__ void gv_store(const WideArgs& a, const GvLane& l, con
         const int64_t base = m * ldy + (l.p ? a.N : 0) + n0;
         const float* bias = a.bias ? a.bias + (l.p ? a.N : 0) : nullptr;
         float v4[4];
+        const float inv = row_unscale(l.xs);  // undo the row's prescale (exact) before the bias
 #pragma unroll
-        for (int v = 0; v < 4; ++v) v4[v] = acc[h][v] + ((bias && n0 + v < a.N) ? bias[n0 + v] : 0.0f);
+        for (int v = 0; v < 4; ++v) v4[v] = acc[h][v] * inv + ((bias && n0 + v < a.N) ? bias[n0 + v] : 0.0f);
         if (a.vec_store && n0 + 4 <= a.N && YDT == RPFQ_F16) {
             uint2 o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
             if (a.res) o = add_res4<YDT>(o, a.res, base);
@@ -792,7 +839,8 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
     const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KS = a.KS;
     const int M = (int)a.M;  // 1 .. 8 (host-checked)
-    const GvLane l = gv_lane(lane, M, a.K);
+    GvLane l = gv_lane(lane, M, a.K);
+    if (XDT != RPFQ_F16 && a.xs) l.xs = a.xs[min(l.r16 >> 1, M - 1)];
     const int chunk = (KS + NW - 1) / NW;
     const int kb = min(wave * chunk, KS), ke = min(kb + chunk, KS);  // this wave's k-steps
     const int tile0 = (int)blockIdx.x * TPG;
@@ -882,7 +930,7 @@ static hipError_t wide_sk_go(WideArgs& a, hipStream_t s) {
 
 template <int XDT, int YDT, int CB, int NW>
 static hipError_t wide_sk_ln_go(WideArgs& a, hipStream_t s) {
-    const int lds = sk_lds(NW) + 16 * (4 * a.K + 8);
+    const int lds = sk_lds(NW) + 16 * (4 * a.K + 8) + 16 * 4;  // + the prepared rows' prescales
     hipLaunchKernelGGL((wide_linear_skinny_kernel<XDT, YDT, CB, false, false, NW, true>), dim3((unsigned)sk_groups(a)),
                        dim3(64 * NW), lds, s, a);
     return hipGetLastError();

@@ -37,6 +37,23 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
     uint32_t* lut = reinterpret_cast<uint32_t*>(smem + 2 * XSTAGE) + wave * 1024;
     const int64_t ldx = 2 * (int64_t)a.K;
 
+    // Per-row prescales of float32 / bf16 x (a.xs): this thread's CPT staging
+    // rows in registers, the tile's BM rows in LDS past the LUTs for the
+    // epilogue (written here, read after the k-loop's barriers)
+    float xsr[CPT];
+    float* xs_lds = reinterpret_cast<float*>(smem + wide_lds_bytes<BM>());
+    if (XDT != RPFQ_F16 && a.xs) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int64_t m = m0 + ((tid + 256 * j) >> 2);
+            xsr[j] = m < a.M ? a.xs[m] : 1.0f;
+        }
+        if (tid < BM) xs_lds[tid] = m0 + tid < a.M ? a.xs[m0 + tid] : 1.0f;
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) xsr[j] = 1.0f;
+    }
+
     // Raw activation prefetch: the loads for k-step ks+1 are issued before
     // the MFMAs of k-step ks and converted/interleaved only when stored to
     // LDS afterwards, so their latency overlaps the math.  Out-of-range
@@ -113,6 +130,11 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
                             fr[4 * t] = r4.x; fr[4 * t + 1] = r4.y; fr[4 * t + 2] = r4.z; fr[4 * t + 3] = r4.w;
                             fi[4 * t] = i4.x; fi[4 * t + 1] = i4.y; fi[4 * t + 2] = i4.z; fi[4 * t + 3] = i4.w;
                         }
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {  // the row's prescale (1 without a.xs): exact
+                        fr[t] *= xsr[j];
+                        fi[t] *= xsr[j];
                     }
                     o0 = make_uint4(cvt_pk(fr[0], fi[0]), cvt_pk(fr[1], fi[1]), cvt_pk(fr[2], fi[2]),
                                     cvt_pk(fr[3], fi[3]));
@@ -209,6 +231,17 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
         }
     }
 
+    if (XDT != RPFQ_F16 && a.xs) {  // undo the rows' prescales (exact) before the bias
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float inv = row_unscale(xs_lds[i * 32 + acc_row(v, g)]);
+                acc_re[i][v] *= inv;
+                acc_im[i][v] *= inv;
+            }
+        }
+    }
     const bool n_ok = active && n < a.N;
     const float br = (a.bias && n_ok) ? a.bias[n] : 0.0f;
     const float bi = (a.bias && n_ok) ? a.bias[a.N + n] : 0.0f;
@@ -285,7 +318,7 @@ __global__ void __launch_bounds__(256, 2) wide_linear_kernel(WideArgs a) {
 template <int BM, int XDT, int YDT, int CB>
 static hipError_t wide_go(WideArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
-    constexpr int lds = wide_lds_bytes<BM>();
+    constexpr int lds = wide_lds_bytes<BM>() + BM * 4;  // + the tile's row prescales
     const hipError_t e = set_lds_attr_once(reinterpret_cast<const void*>(&wide_linear_kernel<BM, XDT, YDT, CB>), lds,
                                            attr_done);
     if (e != hipSuccess) return e;

@@ -63,6 +63,8 @@ EXPORTED = (
     "rpfq_quantize_workspace_bytes",
     "rpfq_quantize_wide",
     "rpfq_quantize_wide_noalloc",
+    "rpfq_row_scales",
+    "rpfq_wide_linear_scaled",
 )
 
 
@@ -153,6 +155,8 @@ def load() -> ctypes.CDLL:
         lib.rpfq_quantize_workspace_bytes.restype = sz
         lib.rpfq_quantize_wide.argtypes = [qp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.rpfq_quantize_wide_noalloc.argtypes = [qp, vp, vp, vp, vp, vp, vp]
+        lib.rpfq_row_scales.argtypes = [vp, i32, i64, i64, vp, vp]
+        lib.rpfq_wide_linear_scaled.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, vp, i32, i32, vp]
         for name in EXPORTED[2:]:
             if name not in ("rpfq_wide_packed_bytes", "rpfq_wide_adjoint_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32

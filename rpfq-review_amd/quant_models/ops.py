@@ -24,6 +24,25 @@ def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
     return t.clone(memory_format=torch.contiguous_format)
 
 
+# The forward's range guard: float32 / bf16 activations get per-row
+# power-of-two prescales (rpfq_row_scales) so the kernels' fp16 operands keep
+# the input's range (rpfq_wide_linear_scaled).  RPFQ_RANGE_GUARD=0 skips it
+# (for measurement; rows outside fp16's range then overflow or underflow).
+RANGE_GUARD = __import__("os").environ.get("RPFQ_RANGE_GUARD", "1") != "0"
+
+
+def row_scales(x2: torch.Tensor) -> torch.Tensor:
+    """Per-row power-of-two prescales of a [M, C] device tensor
+    (rpfq_row_scales): 2^(14 - floor(log2 max|row|)), 1 for zero rows."""
+    N.require_device(x2)
+    m, c = x2.shape
+    s = torch.empty(m, dtype=torch.float32, device=x2.device)
+    if m:
+        N.check("rpfq_row_scales", N.load().rpfq_row_scales(x2.data_ptr(), N.dtype_code(x2.dtype), m, c,
+                                                          s.data_ptr(), N.stream_of(x2)))
+    return s
+
+
 # Optional per-launch timing hook: when set, PackedWide.linear records HIP
 # events around each wide-linear launch on the launch stream and hands
 # (start_event, end_event, flops, algorithmic_bytes, shape) to the recorder.
@@ -202,15 +221,20 @@ class PackedWide:
 
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, flags: int = 0,
-               residual: torch.Tensor | None = None, gelu: bool = False) -> torch.Tensor:
+               residual: torch.Tensor | None = None, gelu: bool = False,
+               row_scale: torch.Tensor | None = None) -> torch.Tensor:
         """y = U x + W conj(x) + bias on [..., 2K'] -> [..., 2N'].
         flags: 0 (kernel chosen from the shape), _native.FLAG_TILE_M128,
         _native.FLAG_NO_STREAM or _native.FLAG_STREAM.  residual ([..., 2N'] of out_dtype): y =
         residual + layer(x), fused into the kernel's store and rounded as the
         unfused add would round it (rpfq_wide_linear_residual).  gelu: y =
         GELU(layer(x)) in the store (within 1 ulp of out_dtype of the exact
-        GELU of the rounded output; not with a residual)."""
-        N.require_device(x, bias, residual)
+        GELU of the rounded output; not with a residual).  float32 / bf16 x:
+        the rows are prescaled by powers of two (row_scale, float32 [M] as
+        row_scales() computes it, or computed here) so any magnitude keeps
+        its relative accuracy through the fp16 operands
+        (rpfq_wide_linear_scaled)."""
+        N.require_device(x, bias, residual, row_scale)
         if gelu:
             if residual is not None:
                 raise ValueError("gelu and residual cannot be fused together")
@@ -222,30 +246,33 @@ class PackedWide:
         m = x2.shape[0]
         out_dtype = out_dtype or x.dtype
         y = torch.empty(m, self.out_features, dtype=out_dtype, device=x.device)
+        r2 = None
         if residual is not None:
             if residual.shape[:-1] != lead or residual.shape[-1] != self.out_features:
                 raise ValueError(f"residual must have shape {tuple(lead) + (self.out_features,)}")
             r2 = _aligned_rows(residual.to(out_dtype).reshape(-1, self.out_features))
+        if row_scale is not None:
+            if row_scale.shape != (m,) or row_scale.dtype != torch.float32:
+                raise ValueError(f"row_scale must be a float32 tensor of shape ({m},)")
+            row_scale = _aligned_rows(row_scale)
         if m == 0:
             return y.reshape(*lead, self.out_features)
         if bias is not None:
             bias = bias.contiguous().float()
         lib = N.load()
+        # float32 / bf16 rows: the range guard's prescales (fp16 x is the
+        # MFMA operand as it stands); supplied rows scales are used as given
+        if row_scale is None and RANGE_GUARD and x2.dtype != torch.float16:
+            row_scale = row_scales(x2)
         rec = _launch_recorder
         if rec is not None:
             ev0 = torch.cuda.Event(enable_timing=True)
             ev1 = torch.cuda.Event(enable_timing=True)
             ev0.record()
-        if residual is None:
-            N.check("rpfq_wide_linear", lib.rpfq_wide_linear(
-                ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
-                N.dtype_code(x2.dtype), m, N.ptr(bias), y.data_ptr(), N.dtype_code(out_dtype), int(flags),
-                N.stream_of(x2)))
-        else:
-            N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
-                ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(),
-                N.dtype_code(x2.dtype), m, N.ptr(bias), r2.data_ptr(), y.data_ptr(), N.dtype_code(out_dtype),
-                int(flags), N.stream_of(x2)))
+        N.check("rpfq_wide_linear_scaled", lib.rpfq_wide_linear_scaled(
+            ctypes.byref(self.desc), self.blob.data_ptr(), self.blob.numel(), x2.data_ptr(), N.dtype_code(x2.dtype),
+            m, N.ptr(row_scale), N.ptr(bias), N.ptr(r2), y.data_ptr(), N.dtype_code(out_dtype), int(flags),
+            N.stream_of(x2)))
         if rec is not None:
             ev1.record()
             nbytes = wide_bytes(m, self.n_complex, self.k_complex, x2.element_size(), y.element_size(),

@@ -309,6 +309,116 @@ def test_wide_linear_dtypes(xdt, ydt, m):
     check_against_oracle(y, xf, None, oplanes, codebook, rotation, out_ulp)
 
 
+# row magnitudes of the range-guard tests: far below fp16's normal range,
+# inside it, at and beyond its overflow threshold, a zero row
+# (the extremes first, so a launch of a few rows holds them too)
+RANGE_MAGS = [1e30, 1e-30, 7e4, 0.0, 1e-3, 1e20, 3e-8, 6.5e4, 1.0, 1e10, 1e-20]
+
+
+def _range_rows(r, m, k_in, xdt):
+    mags = np.array([RANGE_MAGS[i % len(RANGE_MAGS)] for i in range(m)])
+    x = r.standard_normal((m, k_in)) * mags[:, None]
+    return torch.from_numpy(x.astype(np.float32)).to(xdt), mags
+
+
+def _check_range(y, xf, a16, bias, mags, u_op):
+    """Per row: |y - x A16^T - b| <= (u_op + 1e-5) sum |x||A16| + 2^-20 |b|,
+    relative to the row's own magnitude (the guard keeps every row inside
+    the fp16 operand's range); zero rows give exactly the bias."""
+    ref = xf @ a16.T + bias
+    scale = np.abs(xf) @ np.abs(a16).T
+    assert np.all(np.isfinite(y)), "non-finite outputs"
+    bound = (u_op + 1e-5) * scale + 2.0 ** -20 * np.abs(bias) + 1e-44
+    bad = np.abs(y - ref) > bound
+    assert not bad.any(), [(float(mags[i]), float((np.abs(y - ref)[i] / bound[i]).max()))
+                           for i in sorted(set(np.nonzero(bad)[0].tolist()))[:5]]
+    zero = mags == 0
+    assert np.array_equal(y[zero], np.broadcast_to(bias.astype(np.float32), y[zero].shape))
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,flags,kern", [(300, 2, "dma"), (300, 1, "tiled"), (45, 4, "stream"), (5, 0, "gemv"),
+                                          (1, 0, "gemv")])
+def test_wide_linear_range_guard(xdt, m, flags, kern):
+    """The forward's range guard: float32 / bf16 rows at 1e-30 .. 1e30, at and
+    past fp16's overflow threshold (6.5e4, 7e4) and a zero row, on the LDS-DMA
+    (bf16), register-staged, row-chunked and column-split kernels.  Every row
+    keeps the relative accuracy of an in-range row: bf16 operands exact
+    (float32 accumulation only), float32 operands within one fp16 rounding
+    (2^-11), both relative to the row's own sum |x||A16|; the zero row gives
+    the bias exactly.  Without the prescales (rpfq_wide_linear) the 7e4 and
+    larger rows overflow to inf."""
+    ops, N = qm()
+    r = rng(2500 + m + flags)
+    case = (384, 384, "axis", 2, 0, None)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    want = {"dma": N.KERNEL_DMA, "tiled": N.KERNEL_TILED, "stream": N.KERNEL_STREAM, "gemv": N.KERNEL_GEMV}[kern]
+    if kern == "dma" and xdt == torch.float32:
+        want = N.KERNEL_TILED  # float32 x is staged through registers
+    assert pw.kernel_for(m, xdt, torch.float32, flags) == want
+    x, mags = _range_rows(r, m, 2 * case[1], xdt)
+    # no bias: a row of 1e-30 would vanish in it
+    y = pw.linear(x.to(DEV), None, out_dtype=torch.float32, flags=flags).cpu().numpy().astype(np.float64)
+    xf = x.float().numpy().astype(np.float64)
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=operand(pw, m, xdt, torch.float32, flags)).astype(np.float64)
+    _check_range(y, xf, a16, np.zeros(2 * case[0]), mags, 2.0 ** -11 if xdt == torch.float32 else 0.0)
+    # the prescales are what keeps the large rows finite
+    y0 = torch.empty(m, 2 * case[0], dtype=torch.float32, device=DEV)
+    pw.linear_into(x.to(DEV), None, y0, flags)
+    big = mags >= 7e4
+    assert big.any() and not torch.isfinite(y0.cpu()[torch.from_numpy(big)]).all()
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_row_scales(xdt):
+    """rpfq_row_scales: 2^(14 - floor(log2 max|row|)) per row (the scaled
+    maximum in [2^14, 2^15)), clamped to [2^-126, 2^126]; 1 for zero and
+    non-finite rows; any C (element loads when C % 8 != 0)."""
+    ops, _ = qm()
+    r = rng(2600)
+    for c in (768, 13):
+        x, mags = _range_rows(r, 40, c, xdt)
+        x[3] = float("inf")
+        x[4, 2] = float("nan")
+        s = ops.row_scales(x.to(DEV)).cpu().numpy().astype(np.float64)
+        ax = x.float().abs()
+        mx = torch.where(torch.isnan(ax), torch.zeros_like(ax), ax).amax(dim=1).numpy().astype(np.float64)
+        for i in range(40):
+            if mx[i] == 0 or not np.isfinite(mx[i]):
+                assert s[i] == 1.0, (i, s[i])
+                continue
+            k = int(np.clip(14 - np.floor(np.log2(mx[i])), -126, 126))
+            assert s[i] == 2.0 ** k, (i, mx[i], s[i])
+            if -126 < k < 126:
+                assert 2.0 ** 14 <= mx[i] * s[i] < 2.0 ** 15
+
+
+def test_act_quant_prologue_range_guard():
+    """The streaming kernel's act-quant row prologue on bf16 rows of every
+    magnitude (1e-30 .. 1e30): the quantized rows take the prescale of their
+    largest magnitude as rpfq_row_scales gives it to the row kernel's output,
+    so the fused launch is bit-identical to act_quant followed by the
+    guarded layer, and both meet the exact-operand bound."""
+    ops, N = qm()
+    r = rng(2700)
+    case = (384, 384, "axis", 2, 0, None)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    m = 22
+    assert pw.ln_fusable(m, torch.bfloat16)
+    x, mags = _range_rows(r, m, 768, torch.bfloat16)
+    bias = r.standard_normal(768).astype(np.float32)
+    xd = x.to(DEV)
+    y = pw.act_quant_linear(xd, 4, tdev(bias), out_dtype=torch.float32)
+    h = ops.act_quant(xd, 4)
+    y_sep = pw.linear(h, tdev(bias), out_dtype=torch.float32)
+    assert torch.equal(y, y_sep)
+    hf = h.float().cpu().numpy().astype(np.float64)
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    hm = np.abs(hf).max(axis=1)
+    _check_range(y.cpu().numpy().astype(np.float64), hf, a16, bias.astype(np.float64), np.where(hm > 0, mags, 0.0),
+                 0.0)
+
+
 def test_wide_linear_matches_reference_android_runtime():
     """Same packed planes through the compiled reference (oracle/_ref,
     wideLinearReference) and through the HIP kernel."""
