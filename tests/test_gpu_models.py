@@ -502,6 +502,190 @@ def test_act_quant_layers_on_reference_trajectory(name):
     assert len(seen) == sum(1 for _ in quant_layers(model))
 
 
+def _aq_levels(x, bits, amax=None):
+    """Integer levels q of the reference's act quant (quant_i.py:438-455) of
+    float32 rows [..., 2K'] per half, in its float32 arithmetic: scale =
+    (1 / max(amax, 1e-5)) * qmax (torch's reciprocal-times form), q =
+    clamp(rint(x * scale)); also the scale.  amax: per-(row, half) maxima to
+    use instead of the rows' own."""
+    x = np.asarray(x, dtype=np.float32)
+    h = x.shape[-1] // 2
+    qmax, qmin = np.float32(2 ** (bits - 1) - 1), np.float32(-(2 ** (bits - 1)))
+    qs, ss = [], []
+    for i, part in enumerate((x[..., :h], x[..., h:])):
+        m = np.abs(part).max(axis=-1, keepdims=True) if amax is None else amax[i]
+        sc = (np.float32(1.0) / np.maximum(m, np.float32(1e-5))).astype(np.float32) * qmax
+        qs.append(np.clip(np.rint(part * sc), qmin, qmax))
+        ss.append(sc.astype(np.float32))
+    return np.concatenate(qs, axis=-1), ss
+
+
+@pytest.mark.parametrize("name", ["rpfq_vit_base_patch16_224_q", "rpfq_swin_tiny_patch4_window7_224_q",
+                                  "rpfq_deit_tiny_patch16_224_q"])
+def test_act_quant_level_flips_from_input_rounding(name):
+    """Level-flip count of the 4-bit act quant when its float32 input is
+    first rounded to fp16 -- what an fp16 activation stream does to every
+    stored activation -- against the reference's levels on the float32 input
+    (every packed layer of the reference trajectory, as in
+    test_act_quant_layers_on_reference_trajectory).  The device act quant
+    (rpfq_act_quant) is bit-exact on what it is given, so a level can move
+    only where rounding x to fp16 (half an ulp, 2^-11 relative, 2^-25
+    absolute for subnormals) and the row maximum's rounding (2^-11 of the
+    scale) can carry x * scale across a half-integer: every flip lies in
+    that candidate set.  The flip and candidate fractions are printed."""
+    from quant_models import ops
+    from quant_models.inference import prepare_inference, quant_layers
+    import quant_models as qm
+
+    model, ref_state = _synthetic_model(name, 41, act_quant=True)
+    prepare_inference(model, DEV, torch.float16)
+    x = torch.randn(2, 3, 224, 224, generator=torch.Generator().manual_seed(43))
+    ref = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                          quant_method_w="complex_phase_v2", enable_act_quant=True, enable_rotation=False)
+    ref.load_state_dict({k: v.float().cpu() for k, v in ref_state.items()})
+    ref.eval()
+    seen = []
+    for (n_g, l_g), (n_c, l_c) in zip(quant_layers(model), quant_layers(ref)):
+        a_q = _decoded_weight(l_g._override)
+        bias = None if l_c.bias is None else l_c.bias.detach().float()
+        bits = l_c.act_quantizer.num_bits
+
+        def fwd(xx, a_q=a_q, bias=bias, bits=bits):
+            seen.append((xx.reshape(-1, xx.shape[-1]).clone(), bits))
+            return F.linear(_oracle_act_quant(xx, bits), a_q, bias)
+        l_c.forward = fwd
+    with torch.no_grad():
+        ref(x)
+    n_el = n_flip = n_cand = 0
+    for xx, bits in seen:
+        xr = xx.numpy().astype(np.float32)
+        q_ref, s_ref = _aq_levels(xr, bits)
+        x16 = xx.to(torch.float16)
+        with torch.no_grad():
+            xh = ops.act_quant(x16.to(DEV), bits, out_dtype=torch.float32).cpu().numpy()
+        q_gpu, _ = _aq_levels(x16.float().numpy(), bits)
+        h = xr.shape[1] // 2
+        # the device output is q / scale of the fp16 rows: recover its levels exactly
+        _, s16 = _aq_levels(x16.float().numpy(), bits)
+        lev = np.concatenate([np.rint(xh[:, :h] * s16[0]), np.rint(xh[:, h:] * s16[1])], axis=1)
+        assert np.array_equal(lev, q_gpu)
+        sref = np.concatenate([np.broadcast_to(s_ref[0], (xr.shape[0], h)), np.broadcast_to(s_ref[1], (xr.shape[0], h))],
+                              axis=1).astype(np.float64)
+        v = xr.astype(np.float64) * sref
+        d = (np.abs(xr.astype(np.float64)) * 2.0 ** -11 + 2.0 ** -25) * sref + np.abs(v) * (2.0 ** -10 + 2.0 ** -22)
+        qmax, qmin = 2 ** (bits - 1) - 1, -(2 ** (bits - 1))
+        cand = np.clip(np.rint(v - d), qmin, qmax) != np.clip(np.rint(v + d), qmin, qmax)
+        flip = q_gpu != q_ref
+        assert not (flip & ~cand).any(), int((flip & ~cand).sum())
+        n_el += flip.size
+        n_flip += int(flip.sum())
+        n_cand += int(cand.sum())
+    rep = {"layer_calls": len(seen), "elements": n_el, "flip_frac": n_flip / n_el, "candidate_frac": n_cand / n_el}
+    print(f"PARITY {name} act4 level flips from fp16 input rounding {rep}", flush=True)
+    log = os.environ.get("RPFQ_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps({"case": f"{name} act4 level flips", **rep}) + "\n")
+
+
+# (name, act quant, batch, batches): the end-to-end share of the packed
+# contraction on >= 1,000 images
+ISOLATED_CASES = [
+    ("rpfq_deit_tiny_patch16_224_q", True, 64, 16),
+    ("rpfq_deit_tiny_patch16_224_q", False, 64, 16),
+    ("rpfq_vit_base_patch16_224_q", False, 256, 4),
+    ("rpfq_vit_base_patch16_224_q", True, 256, 4),
+]
+
+
+@pytest.mark.parametrize("case", ISOLATED_CASES, ids=[f"{c[0].split('_')[1]}-aq{int(c[1])}-bs{c[2]}"
+                                                      for c in ISOLATED_CASES])
+def test_packed_contraction_end_to_end_share(case):
+    """The packed layers' own share of the end-to-end error, isolated: the
+    same fp16 GPU forward (same fused LayerNorm / act quant / GELU kernels,
+    same attention, same rounding of every stored activation) run twice --
+    once with the packed HIP contraction, once with every packed layer's
+    contraction replaced by the reference's F.linear (quant_i.py:554) in
+    float64 on the reference's float32 A_q (the oracle's decoding of the same
+    codes), rounded to the activation dtype where the packed path rounds.
+    Over >= 1,000 images: max |d logit|, raw top-1 agreement and agreement on
+    margin-confident images (margin > 4x the max error, which must be 100%),
+    printed as PARITY lines.  Without act quant the logits stay within
+    1e-2 * max|logit| + 1e-3; with it, a 1-ulp difference next to a 4-bit
+    rounding boundary moves a whole level, so only the printed figures and
+    the confident agreement are asserted."""
+    from quant_models import ops
+    from quant_models.inference import prepare_inference, quant_layers
+
+    name, aq, batch, nb = case
+    model, _ = _synthetic_model(name, 61, act_quant=aq)
+    prepare_inference(model, DEV, torch.float16)
+    aqs = {}
+    for _, layer in quant_layers(model):
+        aqs[id(layer.packed(torch.device(DEV)))] = _decoded_weight(layer._override).to(DEV, torch.float64)
+    linear, ln_linear, aq_linear = ops.PackedWide.linear, ops.PackedWide.layer_norm_linear, \
+        ops.PackedWide.act_quant_linear
+
+    prec = [torch.float64]
+
+    def ref_linear(self, x, bias=None, out_dtype=None, flags=0, residual=None, gelu=False, row_scale=None):
+        a = aqs[id(self)].to(prec[0])
+        out_dtype = out_dtype or x.dtype
+        y = x.reshape(-1, x.shape[-1]).to(prec[0]) @ a.T
+        if bias is not None:
+            y = y + bias.to(prec[0])
+        y = y.to(out_dtype)
+        if gelu:
+            y = F.gelu(y.float()).to(out_dtype)
+        if residual is not None:
+            y = (residual.reshape(y.shape).float() + y.float()).to(out_dtype)
+        return y.reshape(*x.shape[:-1], a.shape[0])
+
+    def ref_aq_linear(self, x, bits, bias=None, out_dtype=None, gelu=False, residual=None, layer_norm=None):
+        # the row prologue's quantized rows are rpfq_act_quant's /
+        # rpfq_layer_norm_act_quant's bit for bit (test_act_quant_wide_linear)
+        h = ops.act_quant(x, bits) if layer_norm is None else ops.layer_norm(x, *layer_norm, act_bits=bits)
+        return ref_linear(self, h, bias, out_dtype, 0, residual, gelu)
+
+    def ref_ln_linear(self, x, ln_weight, ln_bias, eps, bias=None, out_dtype=None, gelu=False):
+        return ref_linear(self, ops.layer_norm(x, ln_weight, ln_bias, eps), bias, out_dtype, 0, None, gelu)
+    g = torch.Generator().manual_seed(63)
+    ys, yr, y32 = [], [], []
+    try:
+        for _ in range(nb):
+            x = torch.randn(batch, 3, 224, 224, generator=g).to(DEV, torch.float16)
+            with torch.no_grad():
+                ops.PackedWide.linear, ops.PackedWide.layer_norm_linear, ops.PackedWide.act_quant_linear = \
+                    linear, ln_linear, aq_linear
+                ys.append(model(x).float().cpu())
+                ops.PackedWide.linear, ops.PackedWide.layer_norm_linear, ops.PackedWide.act_quant_linear = \
+                    ref_linear, ref_ln_linear, ref_aq_linear
+                prec[0] = torch.float64
+                yr.append(model(x).float().cpu())
+                if aq:  # the same reference contraction summed in float32 instead
+                    prec[0] = torch.float32
+                    y32.append(model(x).float().cpu())
+    finally:
+        ops.PackedWide.linear, ops.PackedWide.layer_norm_linear, ops.PackedWide.act_quant_linear = \
+            linear, ln_linear, aq_linear
+    y, y_ref = torch.cat(ys), torch.cat(yr)
+    err, agree, confident, rep = _logit_report(f"{name} act{4 if aq else 0} packed-vs-reference-contraction "
+                                               f"{y.shape[0]} images", y, y_ref)
+    assert y.shape[0] >= 1000
+    assert bool(agree[confident].all()), rep
+    if not aq:
+        tol = LOGIT_TOL["fp16"]
+        assert err.max() <= tol * y_ref.abs().max() + tol / 10, rep
+    else:
+        # the act-quant envelope: two faithful references of the same
+        # formula, float32 against float64 sums, on the same pipeline; a
+        # systematic error (a wrong level, scale or rounding point) would
+        # leave chance agreement (1 / 1000), far below half the envelope's
+        _, _, _, env = _logit_report(f"{name} act4 float32-vs-float64-reference-contraction {y.shape[0]} images",
+                                     torch.cat(y32), y_ref)
+        assert rep["top1"] >= 0.5 * env["top1"], (rep, env)
+
+
 @pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_swin_tiny_patch4_window7_224_q"])
 def test_fused_blocks_match_unfused(name):
     """Eval forward with the fused block path (device LayerNorm, residual adds
