@@ -545,6 +545,43 @@ def test_wide_linear_full_batch_rows(case):
     check_against_oracle(ys, xf, bias, oplanes, codebook, rotation, out_ulp=2.0 ** -11)
 
 
+DMA_ROUND_CASES = [
+    ((1152, 384, "axis", 2, 0, None), 20000, True),    # 1,413 tiles: 2.8 rounds, last m-tile shifted
+    ((128, 96, "axis", 2, 0, None), 70001, False),     # K' = 96: 3 k-steps, no bias, shifted
+    ((256, 512, "psk16", 1, 0, None), 65536, True),    # 16-PSK, 1,024 tiles: exactly 2 rounds
+    ((128, 128, "sign", 2, 0, ((0.8, 0.6), (0.6, -0.8))), 30001, True),  # sign codes, rotation
+]
+
+
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case,m,with_bias", DMA_ROUND_CASES,
+                         ids=[f"{c[0][0]}x{c[0][1]}-{c[0][2]}-m{c[1]}" for c in DMA_ROUND_CASES])
+def test_wide_linear_dma_rounds(case, m, with_bias, ydt):
+    """The DMA kernel over several rounds of its persistent grid (each
+    workgroup's later tiles take their first loads from the previous tile's
+    prefetch), with and without bias, 16-bit outputs, the shifted last m-tile,
+    three codebooks: sampled rows (first and last m-tile, 256 random) against
+    the oracle, and the whole output bit-identical to a second launch and to
+    the same launch with a zero residual added in the store."""
+    ops, N = qm()
+    r = rng(1650 + case[0] + case[1] + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    assert pw.kernel_for(m, torch.float16, ydt) == N.KERNEL_DMA
+    x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16).to(DEV)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32) if with_bias else None
+    bd = tdev(bias) if with_bias else None
+    y = pw.linear(x, bd, out_dtype=ydt)
+    assert torch.equal(y, pw.linear(x, bd, out_dtype=ydt))
+    zero = torch.zeros(m, 2 * case[0], dtype=ydt, device=DEV)
+    assert torch.equal(y, pw.linear(x, bd, out_dtype=ydt, residual=zero))
+    rows = np.unique(np.concatenate([np.arange(128), np.arange(m - 128, m), r.choice(m, size=256, replace=False)]))
+    idx = torch.from_numpy(rows).to(DEV)
+    ys = y.index_select(0, idx).float().cpu().numpy()
+    xf = x.index_select(0, idx).float().cpu().numpy().astype(np.float64)
+    out_ulp = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[ydt]
+    check_against_oracle(ys, xf, bias, oplanes, codebook, rotation, out_ulp=out_ulp)
+
+
 def test_wide_linear_kernels_consistent():
     """Both kernels contract the same fp16 operands (they differ only in the
     k order inside each MFMA), so float32 outputs agree to accumulation order."""
