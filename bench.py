@@ -348,7 +348,8 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
     dt = dtype or torch.float16
     from quant_models import _native as N
     kname = {N.KERNEL_STREAM: "rpfq::wide_linear_skinny_kernel", N.KERNEL_GEMV: "rpfq::wide_linear_gemv_kernel",
-             N.KERNEL_DMA: "rpfq::wide_linear_dma_kernel", N.KERNEL_TILED: "rpfq::wide_linear_kernel"}[
+             N.KERNEL_DMA: "rpfq::wide_linear_dma_kernel", N.KERNEL_TILED: "rpfq::wide_linear_kernel",
+             N.KERNEL_RESIDENT: "rpfq::wide_linear_resident_kernel"}[
         layers[0].kernel_for(m, dt, dt)]
     x = torch.randn(m, 2 * k_c, device=dev, generator=g).to(dt)
     bias = torch.randn(2 * n_layer, device=dev, generator=g)
@@ -413,28 +414,33 @@ def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, r
     return rows
 
 
-def layer_probe(n_c: int, k_c: int, m: int, steps: int) -> int:
+def layer_probe(n_c: int, k_c: int, m: int, steps: int, flags: int = 0) -> int:
     """One q2 layer of N' x K' (uniformly random code bytes, per-row scales)
-    on m fp16 rows: `steps` launches of the packed kernel, timed with HIP
-    events; prints one JSON line."""
+    on m fp16 rows: `steps` launches of the packed kernel (the one `flags`
+    select), timed with HIP events; prints one JSON line with the kernel,
+    the time per launch and the algorithmic HBM rate (ops.wide_bytes)."""
     import torch
+    from quant_models import ops
 
     pw = stream_layer(k_c, n_c, 1)[0]
     g = torch.Generator(device="cuda").manual_seed(1)
     x = torch.randn(m, 2 * k_c, device="cuda", generator=g).half()
     y = torch.empty(m, 2 * n_c, device="cuda", dtype=torch.float16)
-    pw.linear_into(x, None, y)
+    pw.linear_into(x, None, y, flags)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
     for _ in range(steps):
-        pw.linear_into(x, None, y)
+        pw.linear_into(x, None, y, flags)
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / max(1, steps)
     flops = 2 * m * 2 * k_c * 2 * n_c
-    print(json.dumps({"layer_probe": [n_c, k_c], "m": m, "launches": steps + 1, "avg_us": round(us, 2),
-                      "tflops": round(flops / us / 1e6, 1)}))
+    gbs = ops.wide_bytes(m, n_c, k_c) / us / 1e3
+    print(json.dumps({"layer_probe": [n_c, k_c], "m": m, "flags": flags,
+                      "kernel": pw.kernel_for(m, torch.float16, torch.float16, flags), "launches": steps + 1,
+                      "avg_us": round(us, 2), "tflops": round(flops / us / 1e6, 1), "gbs": round(gbs, 1),
+                      "frac": round(gbs / PEAK_HBM_GBS, 4)}))
     return 0
 
 
@@ -721,6 +727,9 @@ def main() -> int:
     ap.add_argument("--layer-probe", default=None, metavar="NC,KC",
                     help="time one q2 layer of N' x K' complex (random codes) on 50,432 fp16 rows instead "
                          "(--steps launches; for counter runs)")
+    ap.add_argument("--probe-flags", type=int, default=0,
+                    help="rpfq_wide_linear flags of the --layer-probe launches (e.g. 2: no streaming, "
+                         "16: the resident-weight kernel)")
     ap.add_argument("--vs-library", action="store_true",
                     help="only time the ViT-B/16 layer forwards on the packed kernel against the dense library GEMM "
                          "on the decoded weight (same box)")
@@ -734,7 +743,8 @@ def main() -> int:
                     help="skip the bf16-activation sub-block of the default (fp16) bench line")
     args = ap.parse_args()
     if args.layer_probe:
-        return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps)
+        return layer_probe(*(int(v) for v in args.layer_probe.split(",")), args.batch or 50432, args.steps,
+                           args.probe_flags)
     if args.grad_x:
         return grad_x_bench(args.batch * 197 if args.batch else 50432, args.steps)
     if args.vs_library:

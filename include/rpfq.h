@@ -51,18 +51,26 @@ extern "C" {
 /* rpfq_wide_linear flags.  Default (0): the kernel is chosen from the shape
  * (M <= 16, and small-M launches where a cost model predicts it faster --
  * e.g. a ViT-B layer at one image -- stream the packed codes, 32-row tiles
- * against 16-row chunks of x; fp16 x with K' % 32 == 0 and M >= 128 stages
- * activations by LDS DMA; other cases stage them through registers with a
- * 32/64/128-row tile).
+ * against 16-row chunks of x; M >= 32768 with a small layer -- N' % 16 == 0,
+ * K' in {48, 96, 192}, the decoded 2N' x 2K' fp16 matrix and the bias within
+ * 160 KB of LDS, fp16 / bf16 x and y, y 16-byte aligned: Swin-T stage 0 --
+ * keeps the decoded layer resident in LDS and streams rows of x; fp16 / bf16
+ * x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA; other cases
+ * stage them through registers with a 32/64/128-row tile).
  * RPFQ_FLAG_TILE_M128 forces the register-staged 128-row kernel;
- * RPFQ_FLAG_NO_STREAM keeps every M on the tiled kernels;
+ * RPFQ_FLAG_NO_STREAM keeps every M on the tiled kernels (not the resident
+ * one);
  * RPFQ_FLAG_STREAM forces the streaming kernel for any M (one workgroup per
  * 16-row chunk of x and 32-row tile of the codes; at most 2^24 of them,
- * else RPFQ_ERR_SHAPE; not combinable with the other two, RPFQ_ERR_VALUE).
+ * else RPFQ_ERR_SHAPE; not combinable with the other two, RPFQ_ERR_VALUE);
+ * RPFQ_FLAG_RESIDENT forces the resident-weight kernel for any M (the layer
+ * and dtypes as above, else RPFQ_ERR_SHAPE / RPFQ_ERR_DTYPE, y not 16-byte
+ * aligned RPFQ_ERR_ALIGN; not combinable with the other three).
  * Every kernel feeds the MFMA the same fp16 coefficients. */
 #define RPFQ_FLAG_TILE_M128 1
 #define RPFQ_FLAG_NO_STREAM 2
 #define RPFQ_FLAG_STREAM 4
+#define RPFQ_FLAG_RESIDENT 16
 /* RPFQ_FLAG_GELU (rpfq_wide_linear only; the residual entry point rejects
  * it, RPFQ_ERR_VALUE): y = gelu(layer output), exact erf GELU applied in the
  * store to the output rounded to y's dtype, computed in float32 and rounded
@@ -185,6 +193,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
 #define RPFQ_KERNEL_DMA 1     /* 128-row tiles, activations staged by LDS DMA */
 #define RPFQ_KERNEL_TILED 2   /* 32/64/128-row tiles staged through registers */
 #define RPFQ_KERNEL_GEMV 3    /* weight streaming for M <= 8, U and W as separate MFMA operands */
+#define RPFQ_KERNEL_RESIDENT 4 /* decoded layer resident in LDS, 32-row subtiles of x per wave */
 
 /*
  * *kernel := the RPFQ_KERNEL_* that rpfq_wide_linear runs for this layer, M,

@@ -143,15 +143,29 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
 }
 
 // Flags: known bits, no contradictory pair, GELU only without a residual,
-// and a streaming launch (one workgroup per 16-row chunk and 32-row tile)
-// within the grid.
-static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M, bool residual) {
-    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM | RPFQ_FLAG_GELU))
+// a streaming launch (one workgroup per 16-row chunk and 32-row tile)
+// within the grid, and a forced resident-weight launch on a layer, dtypes
+// and y it takes (y NULL: a kernel-choice query).
+static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M, bool residual, int x_dtype, int y_dtype,
+                       const void* y) {
+    if (flags & ~(RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM | RPFQ_FLAG_GELU | RPFQ_FLAG_RESIDENT))
         return fail(RPFQ_ERR_VALUE, "flags=%d: unknown flag bits", flags);
     if (residual && (flags & RPFQ_FLAG_GELU))
         return fail(RPFQ_ERR_VALUE, "RPFQ_FLAG_GELU is not defined with a residual");
     if ((flags & RPFQ_FLAG_STREAM) && (flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)))
         return fail(RPFQ_ERR_VALUE, "flags=%d: RPFQ_FLAG_STREAM excludes the tiled-kernel flags", flags);
+    if ((flags & RPFQ_FLAG_RESIDENT) && (flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM | RPFQ_FLAG_STREAM)))
+        return fail(RPFQ_ERR_VALUE, "flags=%d: RPFQ_FLAG_RESIDENT excludes the other kernel flags", flags);
+    if (flags & RPFQ_FLAG_RESIDENT) {
+        if ((x_dtype != RPFQ_F16 && x_dtype != RPFQ_BF16) || (y_dtype != RPFQ_F16 && y_dtype != RPFQ_BF16))
+            return fail(RPFQ_ERR_DTYPE, "RPFQ_FLAG_RESIDENT takes fp16 / bf16 x and y (x=%d y=%d)", x_dtype, y_dtype);
+        if (!rpfq::wide_resident_eligible(g, x_dtype, y_dtype))
+            return fail(RPFQ_ERR_SHAPE,
+                        "RPFQ_FLAG_RESIDENT: N'=%lld K'=%lld (needs N' %% 16 == 0, K' in {48, 96, 192}, "
+                        "the decoded layer within 160 KB)",
+                        (long long)g.N, (long long)g.K);
+        if (y && !aligned(y, 16)) return fail(RPFQ_ERR_ALIGN, "RPFQ_FLAG_RESIDENT needs y 16-byte aligned");
+    }
     if ((flags & RPFQ_FLAG_STREAM) && (int64_t)g.NT * ((M + 15) / 16) > ((int64_t)1 << 24))
         return fail(RPFQ_ERR_SHAPE, "M=%lld: RPFQ_FLAG_STREAM allows at most 2^24 (chunk, tile) workgroups",
                     (long long)M);
@@ -167,7 +181,7 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M, false))) return rc;
+    if ((rc = check_flags(flags, g, M, false, x_dtype, y_dtype, y))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16))
@@ -187,7 +201,7 @@ int rpfq_wide_linear_kernel(const rpfq_wide_desc* desc, int64_t M, int x_dtype, 
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M, false))) return rc;
+    if ((rc = check_flags(flags, g, M, false, x_dtype, y_dtype, nullptr))) return rc;
     if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
     *kernel = rpfq::wide_linear_kernel_choice(g, x_dtype, M, y_dtype, flags);
     return RPFQ_OK;
@@ -274,7 +288,7 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M, true))) return rc;
+    if ((rc = check_flags(flags, g, M, true, x_dtype, y_dtype, y))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16) || !aligned(residual, 16))
@@ -296,7 +310,7 @@ int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size
         return fail(RPFQ_ERR_DTYPE, "unsupported dtype x=%d y=%d", x_dtype, y_dtype);
     if (M <= 0) return fail(RPFQ_ERR_SHAPE, "M=%lld must be positive", (long long)M);
     rpfq::WideGeom g = rpfq::wide_geom(*desc);
-    if ((rc = check_flags(flags, g, M, residual != nullptr))) return rc;
+    if ((rc = check_flags(flags, g, M, residual != nullptr, x_dtype, y_dtype, y))) return rc;
     if (packed_bytes < g.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffer holds %zu bytes, need %zu", packed_bytes, g.total_bytes);
     if (!aligned(packed, 256) || !aligned(x, 16) || (residual && !aligned(residual, 16)))

@@ -153,6 +153,25 @@ hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t
 template <int CB> hipError_t launch_wide_dma(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int ydt, hipStream_t s);
+template <int CB> hipError_t launch_wide_resident(WideArgs& a, int xdt, int ydt, hipStream_t s);
+
+// Resident-weight kernel (wide_resident.hip): one workgroup of kResWaves
+// waves per CU holds the whole decoded layer in LDS (2N' x 2K' fp16 as MFMA
+// A operands, plus the float32 bias) and streams 16-row subtiles of x, each
+// wave holding whole output rows.  Shapes: N' % 16 == 0, N' <= 192 (the
+// accumulators of a row block), K' in {48, 96, 192}, the LDS within 160 KB
+// (K' = 192: N' <= 96); fp16 / bf16 x and y.
+constexpr int kResWaves = 8;
+constexpr int kResLdsMax = 160 * 1024;
+inline int resident_lds(const WideArgs& a) { return (a.N / 8) * (a.K / 16) * 1024 + 8 * a.N; }
+// shape and dtypes of a layer the kernel takes (wide_dispatch.hip)
+bool wide_resident_eligible(const WideGeom& g, int xdt, int ydt);
+inline bool resident_shape(const WideArgs& a) {
+    if (a.N <= 0 || a.N % 16 != 0 || a.N > 192) return false;
+    if (a.K != 48 && a.K != 96 && a.K != 192) return false;
+    return resident_lds(a) <= kResLdsMax;
+}
+
 // workgroups of the streaming kernel: one per (16-row chunk, 32-row tile)
 inline int64_t sk_groups(const WideArgs& a) { return a.NT * ((a.M + 15) / 16); }
 

@@ -29,6 +29,20 @@ hipError_t set_lds_attr_once(const void* kernel, int bytes, std::atomic<uint64_t
     return e;
 }
 
+// Shape fields of the launch arguments (what the kernel choice reads).
+static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
+    WideArgs a = {};
+    a.M = M;
+    a.K = (int)g.K;
+    a.N = (int)g.N;
+    a.NT = (int)g.NT;
+    a.KS = (int)g.KS;
+    a.nblk = (int)g.nblk;
+    a.block_ks = (int)g.block_ks;
+    a.act = (flags & RPFQ_FLAG_GELU) ? 1 : 0;  // an epilogue op, not a kernel choice
+    return a;
+}
+
 // Kernel choice for a small M.  A tiled kernel gives each workgroup one
 // 128-row x 128-column output tile through all of K, so while the launch is
 // at most one tile deep it costs about one tile's latency, ~5 + KS us on
@@ -53,11 +67,29 @@ static bool stream_pays(const WideArgs& a) {
 #ifndef RPFQ_DMA_MIN_M
 #define RPFQ_DMA_MIN_M 128
 #endif
+#ifndef RPFQ_RES_MIN_M
+#define RPFQ_RES_MIN_M 32768
+#endif
+// Layers the resident-weight kernel takes (shape and dtypes; y 16-byte
+// aligned, a NULL y counting as aligned for kernel-choice queries).
+static bool resident_ok(const WideArgs& a, int xdt, int ydt) {
+    return (xdt == RPFQ_F16 || xdt == RPFQ_BF16) && (ydt == RPFQ_F16 || ydt == RPFQ_BF16) && resident_shape(a) &&
+           reinterpret_cast<uintptr_t>(a.y) % 16 == 0;
+}
+
+bool wide_resident_eligible(const WideGeom& g, int xdt, int ydt) {
+    return resident_ok(wide_shape(g, 1, 0), xdt, ydt);
+}
+
 // The kernel a launch runs (RPFQ_KERNEL_*), from the shape, dtypes and the
-// kernel-choice flags (the GELU bit already moved into a.act).
+// kernel-choice flags (the GELU bit already moved into a.act).  The
+// resident-weight kernel runs for large M where the layer fits, unless a
+// flag asks for another kernel.
 static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
+    if (flags & RPFQ_FLAG_RESIDENT) return RPFQ_KERNEL_RESIDENT;  // eligibility checked by the C API
     if ((flags & RPFQ_FLAG_STREAM) || (!(flags & (RPFQ_FLAG_TILE_M128 | RPFQ_FLAG_NO_STREAM)) && stream_pays(a)))
         return gemv_pays(a) ? RPFQ_KERNEL_GEMV : RPFQ_KERNEL_STREAM;
+    if (flags == 0 && a.M >= RPFQ_RES_MIN_M && resident_ok(a, xdt, ydt)) return RPFQ_KERNEL_RESIDENT;
     flags &= ~RPFQ_FLAG_NO_STREAM;
     // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
     // spill in its k-loop, so they take the register-staged kernel)
@@ -72,23 +104,10 @@ static hipError_t wide_cb(WideArgs& a, int xdt, int ydt, int flags, hipStream_t 
     const int k = choose_kernel(a, xdt, ydt, flags);
     if (k == RPFQ_KERNEL_STREAM || k == RPFQ_KERNEL_GEMV) return launch_wide_stream<CB>(a, xdt, ydt, s);
     if (k == RPFQ_KERNEL_DMA) return launch_wide_dma<CB>(a, xdt, ydt, s);
+    if (k == RPFQ_KERNEL_RESIDENT) return launch_wide_resident<CB>(a, xdt, ydt, s);
     flags &= ~RPFQ_FLAG_NO_STREAM;
     const int bm = (flags & RPFQ_FLAG_TILE_M128) ? 128 : a.M <= 32 ? 32 : a.M <= 64 ? 64 : 128;
     return launch_wide_tiled<CB>(a, bm, xdt, ydt, s);
-}
-
-// Shape fields of the launch arguments (what the kernel choice reads).
-static WideArgs wide_shape(const WideGeom& g, int64_t M, int flags) {
-    WideArgs a = {};
-    a.M = M;
-    a.K = (int)g.K;
-    a.N = (int)g.N;
-    a.NT = (int)g.NT;
-    a.KS = (int)g.KS;
-    a.nblk = (int)g.nblk;
-    a.block_ks = (int)g.block_ks;
-    a.act = (flags & RPFQ_FLAG_GELU) ? 1 : 0;  // an epilogue op, not a kernel choice
-    return a;
 }
 
 // The fused LayerNorm runs in the streaming kernel split over 4 waves (for

@@ -1,0 +1,290 @@
+// Widely-linear GEMM for small layers at large M: the decoded layer stays in
+// LDS for the whole launch and the waves stream rows of x past it.
+// Compiled once per codebook (RPFQ_CB_SEL).
+#include "rpfq_device.h"
+
+#ifndef RPFQ_CB_SEL
+#error "compile once per codebook with -DRPFQ_CB_SEL=<RPFQ_CB_*>"
+#endif
+
+namespace rpfq {
+
+// ---------------------------------------------------------------------------
+// Resident-weight kernel (RPFQ_KERNEL_RESIDENT).
+//
+// The layer is one real GEMM y [M, 2N'] = x [M, 2K'] A_r^T with
+//   A_r [2N'][2K'] = [[A11, A12], [A21, A22]]
+// (rows n < N' give Re y_n, rows N' + n give Im y_n; columns k < K' multiply
+// Re x_k, columns K' + k multiply Im x_k).  A persistent workgroup of
+// kResWaves waves (one per CU) decodes all of A_r into LDS once, as the A
+// operands of v_mfma_f32_16x16x32_f16: tile (b, c) holds rows 16 b .. +15
+// and columns 32 c .. +31, lane l = (o, q) = (l % 16, l / 16) the 8 fp16
+// A_r[16 b + o][32 c + 8 q ..] at byte ((b * KC + c) * 64 + l) * 16
+// (KC = 2K' / 32 tiles per row block).  Every wave then takes 16-row
+// subtiles of x on its own, with no barrier, and holds the whole output row
+// block of its subtile in registers (2N' / 16 accumulator tiles):
+//   * B operand: lane (r, q) loads row m0 + r, columns 32 c + 8 q .. + 7 of
+//     every k-chunk c (16 B; 64 contiguous bytes per row and instruction;
+//     bf16 rows converted to fp16 after the row's prescale, as every kernel
+//     converts them); the next subtile's rows are requested before the
+//     current one's MFMAs;
+//   * D: lane (r, q) holds x row r's outputs 16 b + 4 q .. + 3;
+//     after bias and rounding, v_permlane16_swap pairs blocks 2p and 2p + 1
+//     so that lane (r, q) holds the 8 outputs 32 p + 16 (q & 1) + 8 (q >> 1)
+//     .. + 7: one 16-B store, 64 contiguous bytes per row and instruction;
+//   * the subtile's rows are stored in one burst of 2N' / 32 instructions
+//     (whole rows, so the L2 merges every 128-B line before it writes it back;
+//     write-back stores: non-temporal ones reach HBM as partial lines and
+//     halve the rate).
+// Every coefficient is the fp16 value the other kernels feed the MFMA
+// (lut_entry, de-rotation, cvt_pk, fuse_h), and the epilogue rounds as theirs.
+// ---------------------------------------------------------------------------
+constexpr int kResMaxTasks = 5;  // decode tasks per thread: N' K' / 8 <= 5 * 512 for every layer taken
+
+// Decodes the layer into the LDS tiles above and the bias after them.
+// Task (n, k0): complex row n, columns k0 .. k0 + 7 (one 4-byte code word
+// in each lane-group half of the row's k-step), giving 8 columns of each of
+// A11, A12, A21, A22.  Every global load of the thread is issued first.
+template <int CB, int KC>
+__device__ __forceinline__ void res_decode(const WideArgs& a, char* smem, float* bias_s) {
+    const int k8n = a.K >> 3;
+    const int tasks = a.N * k8n;
+    uint32_t w0[kResMaxTasks], w1[kResMaxTasks];
+    float4 pu[kResMaxTasks], pw[kResMaxTasks];
+#pragma unroll
+    for (int i = 0; i < kResMaxTasks; ++i) {
+        const int t = threadIdx.x + i * (int)blockDim.x;
+        if (t >= tasks) break;
+        const int n = t / k8n, k0 = (t - n * k8n) * 8;
+        // byte 16 g + 4 s + e of (row n, k-step) holds column 32 ks + 8 s + 4 g + e
+        const uint8_t* cw = reinterpret_cast<const uint8_t*>(a.codes) +
+                            (((int64_t)(n >> 5) * a.KS + (k0 >> 5)) * 32 + (n & 31)) * 32 + 4 * ((k0 >> 3) & 3);
+        w0[i] = *reinterpret_cast<const uint32_t*>(cw);       // columns k0 .. k0 + 3
+        w1[i] = *reinterpret_cast<const uint32_t*>(cw + 16);  // columns k0 + 4 .. k0 + 7
+        if constexpr (CB != RPFQ_CB_TABLE) {
+            const int blk = a.nblk > 1 ? k0 / (a.block_ks * 32) : 0;
+            const float4* p = a.params + ((int64_t)n * a.nblk + blk) * 2;
+            pu[i] = p[0];
+            pw[i] = p[1];
+        }
+    }
+    const int nb = 2 * a.N;
+    const float bv = (int)threadIdx.x < nb && a.bias ? a.bias[threadIdx.x] : 0.0f;  // 2N' <= 384 < blockDim.x
+#pragma unroll
+    for (int i = 0; i < kResMaxTasks; ++i) {
+        const int t = threadIdx.x + i * (int)blockDim.x;
+        if (t >= tasks) break;
+        const int n = t / k8n, k0 = (t - n * k8n) * 8;
+        const float2* tab = nullptr;
+        if constexpr (CB == RPFQ_CB_TABLE) tab = reinterpret_cast<const float2*>(a.params) + (int64_t)n * 32;
+        uint32_t p1[8], p2[8];  // (A11, A12) and (A21, A22) fp16 pairs of the 8 columns
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t code = ((j < 4 ? w0[i] : w1[i]) >> (8 * (j & 3))) & 0xffu;
+            float2 u, w;
+            if constexpr (CB == RPFQ_CB_TABLE) {
+                u = tab[code & 15u];
+                w = tab[16 + (code >> 4)];
+            } else {
+                u = lut_entry<CB>(code & 15u, pu[i]);
+                w = lut_entry<CB>(code >> 4, pw[i]);
+            }
+            if (a.rot.rotate) {
+                u = derotate(u, a.rot.cu, a.rot.su);
+                w = derotate(w, a.rot.cw, a.rot.sw);
+            }
+            fuse_h(cvt_pk(u.x, u.y), cvt_pk(w.x, w.y), p1[j], p2[j]);
+        }
+        uint4 a11, a12, a21, a22;  // 8 consecutive columns of each kind
+        uint32_t* q11 = &a11.x;
+        uint32_t* q12 = &a12.x;
+        uint32_t* q21 = &a21.x;
+        uint32_t* q22 = &a22.x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            q11[e] = __builtin_amdgcn_perm(p1[2 * e + 1], p1[2 * e], 0x05040100u);
+            q12[e] = __builtin_amdgcn_perm(p1[2 * e + 1], p1[2 * e], 0x07060302u);
+            q21[e] = __builtin_amdgcn_perm(p2[2 * e + 1], p2[2 * e], 0x05040100u);
+            q22[e] = __builtin_amdgcn_perm(p2[2 * e + 1], p2[2 * e], 0x07060302u);
+        }
+        // A_r[o][j0 .. j0 + 7] (j0 % 8 == 0) -> tile (o / 16, j0 / 32), lane (o % 16, (j0 / 8) % 4)
+        auto at = [&](int o, int j0) -> uint4* {
+            return reinterpret_cast<uint4*>(smem) + ((o >> 4) * KC + (j0 >> 5)) * 64 + (o & 15) + 16 * ((j0 >> 3) & 3);
+        };
+        *at(n, k0) = a11;
+        *at(n, a.K + k0) = a12;
+        *at(a.N + n, k0) = a21;
+        *at(a.N + n, a.K + k0) = a22;
+    }
+    if ((int)threadIdx.x < nb) bias_s[threadIdx.x] = bv;
+}
+
+// 16 B of x (8 fp16 or bf16) -> the fp16 MFMA operand; bf16 after the row's
+// prescale sc (1 without one): the same conversion as every other kernel.
+template <int XDT>
+__device__ __forceinline__ half8 res_x16(uint4 v, float sc) {
+    if constexpr (XDT == RPFQ_BF16) {
+        uint4 o;
+        o.x = pack_h2(bf16_to_f32(v.x & 0xffffu) * sc, bf16_to_f32(v.x >> 16) * sc);
+        o.y = pack_h2(bf16_to_f32(v.y & 0xffffu) * sc, bf16_to_f32(v.y >> 16) * sc);
+        o.z = pack_h2(bf16_to_f32(v.z & 0xffffu) * sc, bf16_to_f32(v.z >> 16) * sc);
+        o.w = pack_h2(bf16_to_f32(v.w & 0xffffu) * sc, bf16_to_f32(v.w >> 16) * sc);
+        return as_half8(o);
+    } else {
+        return as_half8(v);
+    }
+}
+
+template <int YDT>
+__device__ __forceinline__ uint32_t res_pack2(float lo, float hi) {
+    if constexpr (YDT == RPFQ_F16) return cvt_pk(lo, hi);
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// KC: 32-column k-chunks of the real row (2K' / 32); NBMAX: accumulator
+// tiles held (>= 2N' / 16); ACT: fused GELU.
+template <int KC, int NBMAX, int XDT, int YDT, int CB, int ACT>
+__global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(WideArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const int nb = a.N >> 3;  // 16-row blocks of A_r (even: N' % 16 == 0)
+    float* bias_s = reinterpret_cast<float*>(smem + nb * KC * 1024);
+    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+    const int64_t nsub = (a.M + 15) >> 4;
+    const int64_t wstride = (int64_t)gridDim.x * kResWaves;
+    int64_t t = (int64_t)blockIdx.x * kResWaves + (threadIdx.x >> 6);
+    const int64_t ldx = 2 * (int64_t)a.K, ldy = 2 * (int64_t)a.N;
+    const bool scaled = XDT == RPFQ_BF16 && a.xs != nullptr;
+    const int ocol = 16 * (q & 1) + 8 * (q >> 1);  // this lane's 8 outputs within each 32
+
+    // x row of subtile tt held by this lane (rows past M repeat row M - 1;
+    // their outputs are not stored)
+    auto xrow = [&](int64_t tt) -> int64_t {
+        const int64_t m = tt * 16 + r;
+        return m < a.M ? m : a.M - 1;
+    };
+    uint4 xr[KC];
+    float xsc = 1.0f;
+    auto load_x = [&](int64_t tt) {
+        const int64_t m = xrow(tt);
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(a.x) + m * ldx + 8 * q;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) xr[c] = *reinterpret_cast<const uint4*>(p + 32 * c);
+        if (scaled) xsc = a.xs[m];
+    };
+    if (t < nsub) load_x(t);  // the first subtile's rows are requested before the decode
+    res_decode<CB, KC>(a, smem, bias_s);
+    __syncthreads();
+
+    const uint4* wl = reinterpret_cast<const uint4*>(smem) + lane;
+    for (; t < nsub; t += wstride) {
+        const int64_t m = t * 16 + r;
+        const bool row_in = m < a.M;
+        const float inv = scaled ? row_unscale(xsc) : 1.0f;
+        half8 xh[KC];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) xh[c] = res_x16<XDT>(xr[c], xsc);
+        if (t + wstride < nsub) load_x(t + wstride);
+        uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + (row_in ? m : 0) * ldy + ocol;
+        uint4 rres[NBMAX / 2];
+        if (a.res) {
+            const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.res) + (row_in ? m : 0) * ldy + ocol;
+#pragma unroll
+            for (int p = 0; p < NBMAX / 2; ++p)
+                if (2 * p < nb) rres[p] = *reinterpret_cast<const uint4*>(rrow + 32 * p);
+        }
+        f32x4 acc[NBMAX];
+#pragma unroll
+        for (int b = 0; b < NBMAX; ++b) acc[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+#pragma unroll
+            for (int b = 0; b < NBMAX; ++b) {
+                if (b < nb) {
+                    const half8 w = as_half8(wl[(b * KC + c) * 64]);
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, xh[c], acc[b], 0, 0, 0);
+                }
+            }
+        }
+        // epilogue: blocks 2p, 2p + 1 -> 32 outputs, 8 per lane, one store each
+#pragma unroll
+        for (int p = 0; p < NBMAX / 2; ++p) {
+            if (2 * p >= nb) break;
+            uint32_t d[4];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const f32x4 v = acc[2 * p + hb];
+                const float4 bq = *reinterpret_cast<const float4*>(bias_s + 32 * p + 16 * hb + 4 * q);
+                float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+                if (scaled) {  // undo the row's prescale (exact) before the bias
+                    v0 *= inv;
+                    v1 *= inv;
+                    v2 *= inv;
+                    v3 *= inv;
+                }
+                d[2 * hb] = res_pack2<YDT>(v0 + bq.x, v1 + bq.y);
+                d[2 * hb + 1] = res_pack2<YDT>(v2 + bq.z, v3 + bq.w);
+            }
+            // lane row q (16 lanes) holds outputs 4 q .. 4 q + 3 of both blocks;
+            // swapping odd rows of block 2p with even rows of block 2p + 1
+            // leaves 8 consecutive outputs in each lane
+            const auto s0 = __builtin_amdgcn_permlane16_swap(d[0], d[2], false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(d[1], d[3], false, false);
+            uint4 o = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+            if (a.res) {
+                const bool f16 = YDT == RPFQ_F16;
+                const uint4 rv = rres[p];
+                o = make_uint4(add2_y(o.x, rv.x, f16), add2_y(o.y, rv.y, f16), add2_y(o.z, rv.z, f16),
+                               add2_y(o.w, rv.w, f16));
+            }
+            if constexpr (ACT != 0) o = gelu8_rolled(o, YDT == RPFQ_F16);
+            if (row_in) *reinterpret_cast<uint4*>(yrow + 32 * p) = o;
+        }
+    }
+}
+
+template <int KC, int NBMAX, int XDT, int YDT, int CB, int ACT>
+static hipError_t wide_res_go(WideArgs& a, hipStream_t s) {
+    static std::atomic<uint64_t> attr_done{0};
+    const void* kern = reinterpret_cast<const void*>(&wide_linear_resident_kernel<KC, NBMAX, XDT, YDT, CB, ACT>);
+    const hipError_t e = set_lds_attr_once(kern, kResLdsMax, attr_done);
+    if (e != hipSuccess) return e;
+    const int64_t nsub = (a.M + 15) / 16;
+    // as few waves as give every wave the same number of subtiles (+- 1) in
+    // the fewest rounds: the last round is then full
+    const int64_t slots = (int64_t)device_cus() * kResWaves;
+    const int64_t rounds = (nsub + slots - 1) / slots;
+    const int64_t waves = (nsub + rounds - 1) / rounds;
+    const int grid = (int)((waves + kResWaves - 1) / kResWaves);
+    hipLaunchKernelGGL((wide_linear_resident_kernel<KC, NBMAX, XDT, YDT, CB, ACT>), dim3(grid),
+                       dim3(kResWaves * 64), resident_lds(a), s, a);
+    return hipGetLastError();
+}
+
+template <int KC, int NBMAX, int XDT, int YDT, int CB>
+static hipError_t wide_res_act(WideArgs& a, hipStream_t s) {
+    return a.act ? wide_res_go<KC, NBMAX, XDT, YDT, CB, 1>(a, s) : wide_res_go<KC, NBMAX, XDT, YDT, CB, 0>(a, s);
+}
+
+template <int KC, int NBMAX, int CB>
+static hipError_t wide_res_dt(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+    if (xdt == RPFQ_BF16)
+        return ydt == RPFQ_BF16 ? wide_res_act<KC, NBMAX, RPFQ_BF16, RPFQ_BF16, CB>(a, s)
+                                : wide_res_act<KC, NBMAX, RPFQ_BF16, RPFQ_F16, CB>(a, s);
+    return ydt == RPFQ_BF16 ? wide_res_act<KC, NBMAX, RPFQ_F16, RPFQ_BF16, CB>(a, s)
+                            : wide_res_act<KC, NBMAX, RPFQ_F16, RPFQ_F16, CB>(a, s);
+}
+
+template <int CB>
+hipError_t launch_wide_resident(WideArgs& a, int xdt, int ydt, hipStream_t s) {
+    const bool small = a.N <= 96;  // <= 12 accumulator tiles
+    switch (a.K) {
+        case 48: return small ? wide_res_dt<3, 12, CB>(a, xdt, ydt, s) : wide_res_dt<3, 24, CB>(a, xdt, ydt, s);
+        case 96: return small ? wide_res_dt<6, 12, CB>(a, xdt, ydt, s) : wide_res_dt<6, 24, CB>(a, xdt, ydt, s);
+        case 192: return wide_res_dt<12, 12, CB>(a, xdt, ydt, s);  // N' <= 96 (LDS)
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template hipError_t launch_wide_resident<RPFQ_CB_SEL>(WideArgs&, int, int, hipStream_t);
+
+}  // namespace rpfq

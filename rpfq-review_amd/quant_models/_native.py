@@ -33,7 +33,8 @@ FLAG_TILE_M128 = 1  # force the register-staged 128-row kernel
 FLAG_NO_STREAM = 2  # keep every M on the tiled kernels (no weight-streaming kernel)
 FLAG_STREAM = 4  # force the weight-streaming kernel for any M (16-row chunks)
 FLAG_GELU = 8  # exact GELU of the rounded output, fused into the store (no residual)
-KERNEL_STREAM, KERNEL_DMA, KERNEL_TILED, KERNEL_GEMV = 0, 1, 2, 3  # rpfq_wide_linear_kernel
+FLAG_RESIDENT = 16  # force the resident-weight kernel (small layers; fp16 / bf16 x and y)
+KERNEL_STREAM, KERNEL_DMA, KERNEL_TILED, KERNEL_GEMV, KERNEL_RESIDENT = 0, 1, 2, 3, 4  # rpfq_wide_linear_kernel
 STREAM_KERNELS = (KERNEL_STREAM, KERNEL_GEMV)  # the weight-streaming kernels (small M)
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}

@@ -709,7 +709,8 @@ class QATLinearComplexPhase(nn.Linear):
         """F.gelu(self(x)) (exact erf GELU); x already activation-quantized
         for this layer if prequantized.  On the packed HIP path the GELU runs
         in the kernel's store (within 1 ulp of the exact GELU of the rounded
-        output) where the launch streams, and on the tiled kernels for bf16
+        output) where the launch streams or keeps the layer resident in LDS
+        (HBM-bound, its VALU mostly idle), and on the tiled kernels for bf16
         activations.  ViT-B/16 bs256, same box: bf16 15,510 -> 16,197
         images/s fused; fp16 17,603 -> 17,912, but fc1's launch grows by
         ~40% (the GELU's VALU work in the epilogue is not hidden behind the
@@ -726,7 +727,7 @@ class QATLinearComplexPhase(nn.Linear):
                 x = ops.act_quant(x, self.act_quantizer.num_bits)
             m = x.numel() // x.shape[-1]
             kern = pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) if m else None
-            if kern in N.STREAM_KERNELS or x.dtype == torch.bfloat16:
+            if kern in N.STREAM_KERNELS or kern == N.KERNEL_RESIDENT or x.dtype == torch.bfloat16:
                 return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))

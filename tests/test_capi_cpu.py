@@ -73,7 +73,12 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), None, 1 << 20, p, 1, 4, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 7, 4, None, p, 1, 0, None) == 5
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 0, None, p, 1, 0, None) == 2
-    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 16, None) == 6  # unknown flag bit
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 32, None) == 6  # unknown flag bit
+    # RPFQ_FLAG_RESIDENT on a layer it does not take (K' = 64); on a y that is not 16-byte aligned
+    assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 16, None) == 2
+    d48 = _desc(N, n=64, k=48)
+    assert L.rpfq_wide_linear(ctypes.byref(d48), p, 1 << 20, p, 1, 4, None, ctypes.c_void_p(264), 1, 16,
+                              None) == 3
     # RPFQ_FLAG_STREAM with a tiled-kernel flag; a streaming grid past 2^24 workgroups
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 1, None) == 6
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 4 | 2, None) == 6
@@ -116,7 +121,7 @@ def test_residual_and_layer_norm_argument_errors():
     # NULL residual, bad dtype, bad flags, misaligned residual -- all before any HIP call
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, None, p, 1, 0, None) == 1
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 9, 0, None) == 5
-    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 16, None) == 6
+    assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 32, None) == 6
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, p, 1, 8, None) == 6  # GELU
     assert "GELU" in L.rpfq_last_error().decode()
     assert L.rpfq_wide_linear_residual(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, ctypes.c_void_p(258), p, 1, 0,
@@ -338,7 +343,42 @@ def test_wide_linear_kernel_choice():
     out = ctypes.c_int32(-1)
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 0, None) == 1
     assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 0, 1, 1, 0, ctypes.byref(out)) == 2
-    assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 16, ctypes.byref(out)) == 6
+    assert L.rpfq_wide_linear_kernel(ctypes.byref(d), 4, 1, 1, 32, ctypes.byref(out)) == 6
+
+
+def test_wide_linear_resident_choice():
+    """The resident-weight kernel: chosen by default for M >= 32768 on the
+    layers it takes (Swin-T stage 0: N' % 16 == 0, K' in {48, 96, 192}, the
+    decoded matrix within 160 KB of LDS; fp16 / bf16 x and y), never under
+    the other kernel flags; RPFQ_FLAG_RESIDENT forces it at any M and is
+    refused, before any GPU work, for a layer, dtype or flag set it does
+    not take."""
+    L, N = lib()
+
+    def kernel(d, m, xdt=1, ydt=1, flags=0):
+        out = ctypes.c_int32(-1)
+        rc = L.rpfq_wide_linear_kernel(ctypes.byref(d), m, xdt, ydt, flags, ctypes.byref(out))
+        return out.value if rc == 0 else -rc
+    qkv, fc2, proj1 = _desc(N, n=144, k=48), _desc(N, n=48, k=192), _desc(N, n=96, k=96)
+    for d in (qkv, fc2, proj1):
+        assert kernel(d, 401408) == N.KERNEL_RESIDENT
+        assert kernel(d, 32768, xdt=2, ydt=2) == N.KERNEL_RESIDENT
+        assert kernel(d, 401408, flags=N.FLAG_GELU) == N.KERNEL_RESIDENT
+        assert kernel(d, 32767) != N.KERNEL_RESIDENT
+        assert kernel(d, 401408, xdt=0) != N.KERNEL_RESIDENT and kernel(d, 401408, ydt=0) != N.KERNEL_RESIDENT
+        assert kernel(d, 401408, flags=N.FLAG_NO_STREAM) != N.KERNEL_RESIDENT
+        assert kernel(d, 401408, flags=N.FLAG_TILE_M128) == N.KERNEL_TILED
+        assert kernel(d, 5, flags=N.FLAG_RESIDENT) == N.KERNEL_RESIDENT
+    assert kernel(fc2, 401408, flags=N.FLAG_NO_STREAM) == N.KERNEL_DMA
+    # shapes it does not take: N' % 16, K' outside {48, 96, 192}, over 160 KB
+    for n, k in ((50, 48), (144, 64), (384, 384), (192, 192)):
+        d = _desc(N, n=n, k=k)
+        assert kernel(d, 401408) != N.KERNEL_RESIDENT
+        assert kernel(d, 401408, flags=N.FLAG_RESIDENT) == -2
+    assert kernel(qkv, 5, xdt=0, flags=N.FLAG_RESIDENT) == -5
+    assert kernel(qkv, 5, ydt=0, flags=N.FLAG_RESIDENT) == -5
+    for other in (N.FLAG_NO_STREAM, N.FLAG_STREAM, N.FLAG_TILE_M128):
+        assert kernel(qkv, 5, flags=N.FLAG_RESIDENT | other) == -6
 
 
 def test_wide_grad_x_geometry_and_argument_errors():

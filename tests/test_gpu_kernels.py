@@ -745,6 +745,124 @@ def test_wide_linear_gemv_one_wave_dtypes(xdt, ydt):
 
 
 # ---------------------------------------------------------------------------
+# resident-weight kernel (RPFQ_KERNEL_RESIDENT): the decoded layer stays in
+# LDS while the waves stream 32-row subtiles of x (Swin-T stage 0)
+# ---------------------------------------------------------------------------
+RES_CASES = [
+    (144, 48, "axis", 2, 0, None),                        # Swin-T stage 0 qkv (3 groups of 3 blocks)
+    (48, 48, "axis", 2, 0, None),                         # stage 0 proj (one group)
+    (192, 48, "psk16", 1, 0, None),                       # stage 0 fc1 in 16-PSK (72 KB of LDS)
+    (48, 192, "axis", 2, 64, None),                       # stage 0 fc2, 3 scale blocks per row (K' = 192)
+    (96, 96, "sign", 2, 0, ((0.8, 0.6), (0.6, -0.8))),    # stage 1 proj, sign codes, rotation
+    (160, 48, "table", 1, 0, None),                       # per-row tables; 10 blocks: a last group of 1
+]
+RES_IDS = [f"{c[0]}x{c[1]}-{c[2]}-b{c[4]}" for c in RES_CASES]
+
+
+def _res_input(r, m, k_in, xdt, seed):
+    """x [m, k_in] on the device (standard normal, generated there for large
+    m), and the sampled rows the oracle checks: the first and last 64 and
+    192 random ones."""
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(m, k_in, device=DEV, generator=g).to(xdt)
+    rows = np.unique(np.concatenate([np.arange(min(m, 64)), np.arange(max(0, m - 64), m),
+                                     r.choice(m, size=min(m, 192), replace=False)]))
+    return x, rows
+
+
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                     (torch.bfloat16, torch.float16)], ids=["f16", "bf16", "bf16-f16"])
+@pytest.mark.parametrize("m,flags", [(77, 16), (140001, 0)], ids=["m77-forced", "m140001-auto"])
+@pytest.mark.parametrize("case", RES_CASES, ids=RES_IDS)
+def test_wide_linear_resident(case, m, flags, xdt, ydt):
+    """The resident-weight kernel against the oracle on sampled rows (the
+    partial last subtile included) at M = 77 (RPFQ_FLAG_RESIDENT: three
+    subtiles, the last of 13 rows) and M = 140,001 (chosen by default: 4,376
+    subtiles, three rounds of the persistent waves), with bias, five
+    codebook / scale / rotation variants, fp16 and bf16 activations (bf16
+    through the range guard's row prescales) and 16-bit outputs; the launch
+    is deterministic, and a zero residual added in the store changes
+    nothing."""
+    ops, N = qm()
+    r = rng(3100 + case[0] + case[1] + m)
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    assert pw.kernel_for(m, xdt, ydt, flags) == N.KERNEL_RESIDENT
+    x, rows = _res_input(r, m, 2 * case[1], xdt, 3100 + m)
+    bias = r.standard_normal(2 * case[0]).astype(np.float32)
+    y = pw.linear(x, tdev(bias), out_dtype=ydt, flags=flags)
+    assert torch.equal(y, pw.linear(x, tdev(bias), out_dtype=ydt, flags=flags))
+    zero = torch.zeros_like(y)
+    assert torch.equal(y, pw.linear(x, tdev(bias), out_dtype=ydt, flags=flags, residual=zero))
+    idx = torch.from_numpy(rows).to(DEV)
+    ys = y.index_select(0, idx).float().cpu().numpy()
+    # bf16 rows prescaled by a power of two are exact in fp16: the MFMA sees x itself
+    xf = x.index_select(0, idx).float().cpu().numpy().astype(np.float64)
+    out_ulp = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[ydt]
+    check_against_oracle(ys, xf, bias, oplanes, codebook, rotation, out_ulp=out_ulp)
+
+
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", [RES_CASES[1], RES_CASES[3], RES_CASES[0]], ids=["proj", "fc2", "qkv"])
+def test_wide_linear_resident_residual_gelu(case, ydt):
+    """The resident kernel's fused store ops at M = 70,001 (default choice):
+    a residual add bit-identical to the unfused add in y's dtype, also in
+    place (residual == y through the C ABI), and the fused GELU within 1 ulp
+    of the exact GELU of the unfused output (at most 0.1% of the elements
+    off at all)."""
+    import ctypes
+    import math
+
+    ops, N = qm()
+    r = rng(3300 + case[0] + case[1])
+    pw, *_ = build_packed(r, case)
+    m = 70001
+    assert pw.kernel_for(m, torch.float16, ydt) == N.KERNEL_RESIDENT
+    x, _ = _res_input(r, m, 2 * case[1], torch.float16, 3300)
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    g = torch.Generator(device=DEV).manual_seed(3301)
+    res = (torch.randn(m, 2 * case[0], device=DEV, generator=g) * 4).to(ydt)
+    y = pw.linear(x, bias, out_dtype=ydt)
+    want = res + y
+    assert torch.equal(pw.linear(x, bias, out_dtype=ydt, residual=res), want)
+    yi = res.clone()
+    lib = N.load()
+    N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
+        ctypes.byref(pw.desc), pw.blob.data_ptr(), pw.blob.numel(), x.data_ptr(), N.F16, m, bias.data_ptr(),
+        yi.data_ptr(), yi.data_ptr(), N.dtype_code(ydt), 0, N.stream_of(x)))
+    torch.cuda.synchronize()
+    assert torch.equal(yi, want)
+    yg = pw.linear(x, bias, out_dtype=ydt, gelu=True).cpu()
+    yd = y.double().cpu()
+    exact = yd * 0.5 * torch.special.erfc(-yd / math.sqrt(2.0))
+    tiny = exact.abs() < 2.0 ** -126
+    d = torch.where(tiny, torch.zeros_like(yg, dtype=torch.long), ulp_distance(yg, exact.to(ydt)))
+    assert int(d.max()) <= 1 and float((d > 0).float().mean()) <= 1e-3
+
+
+def test_wide_linear_resident_range_guard():
+    """bf16 rows at 1e-30 .. 1e30, past fp16's overflow threshold and a zero
+    row through the resident kernel (RPFQ_FLAG_RESIDENT, bf16 outputs): the
+    row prescales keep each row's relative accuracy -- within the bf16
+    output rounding of x A16^T (the operands exact, float32 accumulation) --
+    and the zero row gives the bias rounded to bf16."""
+    ops, N = qm()
+    r = rng(3400)
+    case = RES_CASES[0]
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    m = 300
+    x, mags = _range_rows(r, m, 2 * case[1], torch.bfloat16)
+    bias = np.zeros(2 * case[0], dtype=np.float32)
+    y = pw.linear(x.to(DEV), tdev(bias), out_dtype=torch.bfloat16, flags=N.FLAG_RESIDENT).float().cpu().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    a16 = O.wide_weight(oplanes, codebook, rotation, fp16=True).astype(np.float64)
+    ref = xf @ a16.T
+    scale = np.abs(xf) @ np.abs(a16).T
+    assert np.all(np.isfinite(y))
+    assert np.all(np.abs(y - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-5 * scale + 1e-44)
+    assert np.all(y[mags == 0] == 0.0)
+
+
+# ---------------------------------------------------------------------------
 # fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
 # followed by the add in y's dtype, on every kernel path
 # ---------------------------------------------------------------------------
