@@ -51,9 +51,9 @@ extern "C" {
 /* rpfq_wide_linear flags.  Default (0): the kernel is chosen from the shape
  * (M <= 16, and small-M launches where a cost model predicts it faster --
  * e.g. a ViT-B layer at one image -- stream the packed codes, 32-row tiles
- * against 16-row chunks of x; M >= 32768 with a small layer -- N' % 16 == 0,
- * K' in {48, 96, 192}, the decoded 2N' x 2K' fp16 matrix and the bias within
- * 160 KB of LDS, fp16 / bf16 x and y, y 16-byte aligned: Swin-T stage 0 --
+ * against 16-row chunks of x; M >= 32768 with a small layer -- K' = 48 and
+ * N' in {48, 96, 144, 192}, K' = 96 and N' in {48, 96}, or K' = 192 and
+ * N' = 48, fp16 / bf16 x and y, y 16-byte aligned: Swin-T stage 0 --
  * keeps the decoded layer resident in LDS and streams rows of x; fp16 / bf16
  * x with K' % 32 == 0 and M >= 128 stages activations by LDS DMA; other cases
  * stage them through registers with a 32/64/128-row tile).
@@ -64,8 +64,9 @@ extern "C" {
  * 16-row chunk of x and 32-row tile of the codes; at most 2^24 of them,
  * else RPFQ_ERR_SHAPE; not combinable with the other two, RPFQ_ERR_VALUE);
  * RPFQ_FLAG_RESIDENT forces the resident-weight kernel for any M (the layer
- * and dtypes as above, else RPFQ_ERR_SHAPE / RPFQ_ERR_DTYPE, y not 16-byte
- * aligned RPFQ_ERR_ALIGN; not combinable with the other three).
+ * and dtypes as above, N' <= 96 with a residual, else
+ * RPFQ_ERR_SHAPE / RPFQ_ERR_DTYPE, y not 16-byte aligned RPFQ_ERR_ALIGN; not
+ * combinable with the other three).
  * Every kernel feeds the MFMA the same fp16 coefficients. */
 #define RPFQ_FLAG_TILE_M128 1
 #define RPFQ_FLAG_NO_STREAM 2

@@ -161,10 +161,12 @@ static int check_flags(int flags, const rpfq::WideGeom& g, int64_t M, bool resid
             return fail(RPFQ_ERR_DTYPE, "RPFQ_FLAG_RESIDENT takes fp16 / bf16 x and y (x=%d y=%d)", x_dtype, y_dtype);
         if (!rpfq::wide_resident_eligible(g, x_dtype, y_dtype))
             return fail(RPFQ_ERR_SHAPE,
-                        "RPFQ_FLAG_RESIDENT: N'=%lld K'=%lld (needs N' %% 16 == 0, K' in {48, 96, 192}, "
-                        "the decoded layer within 160 KB)",
+                        "RPFQ_FLAG_RESIDENT: N'=%lld K'=%lld (takes K' = 48 with N' in {48, 96, 144, 192}, "
+                        "K' = 96 with N' in {48, 96}, K' = 192 with N' = 48)",
                         (long long)g.N, (long long)g.K);
         if (y && !aligned(y, 16)) return fail(RPFQ_ERR_ALIGN, "RPFQ_FLAG_RESIDENT needs y 16-byte aligned");
+        if (residual && g.N > 96)
+            return fail(RPFQ_ERR_SHAPE, "RPFQ_FLAG_RESIDENT with a residual needs N' <= 96 (N'=%lld)", (long long)g.N);
     }
     if ((flags & RPFQ_FLAG_STREAM) && (int64_t)g.NT * ((M + 15) / 16) > ((int64_t)1 << 24))
         return fail(RPFQ_ERR_SHAPE, "M=%lld: RPFQ_FLAG_STREAM allows at most 2^24 (chunk, tile) workgroups",

@@ -158,18 +158,35 @@ template <int CB> hipError_t launch_wide_resident(WideArgs& a, int xdt, int ydt,
 // Resident-weight kernel (wide_resident.hip): one workgroup of kResWaves
 // waves per CU holds the whole decoded layer in LDS (2N' x 2K' fp16 as MFMA
 // A operands, plus the float32 bias) and streams 16-row subtiles of x, each
-// wave holding whole output rows.  Shapes: N' % 16 == 0, N' <= 192 (the
-// accumulators of a row block), K' in {48, 96, 192}, the LDS within 160 KB
-// (K' = 192: N' <= 96); fp16 / bf16 x and y.
+// wave holding whole output rows.  Shapes: K' = 48 with N' in {48, 96, 144,
+// 192}, K' = 96 with N' in {48, 96}, K' = 192 with N' = 48 (Swin-T stage 0
+// and its stage-1 proj); fp16 / bf16 x and y.
 constexpr int kResWaves = 8;
 constexpr int kResLdsMax = 160 * 1024;
-inline int resident_lds(const WideArgs& a) { return (a.N / 8) * (a.K / 16) * 1024 + 8 * a.N; }
+// LDS of the decoded layer (kc = 2K' / 32 k-chunks, nb = 2N' / 16 blocks)
+// and the bias
+constexpr int res_lds_layer(int kc, int nb) { return nb * kc * 1024 + 64 * nb; }
+// Rows of output each wave stages in LDS before its full-line stores: 16
+// (a whole subtile), 8 (half of it) or 0 (no room left beside the layer:
+// direct 16-B stores).  Row bytes: 4N' = 32 nb.
+constexpr int res_stage_rows(int kc, int nb) {
+    return res_lds_layer(kc, nb) + kResWaves * 16 * 32 * nb <= kResLdsMax               ? 16
+           : res_lds_layer(kc, nb) + kResWaves * (8 * 32 * nb + 512) <= kResLdsMax ? 8
+                                                                                         : 0;
+}
+// (staging 8 rows at a time, the lanes of the other 8 rows write a 512-B
+// scratch area per wave instead)
+constexpr int res_lds(int kc, int nb) {
+    return res_lds_layer(kc, nb) + kResWaves * res_stage_rows(kc, nb) * 32 * nb +
+           (res_stage_rows(kc, nb) == 8 ? kResWaves * 512 : 0);
+}
+inline int resident_lds(const WideArgs& a) { return res_lds(a.K / 16, a.N / 8); }
 // shape and dtypes of a layer the kernel takes (wide_dispatch.hip)
 bool wide_resident_eligible(const WideGeom& g, int xdt, int ydt);
 inline bool resident_shape(const WideArgs& a) {
-    if (a.N <= 0 || a.N % 16 != 0 || a.N > 192) return false;
-    if (a.K != 48 && a.K != 96 && a.K != 192) return false;
-    return resident_lds(a) <= kResLdsMax;
+    if (a.K == 48) return a.N == 48 || a.N == 96 || a.N == 144 || a.N == 192;
+    if (a.K == 96) return a.N == 48 || a.N == 96;
+    return a.K == 192 && a.N == 48;
 }
 
 // workgroups of the streaming kernel: one per (16-row chunk, 32-row tile)

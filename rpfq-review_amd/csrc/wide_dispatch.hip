@@ -71,10 +71,11 @@ static bool stream_pays(const WideArgs& a) {
 #define RPFQ_RES_MIN_M 32768
 #endif
 // Layers the resident-weight kernel takes (shape and dtypes; y 16-byte
-// aligned, a NULL y counting as aligned for kernel-choice queries).
+// aligned, a NULL y counting as aligned for kernel-choice queries; a
+// residual only with N' <= 96).
 static bool resident_ok(const WideArgs& a, int xdt, int ydt) {
     return (xdt == RPFQ_F16 || xdt == RPFQ_BF16) && (ydt == RPFQ_F16 || ydt == RPFQ_BF16) && resident_shape(a) &&
-           reinterpret_cast<uintptr_t>(a.y) % 16 == 0;
+           reinterpret_cast<uintptr_t>(a.y) % 16 == 0 && (a.res == nullptr || a.N <= 96);
 }
 
 bool wide_resident_eligible(const WideGeom& g, int xdt, int ydt) {

@@ -26,8 +26,8 @@ namespace rpfq {
 //   * B operand: lane (r, q) loads row m0 + r, columns 32 c + 8 q .. + 7 of
 //     every k-chunk c (16 B; 64 contiguous bytes per row and instruction;
 //     bf16 rows converted to fp16 after the row's prescale, as every kernel
-//     converts them); the next subtile's rows are requested before the
-//     current one's MFMAs;
+//     converts them); a register ring keeps the rows of the wave's next
+//     U - 1 subtiles in flight (res_ring);
 //   * D: lane (r, q) holds x row r's outputs 16 b + 4 q .. + 3;
 //     after bias and rounding, v_permlane16_swap pairs blocks 2p and 2p + 1
 //     so that lane (r, q) holds the 8 outputs 32 p + 16 (q & 1) + 8 (q >> 1)
@@ -141,74 +141,137 @@ __device__ __forceinline__ uint32_t res_pack2(float lo, float hi) {
     return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
-// KC: 32-column k-chunks of the real row (2K' / 32); NBMAX: accumulator
-// tiles held (>= 2N' / 16); ACT: fused GELU.
-template <int KC, int NBMAX, int XDT, int YDT, int CB, int ACT>
+// Subtiles in flight per wave (the register ring).  Deeper rings (4 at
+// K' = 48, 3 at K' = 96) measured no faster: 8 waves per CU with two
+// subtiles each keep enough rows in flight.
+template <int KC> constexpr int res_ring() { return 2; }
+constexpr int kResWAhead = 4;  // weight tiles read ahead of their MFMA
+
+// prescale of bf16 rows launched without row scales (WideArgs::xs NULL)
+__device__ const float kResUnitScale = 1.0f;
+
+// KC: 32-column k-chunks of the real row (2K' / 32); NB: 16-row blocks of
+// A_r (2N' / 16); RES: a residual is added in the store (NB <= 12); ACT:
+// fused GELU.
+//
+// Every vector memory instruction of the subtile loop is issued on every
+// path (rows past M load and store row M - 1's values, the last round
+// refills the ring from the slot's own rows, the prescale of bf16 rows comes
+// from a unit constant without row scales): loads and stores share one
+// counter on gfx950, and with path-dependent counts the compiler waits for
+// every outstanding store and ring load at each slot.
+template <int KC, int NB, int RES, int XDT, int YDT, int CB, int ACT>
 __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
-    const int nb = a.N >> 3;  // 16-row blocks of A_r (even: N' % 16 == 0)
-    float* bias_s = reinterpret_cast<float*>(smem + nb * KC * 1024);
+    constexpr int U = res_ring<KC>();
+    constexpr int J = NB * KC;  // MFMAs per subtile, chunk-major (j = c NB + b)
+    constexpr int D = kResWAhead < J ? kResWAhead : J;
+    static_assert(!RES || NB <= 12, "residual layers: N' <= 96");
+    float* bias_s = reinterpret_cast<float*>(smem + NB * KC * 1024);
     const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+    // output staging: TR rows of RB bytes per wave after the layer
+    constexpr int TR = res_stage_rows(KC, NB);
+    constexpr int RB = 32 * NB;                          // bytes of an output row (4N')
+    constexpr int NI = TR ? (TR * RB + 1023) / 1024 : 0;  // 1-KB stores per staged block
+    constexpr int NOUT = TR ? NI * (16 / TR) : NB / 2;    // 16-B stores per lane and subtile
+    char* stage = smem + res_lds_layer(KC, NB) + (threadIdx.x >> 6) * TR * RB;
+    // byte offset in the staged block of store i: lane l's 16 B of the i-th
+    // KB (the last KB's lanes past the block repeat its last chunk)
+    auto stage_off = [&](int i) -> int {
+        const int o = 1024 * i + 16 * lane;
+        return o < TR * RB ? o : TR * RB - 16;
+    };
     const int64_t nsub = (a.M + 15) >> 4;
-    const int64_t wstride = (int64_t)gridDim.x * kResWaves;
-    int64_t t = (int64_t)blockIdx.x * kResWaves + (threadIdx.x >> 6);
+    const int64_t ws = (int64_t)gridDim.x * kResWaves;
+    const int64_t t0 = (int64_t)blockIdx.x * kResWaves + (threadIdx.x >> 6);
     const int64_t ldx = 2 * (int64_t)a.K, ldy = 2 * (int64_t)a.N;
     const bool scaled = XDT == RPFQ_BF16 && a.xs != nullptr;
     const int ocol = 16 * (q & 1) + 8 * (q >> 1);  // this lane's 8 outputs within each 32
 
-    // x row of subtile tt held by this lane (rows past M repeat row M - 1;
-    // their outputs are not stored)
-    auto xrow = [&](int64_t tt) -> int64_t {
+    // This lane's row of subtile tt (rows past M are row M - 1).  Ring slot
+    // s holds subtile t0 + (i U + s) ws of round i; each chunk is refilled
+    // with the next round's as soon as the MFMAs that read it are issued, so
+    // U - 1 subtiles stay in flight.
+    auto row_of = [&](int64_t tt) -> int64_t {
         const int64_t m = tt * 16 + r;
         return m < a.M ? m : a.M - 1;
     };
-    uint4 xr[KC];
-    float xsc = 1.0f;
-    auto load_x = [&](int64_t tt) {
-        const int64_t m = xrow(tt);
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(a.x) + m * ldx + 8 * q;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) xr[c] = *reinterpret_cast<const uint4*>(p + 32 * c);
-        if (scaled) xsc = a.xs[m];
+    auto xptr = [&](int64_t tt) -> const uint16_t* {
+        return reinterpret_cast<const uint16_t*>(a.x) + row_of(tt) * ldx + 8 * q;
     };
-    if (t < nsub) load_x(t);  // the first subtile's rows are requested before the decode
+    auto xsptr = [&](int64_t tt) -> const float* { return scaled ? a.xs + row_of(tt) : &kResUnitScale; };
+    // element offset in y (and the residual) of this lane's store k of subtile
+    // tt: staged, row hh TR + o / RB of the subtile, byte o % RB of the row,
+    // o = stage_off(i), k = hh NI + i (rows past M go to row M - 1, whose
+    // values they hold); direct, pair k of the lane's own row
+    auto out_at = [&](int64_t tt, int k) -> int64_t {
+        if constexpr (TR == 0) {
+            return row_of(tt) * ldy + ocol + 32 * k;
+        } else {
+            const int hh = k / NI, o = stage_off(k - hh * NI);
+            int64_t row = tt * 16 + hh * TR + o / RB;
+            if (row >= a.M) row = a.M - 1;
+            return row * ldy + (o % RB) / 2;
+        }
+    };
+    uint4 xr[U][KC];
+    float xsc[U];
+#pragma unroll
+    for (int s = 0; s < U; ++s) {  // requested before the decode
+        const int64_t tt = t0 + s * ws < nsub ? t0 + s * ws : t0;
+        const uint16_t* p = xptr(tt);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) xr[s][c] = *reinterpret_cast<const uint4*>(p + 32 * c);
+        xsc[s] = 1.0f;
+        if constexpr (XDT == RPFQ_BF16) xsc[s] = *xsptr(tt);
+    }
     res_decode<CB, KC>(a, smem, bias_s);
     __syncthreads();
 
+    // weight tile of MFMA j: block j % NB, chunk j / NB
     const uint4* wl = reinterpret_cast<const uint4*>(smem) + lane;
-    for (; t < nsub; t += wstride) {
-        const int64_t m = t * 16 + r;
-        const bool row_in = m < a.M;
-        const float inv = scaled ? row_unscale(xsc) : 1.0f;
-        half8 xh[KC];
+    auto wtile = [&](int j) -> half8 { return as_half8(wl[((j % NB) * KC + j / NB) * 64]); };
+    auto slot = [&](int64_t t, uint4 (&xv)[KC], float& xsv) {
+        const int64_t tn = t + U * ws;
+        const int64_t tl = tn < nsub ? tn : t;  // refill source: the slot's own rows on its last round
+        const int64_t m = row_of(t);
+        uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + m * ldy + ocol;
+        // residual chunks of this lane's stores, all read before any store
+        // (in place, residual == y, a chunk stored twice reads the original)
+        uint4 rres[RES ? NOUT : 1];
+        if constexpr (RES != 0) {
 #pragma unroll
-        for (int c = 0; c < KC; ++c) xh[c] = res_x16<XDT>(xr[c], xsc);
-        if (t + wstride < nsub) load_x(t + wstride);
-        uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + (row_in ? m : 0) * ldy + ocol;
-        uint4 rres[NBMAX / 2];
-        if (a.res) {
-            const uint16_t* rrow = reinterpret_cast<const uint16_t*>(a.res) + (row_in ? m : 0) * ldy + ocol;
-#pragma unroll
-            for (int p = 0; p < NBMAX / 2; ++p)
-                if (2 * p < nb) rres[p] = *reinterpret_cast<const uint4*>(rrow + 32 * p);
+            for (int i = 0; i < NOUT; ++i)
+                rres[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) + out_at(t, i));
         }
-        f32x4 acc[NBMAX];
+        const float sc = xsv;
+        const float inv = scaled ? row_unscale(sc) : 1.0f;
+        const uint16_t* pn = xptr(tl);
+        f32x4 acc[NB];
 #pragma unroll
-        for (int b = 0; b < NBMAX; ++b) acc[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < NB; ++b) acc[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        // MFMA j reads the weight tile requested D steps earlier; each step
+        // is fenced so the schedule keeps that distance (unfenced, every
+        // tile's read is hoisted to the top and the registers run out)
+        half8 wq[D];
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
+        for (int j = 0; j < D; ++j) wq[j] = wtile(j);
+        half8 xc = res_x16<XDT>(xv[0], sc);
 #pragma unroll
-            for (int b = 0; b < NBMAX; ++b) {
-                if (b < nb) {
-                    const half8 w = as_half8(wl[(b * KC + c) * 64]);
-                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, xh[c], acc[b], 0, 0, 0);
-                }
+        for (int j = 0; j < J; ++j) {
+            const int c = j / NB, b = j % NB;
+            const half8 w = wq[j % D];
+            if (j + D < J) wq[j % D] = wtile(j + D);
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, xc, acc[b], 0, 0, 0);
+            if (b == NB - 1) {  // chunk c done: refill it with the next subtile's, convert chunk c + 1
+                xv[c] = *reinterpret_cast<const uint4*>(pn + 32 * c);
+                if (c + 1 < KC) xc = res_x16<XDT>(xv[c + 1], sc);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // epilogue: blocks 2p, 2p + 1 -> 32 outputs, 8 per lane, one store each
-#pragma unroll
-        for (int p = 0; p < NBMAX / 2; ++p) {
-            if (2 * p >= nb) break;
+        if constexpr (XDT == RPFQ_BF16) xsv = *xsptr(tl);
+        // epilogue: blocks 2p, 2p + 1 -> 32 outputs, 8 per lane
+        auto pair_out = [&](int p) -> uint4 {
             uint32_t d[4];
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb) {
@@ -229,60 +292,133 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
             // leaves 8 consecutive outputs in each lane
             const auto s0 = __builtin_amdgcn_permlane16_swap(d[0], d[2], false, false);
             const auto s1 = __builtin_amdgcn_permlane16_swap(d[1], d[3], false, false);
-            uint4 o = make_uint4(s0[0], s1[0], s0[1], s1[1]);
-            if (a.res) {
+            return make_uint4(s0[0], s1[0], s0[1], s1[1]);
+        };
+        auto finish = [&](uint4 o, int i) -> uint4 {  // residual and GELU of store i
+            if constexpr (RES != 0) {
                 const bool f16 = YDT == RPFQ_F16;
-                const uint4 rv = rres[p];
+                const uint4 rv = rres[i];
                 o = make_uint4(add2_y(o.x, rv.x, f16), add2_y(o.y, rv.y, f16), add2_y(o.z, rv.z, f16),
                                add2_y(o.w, rv.w, f16));
             }
             if constexpr (ACT != 0) o = gelu8_rolled(o, YDT == RPFQ_F16);
-            if (row_in) *reinterpret_cast<uint4*>(yrow + 32 * p) = o;
+            return o;
+        };
+        if constexpr (TR == 0) {
+#pragma unroll
+            for (int p = 0; p < NB / 2; ++p) *reinterpret_cast<uint4*>(yrow + 32 * p) = finish(pair_out(p), p);
+        } else {
+            // TR rows at a time through this wave's LDS rows (laid out as in
+            // y), then copied out 1 KB per instruction: whole 128-B lines
+            uint4 po[NB / 2];  // the packed outputs, computed once (the accumulators die as they go)
+#pragma unroll
+            for (int p = 0; p < NB / 2; ++p) po[p] = pair_out(p);
+#pragma unroll
+            for (int hh = 0; hh < 16 / TR; ++hh) {
+                // no branch around the writes: with one, the compiler has
+                // placed the block's reads below inside the masked region
+                // (lanes of the other half kept stale registers); those
+                // lanes write the wave's scratch area instead
+                const uint32_t mine = (TR == 16 || (r >> 3) == hh) ? ~0u : 0u;
+                const uint32_t stage_at = (uint32_t)(stage - smem);
+                const uint32_t junk_at = (uint32_t)(res_lds_layer(KC, NB) + kResWaves * TR * RB +
+                                                    (threadIdx.x >> 6) * 512 + 16 * ((r & 7) + 8 * q));
+#pragma unroll
+                for (int p = 0; p < NB / 2; ++p) {
+                    const uint32_t real_at = stage_at + (uint32_t)((r - hh * TR) * RB + 64 * p + 2 * ocol);
+                    const uint32_t at = (real_at & mine) | (junk_at & ~mine);  // a mask, not a branch
+                    *reinterpret_cast<uint4*>(smem + at) = po[p];
+                }
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const uint4 o = *reinterpret_cast<const uint4*>(stage + stage_off(i));
+                    const int k = hh * NI + i;
+                    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.y) + out_at(t, k)) = finish(o, k);
+                }
+            }
         }
+    };
+    // whole rounds without a branch around any slot (so the wait before each
+    // chunk counts exactly the U - 1 slots issued since), then the rest
+    const int64_t n = t0 < nsub ? (nsub - t0 + ws - 1) / ws : 0;  // this wave's subtiles
+    const int64_t full = n / U;
+    int64_t tb = t0;
+#pragma unroll 1
+    for (int64_t i = 0; i < full; ++i, tb += U * ws) {
+#pragma unroll
+        for (int s = 0; s < U; ++s) slot(tb + s * ws, xr[s], xsc[s]);
     }
+    const int rest = (int)(n - full * U);
+#pragma unroll
+    for (int s = 0; s < U - 1; ++s)
+        if (s < rest) slot(tb + s * ws, xr[s], xsc[s]);
 }
 
-template <int KC, int NBMAX, int XDT, int YDT, int CB, int ACT>
+template <int KC, int NB, int RES, int XDT, int YDT, int CB, int ACT>
 static hipError_t wide_res_go(WideArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
-    const void* kern = reinterpret_cast<const void*>(&wide_linear_resident_kernel<KC, NBMAX, XDT, YDT, CB, ACT>);
+    static std::atomic<int> per_cu{0};  // resident workgroups per CU (occupancy at the largest LDS)
+    const void* kern = reinterpret_cast<const void*>(&wide_linear_resident_kernel<KC, NB, RES, XDT, YDT, CB, ACT>);
     const hipError_t e = set_lds_attr_once(kern, kResLdsMax, attr_done);
     if (e != hipSuccess) return e;
+    const int lds = resident_lds(a);
+    int wg = per_cu.load(std::memory_order_relaxed);
+    if (wg <= 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg, kern, kResWaves * 64, lds) != hipSuccess || wg < 1)
+            wg = 1;
+        per_cu.store(wg, std::memory_order_relaxed);  // lds is fixed per (K', N'): one instantiation per shape
+    }
     const int64_t nsub = (a.M + 15) / 16;
     // as few waves as give every wave the same number of subtiles (+- 1) in
     // the fewest rounds: the last round is then full
-    const int64_t slots = (int64_t)device_cus() * kResWaves;
+    const int64_t slots = (int64_t)device_cus() * wg * kResWaves;
     const int64_t rounds = (nsub + slots - 1) / slots;
     const int64_t waves = (nsub + rounds - 1) / rounds;
     const int grid = (int)((waves + kResWaves - 1) / kResWaves);
-    hipLaunchKernelGGL((wide_linear_resident_kernel<KC, NBMAX, XDT, YDT, CB, ACT>), dim3(grid),
-                       dim3(kResWaves * 64), resident_lds(a), s, a);
+    hipLaunchKernelGGL((wide_linear_resident_kernel<KC, NB, RES, XDT, YDT, CB, ACT>), dim3(grid), dim3(kResWaves * 64),
+                       lds, s, a);
     return hipGetLastError();
 }
 
-template <int KC, int NBMAX, int XDT, int YDT, int CB>
+template <int KC, int NB, int XDT, int YDT, int CB>
 static hipError_t wide_res_act(WideArgs& a, hipStream_t s) {
-    return a.act ? wide_res_go<KC, NBMAX, XDT, YDT, CB, 1>(a, s) : wide_res_go<KC, NBMAX, XDT, YDT, CB, 0>(a, s);
+    if constexpr (NB <= 12) {
+        if (a.res) return wide_res_go<KC, NB, 1, XDT, YDT, CB, 0>(a, s);  // GELU is never fused with a residual
+    }
+    return a.act ? wide_res_go<KC, NB, 0, XDT, YDT, CB, 1>(a, s) : wide_res_go<KC, NB, 0, XDT, YDT, CB, 0>(a, s);
 }
 
-template <int KC, int NBMAX, int CB>
+template <int KC, int NB, int CB>
 static hipError_t wide_res_dt(WideArgs& a, int xdt, int ydt, hipStream_t s) {
     if (xdt == RPFQ_BF16)
-        return ydt == RPFQ_BF16 ? wide_res_act<KC, NBMAX, RPFQ_BF16, RPFQ_BF16, CB>(a, s)
-                                : wide_res_act<KC, NBMAX, RPFQ_BF16, RPFQ_F16, CB>(a, s);
-    return ydt == RPFQ_BF16 ? wide_res_act<KC, NBMAX, RPFQ_F16, RPFQ_BF16, CB>(a, s)
-                            : wide_res_act<KC, NBMAX, RPFQ_F16, RPFQ_F16, CB>(a, s);
+        return ydt == RPFQ_BF16 ? wide_res_act<KC, NB, RPFQ_BF16, RPFQ_BF16, CB>(a, s)
+                                : wide_res_act<KC, NB, RPFQ_BF16, RPFQ_F16, CB>(a, s);
+    return ydt == RPFQ_BF16 ? wide_res_act<KC, NB, RPFQ_F16, RPFQ_BF16, CB>(a, s)
+                            : wide_res_act<KC, NB, RPFQ_F16, RPFQ_F16, CB>(a, s);
 }
 
+// The shapes taken (resident_shape): K' = 48 with N' in {48, 96, 144, 192};
+// K' = 96 with N' in {48, 96}; K' = 192 with N' = 48 (Swin-T stage 0, its
+// stage-1 proj).  Larger products leave no LDS for the staged stores and
+// their instantiations spill.
 template <int CB>
 hipError_t launch_wide_resident(WideArgs& a, int xdt, int ydt, hipStream_t s) {
-    const bool small = a.N <= 96;  // <= 12 accumulator tiles
-    switch (a.K) {
-        case 48: return small ? wide_res_dt<3, 12, CB>(a, xdt, ydt, s) : wide_res_dt<3, 24, CB>(a, xdt, ydt, s);
-        case 96: return small ? wide_res_dt<6, 12, CB>(a, xdt, ydt, s) : wide_res_dt<6, 24, CB>(a, xdt, ydt, s);
-        case 192: return wide_res_dt<12, 12, CB>(a, xdt, ydt, s);  // N' <= 96 (LDS)
-        default: return hipErrorInvalidValue;
+    if (a.K == 48) {
+        switch (a.N) {
+            case 48: return wide_res_dt<3, 6, CB>(a, xdt, ydt, s);
+            case 96: return wide_res_dt<3, 12, CB>(a, xdt, ydt, s);
+            case 144: return wide_res_dt<3, 18, CB>(a, xdt, ydt, s);
+            case 192: return wide_res_dt<3, 24, CB>(a, xdt, ydt, s);
+            default: return hipErrorInvalidValue;
+        }
     }
+    if (a.K == 96) {
+        if (a.N == 48) return wide_res_dt<6, 6, CB>(a, xdt, ydt, s);
+        if (a.N == 96) return wide_res_dt<6, 12, CB>(a, xdt, ydt, s);
+        return hipErrorInvalidValue;
+    }
+    if (a.K == 192 && a.N == 48) return wide_res_dt<12, 6, CB>(a, xdt, ydt, s);
+    return hipErrorInvalidValue;
 }
 
 template hipError_t launch_wide_resident<RPFQ_CB_SEL>(WideArgs&, int, int, hipStream_t);

@@ -76,7 +76,7 @@ def test_wide_linear_argument_errors():
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 32, None) == 6  # unknown flag bit
     # RPFQ_FLAG_RESIDENT on a layer it does not take (K' = 64); on a y that is not 16-byte aligned
     assert L.rpfq_wide_linear(ctypes.byref(d), p, 1 << 20, p, 1, 4, None, p, 1, 16, None) == 2
-    d48 = _desc(N, n=64, k=48)
+    d48 = _desc(N, n=48, k=48)
     assert L.rpfq_wide_linear(ctypes.byref(d48), p, 1 << 20, p, 1, 4, None, ctypes.c_void_p(264), 1, 16,
                               None) == 3
     # RPFQ_FLAG_STREAM with a tiled-kernel flag; a streaming grid past 2^24 workgroups
@@ -348,8 +348,9 @@ def test_wide_linear_kernel_choice():
 
 def test_wide_linear_resident_choice():
     """The resident-weight kernel: chosen by default for M >= 32768 on the
-    layers it takes (Swin-T stage 0: N' % 16 == 0, K' in {48, 96, 192}, the
-    decoded matrix within 160 KB of LDS; fp16 / bf16 x and y), never under
+    layers it takes (Swin-T stage 0 and its stage-1 proj: K' = 48 with N' in
+    {48, 96, 144, 192}, K' = 96 with N' in {48, 96}, K' = 192 with N' = 48;
+    fp16 / bf16 x and y), never under
     the other kernel flags; RPFQ_FLAG_RESIDENT forces it at any M and is
     refused, before any GPU work, for a layer, dtype or flag set it does
     not take."""
@@ -370,8 +371,8 @@ def test_wide_linear_resident_choice():
         assert kernel(d, 401408, flags=N.FLAG_TILE_M128) == N.KERNEL_TILED
         assert kernel(d, 5, flags=N.FLAG_RESIDENT) == N.KERNEL_RESIDENT
     assert kernel(fc2, 401408, flags=N.FLAG_NO_STREAM) == N.KERNEL_DMA
-    # shapes it does not take: N' % 16, K' outside {48, 96, 192}, over 160 KB
-    for n, k in ((50, 48), (144, 64), (384, 384), (192, 192)):
+    # shapes it does not take
+    for n, k in ((50, 48), (64, 48), (144, 64), (384, 384), (192, 192), (144, 96), (96, 192), (288, 48)):
         d = _desc(N, n=n, k=k)
         assert kernel(d, 401408) != N.KERNEL_RESIDENT
         assert kernel(d, 401408, flags=N.FLAG_RESIDENT) == -2
@@ -379,6 +380,11 @@ def test_wide_linear_resident_choice():
     assert kernel(qkv, 5, ydt=0, flags=N.FLAG_RESIDENT) == -5
     for other in (N.FLAG_NO_STREAM, N.FLAG_STREAM, N.FLAG_TILE_M128):
         assert kernel(qkv, 5, flags=N.FLAG_RESIDENT | other) == -6
+    # a residual only for N' <= 96 (its chunks are held through the MFMAs)
+    p, y = ctypes.c_void_p(256), ctypes.c_void_p(512)
+    assert L.rpfq_wide_linear_residual(ctypes.byref(qkv), p, 1 << 20, p, 1, 4, None, p, y, 1,
+                                       N.FLAG_RESIDENT, None) == 2
+    assert b"N' <= 96" in L.rpfq_last_error()
 
 
 def test_wide_grad_x_geometry_and_argument_errors():
