@@ -168,16 +168,19 @@ constexpr int kResLdsMax = 160 * 1024;
 constexpr int res_lds_layer(int kc, int nb) { return nb * kc * 1024 + 64 * nb; }
 // Rows of output each wave stages in LDS before its full-line stores: 16
 // (a whole subtile), 8 (half of it) or 0 (no room left beside the layer:
-// direct 16-B stores).  Row bytes: 4N' = 32 nb.
+// direct 16-B stores).  An output row is 4N' = 32 nb bytes, staged at a
+// pitch 16 B longer (res_stage_pitch) so the 16 rows of one staging write
+// fall on distinct banks.
+constexpr int res_stage_pitch(int nb) { return 32 * nb + 16; }
 constexpr int res_stage_rows(int kc, int nb) {
-    return res_lds_layer(kc, nb) + kResWaves * 16 * 32 * nb <= kResLdsMax               ? 16
-           : res_lds_layer(kc, nb) + kResWaves * (8 * 32 * nb + 512) <= kResLdsMax ? 8
-                                                                                         : 0;
+    return res_lds_layer(kc, nb) + kResWaves * 16 * res_stage_pitch(nb) <= kResLdsMax               ? 16
+           : res_lds_layer(kc, nb) + kResWaves * (8 * res_stage_pitch(nb) + 512) <= kResLdsMax ? 8
+                                                                                                  : 0;
 }
 // (staging 8 rows at a time, the lanes of the other 8 rows write a 512-B
 // scratch area per wave instead)
 constexpr int res_lds(int kc, int nb) {
-    return res_lds_layer(kc, nb) + kResWaves * res_stage_rows(kc, nb) * 32 * nb +
+    return res_lds_layer(kc, nb) + kResWaves * res_stage_rows(kc, nb) * res_stage_pitch(nb) +
            (res_stage_rows(kc, nb) == 8 ? kResWaves * 512 : 0);
 }
 inline int resident_lds(const WideArgs& a) { return res_lds(a.K / 16, a.N / 8); }

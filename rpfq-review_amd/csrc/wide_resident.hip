@@ -143,8 +143,10 @@ __device__ __forceinline__ uint32_t res_pack2(float lo, float hi) {
 
 // Subtiles in flight per wave (the register ring).  Deeper rings (4 at
 // K' = 48, 3 at K' = 96) measured no faster: 8 waves per CU with two
-// subtiles each keep enough rows in flight.
-template <int KC> constexpr int res_ring() { return 2; }
+// subtiles each keep enough rows in flight.  With 24 accumulator tiles one
+// slot (each chunk refilled with the next subtile's as its MFMAs issue)
+// keeps the registers within 256.
+template <int KC, int NB> constexpr int res_ring() { return NB >= 24 ? 1 : 2; }
 constexpr int kResWAhead = 4;  // weight tiles read ahead of their MFMA
 
 // prescale of bf16 rows launched without row scales (WideArgs::xs NULL)
@@ -163,7 +165,7 @@ __device__ const float kResUnitScale = 1.0f;
 template <int KC, int NB, int RES, int XDT, int YDT, int CB, int ACT>
 __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(WideArgs a) {
     extern __shared__ __align__(16) char smem[];
-    constexpr int U = res_ring<KC>();
+    constexpr int U = res_ring<KC, NB>();
     constexpr int J = NB * KC;  // MFMAs per subtile, chunk-major (j = c NB + b)
     constexpr int D = kResWAhead < J ? kResWAhead : J;
     static_assert(!RES || NB <= 12, "residual layers: N' <= 96");
@@ -172,15 +174,18 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
     // output staging: TR rows of RB bytes per wave after the layer
     constexpr int TR = res_stage_rows(KC, NB);
     constexpr int RB = 32 * NB;                          // bytes of an output row (4N')
-    constexpr int NI = TR ? (TR * RB + 1023) / 1024 : 0;  // 1-KB stores per staged block
-    constexpr int NOUT = TR ? NI * (16 / TR) : NB / 2;    // 16-B stores per lane and subtile
-    char* stage = smem + res_lds_layer(KC, NB) + (threadIdx.x >> 6) * TR * RB;
-    // byte offset in the staged block of store i: lane l's 16 B of the i-th
-    // KB (the last KB's lanes past the block repeat its last chunk)
+    constexpr int RP = res_stage_pitch(NB);              // its pitch in the staging rows
+    static_assert(TR > 0, "the shapes taken leave LDS for at least 8 staged rows per wave");
+    constexpr int NI = (TR * RB + 1023) / 1024;  // 1-KB stores per staged block
+    constexpr int NOUT = NI * (16 / TR);         // 16-B stores per lane and subtile
+    char* stage = smem + res_lds_layer(KC, NB) + (threadIdx.x >> 6) * TR * RP;
+    // byte offset in the staged rows (as in y) of store i: lane l's 16 B of
+    // the i-th KB (the last KB's lanes past the block repeat its last chunk)
     auto stage_off = [&](int i) -> int {
         const int o = 1024 * i + 16 * lane;
         return o < TR * RB ? o : TR * RB - 16;
     };
+    auto stage_at = [&](int o) -> int { return (o / RB) * RP + o % RB; };  // its LDS offset
     const int64_t nsub = (a.M + 15) >> 4;
     const int64_t ws = (int64_t)gridDim.x * kResWaves;
     const int64_t t0 = (int64_t)blockIdx.x * kResWaves + (threadIdx.x >> 6);
@@ -200,19 +205,17 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
         return reinterpret_cast<const uint16_t*>(a.x) + row_of(tt) * ldx + 8 * q;
     };
     auto xsptr = [&](int64_t tt) -> const float* { return scaled ? a.xs + row_of(tt) : &kResUnitScale; };
-    // element offset in y (and the residual) of this lane's store k of subtile
-    // tt: staged, row hh TR + o / RB of the subtile, byte o % RB of the row,
-    // o = stage_off(i), k = hh NI + i (rows past M go to row M - 1, whose
-    // values they hold); direct, pair k of the lane's own row
-    auto out_at = [&](int64_t tt, int k) -> int64_t {
-        if constexpr (TR == 0) {
-            return row_of(tt) * ldy + ocol + 32 * k;
-        } else {
-            const int hh = k / NI, o = stage_off(k - hh * NI);
-            int64_t row = tt * 16 + hh * TR + o / RB;
-            if (row >= a.M) row = a.M - 1;
-            return row * ldy + (o % RB) / 2;
-        }
+    // This lane's stores of subtile tt go to out_base(tt) + out_off(tt, k)
+    // bytes of y (and read the residual there): byte o = stage_off(i) of the
+    // staged rows hh TR .. of the subtile, k = hh NI + i, i.e. row
+    // hh TR + o / RB, byte o % RB (rows past M go to row M - 1, whose values
+    // they hold).
+    auto out_base = [&](int64_t tt) -> int64_t { return 2 * tt * 16 * ldy; };  // bytes
+    auto out_off = [&](int64_t tt, int k) -> uint32_t {
+        const int last = a.M - 1 - tt * 16 < 15 ? (int)(a.M - 1 - tt * 16) : 15;  // last row in y
+        const int hh = k / NI, o = stage_off(k - hh * NI);
+        const int row = hh * TR + o / RB;
+        return (uint32_t)((row < last ? row : last) * RB + o % RB);
     };
     uint4 xr[U][KC];
     float xsc[U];
@@ -234,15 +237,14 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
     auto slot = [&](int64_t t, uint4 (&xv)[KC], float& xsv) {
         const int64_t tn = t + U * ws;
         const int64_t tl = tn < nsub ? tn : t;  // refill source: the slot's own rows on its last round
-        const int64_t m = row_of(t);
-        uint16_t* yrow = reinterpret_cast<uint16_t*>(a.y) + m * ldy + ocol;
         // residual chunks of this lane's stores, all read before any store
         // (in place, residual == y, a chunk stored twice reads the original)
         uint4 rres[RES ? NOUT : 1];
         if constexpr (RES != 0) {
 #pragma unroll
             for (int i = 0; i < NOUT; ++i)
-                rres[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.res) + out_at(t, i));
+                rres[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(a.res) + out_base(t) +
+                                                          out_off(t, i));
         }
         const float sc = xsv;
         const float inv = scaled ? row_unscale(sc) : 1.0f;
@@ -304,37 +306,33 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
             if constexpr (ACT != 0) o = gelu8_rolled(o, YDT == RPFQ_F16);
             return o;
         };
-        if constexpr (TR == 0) {
+        // TR rows at a time through this wave's LDS rows (laid out as in
+        // y), then copied out 1 KB per instruction: whole 128-B lines
+        uint4 po[NB / 2];  // the packed outputs, computed once (the accumulators die as they go)
 #pragma unroll
-            for (int p = 0; p < NB / 2; ++p) *reinterpret_cast<uint4*>(yrow + 32 * p) = finish(pair_out(p), p);
-        } else {
-            // TR rows at a time through this wave's LDS rows (laid out as in
-            // y), then copied out 1 KB per instruction: whole 128-B lines
-            uint4 po[NB / 2];  // the packed outputs, computed once (the accumulators die as they go)
+        for (int p = 0; p < NB / 2; ++p) po[p] = pair_out(p);
 #pragma unroll
-            for (int p = 0; p < NB / 2; ++p) po[p] = pair_out(p);
+        for (int hh = 0; hh < 16 / TR; ++hh) {
+            // no branch around the writes: with one, the compiler has
+            // placed the block's reads below inside the masked region
+            // (lanes of the other half kept stale registers); those
+            // lanes write the wave's scratch area instead
+            const uint32_t mine = (TR == 16 || (r >> 3) == hh) ? ~0u : 0u;
+            const uint32_t stage0 = (uint32_t)(stage - smem);
+            const uint32_t junk_at = (uint32_t)(res_lds_layer(KC, NB) + kResWaves * TR * RP +
+                                                (threadIdx.x >> 6) * 512 + 16 * ((r & 7) + 8 * q));
 #pragma unroll
-            for (int hh = 0; hh < 16 / TR; ++hh) {
-                // no branch around the writes: with one, the compiler has
-                // placed the block's reads below inside the masked region
-                // (lanes of the other half kept stale registers); those
-                // lanes write the wave's scratch area instead
-                const uint32_t mine = (TR == 16 || (r >> 3) == hh) ? ~0u : 0u;
-                const uint32_t stage_at = (uint32_t)(stage - smem);
-                const uint32_t junk_at = (uint32_t)(res_lds_layer(KC, NB) + kResWaves * TR * RB +
-                                                    (threadIdx.x >> 6) * 512 + 16 * ((r & 7) + 8 * q));
+            for (int p = 0; p < NB / 2; ++p) {
+                const uint32_t real_at = stage0 + (uint32_t)((r - hh * TR) * RP + 64 * p + 2 * ocol);
+                const uint32_t at = (real_at & mine) | (junk_at & ~mine);  // a mask, not a branch
+                *reinterpret_cast<uint4*>(smem + at) = po[p];
+            }
 #pragma unroll
-                for (int p = 0; p < NB / 2; ++p) {
-                    const uint32_t real_at = stage_at + (uint32_t)((r - hh * TR) * RB + 64 * p + 2 * ocol);
-                    const uint32_t at = (real_at & mine) | (junk_at & ~mine);  // a mask, not a branch
-                    *reinterpret_cast<uint4*>(smem + at) = po[p];
-                }
-#pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const uint4 o = *reinterpret_cast<const uint4*>(stage + stage_off(i));
-                    const int k = hh * NI + i;
-                    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.y) + out_at(t, k)) = finish(o, k);
-                }
+            for (int i = 0; i < NI; ++i) {
+                const uint4 o = *reinterpret_cast<const uint4*>(stage + stage_at(stage_off(i)));
+                const int k = hh * NI + i;
+                *reinterpret_cast<uint4*>(reinterpret_cast<char*>(a.y) + out_base(t) + out_off(t, k)) =
+                    finish(o, k);
             }
         }
     };

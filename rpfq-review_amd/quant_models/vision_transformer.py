@@ -142,7 +142,9 @@ class PatchEmbed(nn.Module):
                      None if self.proj.bias is None else self.proj.bias.to(patches.dtype))
         if not self.flatten:
             x = x.reshape(b, gh, gw, -1)  # B, H, W, C
-        return self.norm(x)
+        # Swin's patch norm (C = 96 over 401,408 rows at bs128) on the device
+        # row kernel: torch's took 407 us a forward there
+        return norm_fwd(self.norm, x)
 
 
 class Mlp(nn.Module):
