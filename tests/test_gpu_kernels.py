@@ -1273,6 +1273,39 @@ def test_gelu_act_quant_near_boundaries(c, bits, big):
     assert torch.equal(fused.cpu(), torch.from_numpy(np.concatenate([qr, qi], axis=1)))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gelu_act_quant_maximum_candidates(bits):
+    """The GELU + act-quant pass evaluates a fast GELU and torch's erf form
+    only where they could quantize differently; the half's maximum must
+    still be torch's: rows whose largest elements sit within a few ulps of
+    each other (every one a candidate; ties included), rows whose maximum
+    is below 0.25 (computed in torch's form throughout), a maximum from the
+    negative branch, against torch's GELU + act quant bit for bit at 64
+    lanes per row (M = 1,100)."""
+    import torch.nn.functional as F
+
+    ops, _ = qm()
+    r = rng(1600 + bits)
+    c, m = 3072, 1100
+    x = (r.standard_normal((m, c)) * 0.5).astype(np.float32)
+    for i in range(m):
+        kind = i % 4
+        top = np.float32(1.0 + 6.0 * r.random())
+        idx = r.choice(c, size=24, replace=False)
+        if kind == 0:    # near-ties below the maximum, both halves
+            x[i, idx] = top - np.arange(24, dtype=np.float32) * np.spacing(top)
+        elif kind == 1:  # exact ties
+            x[i, idx] = top
+        elif kind == 2:  # maxima below 0.25 (GELU of x < 0.4), negative branch included
+            x[i] = (r.random(c).astype(np.float32) - 0.75) * 0.5
+        else:            # the largest |GELU| from the negative branch (min GELU ~ -0.17 at x ~ -0.75)
+            x[i] = (r.random(c).astype(np.float32) * 0.2 - 0.85)
+    xd = tdev(x)
+    fused = ops.gelu_act_quant(xd, bits, out_dtype=torch.float32)
+    ref = ops.act_quant(F.gelu(xd), bits, out_dtype=torch.float32)
+    assert torch.equal(fused, ref)
+
+
 @pytest.mark.parametrize("k", [8, 384, 1536])
 def test_act_quant_row_kernel_matches_oracle(k):
     """The register-resident act-quant kernel (K' % 8 == 0) is bit-exact with
