@@ -307,6 +307,9 @@ DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
 # kernel's row prologue, rpfq_act_quant_wide_linear) where that launch
 # qualifies; RPFQ_FUSE_AQ_PROLOGUE=0 runs the separate act-quant pass.
 FUSE_AQ_PROLOGUE = os.environ.get("RPFQ_FUSE_AQ_PROLOGUE", "1") != "0"
+# RPFQ_FUSE_GELU=2: the MLP's GELU in fc1's store on every kernel (default:
+# where fc1 streams or keeps its layer resident, and for bf16 activations).
+GELU_ON_TILED = os.environ.get("RPFQ_FUSE_GELU", "1") == "2"
 # Input gradient of the HIP training forward on the packed blob of the
 # step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
 # A_q: "1" on (each grad_y element of a float32 step then carries one fp16
@@ -727,7 +730,7 @@ class QATLinearComplexPhase(nn.Linear):
                 x = ops.act_quant(x, self.act_quantizer.num_bits)
             m = x.numel() // x.shape[-1]
             kern = pw.kernel_for(m, x.dtype, x.dtype, N.FLAG_GELU) if m else None
-            if kern in N.STREAM_KERNELS or kern == N.KERNEL_RESIDENT or x.dtype == torch.bfloat16:
+            if kern in N.STREAM_KERNELS or kern == N.KERNEL_RESIDENT or x.dtype == torch.bfloat16 or GELU_ON_TILED:
                 return pw.linear(x, bias, out_dtype=x.dtype, gelu=True)
             return F.gelu(pw.linear(x, bias, out_dtype=x.dtype))
         return F.gelu(self.forward_prequantized(x) if prequantized else self.forward(x))
