@@ -347,6 +347,8 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     dt = dtype or torch.float16
     from quant_models import _native as N
+    # (KERNEL_GEMV: the persistent form wide_linear_gemv_persist_kernel at
+    # 12 k-steps from 4096 tiles, whole 64-row groups and 16-bit y)
     kname = {N.KERNEL_STREAM: "rpfq::wide_linear_skinny_kernel", N.KERNEL_GEMV: "rpfq::wide_linear_gemv_kernel",
              N.KERNEL_DMA: "rpfq::wide_linear_dma_kernel", N.KERNEL_TILED: "rpfq::wide_linear_kernel",
              N.KERNEL_RESIDENT: "rpfq::wide_linear_resident_kernel"}[

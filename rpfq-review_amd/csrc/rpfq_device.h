@@ -430,4 +430,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
 }
 
+// LDS DMA: lane l copies 16 B from gbase + voff[l] to LDS address lds + 16 l.
+// Written as asm so that the compiler's wait-count pass does not see the LDS
+// write (it would otherwise wait for every outstanding DMA before each LDS
+// read); every consumer waits explicitly (s_waitcnt vmcnt, and s_barrier
+// when another wave reads the destination) before reading it.  The
+// compiler's own waits stay correct: loads it does not count only make
+// them wait longer.
+__device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
+}
+
+// LDS DMA of one dword per lane (lane l: 4 B from gbase + voff[l] to lds + 4 l).
+__device__ __forceinline__ void dma_dword(const void* gbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
+}
+
 }  // namespace rpfq

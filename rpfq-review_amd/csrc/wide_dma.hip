@@ -63,20 +63,6 @@ static_assert(4 * 64 * kTRow <= kDmaStages * dma_stage<128>(), "epilogue half ti
 static_assert(4 * 128 * kTRow <= kDmaStages * dma_stage<256>(), "epilogue half tile fits the stages");
 
 
-// LDS DMA: lane l copies 16 B from gbase + voff[l] to LDS address lds + 16 l.
-// Written as asm so that the compiler's wait-count pass does not see the LDS
-// write (it would otherwise wait for every outstanding DMA before each LDS
-// read); every consumer waits explicitly (s_waitcnt vmcnt + s_barrier)
-// before reading the destination.
-__device__ __forceinline__ void dma_dwordx4(const void* gbase, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
-}
-
-// LDS DMA of one dword per lane (lane l: 4 B from gbase + voff[l] to lds + 4 l).
-__device__ __forceinline__ void dma_dword(const void* gbase, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(gbase) : "memory", "m0");
-}
-
 // LUT of one output row in the wave-pair layout: entry e (0..15 U, 16..31 W)
 // of row slot `slot` at lut_pair[64 e + slot]; lane group g writes the even
 // or odd indices.  Same values as build_lut.

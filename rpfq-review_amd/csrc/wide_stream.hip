@@ -913,6 +913,191 @@ __global__ void __launch_bounds__(64 * NW, RPFQ_GV_OCC) wide_linear_gemv_kernel(
     gv_store<YDT, H>(a, l, acc, tile0, M);
 }
 
+// Persistent form of the one-wave column-split kernel (H = 4: two packed
+// 32-row tiles, a "group", per wave) for long streams of groups below 16
+// k-steps: a grid of the resident waves walks the groups; the code ring runs
+// on into the next group's first k-steps while the current group's last ones
+// decode, the next group's row scales are prefetched into registers and its
+// LUT is built from them, so a group's start waits for no global load (the
+// one-group-per-wave launch pays the LUT's scale loads and the first code
+// loads at every group).  The bias and the residual of a group go to LDS by
+// DMA at the group's start, so the epilogue waits for no load issued after
+// the ring's (vmcnt counts in issue order: a load the epilogue waited for
+// would drain the ring).  Every ring load is issued on every path, so the
+// wait counts stay exact across groups; rows past M store row M - 1's values
+// (the same bits).  Taken for whole groups (NT even, N' % 32 == 0),
+// K' % (32 SK_PF) == 0, per-row scales, not TABLE, 16-bit y (vec_store).
+__device__ __align__(16) const float kGvZeroBias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+// LDS bytes past the two LUTs: the group's bias, [part][64 outputs] float,
+// and residual, [row][part][64 outputs] 16-bit
+constexpr int kGpBias = 2 * 64 * 4, kGpRes = 8 * 2 * 64 * 2;
+constexpr int gp_lds(bool res) { return gv_lds(4, 1) + kGpBias + (res ? kGpRes : 0); }
+
+// Three waves per SIMD (168 VGPRs: the next group's scales and the ring
+// across the group boundary do not fit 128); the 16.5-KB LDS share caps a CU
+// at 9 such waves anyway.
+template <int XDT, int YDT, int CB, bool RES>
+__global__ void __launch_bounds__(64, 3) wide_linear_gemv_persist_kernel(WideArgs a) {
+    constexpr int H = 4, TPG = 2, GN = 64;  // row groups, tiles and output rows per group
+    extern __shared__ __align__(16) char smem[];
+    uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
+    const float* bias_s = reinterpret_cast<const float*>(smem + gv_lds(H, 1));
+    const uint16_t* res_s = reinterpret_cast<const uint16_t*>(smem + gv_lds(H, 1) + kGpBias);
+    const int lane = threadIdx.x & 63;
+    const int KS = a.KS;
+    const int M = (int)a.M;  // 1 .. 8 (host-checked)
+    GvLane l = gv_lane(lane, M, a.K);
+    if (XDT != RPFQ_F16 && a.xs) l.xs = a.xs[min(l.r16 >> 1, M - 1)];
+    const int groups = a.NT / TPG, gs = (int)gridDim.x;
+    int grp = (int)blockIdx.x;
+    const int64_t tile_u2 = (int64_t)KS * 128;  // uint2 of codes per tile
+    // step s of group gg: its own for s < KS, else step s - KS of the next
+    // group of this wave (past the last group: the last step again)
+    auto load_codes = [&](int gg, int s, uint2* c) {
+        int g2 = gg, k = s;
+        if (s >= KS) {
+            g2 = gg + gs;
+            k = s - KS;
+            if (g2 >= groups) {
+                g2 = gg;
+                k = KS - 1;
+            }
+        }
+        const uint2* base = reinterpret_cast<const uint2*>(a.codes) + (int64_t)(TPG * g2) * tile_u2 + k * 128;
+#pragma unroll
+        for (int h = 0; h < H; ++h) c[h] = base[(h >> 1) * tile_u2 + l.coff + 64 * (h & 1)];
+    };
+    // (pu, pw) of this lane's LUT row in the group's tiles
+    auto load_params = [&](int gg, float4 (&pp)[TPG][2]) {
+#pragma unroll
+        for (int t = 0; t < TPG; ++t) {
+            const float4* p = a.params + ((int64_t)(TPG * gg + t) * 32 + l.R) * 2;
+            pp[t][0] = p[0];
+            pp[t][1] = p[1];
+        }
+    };
+    // bias (both parts) and residual (rows 0 .. M - 1, both parts) of group
+    // gg into LDS, one dword per lane and DMA
+    const int64_t N = a.N;
+    auto stage_epilogue = [&](int gg) {
+        const int64_t n0 = (int64_t)gg * GN;
+        const bool hb = a.bias != nullptr;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)  // a part's 64 outputs per DMA
+            dma_dword(hb ? (const void*)(a.bias + p * N + n0) : (const void*)kGvZeroBias, hb ? 4u * lane : 0u,
+                      lds_addr(bias_s + 64 * p));
+        if constexpr (RES) {  // one row per DMA: lane = (part, output pair)
+            const uint16_t* r = reinterpret_cast<const uint16_t*>(a.res) + n0;
+            const uint32_t voff = (uint32_t)(((lane >> 5) * N + 2 * (lane & 31)) * 2);
+#pragma unroll 1
+            for (int m = 0; m < M; ++m) dma_dword(r + 2 * N * m, voff, lds_addr(res_s + 128 * m));
+        }
+    };
+    // issue order: the scales, then as in the loop (activations of a k-step
+    // before its codes), so that the wait counts merged at the loop heads are
+    // the steady state's
+    float4 pp[TPG][2];
+    uint2 cring[SK_PF][H];
+    uint2 xring[GV_XPF][4];
+    load_params(grp, pp);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < GV_XPF; ++i) gv_load_x<XDT, false>(a, l, i, xring[i]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < SK_PF; ++i) load_codes(grp, i, cring[i]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int m = min(l.r16 >> 1, M - 1);  // rows past M store row M - 1's values
+    const int64_t ldy = 2 * N;
+    const bool f16 = YDT == RPFQ_F16;
+#pragma unroll 1
+    for (; grp < groups; grp += gs) {
+#pragma unroll
+        for (int t = 0; t < TPG; ++t)
+            build_lut_sk_regs<CB, 8>(lut + t * (kSkLut / 4), pp[t][0], pp[t][1], a.rot, l.R, l.g, 0);
+        load_params(grp + gs < groups ? grp + gs : grp, pp);  // the next group's
+        // the previous group's epilogue has consumed its LDS reads of the
+        // staging area (its stores depend on them)
+        stage_epilogue(grp);
+        floatx4 acc[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[h] = floatx4{0, 0, 0, 0};
+        int ks0 = 0;  // KS >= SK_PF: at least one round, so every path has the same loads in flight
+#pragma unroll 1
+        do {
+#pragma unroll
+            for (int i = 0; i < SK_PF; ++i) {
+                const int ks = ks0 + i;
+                gv_kstep<XDT, false, H, 1>(acc, l, ks, a.K, cring[i], xring[i % GV_XPF]);
+                const int kx = ks + GV_XPF < KS ? ks + GV_XPF : ks + GV_XPF - KS;
+                gv_load_x<XDT, false>(a, l, kx, xring[i % GV_XPF]);
+                load_codes(grp, ks + SK_PF, cring[i]);
+            }
+            ks0 += SK_PF;
+        } while (ks0 < KS);
+        // the loop issued 8 loads per k-step (4 code, 4 activation) after the
+        // staging DMAs, at least 8 SK_PF of them: 32 outstanding at most
+        // means the DMAs have landed
+        static_assert(8 * SK_PF == 32, "the wait count below");
+        asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+        // outputs n = GN grp + 16 h + 4 q + v of part p of row m
+        const float inv = row_unscale(l.xs);  // undo the row's prescale (exact) before the bias
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const int j = 16 * h + 4 * l.q;
+            const int64_t base = m * ldy + (l.p ? N : 0) + (int64_t)grp * GN + j;
+            const float4 bq = *reinterpret_cast<const float4*>(bias_s + GN * l.p + j);
+            float v4[4] = {acc[h][0] * inv + bq.x, acc[h][1] * inv + bq.y, acc[h][2] * inv + bq.z,
+                           acc[h][3] * inv + bq.w};
+            uint2 o;
+            if constexpr (YDT == RPFQ_F16) {
+                o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
+            } else {
+                o = make_uint2((uint32_t)f32_to_bf16(v4[0]) | ((uint32_t)f32_to_bf16(v4[1]) << 16),
+                               (uint32_t)f32_to_bf16(v4[2]) | ((uint32_t)f32_to_bf16(v4[3]) << 16));
+            }
+            if constexpr (RES) {
+                const uint2 rv = *reinterpret_cast<const uint2*>(res_s + 2 * GN * m + GN * l.p + j);
+                o = make_uint2(add2_y(o.x, rv.x, f16), add2_y(o.y, rv.y, f16));
+            } else if (a.act) {
+                o = make_uint2(gelu2_y(o.x, f16), gelu2_y(o.y, f16));
+            }
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) = o;
+        }
+    }
+}
+
+template <int XDT, int YDT, int CB, bool RES>
+static hipError_t wide_gv_persist_launch(WideArgs& a, hipStream_t s) {
+    static std::atomic<int> per_cu{0};  // resident workgroups (one wave) per CU
+    const void* kern = reinterpret_cast<const void*>(&wide_linear_gemv_persist_kernel<XDT, YDT, CB, RES>);
+    const int lds = gp_lds(RES);
+    int wg = per_cu.load(std::memory_order_relaxed);
+    if (wg <= 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg, kern, 64, lds) != hipSuccess || wg < 1) wg = 1;
+        per_cu.store(wg, std::memory_order_relaxed);
+    }
+    const int64_t groups = a.NT / 2;
+    const int64_t slots = (int64_t)device_cus() * wg;
+    const int grid = (int)(groups < slots ? groups : slots);
+    hipLaunchKernelGGL((wide_linear_gemv_persist_kernel<XDT, YDT, CB, RES>), dim3((unsigned)grid), dim3(64), lds, s,
+                       a);
+    return hipGetLastError();
+}
+template <int XDT, int YDT, int CB>
+static hipError_t wide_gv_persist_go(WideArgs& a, hipStream_t s) {
+    return a.res ? wide_gv_persist_launch<XDT, YDT, CB, true>(a, s) : wide_gv_persist_launch<XDT, YDT, CB, false>(a, s);
+}
+
+// The persistent form's conditions (above): the launches of the one-wave
+// form (12 .. 15 k-steps from 4096 tiles) that it can take.  The longer ones
+// stay on the two-wave form: the persistent one-wave kernel measured slower
+// there, and so did a one-tile-per-wave persistent form at any length.
+static bool gv_persist_ok(const WideArgs& a, int ydt, int cb) {
+    return gemv_single_wave(a) && a.NT % 2 == 0 && a.N % 32 == 0 && a.K % 32 == 0 && a.KS % SK_PF == 0 &&
+           a.nblk == 1 && cb != RPFQ_CB_TABLE && (ydt == RPFQ_F16 || ydt == RPFQ_BF16) && a.vec_store;
+}
+
 template <int XDT, int YDT, int CB, bool KT, int NW, int H>
 static hipError_t wide_gv_go(WideArgs& a, hipStream_t s) {
     const int64_t groups = (a.NT + H / 2 - 1) / (H / 2);
@@ -945,6 +1130,9 @@ static hipError_t wide_sk_ln_go(WideArgs& a, hipStream_t s) {
 // below 16 k-steps).
 template <int XDT, int YDT, int CB, bool KT>
 static hipError_t wide_gv(WideArgs& a, hipStream_t s) {
+    if constexpr (!KT && CB != RPFQ_CB_TABLE && YDT != RPFQ_F32) {
+        if (gv_persist_ok(a, YDT, CB)) return wide_gv_persist_go<XDT, YDT, CB>(a, s);
+    }
     if (gemv_single_wave(a)) return wide_gv_go<XDT, YDT, CB, KT, 1, 4>(a, s);
     if (a.NT >= kSkSplitTiles) return wide_gv_go<XDT, YDT, CB, KT, 2, 4>(a, s);
     if (a.NT >= kSkNw2Groups) return wide_gv_go<XDT, YDT, CB, KT, 2, 2>(a, s);

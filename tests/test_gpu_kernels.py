@@ -744,6 +744,90 @@ def test_wide_linear_gemv_one_wave_dtypes(xdt, ydt):
                          fp16="split")
 
 
+def _device_axis_layer(n_c, k_c, seed):
+    """A two-stage axis layer too large for the host-side generator: packed
+    2-bit planes (4 codes per byte, oracle.pack_codes order) and per-row
+    scales ~U(0.01, 0.1) drawn on the device."""
+    ops, N = qm()
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    packed = [torch.randint(0, 256, (n_c, k_c // 4), dtype=torch.uint8, device=DEV, generator=g) for _ in range(4)]
+    sre = [torch.rand(n_c, 1, device=DEV, generator=g) * 0.09 + 0.01 for _ in range(4)]
+    sim = [torch.rand(n_c, 1, device=DEV, generator=g) * 0.09 + 0.01 for _ in range(4)]
+    pw = ops.PackedWide.from_planes(packed, sre, sim, n_c, k_c, N.CB_AXIS, 2, 0, None)
+    return pw, packed, sre, sim
+
+
+def _oracle_rows(packed, sre, sim, k_c, sel):
+    """Oracle planes of the complex output rows `sel` only (the output's
+    columns sel and N' + sel)."""
+    idx = torch.from_numpy(sel).to(DEV)
+    planes = [O.unpack_codes(p.index_select(0, idx).cpu().numpy(), k_c) for p in packed]
+    s1 = [s.index_select(0, idx).cpu().numpy() for s in sre]
+    s2 = [s.index_select(0, idx).cpu().numpy() for s in sim]
+    return oracle_planes(planes, s1, s2, ["u", "u", "w", "w"], k_c, 0)
+
+
+@pytest.mark.parametrize("m,n_c,k_c,xdt,ydt", [
+    (1, 300032, 384, torch.float16, torch.float16),
+    (4, 300032, 384, torch.bfloat16, torch.bfloat16),
+    (8, 300032, 384, torch.float16, torch.bfloat16),
+    (3, 300032, 384, torch.float32, torch.float16),
+    (5, 300032, 384, torch.bfloat16, torch.float16),
+    (7, 131072, 384, torch.float16, torch.float16),
+], ids=["m1-f16", "m4-bf16", "m8-f16-bf16", "m3-f32-f16", "m5-bf16-f16", "m7-f16-n131072"])
+def test_wide_linear_gemv_persistent(m, n_c, k_c, xdt, ydt):
+    """The column-split kernel's persistent one-wave form (12 k-steps from
+    4096 tiles, whole 64-row groups, per-row scales, 16-bit y): 4,688 groups
+    at N' = 300,032, so the resident waves walk two or three each and the
+    code ring runs across group boundaries, and 2,048 at N' = 131,072 (at
+    most one per wave).  On 2,176 sampled rows (the first and last groups
+    among them) against the oracle on the split operand it contracts, with
+    bias and without (the LDS-staged bias is the only difference); a
+    residual added in the store bit-identical to the unfused add (also in
+    place, residual == y through the C ABI); the fused GELU within 1 ulp of
+    the exact GELU of the unfused output."""
+    import ctypes
+    import math
+
+    ops, N = qm()
+    r = rng(1400 + m + k_c)
+    pw, packed, sre, sim = _device_axis_layer(n_c, k_c, 1400 + m)
+    assert pw.kernel_for(m, xdt, ydt) == N.KERNEL_GEMV
+    g = torch.Generator(device=DEV).manual_seed(1401 + m)
+    x = torch.randn(m, 2 * k_c, device=DEV, generator=g).to(xdt)
+    bias = torch.randn(2 * n_c, device=DEV, generator=g)
+    y = pw.linear(x, bias, out_dtype=ydt)
+    sel = np.unique(np.concatenate([np.arange(64), np.arange(n_c - 64, n_c), r.choice(n_c, 2048, replace=False)]))
+    oplanes = _oracle_rows(packed, sre, sim, k_c, sel)
+    cols = np.concatenate([sel, n_c + sel])
+    ys = y.float().cpu().numpy()[:, cols]
+    xf = x.float().to(torch.float16).float().cpu().numpy().astype(np.float64)
+    out_ulp = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[ydt]
+    check_against_oracle(ys, xf, bias.cpu().numpy()[cols].astype(np.float64), oplanes, "axis", None, out_ulp,
+                         fp16="split")
+    y0 = pw.linear(x, None, out_dtype=ydt).float().cpu().numpy()[:, cols]
+    check_against_oracle(y0, xf, None, oplanes, "axis", None, out_ulp, fp16="split")
+    assert torch.equal(pw.linear(x, bias, out_dtype=ydt), y)  # deterministic
+    if xdt != torch.float32:
+        res = (torch.randn(m, 2 * n_c, device=DEV, generator=g) * 4).to(ydt)
+        want = res + y
+        assert torch.equal(pw.linear(x, bias, out_dtype=ydt, residual=res), want)
+        if xdt == torch.float16:  # (bf16 x takes row prescales, which this entry point has no argument for)
+            yi = res.clone()
+            lib = N.load()
+            N.check("rpfq_wide_linear_residual", lib.rpfq_wide_linear_residual(
+                ctypes.byref(pw.desc), pw.blob.data_ptr(), pw.blob.numel(), x.data_ptr(), N.F16, m,
+                bias.data_ptr(), yi.data_ptr(), yi.data_ptr(), N.dtype_code(ydt), 0, N.stream_of(x)))
+            torch.cuda.synchronize()
+            assert torch.equal(yi, want)
+        yg = pw.linear(x, bias, out_dtype=ydt, gelu=True).cpu()
+        yd = y.double().cpu()
+        exact = yd * 0.5 * torch.special.erfc(-yd / math.sqrt(2.0))
+        tiny = exact.abs() < 2.0 ** -126
+        d = torch.where(tiny, torch.zeros_like(yg, dtype=torch.long), ulp_distance(yg, exact.to(ydt)))
+        assert int(d.max()) <= 1 and float((d > 0).float().mean()) <= 1e-3
+
+
 # ---------------------------------------------------------------------------
 # resident-weight kernel (RPFQ_KERNEL_RESIDENT): the decoded layer stays in
 # LDS while the waves stream 32-row subtiles of x (Swin-T stage 0)
