@@ -225,6 +225,31 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
                               const void* residual, void* y, int y_dtype, int flags, void* stream);
 
 /*
+ * The MLP tail of a transformer block in one launch:
+ *   y = residual + fc2(GELU(fc1(x) + bias1)) + bias2
+ * fc1 (desc1: K' -> N1') and fc2 (desc2: N1' -> K') packed widely-linear
+ * layers; the hidden activations stay on chip.  Each hidden value is fc1's
+ * output rounded to fp16 and its GELU rounded again, within 1 ulp of the
+ * exact GELU (the fused GELU of rpfq_wide_linear's RPFQ_FLAG_GELU), and y is
+ * bit-identical to rpfq_wide_linear(fc1, RPFQ_FLAG_GELU) followed by
+ * rpfq_wide_linear_residual(fc2) on the large-M kernel.  x, residual, y:
+ * fp16 [M, 2K'], rows 16-byte aligned; residual may be NULL or y itself.
+ * bias1 [2N1'] / bias2 [2K'] float32 or NULL.  Shapes: K' = 96 (DeiT-Ti,
+ * Swin-T stage 1), N1' a multiple of 96 up to 1536, per-row scales
+ * (block = 0) on both layers, one codebook, M >= 64; others return
+ * RPFQ_ERR_SHAPE.  Replaces the block's
+ *   norm2 -> mlp.fc1 -> mlp.act -> mlp.fc2 -> + residual1 sequence
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:549-556
+ * after the LayerNorm (the reference's two QATLinearComplexPhase.forward
+ * calls, RPFQ-ViT-main/quant_models/quant_i.py:513-554, and the GELU
+ * between them).
+ */
+int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                  const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
+                  int64_t M, const float* bias1, const float* bias2, const void* residual, void* y,
+                  void* stream);
+
+/*
  * Per-row prescales of x [M, C] for rpfq_wide_linear_scaled (the forward's
  * range guard): scale[m] = 2^(14 - floor(log2 max_k |x[m, k]|)), clamped to
  * [2^-126, 2^126], so the row's largest element times scale[m] lies in

@@ -302,6 +302,35 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
 }
 
 
+int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                  const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
+                  int64_t M, const float* bias1, const float* bias2, const void* residual, void* y,
+                  void* stream) {
+    int rc = check_desc(desc1);
+    if (rc) return rc;
+    if ((rc = check_desc(desc2))) return rc;
+    if (!packed1 || !packed2 || !x || !y) return fail(RPFQ_ERR_NULL, "packed1/packed2/x/y must not be NULL");
+    if (M <= 0 || M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld out of range", (long long)M);
+    const rpfq::WideGeom g1 = rpfq::wide_geom(*desc1), g2 = rpfq::wide_geom(*desc2);
+    if (g2.K != g1.N || g2.N != g1.K)
+        return fail(RPFQ_ERR_SHAPE, "fc2 (%lld -> %lld) does not invert fc1 (%lld -> %lld)", (long long)g2.K,
+                    (long long)g2.N, (long long)g1.K, (long long)g1.N);
+    if (!rpfq::wide_mlp_shape(g1, g2, desc1->codebook, desc2->codebook, M))
+        return fail(RPFQ_ERR_SHAPE,
+                    "rpfq_wide_mlp takes K'=96, N1' a multiple of 96 up to 1536, block=0 on both layers, one "
+                    "codebook and M >= 64 (K'=%lld N1'=%lld M=%lld)",
+                    (long long)g1.K, (long long)g1.N, (long long)M);
+    if (packed1_bytes < g1.total_bytes || packed2_bytes < g2.total_bytes)
+        return fail(RPFQ_ERR_SHAPE, "packed buffers hold %zu / %zu bytes, need %zu / %zu", packed1_bytes,
+                    packed2_bytes, g1.total_bytes, g2.total_bytes);
+    if (!aligned(packed1, 256) || !aligned(packed2, 256) || !aligned(x, 16) || !aligned(y, 16) ||
+        (residual && !aligned(residual, 16)))
+        return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x, y and residual 16-byte aligned");
+    return hip_status(rpfq::launch_wide_mlp_layers(*desc1, g1, packed1, *desc2, g2, packed2, x, M, bias1, bias2,
+                                                   residual, y, reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_wide_mlp");
+}
+
 int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,
                             int x_dtype, int64_t M, const float* row_scale, const float* bias, const void* residual,
                             void* y, int y_dtype, int flags, void* stream) {

@@ -155,6 +155,34 @@ template <int CB> hipError_t launch_wide_stream(WideArgs& a, int xdt, int ydt, h
 template <int CB> hipError_t launch_wide_tiled(WideArgs& a, int bm, int xdt, int ydt, hipStream_t s);
 template <int CB> hipError_t launch_wide_resident(WideArgs& a, int xdt, int ydt, hipStream_t s);
 
+// Fused MLP (wide_mlp.hip): y = residual + fc2(GELU(fc1(x))) for fp16 x / y,
+// fc1 K' -> N1', fc2 N1' -> K', one 64-row tile of x per workgroup of
+// K' / 32 waves, the hidden activations in LDS.
+struct MlpArgs {
+    const void* x;  // [M, 2 K'] fp16
+    int64_t M;
+    int K, N1;  // fc1: K' inputs, N1' outputs; fc2: N1' inputs, K' outputs
+    const uint4* codes1;
+    const float4* params1;
+    RotParams rot1;
+    const float* bias1;  // [2 N1'] or NULL
+    const uint4* codes2;
+    const float4* params2;
+    RotParams rot2;
+    const float* bias2;  // [2 K'] or NULL
+    const void* res;     // [M, 2 K'] fp16 or NULL (may be y)
+    void* y;             // [M, 2 K'] fp16
+    int tiles;           // row tiles (set by the launcher)
+};
+template <int CB> hipError_t launch_wide_mlp(const MlpArgs& a, hipStream_t s);
+// The fused MLP's shapes: K' = 96 (three waves), N1' a multiple of 96 up
+// to 1536, per-row scales on both layers, one codebook, M >= 64.
+bool wide_mlp_shape(const WideGeom& g1, const WideGeom& g2, int cb1, int cb2, int64_t M);
+hipError_t launch_wide_mlp_layers(const rpfq_wide_desc& d1, const WideGeom& g1, const void* packed1,
+                                  const rpfq_wide_desc& d2, const WideGeom& g2, const void* packed2, const void* x,
+                                  int64_t M, const float* bias1, const float* bias2, const void* res, void* y,
+                                  hipStream_t s);
+
 // Resident-weight kernel (wide_resident.hip): one workgroup of kResWaves
 // waves per CU holds the whole decoded layer in LDS (2N' x 2K' fp16 as MFMA
 // A operands, plus the float32 bias) and streams 16-row subtiles of x, each

@@ -204,6 +204,39 @@ hipError_t launch_wide_linear_grad_x(const rpfq_wide_desc& d, const WideGeom& g,
     return launch_wide_grad_x(a, gdt, xdt, s);
 }
 
+bool wide_mlp_shape(const WideGeom& g1, const WideGeom& g2, int cb1, int cb2, int64_t M) {
+    return g1.K == 96 && g1.N % 96 == 0 && g1.N <= 1536 && g2.K == g1.N && g2.N == g1.K && g1.nblk == 1 &&
+           g2.nblk == 1 && cb1 == cb2 && M >= 64;
+}
+
+hipError_t launch_wide_mlp_layers(const rpfq_wide_desc& d1, const WideGeom& g1, const void* packed1,
+                                  const rpfq_wide_desc& d2, const WideGeom& g2, const void* packed2, const void* x,
+                                  int64_t M, const float* bias1, const float* bias2, const void* res, void* y,
+                                  hipStream_t s) {
+    if (!wide_mlp_shape(g1, g2, d1.codebook, d2.codebook, M)) return hipErrorInvalidValue;
+    MlpArgs a = {};
+    a.x = x;
+    a.M = M;
+    a.K = (int)g1.K;
+    a.N1 = (int)g1.N;
+    a.codes1 = reinterpret_cast<const uint4*>(packed1);
+    a.params1 = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed1) + g1.codes_bytes);
+    a.rot1 = rot_of(d1);
+    a.bias1 = bias1;
+    a.codes2 = reinterpret_cast<const uint4*>(packed2);
+    a.params2 = reinterpret_cast<const float4*>(reinterpret_cast<const char*>(packed2) + g2.codes_bytes);
+    a.rot2 = rot_of(d2);
+    a.bias2 = bias2;
+    a.res = res;
+    a.y = y;
+    switch (d1.codebook) {
+        case RPFQ_CB_SIGN: return launch_wide_mlp<RPFQ_CB_SIGN>(a, s);
+        case RPFQ_CB_PSK16: return launch_wide_mlp<RPFQ_CB_PSK16>(a, s);
+        case RPFQ_CB_TABLE: return launch_wide_mlp<RPFQ_CB_TABLE>(a, s);
+        default: return launch_wide_mlp<RPFQ_CB_AXIS>(a, s);
+    }
+}
+
 hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const void* packed, const void* x,
                               int xdt, int64_t M, const float* xs, const float* bias, const void* res, void* y,
                               int ydt, int flags, hipStream_t s) {

@@ -66,6 +66,7 @@ EXPORTED = (
     "rpfq_quantize_wide_noalloc",
     "rpfq_row_scales",
     "rpfq_wide_linear_scaled",
+    "rpfq_wide_mlp",
 )
 
 
@@ -158,6 +159,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_quantize_wide_noalloc.argtypes = [qp, vp, vp, vp, vp, vp, vp]
         lib.rpfq_row_scales.argtypes = [vp, i32, i64, i64, vp, vp]
         lib.rpfq_wide_linear_scaled.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, vp, i32, i32, vp]
+        lib.rpfq_wide_mlp.argtypes = [dp, vp, sz, dp, vp, sz, vp, i64, vp, vp, vp, vp, vp]
         for name in EXPORTED[2:]:
             if name not in ("rpfq_wide_packed_bytes", "rpfq_wide_adjoint_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32

@@ -588,6 +588,60 @@ def make_desc(n_complex, k_complex, codebook, stages, block, rotation) -> N.Wide
     return d
 
 
+def mlp_fusable(fc1, fc2, m: int, dtype: torch.dtype) -> bool:
+    """Whether wide_mlp() takes fc1 -> GELU -> fc2 as one launch: single-group
+    packed layers (PackedWide) with K' = 96, N1' a multiple of 96 up to
+    1536, fc2 the inverse shape, per-row scales and one codebook, fp16
+    activations, m >= 64 rows (the shapes rpfq_wide_mlp accepts)."""
+    return (isinstance(fc1, PackedWide) and isinstance(fc2, PackedWide) and dtype == torch.float16 and m >= 64
+            and fc1.k_complex == 96 and fc1.n_complex % 96 == 0 and fc1.n_complex <= 1536
+            and fc2.k_complex == fc1.n_complex and fc2.n_complex == fc1.k_complex and fc1.block == 0
+            and fc2.block == 0 and fc1.codebook == fc2.codebook)
+
+
+def wide_mlp(fc1: "PackedWide", fc2: "PackedWide", x: torch.Tensor, bias1: torch.Tensor | None = None,
+             bias2: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """residual + fc2(GELU(fc1(x) + bias1)) + bias2 on fp16 [..., 2K'] in one
+    launch (rpfq_wide_mlp): the hidden activations stay in LDS, each the fp16
+    rounding of fc1's output passed through the stores' GELU (within 1 ulp of
+    the exact GELU), so y equals fc1.linear(x, bias1, gelu=True) followed by
+    fc2.linear(h, bias2, residual=residual) on the large-M kernel bit for
+    bit."""
+    N.require_device(x, bias1, bias2, residual)
+    if x.dtype != torch.float16:
+        raise ValueError("wide_mlp takes fp16 activations")
+    if x.shape[-1] != fc1.in_features:
+        raise ValueError(f"expected last dim {fc1.in_features}, got {x.shape[-1]}")
+    lead = x.shape[:-1]
+    x2 = _aligned_rows(x.reshape(-1, fc1.in_features))
+    m = x2.shape[0]
+    if not mlp_fusable(fc1, fc2, m, x.dtype):
+        raise ValueError("wide_mlp: unsupported layers or row count (see mlp_fusable)")
+    y = torch.empty(m, fc2.out_features, dtype=torch.float16, device=x.device)
+    r2 = None
+    if residual is not None:
+        if residual.shape[:-1] != lead or residual.shape[-1] != fc2.out_features:
+            raise ValueError(f"residual must have shape {tuple(lead) + (fc2.out_features,)}")
+        r2 = _aligned_rows(residual.to(torch.float16).reshape(-1, fc2.out_features))
+    b1 = None if bias1 is None else bias1.contiguous().float()
+    b2 = None if bias2 is None else bias2.contiguous().float()
+    rec = _launch_recorder
+    if rec is not None:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    N.check("rpfq_wide_mlp", N.load().rpfq_wide_mlp(
+        ctypes.byref(fc1.desc), fc1.blob.data_ptr(), fc1.blob.numel(), ctypes.byref(fc2.desc), fc2.blob.data_ptr(),
+        fc2.blob.numel(), x2.data_ptr(), m, N.ptr(b1), N.ptr(b2), N.ptr(r2), y.data_ptr(), N.stream_of(x2)))
+    if rec is not None:
+        ev1.record()
+        n1, k = fc1.n_complex, fc1.k_complex
+        nbytes = (wide_bytes(m, n1, k) + wide_bytes(m, k, n1) - 2 * m * 2 * n1 * 2
+                  + (m * 2 * k * 2 if residual is not None else 0))
+        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "mlp"))
+    return y.reshape(*lead, fc2.out_features)
+
+
 def wide_flops(m: int, n_complex: int, k_complex: int) -> int:
     """Algorithmic FLOPs of one widely-linear layer (one real GEMM)."""
     return 2 * m * (2 * k_complex) * (2 * n_complex)

@@ -688,6 +688,17 @@ class QATLinearComplexPhase(nn.Linear):
         m = x.numel() // x.shape[-1] if x.dim() else 0
         return FUSE_AQ_PROLOGUE and hasattr(pw, "ln_fusable") and m > 0 and pw.ln_fusable(m, x.dtype)
 
+    def packed_inference(self, x: torch.Tensor):
+        """The packed layer (ops.PackedWide or a stage-group container) the
+        inference path would contract x with when that path applies without
+        an activation quantizer (eval mode, device tensors, no autograd
+        recording), else None: what a caller fusing this layer with its
+        neighbours (ops.wide_mlp) may use in its place."""
+        if self.act_quantizer is not None or not (x.is_cuda and not self.training and self.use_packed) \
+                or self._records_grad(x):
+            return None
+        return self.packed(x.device)
+
     def packed_act_bits(self, x: torch.Tensor) -> int:
         """Bits of the activation quantization the packed inference path would
         apply to x (0 if none, if x does not take the packed path, or if

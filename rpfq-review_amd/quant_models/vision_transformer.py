@@ -30,6 +30,10 @@ FUSE_ACT_QUANT = os.environ.get("RPFQ_FUSE_AQ", "1") != "0"
 # Within the fused path, the MLP's exact GELU runs in fc1's store when fc1 is
 # a packed phase-quantized Linear (rpfq_wide_linear with RPFQ_FLAG_GELU).
 FUSE_GELU = os.environ.get("RPFQ_FUSE_GELU", "1") != "0"
+# Within the fused path, fc1 -> GELU -> fc2 (+ the residual) as one launch
+# with the hidden activations on chip (ops.wide_mlp) where both layers are
+# packed and the shapes fit it (DeiT-Ti, Swin-T stage 1: K' = 96).
+FUSE_MLP = os.environ.get("RPFQ_FUSE_MLP", "1") != "0"
 # LayerNorm in the following packed layer's launch (norm1 -> qkv, norm2 ->
 # fc1) where that layer streams: a block at batch 1-2.  RPFQ_FUSE_LN=0 keeps
 # the LayerNorm kernel.
@@ -166,7 +170,12 @@ class Mlp(nn.Module):
         already activation-quantized for fc1 if prequantized.  When fc2
         quantizes its input, the GELU and that quantization run as one pass
         over fc1's output instead (rpfq_gelu_act_quant, float32 GELU
-        quantized without rounding in between)."""
+        quantized without rounding in between).  Where both layers are packed
+        and fit rpfq_wide_mlp, the whole MLP and the add are one launch."""
+        if not prequantized:
+            y = self._wide_mlp(x, residual)
+            if y is not None:
+                return y
         gelu_exact = type(self.act) is nn.GELU and self.act.approximate == "none"
         bits = self._gelu_act_quant_bits(x)
         if bits:
@@ -180,6 +189,31 @@ class Mlp(nn.Module):
         else:
             h = self.act(call_layer(self.fc1, x, prequantized))
         return self.forward_hidden_residual(h, residual)
+
+    def _wide_mlp(self, x, residual):
+        """residual + fc2(GELU(fc1(x))) as one packed launch (ops.wide_mlp:
+        the hidden activations stay on chip, the GELU as in the packed
+        stores, within 1 ulp of the exact GELU), or None where that does not
+        apply: fusion off, another activation, no packed inference path on
+        either layer (training, autograd, activation quantization), or
+        shapes the kernel does not take."""
+        if not (FUSE_MLP and FUSE_GELU and type(self.act) is nn.GELU and self.act.approximate == "none"
+                and type(self.norm) is nn.Identity and x.dtype == torch.float16 and x.is_cuda):
+            return None
+        inf1 = getattr(self.fc1, "packed_inference", None)
+        inf2 = getattr(self.fc2, "packed_inference", None)
+        if inf1 is None or inf2 is None:
+            return None
+        p1, p2 = inf1(x), inf2(x)
+        if p1 is None or p2 is None:
+            return None
+        from . import ops
+
+        if not ops.mlp_fusable(p1, p2, x.numel() // x.shape[-1], x.dtype):
+            return None
+        b1 = None if self.fc1.bias is None else self.fc1.bias.detach()
+        b2 = None if self.fc2.bias is None else self.fc2.bias.detach()
+        return ops.wide_mlp(p1, p2, x, b1, b2, residual)
 
     def _gelu_act_quant_bits(self, x) -> int:
         """Bits of fc2's activation quantization when the exact GELU and that

@@ -387,6 +387,36 @@ def test_wide_linear_resident_choice():
     assert b"N' <= 96" in L.rpfq_last_error()
 
 
+def test_wide_mlp_argument_errors():
+    """rpfq_wide_mlp's host checks, all before any HIP call: NULL operands,
+    fc2 not the inverse shape of fc1, the fused shapes (K' = 96, N1' a
+    multiple of 96 up to 1536, block = 0, one codebook, M >= 64), short
+    blobs and misaligned rows."""
+    L, N = lib()
+    p, y = ctypes.c_void_p(256), ctypes.c_void_p(512)
+    fc1, fc2 = _desc(N, n=384, k=96), _desc(N, n=96, k=384)
+    big = 1 << 24
+
+    def mlp(d1, d2, m=12672, x=p, out=y, res=None, n1=big, n2=big, p1=p, p2=p):
+        return L.rpfq_wide_mlp(ctypes.byref(d1), p1, n1, ctypes.byref(d2), p2, n2, x, m, None, None, res, out, None)
+
+    assert mlp(fc1, fc2, x=None) == 1
+    assert mlp(fc1, fc2, p2=None) == 1
+    assert mlp(fc1, fc2, out=None) == 1
+    assert mlp(fc1, _desc(N, n=96, k=288)) == 2 and b"invert" in L.rpfq_last_error()
+    assert mlp(_desc(N, n=384, k=192), _desc(N, n=192, k=384)) == 2 and b"K'=96" in L.rpfq_last_error()
+    assert mlp(_desc(N, n=400, k=96), _desc(N, n=96, k=400)) == 2      # N1' % 96
+    assert mlp(_desc(N, n=1632, k=96), _desc(N, n=96, k=1632)) == 2    # N1' > 1536
+    assert mlp(_desc(N, n=384, k=96, block=64), fc2) == 2                # per-block scales
+    assert mlp(fc1, _desc(N, n=96, k=384, cb=N.CB_SIGN)) == 2           # two codebooks
+    assert mlp(fc1, fc2, m=63) == 2
+    assert mlp(fc1, fc2, m=0) == 2
+    assert mlp(fc1, fc2, n1=1024) == 2                                   # short blob
+    assert mlp(fc1, fc2, x=ctypes.c_void_p(264)) == 3
+    assert mlp(fc1, fc2, res=ctypes.c_void_p(520)) == 3
+    assert mlp(fc1, fc2, p1=ctypes.c_void_p(384)) == 3
+
+
 def test_wide_grad_x_geometry_and_argument_errors():
     """rpfq_wide_adjoint_bytes is one 1 KiB code tile per (32-row tile,
     k-step) plus a 128-B U / W table per (row, scale block) of the padded

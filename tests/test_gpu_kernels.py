@@ -950,6 +950,111 @@ def test_wide_linear_resident_range_guard():
     assert np.all(y[mags == 0] == 0.0)
 
 
+
+# ---------------------------------------------------------------------------
+# fused MLP (rpfq_wide_mlp): fc1 -> GELU -> fc2 (+ residual) in one launch,
+# equal bit for bit to the two large-M launches it replaces
+# ---------------------------------------------------------------------------
+MLP_CASES = [
+    # (N1', codebook, stages, rotation): fc1 96 -> N1', fc2 N1' -> 96
+    (384, "axis", 2, None),                                   # DeiT-Ti / Swin-T stage 1
+    (768, "sign", 2, ((0.8, 0.6), (0.6, -0.8))),              # 8 chunks, sign codes, rotation
+    (192, "psk16", 1, None),                                  # 16-PSK, 2 chunks
+    (96, "table", 1, None),                                   # per-row tables, 1 chunk
+    (1536, "axis", 1, None),                                  # the largest N1' (16 chunks)
+]
+MLP_IDS = [f"{c[0]}-{c[1]}{c[2]}-r{int(c[3] is not None)}" for c in MLP_CASES]
+
+
+def _mlp_layers(r, case):
+    n1, codebook, stages, rot = case
+    p1, *_ = build_packed(r, (n1, 96, codebook, stages, 0, rot))
+    p2, *_ = build_packed(r, (96, n1, codebook, stages, 0, rot))
+    return p1, p2
+
+
+def _two_launches(p1, p2, x, b1, b2, res):
+    """fc1 with the fused GELU, then fc2 with the residual, both on the LDS-DMA
+    kernel (RPFQ_FLAG_NO_STREAM at >= 128 rows); x padded to 128 rows (its
+    first rows repeated) where it has fewer, the rows being independent."""
+    _, N = qm()
+    m = x.shape[0]
+    xp, rp = x, res
+    if m < 128:
+        idx = torch.arange(128, device=x.device) % m
+        xp = x[idx]
+        rp = None if res is None else res[idx]
+    assert p1.kernel_for(xp.shape[0], torch.float16, torch.float16, N.FLAG_NO_STREAM | N.FLAG_GELU) == N.KERNEL_DMA
+    assert p2.kernel_for(xp.shape[0], torch.float16, torch.float16, N.FLAG_NO_STREAM) == N.KERNEL_DMA
+    h = p1.linear(xp, b1, out_dtype=torch.float16, flags=N.FLAG_NO_STREAM, gelu=True)
+    y = p2.linear(h, b2, out_dtype=torch.float16, flags=N.FLAG_NO_STREAM, residual=rp)
+    return y[:m]
+
+
+@pytest.mark.parametrize("m", [64, 100, 128, 300, 12672], ids=["m64", "m100", "m128", "m300", "m12672"])
+@pytest.mark.parametrize("case", MLP_CASES, ids=MLP_IDS)
+def test_wide_mlp_matches_two_launches(case, m):
+    """rpfq_wide_mlp against fc1 (RPFQ_FLAG_GELU) and fc2 (with the residual)
+    launched separately on the large-M kernel, bit for bit: five codebook /
+    rotation / width cases (1-16 chunks of fc1 outputs), M = 64 (one tile),
+    100 and 300 (the last tile shifted back over the previous one), 128 and
+    12,672 (DeiT-Ti at batch 64), with biases and residual, without either,
+    and in place (residual == y through the C ABI)."""
+    import ctypes
+
+    ops, N = qm()
+    r = rng(3500 + case[0] + m)
+    p1, p2 = _mlp_layers(r, case)
+    g = torch.Generator(device=DEV).manual_seed(3501 + m)
+    x = torch.randn(m, 192, device=DEV, generator=g).half()
+    b1 = torch.randn(2 * case[0], device=DEV, generator=g)
+    b2 = torch.randn(192, device=DEV, generator=g)
+    res = (torch.randn(m, 192, device=DEV, generator=g) * 4).half()
+    assert ops.mlp_fusable(p1, p2, m, torch.float16)
+    want = _two_launches(p1, p2, x, b1, b2, res)
+    got = ops.wide_mlp(p1, p2, x, b1, b2, res)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
+    assert torch.equal(ops.wide_mlp(p1, p2, x), _two_launches(p1, p2, x, None, None, None))
+    yi = res.clone()
+    N.check("rpfq_wide_mlp", N.load().rpfq_wide_mlp(
+        ctypes.byref(p1.desc), p1.blob.data_ptr(), p1.blob.numel(), ctypes.byref(p2.desc), p2.blob.data_ptr(),
+        p2.blob.numel(), x.data_ptr(), m, b1.data_ptr(), b2.data_ptr(), yi.data_ptr(), yi.data_ptr(),
+        N.stream_of(x)))
+    torch.cuda.synchronize()
+    assert torch.equal(yi, want)
+
+
+def test_wide_mlp_against_oracle():
+    """The fused MLP against the oracle in float64 on the fp16 operands it
+    contracts (DeiT-Ti's fc1 / fc2, axis codes, 300 rows): the hidden values
+    GELU(fp16(x A1^T + b1)) within fc1's fp16 rounding and the GELU's 1 ulp,
+    y within that propagated through fc2 plus fc2's own float32 accumulation
+    and fp16 output rounding."""
+    import math
+
+    ops, N = qm()
+    r = rng(3600)
+    n1, m = 384, 300
+    p1, o1, _, cb, rot = build_packed(r, (n1, 96, "axis", 2, 0, None))
+    p2, o2, _, _, _ = build_packed(r, (96, n1, "axis", 2, 0, None))
+    x = torch.from_numpy(r.standard_normal((m, 192)).astype(np.float32)).half()
+    b1 = r.standard_normal(2 * n1).astype(np.float32)
+    b2 = r.standard_normal(192).astype(np.float32)
+    y = ops.wide_mlp(p1, p2, x.to(DEV), tdev(b1), tdev(b2)).double().cpu().numpy()
+    a1 = O.wide_weight(o1, cb, rot, fp16=True).astype(np.float64)
+    a2 = O.wide_weight(o2, cb, rot, fp16=True).astype(np.float64)
+    xf = x.double().numpy()
+    pre = xf @ a1.T + b1
+    erf = np.vectorize(math.erf)
+    h = pre * 0.5 * (1.0 + erf(pre / math.sqrt(2.0)))
+    # |GELU'| <= 1.13: fc1's error (float32 sum + fp16 rounding) and the GELU's ulp carry into h
+    hs = np.abs(xf) @ np.abs(a1).T + np.abs(b1)
+    dh = 1.13 * (1e-5 * hs + 2.0 ** -11 * np.abs(pre)) + 2.0 ** -10 * np.abs(h) + 1e-7
+    ref = h @ a2.T + b2
+    tol = np.abs(dh) @ np.abs(a2).T + 1e-5 * (np.abs(h) @ np.abs(a2).T + np.abs(b2)) + 2.0 ** -10 * np.abs(ref)
+    assert np.all(np.abs(y - ref) <= tol + 1e-4)
+
 # ---------------------------------------------------------------------------
 # fused residual add (rpfq_wide_linear_residual): bit-identical to the layer
 # followed by the add in y's dtype, on every kernel path

@@ -911,6 +911,59 @@ def test_fused_gelu_wiring(name, dt, batch):
     assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
 
 
+@pytest.mark.parametrize("name,batch,want", [("rpfq_deit_tiny_patch16_224_q", 16, 12),
+                                             ("rpfq_swin_tiny_patch4_window7_224_q", 4, 2)])
+def test_fused_mlp_wiring(name, batch, want):
+    """The fused block path runs fc1 -> GELU -> fc2 (+ the residual) as one
+    rpfq_wide_mlp launch where both layers fit it (DeiT-Ti: all 12 blocks;
+    Swin-T: the two stage-1 blocks, K' = 96): counted, and the logits within
+    LOGIT_TOL * max|logit| + LOGIT_TOL / 10 of the same model with that
+    fusion off (fc1, torch's exact GELU, fc2: the fused GELU is within 1 ulp
+    of it), identical top-1 on margin-confident samples.  A hidden chunk
+    dropped or the GELU skipped moves them by orders of magnitude more."""
+    import quant_models as qm
+    from quant_models import ops
+    from quant_models import vision_transformer as vt
+    from quant_models.inference import load_synthetic_codes, prepare_inference
+
+    torch.manual_seed(21)
+    model = qm.create_model(name, img_size=224, quant_method_u="complex_phase_v2",
+                            quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    load_synthetic_codes(model, 21)
+    prepare_inference(model, DEV, torch.float16)
+    x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(22)).to(DEV, torch.float16)
+    calls = []
+    mlp = ops.wide_mlp
+
+    def counting(*args, **kw):
+        calls.append(1)
+        return mlp(*args, **kw)
+    saved = vt.FUSED_BLOCKS, vt.FUSE_MLP
+    try:
+        ops.wide_mlp = counting
+        with torch.no_grad():
+            vt.FUSED_BLOCKS, vt.FUSE_MLP = True, True
+            y_f = model(x)
+            n_fused = len(calls)
+            vt.FUSE_MLP = False
+            y_u = model(x)
+    finally:
+        ops.wide_mlp = mlp
+        vt.FUSED_BLOCKS, vt.FUSE_MLP = saved
+    assert n_fused == want, n_fused
+    assert len(calls) == n_fused
+    assert torch.isfinite(y_f).all()
+    y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
+    err = float((y_f - y_u).abs().max())
+    tol = LOGIT_TOL["fp16"]
+    print(f"{name} bs{batch}: fused MLP vs two launches max|dlogit| {err:.4g} (max|logit| "
+          f"{float(y_u.abs().max()):.3g}), {n_fused} fused launches")
+    assert err <= tol * float(y_u.abs().max()) + tol / 10
+    top = y_u.topk(2, dim=1).values
+    confident = (top[:, 0] - top[:, 1]) > 4 * err
+    assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
+
+
 @pytest.mark.parametrize("name,dt", [("rpfq_vit_base_patch16_224_q", "fp16"), ("rpfq_vit_base_patch16_224_q", "bf16"),
                                      ("rpfq_deit_tiny_patch16_224_q", "fp16"),
                                      ("rpfq_swin_tiny_patch4_window7_224_q", "fp16")])
