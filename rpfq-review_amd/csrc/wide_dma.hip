@@ -258,6 +258,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     const uint32_t srow = scaled ? lds_addr(xs_lds + xb * BM + RPW * wave) : 0u;
     if (vb == (int)blockIdx.x) {  // later tiles had these requested before the previous epilogue
         issue_codes(0, 0);
+        if (a.KS > 1) issue_codes(1, 1);
         issue_x(0, 2);
         issue_params(vb);
         issue_xs(vb, xb);
@@ -292,14 +293,18 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
-    // One k-step on stage `st`: first the codes of k-step ks + 1 and the
-    // activations of ks + 2 (into the buffers read at ks - 1, free since the
-    // last barrier), then the math.  The loop below is unrolled by 3 so stage
-    // offsets are static.
+    // One k-step on stage `st`: the lane's codes of k-step ks into
+    // registers, which frees their buffer for the codes of ks + 2; then the
+    // codes and activations of ks + 2 (the activation stage read at ks - 1,
+    // free since the last barrier), so both arrive two k-steps ahead; then
+    // the math.  The loop below is unrolled by 3 so stage offsets are static.
     auto kstep = [&](int ks, int st) {
-        if (ks + 1 < a.KS) issue_codes(ks + 1, (ks + 1) & 1);
-        if (ks + 2 < a.KS) issue_x(ks + 2, st == 0 ? 2 : st - 1);
         const uint4 cw = read_codes(ks & 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // cw landed: its buffer takes k-step ks + 2
+        if (ks + 2 < a.KS) {
+            issue_codes(ks + 2, ks & 1);
+            issue_x(ks + 2, st == 0 ? 2 : st - 1);
+        }
         const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
         auto read_sub = [&](int s, uint32_t (&U)[4], uint32_t (&W)[4], half8 (&ax)[MB]) {
             const uint32_t word = words[s];
@@ -381,7 +386,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                         else
                             asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
                     } else {
-                        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+                        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                     }
                     stage_to_f16<XDT, RPW>(lds_stages + (st == 2 ? 0 : st + 1) * kDmaStage, lane, srow);
                 }
@@ -396,15 +401,15 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                 cur_blk = nb;
             }
         }
-        // codes ks + 1 and stage ks + 1 landed: only the newest RPW / 8 loads
-        // (activations of ks + 2) may still be in flight; every LDS read of
-        // this k-step is complete.  Near the end nothing is prefetched, so
-        // everything must land.
+        // codes ks + 1 and stage ks + 1 landed: only the newest 1 + RPW / 8
+        // loads (codes and activations of ks + 2) may still be in flight;
+        // every LDS read of this k-step is complete.  Near the end nothing is
+        // prefetched, so everything must land.
         if (ks + 2 < a.KS) {
             if (RPW == 32)
-                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
+                asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)" ::: "memory");
             else
-                asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+                asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)" ::: "memory");
         } else
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -423,6 +428,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     if (vb + (int)gridDim.x < total) {
         tile_src(vb + (int)gridDim.x);
         issue_codes(0, 0);
+        if (a.KS > 1) issue_codes(1, 1);
         issue_x(0, 2);
         issue_params(vb + (int)gridDim.x);
         issue_xs(vb + (int)gridDim.x, xb ^ 1);
