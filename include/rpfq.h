@@ -250,6 +250,24 @@ int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packe
                   void* stream);
 
 /*
+ * rpfq_wide_mlp with the block's LayerNorm before fc1 and x itself as the
+ * residual, one launch:
+ *   y = x + fc2(GELU(fc1(LayerNorm(x)) + bias1)) + bias2
+ * The normalized rows are the bits rpfq_layer_norm(x, M, 2K', gamma, beta,
+ * eps) writes in fp16 (same arithmetic and summation order for this M), so
+ * y equals rpfq_layer_norm followed by rpfq_wide_mlp(residual = x) bit for
+ * bit.  gamma / beta: float32 [2K'], 16-byte aligned, or NULL (ones /
+ * zeros); eps >= 0 (else RPFQ_ERR_VALUE); y may be x.  Shapes and the other
+ * arguments as rpfq_wide_mlp.  Replaces
+ *   norm2 -> mlp.fc1 -> mlp.act -> mlp.fc2 -> + residual1
+ *   RPFQ-ViTApple/scripts/audit_rpfq_vit_ios_parity.py:548-556.
+ */
+int rpfq_layer_norm_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                             const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
+                             int64_t M, const float* gamma, const float* beta, float eps, const float* bias1,
+                             const float* bias2, void* y, void* stream);
+
+/*
  * Per-row prescales of x [M, C] for rpfq_wide_linear_scaled (the forward's
  * range guard): scale[m] = 2^(14 - floor(log2 max_k |x[m, k]|)), clamped to
  * [2^-126, 2^126], so the row's largest element times scale[m] lies in

@@ -302,10 +302,11 @@ int rpfq_wide_linear_residual(const rpfq_wide_desc* desc, const void* packed, si
 }
 
 
-int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
-                  const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
-                  int64_t M, const float* bias1, const float* bias2, const void* residual, void* y,
-                  void* stream) {
+namespace {
+int mlp_checked(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x, int64_t M,
+                const float* bias1, const float* bias2, const void* residual, void* y, void* stream,
+                const float* gamma, const float* beta, float eps, const char* fn) {
     int rc = check_desc(desc1);
     if (rc) return rc;
     if ((rc = check_desc(desc2))) return rc;
@@ -317,9 +318,9 @@ int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packe
                     (long long)g2.N, (long long)g1.K, (long long)g1.N);
     if (!rpfq::wide_mlp_shape(g1, g2, desc1->codebook, desc2->codebook, M))
         return fail(RPFQ_ERR_SHAPE,
-                    "rpfq_wide_mlp takes K'=96, N1' a multiple of 96 up to 1536, block=0 on both layers, one "
+                    "%s takes K'=96, N1' a multiple of 96 up to 1536, block=0 on both layers, one "
                     "codebook and M >= 64 (K'=%lld N1'=%lld M=%lld)",
-                    (long long)g1.K, (long long)g1.N, (long long)M);
+                    fn, (long long)g1.K, (long long)g1.N, (long long)M);
     if (packed1_bytes < g1.total_bytes || packed2_bytes < g2.total_bytes)
         return fail(RPFQ_ERR_SHAPE, "packed buffers hold %zu / %zu bytes, need %zu / %zu", packed1_bytes,
                     packed2_bytes, g1.total_bytes, g2.total_bytes);
@@ -327,8 +328,29 @@ int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packe
         (residual && !aligned(residual, 16)))
         return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x, y and residual 16-byte aligned");
     return hip_status(rpfq::launch_wide_mlp_layers(*desc1, g1, packed1, *desc2, g2, packed2, x, M, bias1, bias2,
-                                                   residual, y, reinterpret_cast<hipStream_t>(stream)),
-                      "rpfq_wide_mlp");
+                                                   residual, y, reinterpret_cast<hipStream_t>(stream), gamma, beta,
+                                                   eps),
+                      fn);
+}
+}  // namespace
+
+int rpfq_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                  const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
+                  int64_t M, const float* bias1, const float* bias2, const void* residual, void* y,
+                  void* stream) {
+    return mlp_checked(desc1, packed1, packed1_bytes, desc2, packed2, packed2_bytes, x, M, bias1, bias2, residual, y,
+                       stream, nullptr, nullptr, -1.0f, "rpfq_wide_mlp");
+}
+
+int rpfq_layer_norm_wide_mlp(const rpfq_wide_desc* desc1, const void* packed1, size_t packed1_bytes,
+                             const rpfq_wide_desc* desc2, const void* packed2, size_t packed2_bytes, const void* x,
+                             int64_t M, const float* gamma, const float* beta, float eps, const float* bias1,
+                             const float* bias2, void* y, void* stream) {
+    if (!(eps >= 0.0f)) return fail(RPFQ_ERR_VALUE, "eps=%g must be >= 0", (double)eps);
+    if ((gamma && !aligned(gamma, 16)) || (beta && !aligned(beta, 16)))
+        return fail(RPFQ_ERR_ALIGN, "gamma and beta must be 16-byte aligned");
+    return mlp_checked(desc1, packed1, packed1_bytes, desc2, packed2, packed2_bytes, x, M, bias1, bias2, x, y, stream,
+                       gamma, beta, eps, "rpfq_layer_norm_wide_mlp");
 }
 
 int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes, const void* x,

@@ -420,6 +420,22 @@ __device__ __forceinline__ float row_prescale(float mx) {
 // 1 / s for a prescale s (a power of two in [2^-126, 2^126]): exact.
 __device__ __forceinline__ float row_unscale(float s) { return 1.0f / s; }
 
+// Sum / maximum over the TPR consecutive lanes of a row group (a butterfly:
+// every lane of the group ends with the same value).
+template <int TPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 // LDS address-space views and the LDS byte address of a shared pointer.
 typedef __attribute__((address_space(3))) const uint32_t* lds_u32_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

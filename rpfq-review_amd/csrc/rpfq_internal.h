@@ -173,6 +173,12 @@ struct MlpArgs {
     const void* res;     // [M, 2 K'] fp16 or NULL (may be y)
     void* y;             // [M, 2 K'] fp16
     int tiles;           // row tiles (set by the launcher)
+    // LayerNorm of x's rows before fc1 (ln = the row kernel's lanes per row
+    // for this M, ln_row_lanes: 8 or 64; 0 = none), in that kernel's order
+    int ln;
+    float ln_eps;
+    const float* ln_gamma;  // [2 K'] or NULL (ones)
+    const float* ln_beta;   // [2 K'] or NULL (zeros)
 };
 template <int CB> hipError_t launch_wide_mlp(const MlpArgs& a, hipStream_t s);
 // The fused MLP's shapes: K' = 96 (three waves), N1' a multiple of 96 up
@@ -181,7 +187,8 @@ bool wide_mlp_shape(const WideGeom& g1, const WideGeom& g2, int cb1, int cb2, in
 hipError_t launch_wide_mlp_layers(const rpfq_wide_desc& d1, const WideGeom& g1, const void* packed1,
                                   const rpfq_wide_desc& d2, const WideGeom& g2, const void* packed2, const void* x,
                                   int64_t M, const float* bias1, const float* bias2, const void* res, void* y,
-                                  hipStream_t s);
+                                  hipStream_t s, const float* ln_gamma = nullptr, const float* ln_beta = nullptr,
+                                  float ln_eps = -1.0f);
 
 // Resident-weight kernel (wide_resident.hip): one workgroup of kResWaves
 // waves per CU holds the whole decoded layer in LDS (2N' x 2K' fp16 as MFMA

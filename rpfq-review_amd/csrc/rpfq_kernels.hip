@@ -550,19 +550,6 @@ __device__ __forceinline__ void store8_ln(void* base, int64_t off, const float* 
     }
 }
 
-template <int TPR>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-template <int TPR>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = TPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
 // Row kernel for LayerNorm and / or activation fake quantization.
 // LN: y = (x - mean) / sqrt(var + eps) * gamma + beta (nn.LayerNorm);

@@ -212,7 +212,7 @@ bool wide_mlp_shape(const WideGeom& g1, const WideGeom& g2, int cb1, int cb2, in
 hipError_t launch_wide_mlp_layers(const rpfq_wide_desc& d1, const WideGeom& g1, const void* packed1,
                                   const rpfq_wide_desc& d2, const WideGeom& g2, const void* packed2, const void* x,
                                   int64_t M, const float* bias1, const float* bias2, const void* res, void* y,
-                                  hipStream_t s) {
+                                  hipStream_t s, const float* ln_gamma, const float* ln_beta, float ln_eps) {
     if (!wide_mlp_shape(g1, g2, d1.codebook, d2.codebook, M)) return hipErrorInvalidValue;
     MlpArgs a = {};
     a.x = x;
@@ -229,6 +229,12 @@ hipError_t launch_wide_mlp_layers(const rpfq_wide_desc& d1, const WideGeom& g1, 
     a.bias2 = bias2;
     a.res = res;
     a.y = y;
+    if (ln_eps >= 0.0f) {  // as rpfq_layer_norm would normalize these M rows
+        a.ln = ln_row_lanes(M, 2 * g1.K);
+        a.ln_eps = ln_eps;
+        a.ln_gamma = ln_gamma;
+        a.ln_beta = ln_beta;
+    }
     switch (d1.codebook) {
         case RPFQ_CB_SIGN: return launch_wide_mlp<RPFQ_CB_SIGN>(a, s);
         case RPFQ_CB_PSK16: return launch_wide_mlp<RPFQ_CB_PSK16>(a, s);

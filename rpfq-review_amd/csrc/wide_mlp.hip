@@ -17,7 +17,8 @@ namespace rpfq {
 //   * x's tile goes to LDS once by DMA (k-step w by wave w), in the LDS
 //     activation layout of the DMA kernel: a row of a k-step is 8 chunks of
 //     16 B (re columns 0-7 .. 24-31, then im), chunk c at slot c ^ ((row >> 1)
-//     & 7);
+//     & 7); optionally the block's LayerNorm of those rows follows, in place
+//     (mlp_layer_norm: the row kernel's bits);
 //   * fc1 runs in chunks of 32 NW complex outputs: wave w computes outputs
 //     32 w .. 32 w + 31 of the chunk for all 64 rows, adds the bias, rounds
 //     to fp16 and applies the GELU of the rounded value (as the GEMM stores
@@ -77,7 +78,86 @@ __device__ __forceinline__ void mlp_build_lut(uint32_t* lut, int slot, float4 pu
     }
 }
 
-template <int CB, int NW>
+// LayerNorm of the tile's rows in place in LDS (fp16 in, fp16 out), with
+// TPR lanes per row in the row kernel's arithmetic (layer_norm_kernel: lane
+// sub of a row holds the 8-feature chunks sub, sub + TPR, ..., sums them in
+// that order, then a butterfly over the row's lanes; mean and variance in
+// float32; ((x - mean) * rstd) * gamma + beta rounded once), so the rows
+// are the bits rpfq_layer_norm writes for the same M.  Feature chunk c of
+// [re | im] (K' re features, then K' im) sits at k-step (c mod K'/8) / 4,
+// LDS chunk (c mod 4) (+4 for im) of the row.
+template <int TPR, int NW>
+__device__ __forceinline__ void mlp_layer_norm(uint32_t lds_x, const MlpArgs& a, int wave, int lane) {
+    constexpr int RPP = 64 / TPR;  // rows per wave and pass
+    const int K = a.K, nch = K / 4, nre = K / 8;
+    constexpr int NC = TPR == 8 ? 4 : 1;  // chunks per lane (K' <= 128)
+    const float C = (float)(2 * K);
+    const int sub = lane % TPR;
+    for (int r0 = wave * RPP; r0 < kMlpBM; r0 += NW * RPP) {
+        const int row = r0 + lane / TPR;
+        const uint32_t swz = (uint32_t)((row >> 1) & 7);
+        uint32_t addr[NC];
+        float v[NC][8];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = sub + TPR * j;
+            const int cc = c < nre ? c : c - nre;
+            const uint32_t q = (uint32_t)((cc & 3) + (c < nre ? 0 : 4));
+            addr[j] = lds_x + (uint32_t)(cc >> 2) * kMlpStage + (uint32_t)row * 128u + ((q ^ swz) * 16u);
+            if (c < nch) {
+                const u32x4 u = *reinterpret_cast<__attribute__((address_space(3))) const u32x4*>(addr[j]);
+                const uint32_t w[4] = {u[0], u[1], u[2], u[3]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const half2v h = __builtin_bit_cast(half2v, w[i]);
+                    v[j][2 * i] = (float)h.x;
+                    v[j][2 * i + 1] = (float)h.y;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
+            }
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+            if (sub + TPR * j < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s += v[j][e];
+            }
+        const float mean = group_sum<TPR>(s) / C;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+            if (sub + TPR * j < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = v[j][e] - mean;
+                    s2 += d * d;
+                }
+            }
+        const float rstd = 1.0f / sqrtf(group_sum<TPR>(s2) / C + a.ln_eps);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = sub + TPR * j;
+            if (c < nch) {
+                float gk[8], bk[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    gk[e] = a.ln_gamma ? a.ln_gamma[8 * c + e] : 1.0f;
+                    bk[e] = a.ln_beta ? a.ln_beta[8 * c + e] : 0.0f;
+                }
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (v[j][e] - mean) * rstd * gk[e] + bk[e];
+                *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(addr[j]) =
+                    (u32x4){cvt_pk(o[0], o[1]), cvt_pk(o[2], o[3]), cvt_pk(o[4], o[5]), cvt_pk(o[6], o[7])};
+            }
+        }
+    }
+}
+
+template <int CB, int NW, int LN>
 __global__ void __launch_bounds__(64 * NW, 2) wide_mlp_kernel(MlpArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int MB = kMlpMB;
@@ -223,6 +303,12 @@ __global__ void __launch_bounds__(64 * NW, 2) wide_mlp_kernel(MlpArgs a) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if constexpr (LN != 0) {  // normalize the rows in place; fc1 reads them after the barrier
+        mlp_layer_norm<LN, NW>(lds_x, a, wave, lane);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
 
     floatx16 acc2_re[MB], acc2_im[MB];
 #pragma unroll
@@ -310,14 +396,14 @@ __global__ void __launch_bounds__(64 * NW, 2) wide_mlp_kernel(MlpArgs a) {
     }
 }
 
-template <int CB, int NW>
+template <int CB, int NW, int LN>
 static hipError_t mlp_go(const MlpArgs& a, hipStream_t s) {
     static std::atomic<uint64_t> attr_done{0};
-    const void* kern = reinterpret_cast<const void*>(&wide_mlp_kernel<CB, NW>);
+    const void* kern = reinterpret_cast<const void*>(&wide_mlp_kernel<CB, NW, LN>);
     const int lds = mlp_lds(NW, a.N1);
     hipError_t e = set_lds_attr_once(kern, mlp_lds(NW, kMlpMaxN1), attr_done);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((wide_mlp_kernel<CB, NW>), dim3((unsigned)a.tiles), dim3(64 * NW), lds, s, a);
+    hipLaunchKernelGGL((wide_mlp_kernel<CB, NW, LN>), dim3((unsigned)a.tiles), dim3(64 * NW), lds, s, a);
     return hipGetLastError();
 }
 
@@ -325,8 +411,13 @@ template <int CB>
 hipError_t launch_wide_mlp(const MlpArgs& args, hipStream_t s) {
     MlpArgs a = args;
     a.tiles = (int)((a.M + kMlpBM - 1) / kMlpBM);
-    if (a.K == 96 && a.N1 % 96 == 0 && a.N1 <= kMlpMaxN1 && a.M >= kMlpBM) return mlp_go<CB, 3>(a, s);
-    return hipErrorInvalidValue;
+    if (!(a.K == 96 && a.N1 % 96 == 0 && a.N1 <= kMlpMaxN1 && a.M >= kMlpBM)) return hipErrorInvalidValue;
+    switch (a.ln) {
+        case 0: return mlp_go<CB, 3, 0>(a, s);
+        case 8: return mlp_go<CB, 3, 8>(a, s);
+        case 64: return mlp_go<CB, 3, 64>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template hipError_t launch_wide_mlp<RPFQ_CB_SEL>(const MlpArgs&, hipStream_t);

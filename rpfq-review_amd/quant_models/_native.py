@@ -67,6 +67,7 @@ EXPORTED = (
     "rpfq_row_scales",
     "rpfq_wide_linear_scaled",
     "rpfq_wide_mlp",
+    "rpfq_layer_norm_wide_mlp",
 )
 
 
@@ -160,6 +161,8 @@ def load() -> ctypes.CDLL:
         lib.rpfq_row_scales.argtypes = [vp, i32, i64, i64, vp, vp]
         lib.rpfq_wide_linear_scaled.argtypes = [dp, vp, sz, vp, i32, i64, vp, vp, vp, vp, i32, i32, vp]
         lib.rpfq_wide_mlp.argtypes = [dp, vp, sz, dp, vp, sz, vp, i64, vp, vp, vp, vp, vp]
+        lib.rpfq_layer_norm_wide_mlp.argtypes = [dp, vp, sz, dp, vp, sz, vp, i64, vp, vp, ctypes.c_float, vp, vp, vp,
+                                                 vp]
         for name in EXPORTED[2:]:
             if name not in ("rpfq_wide_packed_bytes", "rpfq_wide_adjoint_bytes", "rpfq_quantize_workspace_bytes"):
                 getattr(lib, name).restype = i32

@@ -642,6 +642,45 @@ def wide_mlp(fc1: "PackedWide", fc2: "PackedWide", x: torch.Tensor, bias1: torch
     return y.reshape(*lead, fc2.out_features)
 
 
+def layer_norm_wide_mlp(fc1: "PackedWide", fc2: "PackedWide", x: torch.Tensor, ln_weight: torch.Tensor | None,
+                        ln_bias: torch.Tensor | None, eps: float, bias1: torch.Tensor | None = None,
+                        bias2: torch.Tensor | None = None) -> torch.Tensor:
+    """x + fc2(GELU(fc1(layer_norm(x)) + bias1)) + bias2 in one launch
+    (rpfq_layer_norm_wide_mlp): the LayerNorm of the rows (float32 weight /
+    bias over the last dim) in the MLP's prologue, equal to layer_norm()
+    followed by wide_mlp(..., residual=x) bit for bit."""
+    N.require_device(x, ln_weight, ln_bias, bias1, bias2)
+    if x.dtype != torch.float16:
+        raise ValueError("layer_norm_wide_mlp takes fp16 activations")
+    if x.shape[-1] != fc1.in_features:
+        raise ValueError(f"expected last dim {fc1.in_features}, got {x.shape[-1]}")
+    lead = x.shape[:-1]
+    x2 = _aligned_rows(x.reshape(-1, fc1.in_features))
+    m = x2.shape[0]
+    if not mlp_fusable(fc1, fc2, m, x.dtype):
+        raise ValueError("layer_norm_wide_mlp: unsupported layers or row count (see mlp_fusable)")
+    y = torch.empty(m, fc2.out_features, dtype=torch.float16, device=x.device)
+    w = None if ln_weight is None else _aligned_rows(ln_weight.detach().float().contiguous())
+    b = None if ln_bias is None else _aligned_rows(ln_bias.detach().float().contiguous())
+    b1 = None if bias1 is None else bias1.contiguous().float()
+    b2 = None if bias2 is None else bias2.contiguous().float()
+    rec = _launch_recorder
+    if rec is not None:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    N.check("rpfq_layer_norm_wide_mlp", N.load().rpfq_layer_norm_wide_mlp(
+        ctypes.byref(fc1.desc), fc1.blob.data_ptr(), fc1.blob.numel(), ctypes.byref(fc2.desc), fc2.blob.data_ptr(),
+        fc2.blob.numel(), x2.data_ptr(), m, N.ptr(w), N.ptr(b), float(eps), N.ptr(b1), N.ptr(b2), y.data_ptr(),
+        N.stream_of(x2)))
+    if rec is not None:
+        ev1.record()
+        n1, k = fc1.n_complex, fc1.k_complex
+        nbytes = wide_bytes(m, n1, k) + wide_bytes(m, k, n1) - 2 * m * 2 * n1 * 2 + m * 2 * k * 2
+        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "ln_mlp"))
+    return y.reshape(*lead, fc2.out_features)
+
+
 def wide_flops(m: int, n_complex: int, k_complex: int) -> int:
     """Algorithmic FLOPs of one widely-linear layer (one real GEMM)."""
     return 2 * m * (2 * k_complex) * (2 * n_complex)

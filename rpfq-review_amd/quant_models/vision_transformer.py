@@ -190,15 +190,20 @@ class Mlp(nn.Module):
             h = self.act(call_layer(self.fc1, x, prequantized))
         return self.forward_hidden_residual(h, residual)
 
-    def _wide_mlp(self, x, residual):
-        """residual + fc2(GELU(fc1(x))) as one packed launch (ops.wide_mlp:
-        the hidden activations stay on chip, the GELU as in the packed
-        stores, within 1 ulp of the exact GELU), or None where that does not
-        apply: fusion off, another activation, no packed inference path on
-        either layer (training, autograd, activation quantization), or
-        shapes the kernel does not take."""
+    def _wide_mlp(self, x, residual, norm=None):
+        """residual + fc2(GELU(fc1(x))) -- with norm: x + fc2(GELU(fc1(
+        norm(x)))) -- as one packed launch (ops.wide_mlp /
+        ops.layer_norm_wide_mlp: the LayerNorm in its prologue, the hidden
+        activations on chip, the GELU as in the packed stores, within 1 ulp
+        of the exact GELU), or None where that does not apply: fusion off,
+        another activation or norm, no packed inference path on either layer
+        (training, autograd, activation quantization), or shapes the kernel
+        does not take."""
         if not (FUSE_MLP and FUSE_GELU and type(self.act) is nn.GELU and self.act.approximate == "none"
                 and type(self.norm) is nn.Identity and x.dtype == torch.float16 and x.is_cuda):
+            return None
+        if norm is not None and not (FUSE_LN and type(norm) is nn.LayerNorm and len(norm.normalized_shape) == 1
+                                     and norm.normalized_shape[0] == x.shape[-1] and residual is x):
             return None
         inf1 = getattr(self.fc1, "packed_inference", None)
         inf2 = getattr(self.fc2, "packed_inference", None)
@@ -209,10 +214,16 @@ class Mlp(nn.Module):
             return None
         from . import ops
 
-        if not ops.mlp_fusable(p1, p2, x.numel() // x.shape[-1], x.dtype):
+        m = x.numel() // x.shape[-1]
+        if not ops.mlp_fusable(p1, p2, m, x.dtype):
             return None
+        if norm is not None and p1.ln_fusable(m, x.dtype):
+            return None  # few rows: norm -> fc1 in fc1's streaming launch (forward_norm_residual) instead
         b1 = None if self.fc1.bias is None else self.fc1.bias.detach()
         b2 = None if self.fc2.bias is None else self.fc2.bias.detach()
+        if norm is not None:
+            w, b = _ln_params(norm)
+            return ops.layer_norm_wide_mlp(p1, p2, x, w, b, norm.eps, b1, b2)
         return ops.wide_mlp(p1, p2, x, b1, b2, residual)
 
     def _gelu_act_quant_bits(self, x) -> int:
@@ -235,7 +246,12 @@ class Mlp(nn.Module):
         """x + self(norm(x)) with norm (and fc1's act quant) fused into fc1's
         launch and the GELU into its store -- or, when fc2 quantizes its
         input, the GELU and that act quant in one pass after fc1 -- or None
-        where that does not apply."""
+        where that does not apply.  Where both layers are packed and fit
+        rpfq_layer_norm_wide_mlp, the norm, the whole MLP and the add are one
+        launch."""
+        y = self._wide_mlp(x, x, norm)
+        if y is not None:
+            return y
         bits = self._gelu_act_quant_bits(x)
         if bits:
             h = norm_layer_fwd(norm, x, self.fc1, False)

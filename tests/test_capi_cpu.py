@@ -415,6 +415,16 @@ def test_wide_mlp_argument_errors():
     assert mlp(fc1, fc2, x=ctypes.c_void_p(264)) == 3
     assert mlp(fc1, fc2, res=ctypes.c_void_p(520)) == 3
     assert mlp(fc1, fc2, p1=ctypes.c_void_p(384)) == 3
+    # the LayerNorm variant: the same checks, then eps and the affine rows' alignment
+    ln = L.rpfq_layer_norm_wide_mlp
+    assert ln(ctypes.byref(fc1), p, big, ctypes.byref(fc2), p, big, p, 12672, None, None, -1.0, None, None, y,
+              None) == 6
+    assert ln(ctypes.byref(fc1), p, big, ctypes.byref(fc2), p, big, p, 12672, ctypes.c_void_p(260), None, 1e-6,
+              None, None, y, None) == 3
+    assert ln(ctypes.byref(fc1), p, big, ctypes.byref(fc2), p, big, None, 12672, None, None, 1e-6, None, None, y,
+              None) == 1
+    assert ln(ctypes.byref(fc1), p, big, ctypes.byref(fc2), p, big, p, 32, None, None, 1e-6, None, None, y,
+              None) == 2 and b"rpfq_layer_norm_wide_mlp" in L.rpfq_last_error()
 
 
 def test_wide_grad_x_geometry_and_argument_errors():

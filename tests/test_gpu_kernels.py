@@ -1025,6 +1025,40 @@ def test_wide_mlp_matches_two_launches(case, m):
     assert torch.equal(yi, want)
 
 
+@pytest.mark.parametrize("m", [64, 300, 8191, 8192, 12672], ids=["m64", "m300", "m8191", "m8192", "m12672"])
+@pytest.mark.parametrize("affine", [True, False], ids=["affine", "plain"])
+def test_layer_norm_wide_mlp_matches(affine, m):
+    """rpfq_layer_norm_wide_mlp against rpfq_layer_norm followed by
+    rpfq_wide_mlp with x as the residual, bit for bit: the row kernel's 64
+    lanes per row (M < 8,192) and 8 (M >= 8,192) reproduced in the prologue,
+    with and without the affine parameters, rows of mixed scale and offset;
+    and in place (y == x through the C ABI)."""
+    import ctypes
+
+    ops, N = qm()
+    r = rng(3700 + m)
+    p1, p2 = _mlp_layers(r, MLP_CASES[0])
+    g = torch.Generator(device=DEV).manual_seed(3701 + m)
+    x = (torch.randn(m, 192, device=DEV, generator=g) * (1 + 3 * torch.rand(m, 1, device=DEV, generator=g))
+         + torch.randn(m, 1, device=DEV, generator=g)).half()
+    w = torch.randn(192, device=DEV, generator=g) * 0.2 + 1 if affine else None
+    b = torch.randn(192, device=DEV, generator=g) * 0.1 if affine else None
+    b1 = torch.randn(768, device=DEV, generator=g)
+    b2 = torch.randn(192, device=DEV, generator=g)
+    eps = 1e-6
+    want = ops.wide_mlp(p1, p2, ops.layer_norm(x, w, b, eps), b1, b2, residual=x)
+    got = ops.layer_norm_wide_mlp(p1, p2, x, w, b, eps, b1, b2)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want)
+    xi = x.clone()
+    N.check("rpfq_layer_norm_wide_mlp", N.load().rpfq_layer_norm_wide_mlp(
+        ctypes.byref(p1.desc), p1.blob.data_ptr(), p1.blob.numel(), ctypes.byref(p2.desc), p2.blob.data_ptr(),
+        p2.blob.numel(), xi.data_ptr(), m, N.ptr(w), N.ptr(b), eps, b1.data_ptr(), b2.data_ptr(), xi.data_ptr(),
+        N.stream_of(x)))
+    torch.cuda.synchronize()
+    assert torch.equal(xi, want)
+
+
 def test_wide_mlp_against_oracle():
     """The fused MLP against the oracle in float64 on the fp16 operands it
     contracts (DeiT-Ti's fc1 / fc2, axis codes, 300 rows): the hidden values

@@ -914,9 +914,10 @@ def test_fused_gelu_wiring(name, dt, batch):
 @pytest.mark.parametrize("name,batch,want", [("rpfq_deit_tiny_patch16_224_q", 16, 12),
                                              ("rpfq_swin_tiny_patch4_window7_224_q", 4, 2)])
 def test_fused_mlp_wiring(name, batch, want):
-    """The fused block path runs fc1 -> GELU -> fc2 (+ the residual) as one
-    rpfq_wide_mlp launch where both layers fit it (DeiT-Ti: all 12 blocks;
-    Swin-T: the two stage-1 blocks, K' = 96): counted, and the logits within
+    """The fused block path runs norm2 -> fc1 -> GELU -> fc2 (+ the residual)
+    as one rpfq_layer_norm_wide_mlp launch where both layers fit it
+    (DeiT-Ti: all 12 blocks; Swin-T: the two stage-1 blocks, K' = 96):
+    counted, and the logits within
     LOGIT_TOL * max|logit| + LOGIT_TOL / 10 of the same model with that
     fusion off (fc1, torch's exact GELU, fc2: the fused GELU is within 1 ulp
     of it), identical top-1 on margin-confident samples.  A hidden chunk
@@ -933,14 +934,18 @@ def test_fused_mlp_wiring(name, batch, want):
     prepare_inference(model, DEV, torch.float16)
     x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(22)).to(DEV, torch.float16)
     calls = []
-    mlp = ops.wide_mlp
+    mlp, ln_mlp = ops.wide_mlp, ops.layer_norm_wide_mlp
 
     def counting(*args, **kw):
         calls.append(1)
         return mlp(*args, **kw)
+
+    def counting_ln(*args, **kw):  # norm2 in the same launch (the fused block path)
+        calls.append(2)
+        return ln_mlp(*args, **kw)
     saved = vt.FUSED_BLOCKS, vt.FUSE_MLP
     try:
-        ops.wide_mlp = counting
+        ops.wide_mlp, ops.layer_norm_wide_mlp = counting, counting_ln
         with torch.no_grad():
             vt.FUSED_BLOCKS, vt.FUSE_MLP = True, True
             y_f = model(x)
@@ -948,9 +953,9 @@ def test_fused_mlp_wiring(name, batch, want):
             vt.FUSE_MLP = False
             y_u = model(x)
     finally:
-        ops.wide_mlp = mlp
+        ops.wide_mlp, ops.layer_norm_wide_mlp = mlp, ln_mlp
         vt.FUSED_BLOCKS, vt.FUSE_MLP = saved
-    assert n_fused == want, n_fused
+    assert n_fused == want and set(calls) == {2}, calls
     assert len(calls) == n_fused
     assert torch.isfinite(y_f).all()
     y_f, y_u = y_f.float().cpu(), y_u.float().cpu()
