@@ -303,7 +303,9 @@ __global__ __launch_bounds__(kResWaves * 64) void wide_linear_resident_kernel(Wi
                 o = make_uint4(add2_y(o.x, rv.x, f16), add2_y(o.y, rv.y, f16), add2_y(o.z, rv.z, f16),
                                add2_y(o.w, rv.w, f16));
             }
-            if constexpr (ACT != 0) o = gelu8_rolled(o, YDT == RPFQ_F16);
+            // the 8 GELUs unrolled (independent chains; the register file has room here):
+            // Swin-T stage-0 fc1 + GELU 193-197 -> 171-177 us against the rolled form
+            if constexpr (ACT != 0) o = gelu8_y(o, YDT == RPFQ_F16);
             return o;
         };
         // TR rows at a time through this wave's LDS rows (laid out as in
