@@ -5,8 +5,9 @@ of the packed complex-phase GEMM and the CPU oracle timed beside it.
 
 One step = one forward pass of the configured model over one synthetic batch
 already resident in HBM.  Prints ONE JSON line (see README of the contract):
-value = images/s; roofline = the wide-linear kernel (every packed layer
-launch in the timed region, timed with HIP events on its launch stream);
+value = images/s; roofline = the packed-layer kernel with the most time in
+the timed region (every launch of it, timed with HIP events on its launch
+stream; roofline.by_kernel gives each packed kernel's own figures);
 cpu_baseline = the numpy oracle's GEMM-only restatement of the same layers on
 a bounded sample, run on this host's cores.
 """
@@ -349,10 +350,7 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
     from quant_models import _native as N
     # (KERNEL_GEMV: the persistent form wide_linear_gemv_persist_kernel at
     # 12 k-steps from 4096 tiles, whole 64-row groups and 16-bit y)
-    kname = {N.KERNEL_STREAM: "rpfq::wide_linear_skinny_kernel", N.KERNEL_GEMV: "rpfq::wide_linear_gemv_kernel",
-             N.KERNEL_DMA: "rpfq::wide_linear_dma_kernel", N.KERNEL_TILED: "rpfq::wide_linear_kernel",
-             N.KERNEL_RESIDENT: "rpfq::wide_linear_resident_kernel"}[
-        layers[0].kernel_for(m, dt, dt)]
+    kname = N.KERNEL_NAMES[layers[0].kernel_for(m, dt, dt)]
     x = torch.randn(m, 2 * k_c, device=dev, generator=g).to(dt)
     bias = torch.randn(2 * n_layer, device=dev, generator=g)
     y = torch.empty(m, 2 * n_layer, dtype=dt, device=dev)
@@ -649,6 +647,27 @@ def train_bench(cfg_name: str, batch: int, steps: int, warmup: int, act_quant: b
     return 0
 
 
+def dominant_kernel(launches):
+    """The roofline's kernel: the device kernel (instantiation; a launch
+    record's shape[3] names it, +gelu for the GELU-in-store one) with the most
+    time among the packed launches.  Returns (its name, (launches, total ms,
+    flops, algorithmic bytes) of it, per-kernel summary)."""
+    by_kernel = {}
+    for e0, e1, fl, by, shape in launches:
+        d = by_kernel.setdefault(shape[3] if len(shape) > 3 else "?", [0, 0.0, 0, 0])
+        d[0] += 1
+        d[1] += e0.elapsed_time(e1)
+        d[2] += fl
+        d[3] += by
+    if not by_kernel:
+        return None, (0, 0.0, 0, 0), {}
+    dominant = max(by_kernel, key=lambda k: by_kernel[k][1])
+    summary = {k: {"launches": v[0], "avg_launch_us": round(1e3 * v[1] / v[0], 2),
+                   "tflops": round(v[2] / (v[1] / 1e3) / 1e12, 1) if v[1] > 0 else None}
+               for k, v in by_kernel.items()}
+    return dominant, tuple(by_kernel[dominant]), summary
+
+
 def time_forward(model, x, steps: int, warmup: int, use_graph: bool):
     """Warm up, then time `steps` forwards of model(x) between two events
     (graph replays with use_graph, after checking every replay against the
@@ -821,9 +840,7 @@ def main() -> int:
     total_ms, launches, graph = time_forward(model, x, args.steps, args.warmup, args.graph)
     ms_step = total_ms / args.steps
     value = batch * args.steps / (total_ms / 1e3)
-    kt = sum(e0.elapsed_time(e1) for e0, e1, *_ in launches)
-    kf = sum(fl for _, _, fl, _, _ in launches)
-    kb = sum(by for _, _, _, by, _ in launches)
+    dominant, (n_dom, kt, kf, kb), by_kernel = dominant_kernel(launches)
     # graph replays launch no recorded events: no per-launch roofline then
     achieved_tflops = kf / (kt / 1e3) / 1e12 if kt > 0 else None
     per_shape = {}
@@ -862,12 +879,13 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": None if achieved_tflops is None else round(achieved_tflops / PEAK_F16_TFLOPS, 4),
             "traffic": None,
-            "kernel": "rpfq::wide_linear_dma_kernel (fp16 / bf16 x, K' % 32 == 0, M >= 128, launches over one tile "
-                      "deep; small launches rpfq::wide_linear_skinny_kernel, else rpfq::wide_linear_kernel): "
-                      "all packed-layer launches in the timed region (none under --graph)",
-            "launches": len(launches),
-            "avg_launch_us": round(1e3 * kt / max(1, len(launches)), 2),
+            "kernel": (f"{dominant}: the packed-layer kernel with the most time in the timed region "
+                       "(every launch of it; +gelu: the instantiation with the GELU in the store)")
+                      if dominant else "none (graph replays record no launches)",
+            "launches": n_dom,
+            "avg_launch_us": round(1e3 * kt / max(1, n_dom), 2),
             "algorithmic_gbs": round(kb / (kt / 1e3) / 1e9, 1) if kt > 0 else None,
+            "by_kernel": by_kernel,
         },
         "cpu_baseline": None,
     }
@@ -886,8 +904,7 @@ def main() -> int:
         model_b = build_model(args.config, args.act_quant, torch.bfloat16)
         xb = x.to(torch.bfloat16)
         tb, lb, _ = time_forward(model_b, xb, args.steps, args.warmup, False)
-        ktb = sum(e0.elapsed_time(e1) for e0, e1, *_ in lb)
-        kfb = sum(fl for _, _, fl, _, _ in lb)
+        dom_b, (n_b, ktb, kfb, _), by_b = dominant_kernel(lb)
         ach_b = kfb / (ktb / 1e3) / 1e12 if ktb > 0 else None
         line["bf16"] = {"value": round(batch * args.steps / (tb / 1e3), 2), "unit": "images/s",
                         "ms_per_step": round(tb / args.steps, 4), "steps": args.steps, "warmup": args.warmup,
@@ -895,7 +912,8 @@ def main() -> int:
                         "roofline": {"bound": "mfma", "achieved": None if ach_b is None else round(ach_b, 2),
                                      "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
                                      "frac": None if ach_b is None else round(ach_b / PEAK_F16_TFLOPS, 4),
-                                     "launches": len(lb), "avg_launch_us": round(1e3 * ktb / max(1, len(lb)), 2)}}
+                                     "kernel": dom_b, "launches": n_b,
+                                     "avg_launch_us": round(1e3 * ktb / max(1, n_b), 2), "by_kernel": by_b}}
         model = model_b
         x = xb
     if not args.no_cpu_baseline:

@@ -278,21 +278,6 @@ __device__ __forceinline__ uint16_t gelu1_y(uint16_t e, bool f16) {
     if (f16) return __builtin_bit_cast(uint16_t, (_Float16)gelu_fast((float)__builtin_bit_cast(_Float16, e)));
     return f32_to_bf16(gelu_fast(bf16_to_f32(e)));
 }
-// The same 8 outputs one at a time in a rolled loop (the 16-bit values shift
-// through the four words), so only one erf body is live: unrolled, the DMA
-// kernel's allocator pays for the epilogue's GELU with spills in its k-loop.
-__device__ __forceinline__ uint4 gelu8_rolled(uint4 v, bool f16) {
-    uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
-#pragma unroll 1
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t o = gelu1_y((uint16_t)(w0 & 0xffffu), f16);
-        w0 = (w0 >> 16) | (w1 << 16);
-        w1 = (w1 >> 16) | (w2 << 16);
-        w2 = (w2 >> 16) | (w3 << 16);
-        w3 = (w3 >> 16) | (o << 16);
-    }
-    return make_uint4(w0, w1, w2, w3);
-}
 
 __device__ __forceinline__ half8 to_half8(const float* v) {
     uint4 u;

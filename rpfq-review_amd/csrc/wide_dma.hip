@@ -536,7 +536,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     constexpr int RPS = EPI / 8;  // store instructions per wave and half
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        uint4 rres[RPS];
+        // zeros where no residual is read: left undefined, the value would
+        // flow around the persistent loop and hold ~10 VGPRs through the k-loop
+        uint4 rres[RPS] = {};
         if (res_vec) {
 #pragma unroll
             for (int j = 0; j < RPS; ++j) {
@@ -589,7 +591,7 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     v = make_uint4(add2_y(v.x, rres[j].x, f16), add2_y(v.y, rres[j].y, f16),
                                    add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
                 }
-                if constexpr (ACT != 0) v = gelu8_rolled(v, YDT == RPFQ_F16);
+                if constexpr (ACT != 0) v = gelu8_y(v, YDT == RPFQ_F16);
                 __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
             } else {
                 const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);

@@ -36,6 +36,11 @@ FLAG_GELU = 8  # exact GELU of the rounded output, fused into the store (no resi
 FLAG_RESIDENT = 16  # force the resident-weight kernel (small layers; fp16 / bf16 x and y)
 KERNEL_STREAM, KERNEL_DMA, KERNEL_TILED, KERNEL_GEMV, KERNEL_RESIDENT = 0, 1, 2, 3, 4  # rpfq_wide_linear_kernel
 STREAM_KERNELS = (KERNEL_STREAM, KERNEL_GEMV)  # the weight-streaming kernels (small M)
+# device kernel behind each id (KERNEL_GEMV: wide_linear_gemv_persist_kernel
+# where that form applies); launch records and reports name kernels by these
+KERNEL_NAMES = {KERNEL_STREAM: "rpfq::wide_linear_skinny_kernel", KERNEL_DMA: "rpfq::wide_linear_dma_kernel",
+                KERNEL_TILED: "rpfq::wide_linear_kernel", KERNEL_GEMV: "rpfq::wide_linear_gemv_kernel",
+                KERNEL_RESIDENT: "rpfq::wide_linear_resident_kernel"}
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 

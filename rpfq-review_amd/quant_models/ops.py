@@ -279,8 +279,10 @@ class PackedWide:
                                 self.code_bytes * 8 // max(1, self.n_complex * self.k_complex))
             if residual is not None:
                 nbytes += m * self.out_features * y.element_size()
+            # the device kernel (a fused GELU is a separate instantiation)
+            kern = N.KERNEL_NAMES.get(self.kernel_for(m, x2.dtype, out_dtype, flags), "?")
             rec(ev0, ev1, wide_flops(m, self.n_complex, self.k_complex), nbytes,
-                (m, self.n_complex, self.k_complex))
+                (m, self.n_complex, self.k_complex, kern + ("+gelu" if flags & N.FLAG_GELU else "")))
         return y.reshape(*lead, self.out_features)
 
     def ln_fusable(self, m: int, x_dtype: torch.dtype, y_dtype: torch.dtype | None = None) -> bool:
@@ -638,7 +640,7 @@ def wide_mlp(fc1: "PackedWide", fc2: "PackedWide", x: torch.Tensor, bias1: torch
         n1, k = fc1.n_complex, fc1.k_complex
         nbytes = (wide_bytes(m, n1, k) + wide_bytes(m, k, n1) - 2 * m * 2 * n1 * 2
                   + (m * 2 * k * 2 if residual is not None else 0))
-        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "mlp"))
+        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "rpfq::wide_mlp_kernel"))
     return y.reshape(*lead, fc2.out_features)
 
 
@@ -677,7 +679,7 @@ def layer_norm_wide_mlp(fc1: "PackedWide", fc2: "PackedWide", x: torch.Tensor, l
         ev1.record()
         n1, k = fc1.n_complex, fc1.k_complex
         nbytes = wide_bytes(m, n1, k) + wide_bytes(m, k, n1) - 2 * m * 2 * n1 * 2 + m * 2 * k * 2
-        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "ln_mlp"))
+        rec(ev0, ev1, wide_flops(m, n1, k) + wide_flops(m, k, n1), nbytes, (m, n1, k, "rpfq::wide_mlp_kernel+ln"))
     return y.reshape(*lead, fc2.out_features)
 
 

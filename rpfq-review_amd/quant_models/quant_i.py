@@ -307,9 +307,10 @@ DEVICE_PACK = os.environ.get("RPFQ_DEVICE_PACK", "0") == "1"
 # kernel's row prologue, rpfq_act_quant_wide_linear) where that launch
 # qualifies; RPFQ_FUSE_AQ_PROLOGUE=0 runs the separate act-quant pass.
 FUSE_AQ_PROLOGUE = os.environ.get("RPFQ_FUSE_AQ_PROLOGUE", "1") != "0"
-# RPFQ_FUSE_GELU=2: the MLP's GELU in fc1's store on every kernel (default:
-# where fc1 streams or keeps its layer resident, and for bf16 activations).
-GELU_ON_TILED = os.environ.get("RPFQ_FUSE_GELU", "1") == "2"
+# The MLP's GELU in fc1's store on every kernel (default); RPFQ_FUSE_GELU=1
+# keeps torch's separate GELU pass after fp16 launches on the tiled kernels
+# (fused only where fc1 streams or keeps its layer resident, and for bf16).
+GELU_ON_TILED = os.environ.get("RPFQ_FUSE_GELU", "2") == "2"
 # Input gradient of the HIP training forward on the packed blob of the
 # step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
 # A_q: "1" on (each grad_y element of a float32 step then carries one fp16
@@ -724,11 +725,10 @@ class QATLinearComplexPhase(nn.Linear):
         for this layer if prequantized.  On the packed HIP path the GELU runs
         in the kernel's store (within 1 ulp of the exact GELU of the rounded
         output) where the launch streams or keeps the layer resident in LDS
-        (HBM-bound, its VALU mostly idle), and on the tiled kernels for bf16
-        activations.  ViT-B/16 bs256, same box: bf16 15,510 -> 16,197
-        images/s fused; fp16 17,603 -> 17,912, but fc1's launch grows by
-        ~40% (the GELU's VALU work in the epilogue is not hidden behind the
-        MFMAs), so fp16 tiled launches keep torch's separate GELU pass."""
+        (HBM-bound, its VALU mostly idle) and on the tiled kernels.  ViT-B/16
+        bs256, same box: bf16 15,510 -> 16,197 images/s fused; fp16 18,079 ->
+        18,458 (fc1's launch grows by ~30%, less than torch's separate pass
+        over the 3072-wide hidden state costs)."""
         if x.is_cuda and not self.training and self.use_packed and not self._records_grad(x):
             from . import _native as N
             from . import ops
