@@ -200,10 +200,10 @@ int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t pack
  * *kernel := the RPFQ_KERNEL_* that rpfq_wide_linear runs for this layer, M,
  * dtypes and flags (no GPU work; same validation as rpfq_wide_linear minus
  * the buffers).  For callers choosing whether to fuse an epilogue op: the
- * fused GELU pays on the streaming kernel, while on the DMA kernel its
- * float32 erf in the per-tile epilogue costs about what the separate
- * (memory-bound) GELU pass does.  No counterpart in the reference: the
- * kernel choice is this library's.
+ * fused GELU pays most on the streaming and resident kernels (HBM-bound,
+ * VALU idle); on the DMA kernel it makes the launch ~30% longer, still less
+ * than a separate GELU pass over the output.  No counterpart in the
+ * reference: the kernel choice is this library's.
  */
 int rpfq_wide_linear_kernel(const rpfq_wide_desc* desc, int64_t M, int x_dtype, int y_dtype, int flags,
                             int* kernel);
