@@ -453,8 +453,9 @@ def vs_library_bench(m: int, steps: int) -> int:
     float32 bias) against the dense library GEMM on the same layer's decoded
     fp16 coefficients (F.linear with the bias, hipBLASLt), on the same box,
     alternating (packed, library) per shape; HIP events over `steps`
-    calls each (both warmed first; medians of three alternations); prints
-    one JSON line."""
+    calls each (both warmed first; medians of three alternations); fc1 also
+    as the model runs it, with its GELU (fused into the packed store; torch's
+    F.gelu after the library GEMM); prints one JSON line."""
     import torch
     import torch.nn.functional as F
 
@@ -491,12 +492,28 @@ def vs_library_bench(m: int, steps: int) -> int:
                "packed_tflops": round(flops / us_p / 1e6, 1), "library_tflops": round(flops / us_d / 1e6, 1)}
         rows[name] = row
         print(f"# vs library {name}: {row}", file=sys.stderr, flush=True)
+        if name == "fc1":
+            # as the model runs fc1: its GELU in the packed store against the
+            # library GEMM followed by torch's GELU
+            from quant_models import _native as N
+            packed, dense = [], []
+            for _ in range(3):
+                packed.append(timed(lambda: pw.linear_into(x, bias, y, N.FLAG_GELU)))
+                dense.append(timed(lambda: F.gelu(F.linear(x, a16, b16))))
+            us_p, us_d = sorted(packed)[1], sorted(dense)[1]
+            row = {"n_complex": n_c, "k_complex": k_c, "packed_us": round(us_p, 1), "library_us": round(us_d, 1)}
+            rows["fc1+gelu"] = row
+            print(f"# vs library fc1+gelu: {row}", file=sys.stderr, flush=True)
         del pw, a16, x, y
         torch.cuda.empty_cache()
-    tot = sum(r["packed_us"] for r in rows.values())
-    lib = sum(r["library_us"] for r in rows.values())
+    plain = ("qkv", "proj", "fc1", "fc2")
+    model = ("qkv", "proj", "fc1+gelu", "fc2")
+    tot = sum(rows[k]["packed_us"] for k in plain)
+    lib = sum(rows[k]["library_us"] for k in plain)
     print(json.dumps({"metric": "ViT-B/16 q2 layer forward, packed kernel vs dense library GEMM on the decoded weight",
                       "m": m, "steps": steps, "block_packed_us": round(tot, 1), "block_library_us": round(lib, 1),
+                      "block_with_gelu_packed_us": round(sum(rows[k]["packed_us"] for k in model), 1),
+                      "block_with_gelu_library_us": round(sum(rows[k]["library_us"] for k in model), 1),
                       "layers": rows}))
     return 0
 
