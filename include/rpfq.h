@@ -182,7 +182,10 @@ int rpfq_wide_pack(const rpfq_wide_desc* desc, const uint8_t* const* planes, int
  * exact for fp16 x and for bf16 x in [2^-14, 65504] and 2^-11 relative for
  * float32 x in that range; larger magnitudes become +-inf and smaller ones
  * lose relative precision.  rpfq_wide_linear_scaled with the row prescales
- * of rpfq_row_scales removes that limit for float32 / bf16 x.
+ * of rpfq_row_scales removes that limit for float32 / bf16 x; with fp16 x
+ * and row_scale, the rows are taken as already prescaled (as
+ * rpfq_layer_norm_prescaled writes them) and the outputs unscaled (DMA
+ * kernel launches only; RPFQ_ERR_VALUE otherwise).
  * flags: the RPFQ_FLAG_* bits above.
  */
 int rpfq_wide_linear(const rpfq_wide_desc* desc, const void* packed, size_t packed_bytes,
@@ -285,8 +288,10 @@ int rpfq_row_scales(const void* x, int x_dtype, int64_t M, int64_t C, float* sca
  * before its fp16 rounding and its layer output by 1 / row_scale[m] (exact)
  * before the bias, the GELU and the residual add.  row_scale: float32 [M],
  * 16-byte aligned, powers of two in [2^-126, 2^126] (as rpfq_row_scales
- * writes them), or NULL (no prescale); ignored for fp16 x, which the MFMA
- * takes exactly.  Power-of-two factors commute with the roundings of the
+ * writes them), or NULL (no prescale).  fp16 x with a row_scale: rows
+ * already prescaled (rpfq_layer_norm_prescaled), only undone in the output;
+ * the launch must take the DMA kernel (rpfq_wide_linear_kernel reports
+ * RPFQ_KERNEL_DMA), else RPFQ_ERR_VALUE.  Power-of-two factors commute with the roundings of the
  * contraction, so a row inside fp16's range gives the same output as
  * rpfq_wide_linear, and a row of any float32 / bf16 range keeps that
  * relative accuracy (2^-11 of sum |x| |A| for float32 x, exact operands for
@@ -401,6 +406,26 @@ int rpfq_layer_norm_wide_linear_fusable(const rpfq_wide_desc* desc, int64_t M, i
  */
 int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma, const float* beta,
                     float eps, void* y, int y_dtype, void* stream);
+
+/*
+ * rpfq_layer_norm of bf16 rows handed to a packed layer as prescaled fp16
+ * rows: each row is normalized and rounded to bf16 exactly as
+ * rpfq_layer_norm(y_dtype = RPFQ_BF16) rounds it, row_scale[m] is what
+ * rpfq_row_scales gives that bf16 row (a power of two), and y [M, C] fp16
+ * holds the bf16 row times row_scale[m], rounded to fp16 -- the operand the
+ * DMA kernel makes of the bf16 row itself.  rpfq_wide_linear_scaled(x = y,
+ * x_dtype = RPFQ_F16, row_scale) then undoes the prescale and returns, bit
+ * for bit, what it returns for the bf16 rows with their row scales, without
+ * converting them in the kernel (only on the DMA kernel: the launch must be
+ * one rpfq_wide_linear_kernel reports as RPFQ_KERNEL_DMA).  x_dtype must be
+ * RPFQ_BF16; row_scale: float32 [M], 16-byte aligned; other arguments as
+ * rpfq_layer_norm (y may equal x).  Replaces norm1 / norm2 before qkv / fc1
+ * (audit_rpfq_vit_ios_parity.py:520, :549) in a bf16 model; no counterpart
+ * in the reference for the prescale (the guard of this library's fp16 MFMA
+ * operands).
+ */
+int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma,
+                              const float* beta, float eps, void* y, float* row_scale, void* stream);
 
 /*
  * rpfq_layer_norm followed by the activation fake quantization of

@@ -370,6 +370,12 @@ int rpfq_wide_linear_scaled(const rpfq_wide_desc* desc, const void* packed, size
         return fail(RPFQ_ERR_ALIGN, "packed must be 256-byte, x and residual 16-byte aligned");
     if (row_scale && !aligned(row_scale, 16)) return fail(RPFQ_ERR_ALIGN, "row_scale must be 16-byte aligned");
     if (M > (int64_t)1 << 30) return fail(RPFQ_ERR_SHAPE, "M=%lld too large", (long long)M);
+    if (row_scale && x_dtype == RPFQ_F16) {
+        const int k = rpfq::wide_linear_kernel_choice(g, x_dtype, M, y_dtype, flags);
+        if (k != RPFQ_KERNEL_DMA)
+            return fail(RPFQ_ERR_VALUE, "prescaled fp16 rows (fp16 x with row_scale) run on the DMA kernel only; "
+                                        "this launch takes kernel %d", k);
+    }
     return hip_status(rpfq::launch_wide_linear(*desc, g, packed, x, x_dtype, M, row_scale, bias, residual, y, y_dtype,
                                                flags, reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_wide_linear_scaled");
@@ -443,6 +449,18 @@ int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const floa
     return hip_status(rpfq::launch_layer_norm(x, x_dtype, M, C, gamma, beta, eps, 0, y, y_dtype,
                                               reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_layer_norm");
+}
+
+int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma,
+                              const float* beta, float eps, void* y, float* row_scale, void* stream) {
+    int rc = check_ln(x, x_dtype, M, C, gamma, beta, eps, y, RPFQ_F16);
+    if (rc) return rc;
+    if (x_dtype != RPFQ_BF16) return fail(RPFQ_ERR_DTYPE, "x must be bf16 (x_dtype=%d)", x_dtype);
+    if (!row_scale) return fail(RPFQ_ERR_NULL, "row_scale must not be NULL");
+    if (!aligned(row_scale, 16)) return fail(RPFQ_ERR_ALIGN, "row_scale must be 16-byte aligned");
+    return hip_status(rpfq::launch_layer_norm_prescaled(x, M, C, gamma, beta, eps, y, row_scale,
+                                                        reinterpret_cast<hipStream_t>(stream)),
+                      "rpfq_layer_norm_prescaled");
 }
 
 int rpfq_layer_norm_act_quant(const void* x, int x_dtype, int64_t M, int64_t C, const float* gamma,

@@ -565,11 +565,17 @@ __device__ __forceinline__ void store8_ln(void* base, int64_t off, const float* 
 // bit-identical to GELU with float32 output followed by AQ.
 // Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
 // the two halves.
-template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ, bool GE = false>
+// PS (LN only, bf16 x, fp16 y): the row rounded to bf16 as rpfq_layer_norm
+// would store it, then multiplied by its power-of-two prescale
+// (row_prescale of its largest magnitude, written to scale[row]) and stored
+// as fp16 -- the bits the DMA kernel's stage makes of the bf16 row with the
+// prescale rpfq_row_scales gives it, so a layer on the fp16 rows undoes the
+// prescale and matches the bf16 path bit for bit.
+template <int XDT, int YDT, int TPR, int NC, bool LN, bool AQ, bool GE = false, bool PS = false>
 __global__ void __launch_bounds__(256) layer_norm_kernel(const void* x, int64_t M, int C,  // y may equal x
                                                          const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float eps, int bits,
-                                                         void* y) {
+                                                         void* y, float* scale) {
     const int sub = threadIdx.x % TPR;
     const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
     if (row >= M) return;  // whole groups leave together: TPR divides the wave
@@ -709,6 +715,24 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* x, int64_t 
                     }
                 }
             }
+        }
+    }
+    if constexpr (PS) {
+        float mx = 0.0f;  // chunks past the row hold zeros
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[j][e] = bf16_to_f32(f32_to_bf16(v[j][e]));
+                mx = fmaxf(mx, fabsf(v[j][e]));
+            }
+        }
+        const float sc = row_prescale(group_max<TPR>(mx));
+        if (sub == 0) scale[row] = sc;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[j][e] *= sc;  // exact (a power of two)
         }
     }
 #pragma unroll
@@ -940,7 +964,7 @@ static hipError_t act_y(const void* x, int64_t M, int64_t K, int bits, void* y, 
 }
 
 static hipError_t row_op(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
-                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s);
+                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s, float* scale = nullptr);
 
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt, hipStream_t s) {
     // rows held in registers when no 8-element chunk straddles the halves
@@ -956,20 +980,26 @@ hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bi
 
 template <int XDT, int YDT, int TPR, int NC>
 static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                            int mode, int bits, void* y, hipStream_t s) {
+                            int mode, int bits, void* y, float* scale, hipStream_t s) {
     const dim3 grid((unsigned)((M + 256 / TPR - 1) / (256 / TPR)));
     if (mode == 1)
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false>), grid, dim3(256), 0, s, x, M, C, gamma,
-                           beta, eps, bits, y);
+                           beta, eps, bits, y, scale);
     else if (mode == 2)
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true>), grid, dim3(256), 0, s, x, M, C, gamma,
-                           beta, eps, bits, y);
+                           beta, eps, bits, y, scale);
     else if (mode == 4)
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true, true>), grid, dim3(256), 0, s, x, M, C,
-                           gamma, beta, eps, bits, y);
-    else
+                           gamma, beta, eps, bits, y, scale);
+    else if (mode == 5) {
+        if constexpr (XDT == RPFQ_BF16 && YDT == RPFQ_F16)
+            hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false, false, true>), grid, dim3(256), 0, s,
+                               x, M, C, gamma, beta, eps, bits, y, scale);
+        else
+            return hipErrorInvalidValue;
+    } else
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, true>), grid, dim3(256), 0, s, x, M, C, gamma,
-                           beta, eps, bits, y);
+                           beta, eps, bits, y, scale);
     return hipGetLastError();
 }
 
@@ -983,16 +1013,16 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
 // quantization.
 template <int XDT, int YDT>
 static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                        int mode, int bits, void* y, hipStream_t s) {
+                        int mode, int bits, void* y, float* scale, hipStream_t s) {
     const int nch = C / 8;
     if (nch <= 256 && ln_row_lanes(M, C) == 64)
-        return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    if (nch <= 256) return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    if (nch <= 384) return ln_launch<XDT, YDT, 64, 6>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-    return ln_launch<XDT, YDT, 64, 8>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+        return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    if (nch <= 32) return ln_launch<XDT, YDT, 8, 4>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    if (nch <= 64) return ln_launch<XDT, YDT, 16, 4>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    if (nch <= 128) return ln_launch<XDT, YDT, 32, 4>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    if (nch <= 256) return ln_launch<XDT, YDT, 64, 4>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    if (nch <= 384) return ln_launch<XDT, YDT, 64, 6>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+    return ln_launch<XDT, YDT, 64, 8>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
 }
 
 // Rows at or below which the act-quant passes (modes 2, 4) take a workgroup
@@ -1011,7 +1041,7 @@ static hipError_t row_block_go(const void* x, int64_t M, int C, int mode, int bi
 
 template <int XDT>
 static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, int mode,
-                       int bits, void* y, int ydt, hipStream_t s) {
+                       int bits, void* y, int ydt, float* scale, hipStream_t s) {
     if ((mode == 2 || mode == 4) && M <= kRowBlockMaxM && C % 16 == 0) {
         switch (ydt) {
             case RPFQ_F32: return row_block_go<XDT, RPFQ_F32>(x, M, C, mode, bits, y, s);
@@ -1020,18 +1050,18 @@ static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, cons
         }
     }
     switch (ydt) {
-        case RPFQ_F32: return ln_go<XDT, RPFQ_F32>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-        case RPFQ_F16: return ln_go<XDT, RPFQ_F16>(x, M, C, gamma, beta, eps, mode, bits, y, s);
-        default: return ln_go<XDT, RPFQ_BF16>(x, M, C, gamma, beta, eps, mode, bits, y, s);
+        case RPFQ_F32: return ln_go<XDT, RPFQ_F32>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+        case RPFQ_F16: return ln_go<XDT, RPFQ_F16>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
+        default: return ln_go<XDT, RPFQ_BF16>(x, M, C, gamma, beta, eps, mode, bits, y, scale, s);
     }
 }
 
 static hipError_t row_op(const void* x, int xdt, int64_t M, int64_t C, const float* gamma, const float* beta,
-                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s) {
+                         float eps, int mode, int bits, void* y, int ydt, hipStream_t s, float* scale) {
     switch (xdt) {
-        case RPFQ_F32: return ln_y<RPFQ_F32>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
-        case RPFQ_F16: return ln_y<RPFQ_F16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
-        default: return ln_y<RPFQ_BF16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, s);
+        case RPFQ_F32: return ln_y<RPFQ_F32>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, scale, s);
+        case RPFQ_F16: return ln_y<RPFQ_F16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, scale, s);
+        default: return ln_y<RPFQ_BF16>(x, M, (int)C, gamma, beta, eps, mode, bits, y, ydt, scale, s);
     }
 }
 
@@ -1043,6 +1073,11 @@ hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const
 hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,
                                  hipStream_t s) {
     return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 4, bits, y, ydt, s);
+}
+
+hipError_t launch_layer_norm_prescaled(const void* x, int64_t M, int64_t C, const float* gamma, const float* beta,
+                                       float eps, void* y, float* scale, hipStream_t s) {
+    return row_op(x, RPFQ_BF16, M, C, gamma, beta, eps, 5, 0, y, RPFQ_F16, s, scale);
 }
 
 template <int CB>

@@ -92,10 +92,10 @@ static int choose_kernel(const WideArgs& a, int xdt, int ydt, int flags) {
         return gemv_pays(a) ? RPFQ_KERNEL_GEMV : RPFQ_KERNEL_STREAM;
     if (flags == 0 && a.M >= RPFQ_RES_MIN_M && resident_ok(a, xdt, ydt)) return RPFQ_KERNEL_RESIDENT;
     flags &= ~RPFQ_FLAG_NO_STREAM;
-    // (bf16 outputs with the fused GELU: the DMA kernel's instantiation would
-    // spill in its k-loop, so they take the register-staged kernel)
+    // (bf16 x and y with the fused GELU take the register-staged kernel,
+    // measured as fast as the DMA kernel's in-LDS conversion plus the GELU)
     if ((xdt == RPFQ_F16 || xdt == RPFQ_BF16) && flags == 0 && a.K % 32 == 0 && a.M >= RPFQ_DMA_MIN_M &&
-        !(a.act && ydt == RPFQ_BF16))
+        !(a.act && ydt == RPFQ_BF16 && xdt == RPFQ_BF16))
         return RPFQ_KERNEL_DMA;
     return RPFQ_KERNEL_TILED;
 }
@@ -249,7 +249,9 @@ hipError_t launch_wide_linear(const rpfq_wide_desc& d, const WideGeom& g, const 
     WideArgs a = wide_shape(g, M, flags);
     flags &= ~RPFQ_FLAG_GELU;
     wide_operands(a, d, g, packed, x, bias, res, y);
-    a.xs = xdt == RPFQ_F16 ? nullptr : xs;  // fp16 x is the MFMA operand as it stands
+    // fp16 x is the MFMA operand as it stands; with xs its rows arrive
+    // prescaled, which only the DMA kernel undoes (the C API checks)
+    a.xs = xdt != RPFQ_F16 || choose_kernel(a, xdt, ydt, flags) == RPFQ_KERNEL_DMA ? xs : nullptr;
     return launch_wide(a, d, xdt, ydt, flags, s);
 }
 

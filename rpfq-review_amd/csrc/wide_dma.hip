@@ -1,5 +1,7 @@
 // Widely-linear GEMM for fp16 or bf16 activations staged by LDS DMA (large M).
 // Compiled once per codebook (RPFQ_CB_SEL).
+#include <type_traits>
+
 #include "rpfq_device.h"
 
 #ifndef RPFQ_CB_SEL
@@ -55,7 +57,7 @@ template <int BM> constexpr int dma_bias_at() { return dma_lut1_at<BM>() + kDmaL
 // per-row scales of the next tile, staged by DMA: [wave][32 rows][pu | pw] float4 pairs
 constexpr int kDmaParams = 4 * 1024;
 template <int BM> constexpr int dma_params_at() { return dma_bias_at<BM>() + kDmaBias; }
-// row prescales of bf16 x (WideArgs::xs) of the current and the next tile: [2][BM] floats
+// row prescales (WideArgs::xs) of the current and the next tile: [2][BM] floats
 template <int BM> constexpr int dma_xs_at() { return dma_params_at<BM>() + kDmaParams; }
 template <int BM> constexpr int dma_lds() { return dma_xs_at<BM>() + 2 * BM * 4; }  // 79872 B (BM = 128)
 static_assert(2 * dma_lds<128>() <= 160 * 1024, "two workgroups per CU");
@@ -221,7 +223,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // bf16 x with row prescales: wave w's RPW rows of a tile, DMA'd with the
     // tile's first loads into buffer (tile iteration & 1), RPW lanes of 4 B
     float* xs_lds = reinterpret_cast<float*>(smem + dma_xs_at<BM>());
-    const bool scaled = XDT == RPFQ_BF16 && a.xs != nullptr;
+    // row prescales: bf16 rows are multiplied in the stage; fp16 rows arrive
+    // prescaled (written so by rpfq_layer_norm_prescaled); both unscaled below
+    const bool scaled = a.xs != nullptr;
     auto issue_xs = [&](int vb_t, int buf) {
         if (!scaled) return;
         const int t = xcd_tile(vb_t, total);
@@ -433,16 +437,14 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         issue_params(vb + (int)gridDim.x);
         issue_xs(vb + (int)gridDim.x, xb ^ 1);
     }
-    if constexpr (XDT == RPFQ_BF16) {
-        if (scaled) {  // undo the rows' prescales (exact) before the bias: subtile i, lane r holds x row 32 i + r
+    if (scaled) {  // undo the rows' prescales (exact) before the bias: subtile i, lane r holds x row 32 i + r
 #pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                const float inv = row_unscale(xs_lds[xb * BM + 32 * i + r]);
+        for (int i = 0; i < MB; ++i) {
+            const float inv = row_unscale(xs_lds[xb * BM + 32 * i + r]);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    acc_re[i][v] *= inv;
-                    acc_im[i][v] *= inv;
-                }
+            for (int v = 0; v < 16; ++v) {
+                acc_re[i][v] *= inv;
+                acc_im[i][v] *= inv;
             }
         }
     }
@@ -534,8 +536,10 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
     // half tile goes through LDS, so their latency overlaps the transpose
     const bool res_vec = a.res && chunk_vec;
     constexpr int RPS = EPI / 8;  // store instructions per wave and half
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    // one half of the tile; h is a compile-time constant so the accumulator
+    // indices stay static (a runtime h would move them to scratch memory)
+    auto epi_half = [&](auto h_c) {
+        constexpr int h = decltype(h_c)::value;
         // zeros where no residual is read: left undefined, the value would
         // flow around the persistent loop and hold ~10 VGPRs through the k-loop
         uint4 rres[RPS] = {};
@@ -609,7 +613,9 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (wg) __builtin_amdgcn_s_barrier(); else __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
-    }
+        };
+    epi_half(std::integral_constant<int, 0>{});
+    epi_half(std::integral_constant<int, 1>{});
     }
     // every wave is done with this tile's LDS before the next tile refills it
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -637,7 +643,8 @@ static hipError_t wide_dma_act(WideArgs& a, hipStream_t s) {
 
 template <int BM, int XDT, int YDT, int CB>
 static hipError_t wide_dma_go(WideArgs& a, hipStream_t s) {
-    if constexpr (YDT == RPFQ_BF16) return wide_dma_act<BM, XDT, YDT, CB, 0>(a, s);  // GELU: not routed here
+    // GELU with bf16 x and y: not routed here (the register-staged kernel measured as fast)
+    if constexpr (YDT == RPFQ_BF16 && XDT == RPFQ_BF16) return wide_dma_act<BM, XDT, YDT, CB, 0>(a, s);
     else return a.act ? wide_dma_act<BM, XDT, YDT, CB, 1>(a, s) : wide_dma_act<BM, XDT, YDT, CB, 0>(a, s);
 }
 

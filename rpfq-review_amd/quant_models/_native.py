@@ -64,6 +64,7 @@ EXPORTED = (
     "rpfq_act_quant_wide_linear",
     "rpfq_wide_linear_kernel",
     "rpfq_layer_norm",
+    "rpfq_layer_norm_prescaled",
     "rpfq_layer_norm_act_quant",
     "rpfq_gelu_act_quant",
     "rpfq_quantize_workspace_bytes",
@@ -156,6 +157,7 @@ def load() -> ctypes.CDLL:
         lib.rpfq_act_quant_wide_linear.argtypes = [dp, vp, sz, vp, i32, i64, i32, i32, vp, vp, ctypes.c_float, vp,
                                                    vp, vp, i32, i32, vp]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
+        lib.rpfq_layer_norm_prescaled.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, vp, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
         lib.rpfq_gelu_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         qp = ctypes.POINTER(QuantDesc)

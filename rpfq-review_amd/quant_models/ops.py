@@ -160,6 +160,31 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
     return y.reshape(x.shape)
 
 
+def layer_norm_prescaled(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
+                         eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, row_scale) for bf16 x (rpfq_layer_norm_prescaled): the rows of
+    layer_norm(x) as bf16, times their power-of-two prescale row_scale
+    (float32 [M], what row_scales() gives those bf16 rows), stored as fp16.
+    PackedWide.linear(y, ..., row_scale=row_scale) on a launch that takes
+    the DMA kernel equals linear(layer_norm(x)) on the bf16 rows bit for
+    bit, without the kernel's in-LDS bf16 conversion or a row-scale pass."""
+    N.require_device(x, weight, bias)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("layer_norm_prescaled takes bf16 rows")
+    c = x.shape[-1]
+    x2 = _aligned_rows(x.reshape(-1, c))
+    m = x2.shape[0]
+    y = torch.empty(x2.shape, dtype=torch.float16, device=x.device)
+    sc = torch.empty(m, dtype=torch.float32, device=x.device)
+    if m:
+        w = None if weight is None else weight.detach().float().contiguous()
+        b = None if bias is None else bias.detach().float().contiguous()
+        N.check("rpfq_layer_norm_prescaled", N.load().rpfq_layer_norm_prescaled(
+            x2.data_ptr(), N.dtype_code(x2.dtype), m, c, N.ptr(w), N.ptr(b), float(eps), y.data_ptr(), sc.data_ptr(),
+            N.stream_of(x2)))
+    return y.reshape(x.shape), sc
+
+
 @dataclass
 class PackedWide:
     """One widely-linear layer in the MI355X tiled layout (a device blob).

@@ -311,6 +311,10 @@ FUSE_AQ_PROLOGUE = os.environ.get("RPFQ_FUSE_AQ_PROLOGUE", "1") != "0"
 # keeps torch's separate GELU pass after fp16 launches on the tiled kernels
 # (fused only where fc1 streams or keeps its layer resident, and for bf16).
 GELU_ON_TILED = os.environ.get("RPFQ_FUSE_GELU", "2") == "2"
+# bf16 rows into a layer on the DMA kernel: the preceding LayerNorm writes
+# them as prescaled fp16 operand rows (forward_layer_norm); "0" keeps the
+# bf16 LayerNorm output and the kernel's in-LDS conversion.
+PRESCALED_LN = os.environ.get("RPFQ_PRESCALED_LN", "1") != "0"
 # Input gradient of the HIP training forward on the packed blob of the
 # step's own codes (rpfq_wide_linear_grad_x) instead of the library GEMM on
 # A_q: "1" on (each grad_y element of a float32 step then carries one fp16
@@ -756,16 +760,32 @@ class QATLinearComplexPhase(nn.Linear):
         in the prologue of every one of qkv's 36 (fc1's 48) tiles it measured
         slower at one ViT-B/16 image (qkv 15.5 vs 5.2 + 9.5 us, fc1 19.3 vs
         5.2 + 12.0 us); the act quant alone pays in the prologue (proj 9.3 vs
-        4.7 + 9.2 us), see _packed_forward / forward_residual."""
+        4.7 + 9.2 us), see _packed_forward / forward_residual.
+        bf16 rows the DMA kernel takes (large M) instead go through the
+        LayerNorm as prescaled fp16 operand rows (rpfq_layer_norm_prescaled):
+        bit-identical to the LayerNorm then the layer on the bf16 rows with
+        their range-guard prescales, without the kernel's in-LDS bf16
+        conversion or the prescale pass (ViT-B/16 qkv at 50,432 rows: 303 ->
+        209 us)."""
         if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None \
                 or self._records_grad(x):
             return None
         pw = self.packed(x.device)
         m = x.numel() // x.shape[-1]
-        if not hasattr(pw, "ln_fusable") or m == 0 or not pw.ln_fusable(m, x.dtype):
+        if not hasattr(pw, "ln_fusable") or m == 0:
             return None
         bias = None if self.bias is None else self.bias.detach()
-        return pw.layer_norm_linear(x, ln_weight, ln_bias, eps, bias, out_dtype=x.dtype, gelu=gelu)
+        if pw.ln_fusable(m, x.dtype):
+            return pw.layer_norm_linear(x, ln_weight, ln_bias, eps, bias, out_dtype=x.dtype, gelu=gelu)
+        from . import _native as N
+        from . import ops
+
+        c = x.shape[-1]
+        if (PRESCALED_LN and x.dtype == torch.bfloat16 and c % 8 == 0 and c <= 4096
+                and pw.kernel_for(m, torch.float16, x.dtype, N.FLAG_GELU if gelu else 0) == N.KERNEL_DMA):
+            h, sc = ops.layer_norm_prescaled(x, ln_weight, ln_bias, eps)
+            return pw.linear(h, bias, out_dtype=x.dtype, gelu=gelu, row_scale=sc)
+        return None
 
     def forward_residual(self, x: torch.Tensor, residual: torch.Tensor, prequantized: bool = False) -> torch.Tensor:
         """residual + self(x); x already activation-quantized for this layer

@@ -137,6 +137,25 @@ def test_residual_and_layer_norm_argument_errors():
     assert L.rpfq_layer_norm(p, 1, 4, 64, ctypes.c_void_p(260), None, 1e-6, p, 1, None) == 3
 
 
+def test_layer_norm_prescaled_argument_errors():
+    """rpfq_layer_norm_prescaled takes bf16 rows and a 16-byte aligned scale
+    array; rpfq_wide_linear_scaled takes prescaled fp16 rows only on a launch
+    the DMA kernel runs."""
+    L, N = lib()
+    p = ctypes.c_void_p(256)
+    assert L.rpfq_layer_norm_prescaled(None, 2, 4, 64, None, None, 1e-6, p, p, None) == 1
+    assert L.rpfq_layer_norm_prescaled(p, 2, 4, 64, None, None, 1e-6, p, None, None) == 1
+    assert L.rpfq_layer_norm_prescaled(p, 1, 4, 64, None, None, 1e-6, p, p, None) == 5  # fp16 x
+    assert "bf16" in L.rpfq_last_error().decode()
+    assert L.rpfq_layer_norm_prescaled(p, 2, 4, 60, None, None, 1e-6, p, p, None) == 2  # C % 8
+    assert L.rpfq_layer_norm_prescaled(p, 2, 4, 64, None, None, -1.0, p, p, None) == 6
+    assert L.rpfq_layer_norm_prescaled(p, 2, 4, 64, None, None, 1e-6, p, ctypes.c_void_p(260), None) == 3
+    d = _desc(N, n=1536, k=384)
+    # fp16 x with row scales at 4 rows (a streaming launch) -> RPFQ_ERR_VALUE
+    assert L.rpfq_wide_linear_scaled(ctypes.byref(d), p, 1 << 30, p, 1, 4, p, None, None, p, 2, 0, None) == 6
+    assert "DMA" in L.rpfq_last_error().decode()
+
+
 def test_layer_norm_act_quant_argument_errors():
     L, _ = lib()
     p = ctypes.c_void_p(256)
@@ -311,7 +330,7 @@ def test_wide_linear_kernel_choice():
     rows and for small one-tile-deep launches (the column-split one for
     M <= 8 on few tiles of short K' or many tiles of long K'), the DMA kernel
     for large fp16 launches, the register-staged kernel for float32 x, bf16
-    output with GELU, or RPFQ_FLAG_TILE_M128; the flags force their
+    x and output with GELU, or RPFQ_FLAG_TILE_M128; the flags force their
     kernels."""
     L, N = lib()
     d = _desc(N, n=1536, k=384)  # ViT-B fc1
@@ -325,7 +344,8 @@ def test_wide_linear_kernel_choice():
     assert kernel(197) == N.KERNEL_STREAM  # one image: 624 (chunk, tile) groups vs one 128-row tile deep
     assert kernel(50432) == N.KERNEL_DMA
     assert kernel(50432, flags=N.FLAG_GELU) == N.KERNEL_DMA
-    assert kernel(50432, ydt=2, flags=N.FLAG_GELU) == N.KERNEL_TILED
+    assert kernel(50432, ydt=2, flags=N.FLAG_GELU) == N.KERNEL_DMA  # prescaled fp16 rows into a bf16 model's fc1
+    assert kernel(50432, xdt=2, ydt=2, flags=N.FLAG_GELU) == N.KERNEL_TILED
     assert kernel(50432, xdt=0) == N.KERNEL_TILED
     assert kernel(300, flags=N.FLAG_TILE_M128) == N.KERNEL_TILED
     assert kernel(197, flags=N.FLAG_NO_STREAM) == N.KERNEL_DMA

@@ -1135,10 +1135,8 @@ def test_wide_linear_gelu(m, flags, ydt):
         pw, *_ = build_packed(r, case)
         x = torch.from_numpy(r.standard_normal((m, 2 * case[1])).astype(np.float32)).to(torch.float16).to(DEV)
         bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
-        # bf16 outputs with GELU leave the DMA kernel for the register-staged
-        # one: the unfused reference comes from that kernel too
-        ref_flags = N.FLAG_TILE_M128 if (ydt == torch.bfloat16 and flags == 2 and m >= 128) else flags
-        y = pw.linear(x, bias, out_dtype=ydt, flags=ref_flags)
+        # (fp16 x: every output dtype keeps its kernel with the GELU)
+        y = pw.linear(x, bias, out_dtype=ydt, flags=flags)
         yg = pw.linear(x, bias, out_dtype=ydt, flags=flags, gelu=True).cpu()
         yd = y.double().cpu()
         exact = yd * 0.5 * torch.special.erfc(-yd / math.sqrt(2.0))
@@ -1235,6 +1233,87 @@ def test_layer_norm(m, c, xdt, ydt):
     y0 = ops.layer_norm(x.to(DEV), None, None, 1e-5, out_dtype=torch.float32).cpu().numpy()
     ref0 = (xd - mu) / np.sqrt(var + 1e-5)
     assert np.abs(y0 - ref0).max() <= 2e-5 * (np.abs(ref0).max() + 1)
+
+
+@pytest.mark.parametrize("gscale", [1.0, 1e6, 1e-9], ids=["g1", "g1e6", "g1e-9"])
+@pytest.mark.parametrize("m,c", [(300, 768), (2047, 768), (2048, 768), (129, 3072), (64, 96)])
+def test_layer_norm_prescaled(m, c, gscale):
+    """rpfq_layer_norm_prescaled against the three steps it stands for:
+    rpfq_layer_norm to bf16, rpfq_row_scales of those rows, and the fp16
+    rounding of each bf16 row times its scale -- scales and fp16 bits equal,
+    at both lane layouts of the row kernel (2,047 / 2,048 rows at C = 768),
+    with affine parameters that put the rows beyond fp16's range (1e6) or
+    below its normal range (1e-9), without them, and in place."""
+    ops, _ = qm()
+    r = rng(2100 + m + c)
+    x = torch.from_numpy((r.standard_normal((m, c)) * 3 + 1).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    g = tdev((r.standard_normal(c) * gscale).astype(np.float32))
+    b = tdev((r.standard_normal(c) * gscale).astype(np.float32))
+    for gg, bb in ((g, b), (None, None)):
+        y, sc = ops.layer_norm_prescaled(x, gg, bb, 1e-6)
+        h = ops.layer_norm(x, gg, bb, 1e-6)
+        sc_ref = ops.row_scales(h)
+        assert torch.equal(sc, sc_ref)
+        y_ref = (h.float() * sc_ref[:, None]).half()
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    # in place: the fp16 rows over the bf16 rows' storage
+    N = qm()[1]
+    x2 = x.clone()
+    y2, sc2 = ops.layer_norm_prescaled(x2, g, b, 1e-6)
+    N.check("rpfq_layer_norm_prescaled", N.load().rpfq_layer_norm_prescaled(
+        x2.data_ptr(), N.dtype_code(x2.dtype), m, c, g.data_ptr(), b.data_ptr(), 1e-6, x2.data_ptr(),
+        sc2.data_ptr(), N.stream_of(x2)))
+    assert torch.equal(x2.view(torch.int16), y2.view(torch.int16))
+
+
+PRESCALED_SHAPES = [REAL_SHAPES[0], REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[5], CASES[7]]
+
+
+@pytest.mark.parametrize("gscale", [1.0, 1e6], ids=["g1", "g1e6"])
+@pytest.mark.parametrize("m,flags", [(128, 2), (300, 2), (12672, 0)])
+@pytest.mark.parametrize("case", PRESCALED_SHAPES, ids=["qkv", "fc1", "fc2", "l-qkv-psk16", "rot"])
+def test_wide_linear_prescaled_fp16_rows(case, m, flags, gscale):
+    """A packed layer on the DMA kernel fed prescaled fp16 rows
+    (rpfq_layer_norm_prescaled, then rpfq_wide_linear_scaled with fp16 x and
+    the row scales) against the same layer on the bf16 LayerNorm output with
+    its range-guard prescales: bf16 outputs bit-identical, with and without
+    bias, with the residual add, and for rows beyond fp16's range; with the
+    GELU in the store (the bf16 rows then take the register-staged kernel)
+    within two bf16 roundings, the GELU's slope times one of them included,
+    of the bf16-row path.  flags 2 (RPFQ_FLAG_NO_STREAM) puts the small
+    launches on the DMA kernel; 12,672 rows take it by default."""
+    ops, N = qm()
+    r = rng(2200 + m + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    c2 = 2 * case[1]
+    assert pw.kernel_for(m, torch.float16, torch.bfloat16, flags) == N.KERNEL_DMA
+    assert pw.kernel_for(m, torch.float16, torch.bfloat16, flags | N.FLAG_GELU) == N.KERNEL_DMA
+    x = torch.from_numpy((r.standard_normal((m, c2)) * 3 + 1).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    g = tdev((r.standard_normal(c2) * gscale).astype(np.float32))
+    b = tdev((r.standard_normal(c2) * gscale).astype(np.float32))
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    h16, sc = ops.layer_norm_prescaled(x, g, b, 1e-6)
+    h = ops.layer_norm(x, g, b, 1e-6)
+    for bb in (bias, None):
+        y = pw.linear(h16, bb, out_dtype=torch.bfloat16, flags=flags, row_scale=sc)
+        y_ref = pw.linear(h, bb, out_dtype=torch.bfloat16, flags=flags)
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), (case, m, bb is None)
+    res = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    y = pw.linear(h16, bias, out_dtype=torch.bfloat16, flags=flags, residual=res, row_scale=sc)
+    y_ref = pw.linear(h, bias, out_dtype=torch.bfloat16, flags=flags, residual=res)
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    if gscale == 1.0 and m <= 300:  # the oracle on the bf16 rows (exact prescales: the unscaled bound)
+        hf = h.float().cpu().numpy().astype(np.float64)
+        y32 = pw.linear(h16, bias, out_dtype=torch.float32, flags=flags, row_scale=sc).cpu().numpy()
+        check_against_oracle(y32, hf, bias.cpu().numpy().astype(np.float64), oplanes, codebook, rotation)
+    yg = pw.linear(h16, bias, out_dtype=torch.bfloat16, flags=flags, gelu=True, row_scale=sc).float()
+    yg_ref = pw.linear(h, bias, out_dtype=torch.bfloat16, flags=flags, gelu=True).float()
+    plain = pw.linear(h, bias, out_dtype=torch.float32, flags=flags).abs()
+    # the two kernels accumulate in different orders: float32 rounding of
+    # sum |h| |A| (2K' terms) on top of the bf16 roundings
+    scale = h.float().abs() @ tdev(np.abs(a_ref).astype(np.float32)).T + bias.abs()
+    bound = 2.0 ** -5 * torch.maximum(yg_ref.abs(), plain) + 2.0 ** -24 * 4 * c2 * scale
+    assert torch.all((yg - yg_ref).abs() <= bound), float(((yg - yg_ref).abs() - bound).max())
 
 
 # LayerNorm fused into the streaming kernel (rpfq_layer_norm_wide_linear):
