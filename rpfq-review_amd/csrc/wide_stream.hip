@@ -295,9 +295,12 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
     };
     if (NW > 1) fetch_epi();
 
-    Step ring[SK_PF];
+    // float32 x holds twice the bytes per ring slot: half the distance keeps
+    // the ring in registers
+    constexpr int PF = XDT == RPFQ_F32 ? SK_PF / 2 : SK_PF;
+    Step ring[PF];
 #pragma unroll
-    for (int i = 0; i < SK_PF; ++i) load_step(kb + i, ring[i]);
+    for (int i = 0; i < PF; ++i) load_step(kb + i, ring[i]);
 
     int blk = 0;
     if (LN) {
@@ -553,13 +556,13 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
             }
         }
     };
-    // Whole groups of SK_PF k-steps with a uniform guard around the compute
+    // Whole groups of PF k-steps with a uniform guard around the compute
     // and each ring slot reloaded after its k-step is consumed: the slots keep
     // their registers across iterations (no copies, whose waits would drain
     // every load in flight), and each wait is for the oldest loads only.
-    for (int ks0 = kb; ks0 < ke; ks0 += SK_PF) {
+    for (int ks0 = kb; ks0 < ke; ks0 += PF) {
 #pragma unroll
-        for (int i = 0; i < SK_PF; ++i) {
+        for (int i = 0; i < PF; ++i) {
             const int ks = ks0 + i;
             if (ks < ke) {
                 if (PB) {  // per-(row, block) scales: new LUT at each block start
@@ -572,7 +575,7 @@ __global__ void __launch_bounds__(64 * NW, LN ? 2 : RPFQ_SK_OCC) wide_linear_ski
                 }
                 compute(ks, ring[i]);
             }
-            load_step(ks + SK_PF, ring[i]);  // past the end: reloads the last k-step, unused
+            load_step(ks + PF, ring[i]);  // past the end: reloads the last k-step, unused
         }
     }
 
