@@ -428,6 +428,19 @@ int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, 
                               const float* beta, float eps, void* y, float* row_scale, void* stream);
 
 /*
+ * The prescaled fp16 operand rows of bf16 rows without a LayerNorm: y [M, C]
+ * fp16 = x times row_scale[m] (what rpfq_row_scales gives x), rounded to
+ * fp16 -- the bits the DMA kernel's stage makes of x with those prescales,
+ * so rpfq_wide_linear_scaled(y, RPFQ_F16, row_scale) on a DMA-kernel launch
+ * equals it on (x, RPFQ_BF16, row_scale) bit for bit, one pass instead of
+ * the row-scale pass plus the in-kernel conversion.  x_dtype must be
+ * RPFQ_BF16; C a multiple of 8 up to 4096; x, y 16-byte aligned (y may
+ * equal x); row_scale float32 [M], 16-byte aligned.  No counterpart in the
+ * reference (the guard of this library's fp16 MFMA operands).
+ */
+int rpfq_row_prescale(const void* x, int x_dtype, int64_t M, int64_t C, void* y, float* row_scale, void* stream);
+
+/*
  * rpfq_layer_norm followed by the activation fake quantization of
  * rpfq_act_quant on its output, in one pass over the rows: the float32
  * LayerNorm output is quantized per row and per half (C/2 columns each;

@@ -565,8 +565,9 @@ __device__ __forceinline__ void store8_ln(void* base, int64_t off, const float* 
 // bit-identical to GELU with float32 output followed by AQ.
 // Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
 // the two halves.
-// PS (LN only, bf16 x, fp16 y): the row rounded to bf16 as rpfq_layer_norm
-// would store it, then multiplied by its power-of-two prescale
+// PS (bf16 x, fp16 y; after the LayerNorm or alone): the row rounded to bf16
+// (the LayerNorm's output as rpfq_layer_norm would store it, or x itself),
+// then multiplied by its power-of-two prescale
 // (row_prescale of its largest magnitude, written to scale[row]) and stored
 // as fp16 -- the bits the DMA kernel's stage makes of the bf16 row with the
 // prescale rpfq_row_scales gives it, so a layer on the fp16 rows undoes the
@@ -991,12 +992,17 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
     else if (mode == 4)
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true, true>), grid, dim3(256), 0, s, x, M, C,
                            gamma, beta, eps, bits, y, scale);
-    else if (mode == 5) {
-        if constexpr (XDT == RPFQ_BF16 && YDT == RPFQ_F16)
-            hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false, false, true>), grid, dim3(256), 0, s,
-                               x, M, C, gamma, beta, eps, bits, y, scale);
-        else
+    else if (mode == 5 || mode == 6) {
+        if constexpr (XDT == RPFQ_BF16 && YDT == RPFQ_F16) {
+            if (mode == 5)
+                hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false, false, true>), grid, dim3(256),
+                                   0, s, x, M, C, gamma, beta, eps, bits, y, scale);
+            else
+                hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, false, false, true>), grid,
+                                   dim3(256), 0, s, x, M, C, gamma, beta, eps, bits, y, scale);
+        } else {
             return hipErrorInvalidValue;
+        }
     } else
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, true>), grid, dim3(256), 0, s, x, M, C, gamma,
                            beta, eps, bits, y, scale);
@@ -1010,7 +1016,7 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
 // workgroups (a batch-1 forward: 197 rows), so the launch spreads over the
 // CUs and each lane's chain of loads and reductions is shorter.
 // mode: 1 LayerNorm, 2 activation quantization, 3 both, 4 GELU + activation
-// quantization.
+// quantization, 5 LayerNorm into prescaled fp16 rows, 6 prescaled fp16 rows.
 template <int XDT, int YDT>
 static hipError_t ln_go(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
                         int mode, int bits, void* y, float* scale, hipStream_t s) {
@@ -1078,6 +1084,10 @@ hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, i
 hipError_t launch_layer_norm_prescaled(const void* x, int64_t M, int64_t C, const float* gamma, const float* beta,
                                        float eps, void* y, float* scale, hipStream_t s) {
     return row_op(x, RPFQ_BF16, M, C, gamma, beta, eps, 5, 0, y, RPFQ_F16, s, scale);
+}
+
+hipError_t launch_row_prescale(const void* x, int64_t M, int64_t C, void* y, float* scale, hipStream_t s) {
+    return row_op(x, RPFQ_BF16, M, C, nullptr, nullptr, 0.0f, 6, 0, y, RPFQ_F16, s, scale);
 }
 
 template <int CB>

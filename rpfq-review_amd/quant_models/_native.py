@@ -65,6 +65,7 @@ EXPORTED = (
     "rpfq_wide_linear_kernel",
     "rpfq_layer_norm",
     "rpfq_layer_norm_prescaled",
+    "rpfq_row_prescale",
     "rpfq_layer_norm_act_quant",
     "rpfq_gelu_act_quant",
     "rpfq_quantize_workspace_bytes",
@@ -158,6 +159,7 @@ def load() -> ctypes.CDLL:
                                                    vp, vp, i32, i32, vp]
         lib.rpfq_layer_norm.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, i32, vp]
         lib.rpfq_layer_norm_prescaled.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, vp, vp, vp]
+        lib.rpfq_row_prescale.argtypes = [vp, i32, i64, i64, vp, vp, vp]
         lib.rpfq_layer_norm_act_quant.argtypes = [vp, i32, i64, i64, vp, vp, ctypes.c_float, i32, vp, i32, vp]
         lib.rpfq_gelu_act_quant.argtypes = [vp, i32, i64, i64, i32, vp, i32, vp]
         qp = ctypes.POINTER(QuantDesc)

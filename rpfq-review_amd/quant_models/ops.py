@@ -43,6 +43,29 @@ def row_scales(x2: torch.Tensor) -> torch.Tensor:
     return s
 
 
+# bf16 rows into a DMA-kernel launch go to the kernel as prescaled fp16 rows
+# (prescale_rows: one pass instead of the row-scale pass plus the kernel's
+# in-LDS conversion, same outputs bit for bit); RPFQ_PRESCALE_ROWS=0 keeps
+# the bf16 rows.
+PRESCALE_ROWS = __import__("os").environ.get("RPFQ_PRESCALE_ROWS", "1") != "0"
+
+
+def prescale_rows(x2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, row_scale) for a [M, C] bf16 device tensor (rpfq_row_prescale):
+    row_scale = row_scales(x2) and y = x2 * row_scale rounded to fp16, the
+    DMA kernel's operand bits for those rows."""
+    N.require_device(x2)
+    if x2.dtype != torch.bfloat16:
+        raise ValueError("prescale_rows takes bf16 rows")
+    m, c = x2.shape
+    y = torch.empty(m, c, dtype=torch.float16, device=x2.device)
+    s = torch.empty(m, dtype=torch.float32, device=x2.device)
+    if m:
+        N.check("rpfq_row_prescale", N.load().rpfq_row_prescale(x2.data_ptr(), N.dtype_code(x2.dtype), m, c,
+                                                              y.data_ptr(), s.data_ptr(), N.stream_of(x2)))
+    return y, s
+
+
 # Optional per-launch timing hook: when set, PackedWide.linear records HIP
 # events around each wide-linear launch on the launch stream and hands
 # (start_event, end_event, flops, algorithmic_bytes, shape) to the recorder.
@@ -286,9 +309,16 @@ class PackedWide:
             bias = bias.contiguous().float()
         lib = N.load()
         # float32 / bf16 rows: the range guard's prescales (fp16 x is the
-        # MFMA operand as it stands); supplied rows scales are used as given
+        # MFMA operand as it stands); supplied rows scales are used as given.
+        # bf16 rows the DMA kernel would take arrive there as prescaled fp16
+        # rows instead (same operand bits, no conversion in the kernel).
         if row_scale is None and RANGE_GUARD and x2.dtype != torch.float16:
-            row_scale = row_scales(x2)
+            c = x2.shape[1]
+            if (PRESCALE_ROWS and x2.dtype == torch.bfloat16 and c % 8 == 0 and c <= 4096
+                    and self.kernel_for(m, torch.float16, out_dtype, flags) == N.KERNEL_DMA):
+                x2, row_scale = prescale_rows(x2)
+            else:
+                row_scale = row_scales(x2)
         rec = _launch_recorder
         if rec is not None:
             ev0 = torch.cuda.Event(enable_timing=True)

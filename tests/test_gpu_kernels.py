@@ -1266,6 +1266,62 @@ def test_layer_norm_prescaled(m, c, gscale):
     assert torch.equal(x2.view(torch.int16), y2.view(torch.int16))
 
 
+@pytest.mark.parametrize("m,c", [(300, 768), (129, 3072), (64, 4096), (37, 96)])
+def test_row_prescale(m, c):
+    """rpfq_row_prescale: the scales equal rpfq_row_scales and the fp16 rows
+    equal the bf16 rows times them, rounded (the DMA kernel's operand bits),
+    for rows of 1e30 .. 1e-30, 7e4, zero and ordinary magnitudes, and in
+    place."""
+    ops, N = qm()
+    r = rng(2300 + m + c)
+    mags = np.array([1.0, 1e30, 1e-30, 7e4, 0.0, 3e-6, 1e-12, 2.5e38])
+    xs = r.standard_normal((m, c)) * mags[np.arange(m) % len(mags)][:, None]
+    x = torch.from_numpy(xs.astype(np.float32)).to(torch.bfloat16).to(DEV)
+    y, sc = ops.prescale_rows(x)
+    sc_ref = ops.row_scales(x)
+    assert torch.equal(sc, sc_ref)
+    y_ref = (x.float() * sc_ref[:, None]).half()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    x2 = x.clone()
+    N.check("rpfq_row_prescale", N.load().rpfq_row_prescale(x2.data_ptr(), N.dtype_code(x2.dtype), m, c,
+                                                          x2.data_ptr(), sc.data_ptr(), N.stream_of(x2)))
+    assert torch.equal(x2.view(torch.int16), y.view(torch.int16))
+
+
+@pytest.mark.parametrize("case", [REAL_SHAPES[0], REAL_SHAPES[3], CASES[7]], ids=["qkv", "fc2", "rot"])
+def test_bf16_rows_prescaled_pass(case, monkeypatch):
+    """bf16 rows into a DMA-kernel launch go through prescale_rows: outputs
+    equal the bf16-row path (row scales, in-kernel conversion) bit for bit,
+    with bias and residual, rows beyond fp16's range and below its normal
+    range included."""
+    ops, N = qm()
+    r = rng(2400 + case[0] + case[1])
+    pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
+    m = 12672
+    c2 = 2 * case[1]
+    mags = np.array([1.0, 1e6, 1e-9, 3.0])
+    xs = (r.standard_normal((m, c2)) * mags[np.arange(m) % 4][:, None]).astype(np.float32)
+    x = torch.from_numpy(xs).to(torch.bfloat16).to(DEV)
+    bias = tdev(r.standard_normal(2 * case[0]).astype(np.float32))
+    res = torch.from_numpy(r.standard_normal((m, 2 * case[0])).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    calls = []
+    pre = ops.prescale_rows
+
+    def counting(*a, **k):
+        calls.append(1)
+        return pre(*a, **k)
+    monkeypatch.setattr(ops, "prescale_rows", counting)
+    y = pw.linear(x, bias, out_dtype=torch.bfloat16)
+    yr = pw.linear(x, bias, out_dtype=torch.bfloat16, residual=res)
+    assert len(calls) == 2
+    monkeypatch.setattr(ops, "PRESCALE_ROWS", False)
+    y_ref = pw.linear(x, bias, out_dtype=torch.bfloat16)
+    yr_ref = pw.linear(x, bias, out_dtype=torch.bfloat16, residual=res)
+    assert len(calls) == 2
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(yr.view(torch.int16), yr_ref.view(torch.int16))
+
+
 PRESCALED_SHAPES = [REAL_SHAPES[0], REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[5], CASES[7]]
 
 
