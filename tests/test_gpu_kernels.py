@@ -1270,12 +1270,13 @@ def test_layer_norm_prescaled(m, c, gscale):
 def test_row_prescale(m, c):
     """rpfq_row_prescale: the scales equal rpfq_row_scales and the fp16 rows
     equal the bf16 rows times them, rounded (the DMA kernel's operand bits),
-    for rows of 1e30 .. 1e-30, 7e4, zero and ordinary magnitudes, and in
-    place."""
+    for rows of 1e30 .. 1e-30, 7e4, zero, maxima near 2e38, an infinite
+    element (scale 1) and ordinary magnitudes, and in place."""
     ops, N = qm()
     r = rng(2300 + m + c)
-    mags = np.array([1.0, 1e30, 1e-30, 7e4, 0.0, 3e-6, 1e-12, 2.5e38])
+    mags = np.array([1.0, 1e30, 1e-30, 7e4, 0.0, 3e-6, 1e-12, 5e37])
     xs = r.standard_normal((m, c)) * mags[np.arange(m) % len(mags)][:, None]
+    xs[min(2, m - 1), 1] = np.inf
     x = torch.from_numpy(xs.astype(np.float32)).to(torch.bfloat16).to(DEV)
     y, sc = ops.prescale_rows(x)
     sc_ref = ops.row_scales(x)
