@@ -408,18 +408,21 @@ int rpfq_layer_norm(const void* x, int x_dtype, int64_t M, int64_t C, const floa
                     float eps, void* y, int y_dtype, void* stream);
 
 /*
- * rpfq_layer_norm of bf16 rows handed to a packed layer as prescaled fp16
- * rows: each row is normalized and rounded to bf16 exactly as
- * rpfq_layer_norm(y_dtype = RPFQ_BF16) rounds it, row_scale[m] is what
- * rpfq_row_scales gives that bf16 row (a power of two), and y [M, C] fp16
- * holds the bf16 row times row_scale[m], rounded to fp16 -- the operand the
- * DMA kernel makes of the bf16 row itself.  rpfq_wide_linear_scaled(x = y,
- * x_dtype = RPFQ_F16, row_scale) then undoes the prescale and returns, bit
- * for bit, what it returns for the bf16 rows with their row scales, without
- * converting them in the kernel (only on the DMA kernel: the launch must be
- * one rpfq_wide_linear_kernel reports as RPFQ_KERNEL_DMA).  x_dtype must be
- * RPFQ_BF16; row_scale: float32 [M], 16-byte aligned; other arguments as
- * rpfq_layer_norm (y may equal x).  Replaces norm1 / norm2 before qkv / fc1
+ * rpfq_layer_norm of bf16 / float32 rows handed to a packed layer as
+ * prescaled fp16 rows: each row is normalized (and, for bf16 x, rounded to
+ * bf16 exactly as rpfq_layer_norm(y_dtype = RPFQ_BF16) rounds it),
+ * row_scale[m] is what rpfq_row_scales gives that row in x's dtype (a power
+ * of two), and y [M, C] fp16 holds the row times row_scale[m], rounded to
+ * fp16 -- the operand the kernels make of the row itself.
+ * rpfq_wide_linear_scaled(x = y, x_dtype = RPFQ_F16, row_scale) then undoes
+ * the prescale on the DMA kernel (the launch must be one
+ * rpfq_wide_linear_kernel reports as RPFQ_KERNEL_DMA): for bf16 x, bit for
+ * bit what that launch returns for the bf16 rows with their row scales,
+ * without converting them in the kernel; for float32 x, the same fp16
+ * operands the register-staged kernel makes of the float32 rows, on the
+ * faster DMA kernel.  x_dtype: RPFQ_BF16 or RPFQ_F32; row_scale: float32
+ * [M], 16-byte aligned; other arguments as rpfq_layer_norm (y may equal x
+ * for bf16 x).  Replaces norm1 / norm2 before qkv / fc1
  * (audit_rpfq_vit_ios_parity.py:520, :549) in a bf16 model; no counterpart
  * in the reference for the prescale (the guard of this library's fp16 MFMA
  * operands).
@@ -428,14 +431,16 @@ int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, 
                               const float* beta, float eps, void* y, float* row_scale, void* stream);
 
 /*
- * The prescaled fp16 operand rows of bf16 rows without a LayerNorm: y [M, C]
- * fp16 = x times row_scale[m] (what rpfq_row_scales gives x), rounded to
- * fp16 -- the bits the DMA kernel's stage makes of x with those prescales,
- * so rpfq_wide_linear_scaled(y, RPFQ_F16, row_scale) on a DMA-kernel launch
- * equals it on (x, RPFQ_BF16, row_scale) bit for bit, one pass instead of
- * the row-scale pass plus the in-kernel conversion.  x_dtype must be
- * RPFQ_BF16; C a multiple of 8 up to 4096; x, y 16-byte aligned (y may
- * equal x); row_scale float32 [M], 16-byte aligned.  No counterpart in the
+ * The prescaled fp16 operand rows of bf16 / float32 rows without a
+ * LayerNorm: y [M, C] fp16 = x times row_scale[m] (what rpfq_row_scales
+ * gives x), rounded to fp16 -- the bits the kernels make of x with those
+ * prescales, so rpfq_wide_linear_scaled(y, RPFQ_F16, row_scale) on a
+ * DMA-kernel launch equals it on bf16 (x, RPFQ_BF16, row_scale) bit for
+ * bit, one pass instead of the row-scale pass plus the in-kernel
+ * conversion, and takes float32 rows to the DMA kernel with the
+ * register-staged kernel's operands.  x_dtype: RPFQ_BF16 or RPFQ_F32; C a
+ * multiple of 8 up to 4096; x, y 16-byte aligned (y may equal x for bf16
+ * x); row_scale float32 [M], 16-byte aligned.  No counterpart in the
  * reference (the guard of this library's fp16 MFMA operands).
  */
 int rpfq_row_prescale(const void* x, int x_dtype, int64_t M, int64_t C, void* y, float* row_scale, void* stream);

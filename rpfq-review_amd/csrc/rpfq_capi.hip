@@ -455,10 +455,11 @@ int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, 
                               const float* beta, float eps, void* y, float* row_scale, void* stream) {
     int rc = check_ln(x, x_dtype, M, C, gamma, beta, eps, y, RPFQ_F16);
     if (rc) return rc;
-    if (x_dtype != RPFQ_BF16) return fail(RPFQ_ERR_DTYPE, "x must be bf16 (x_dtype=%d)", x_dtype);
+    if (x_dtype != RPFQ_BF16 && x_dtype != RPFQ_F32)
+        return fail(RPFQ_ERR_DTYPE, "x must be bf16 or float32 (x_dtype=%d)", x_dtype);
     if (!row_scale) return fail(RPFQ_ERR_NULL, "row_scale must not be NULL");
     if (!aligned(row_scale, 16)) return fail(RPFQ_ERR_ALIGN, "row_scale must be 16-byte aligned");
-    return hip_status(rpfq::launch_layer_norm_prescaled(x, M, C, gamma, beta, eps, y, row_scale,
+    return hip_status(rpfq::launch_layer_norm_prescaled(x, x_dtype, M, C, gamma, beta, eps, y, row_scale,
                                                         reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_layer_norm_prescaled");
 }
@@ -466,10 +467,12 @@ int rpfq_layer_norm_prescaled(const void* x, int x_dtype, int64_t M, int64_t C, 
 int rpfq_row_prescale(const void* x, int x_dtype, int64_t M, int64_t C, void* y, float* row_scale, void* stream) {
     int rc = check_ln(x, x_dtype, M, C, nullptr, nullptr, 0.0f, y, RPFQ_F16);
     if (rc) return rc;
-    if (x_dtype != RPFQ_BF16) return fail(RPFQ_ERR_DTYPE, "x must be bf16 (x_dtype=%d)", x_dtype);
+    if (x_dtype != RPFQ_BF16 && x_dtype != RPFQ_F32)
+        return fail(RPFQ_ERR_DTYPE, "x must be bf16 or float32 (x_dtype=%d)", x_dtype);
     if (!row_scale) return fail(RPFQ_ERR_NULL, "row_scale must not be NULL");
     if (!aligned(row_scale, 16)) return fail(RPFQ_ERR_ALIGN, "row_scale must be 16-byte aligned");
-    return hip_status(rpfq::launch_row_prescale(x, M, C, y, row_scale, reinterpret_cast<hipStream_t>(stream)),
+    return hip_status(rpfq::launch_row_prescale(x, x_dtype, M, C, y, row_scale,
+                                                reinterpret_cast<hipStream_t>(stream)),
                       "rpfq_row_prescale");
 }
 

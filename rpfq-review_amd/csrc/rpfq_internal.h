@@ -304,9 +304,9 @@ hipError_t launch_layer_norm(const void* x, int xdt, int64_t M, int64_t C, const
                              const float* beta, float eps, int bits, void* y, int ydt, hipStream_t s);
 hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, int bits, void* y, int ydt,
                                  hipStream_t s);
-hipError_t launch_layer_norm_prescaled(const void* x, int64_t M, int64_t C, const float* gamma, const float* beta,
-                                       float eps, void* y, float* scale, hipStream_t s);
-hipError_t launch_row_prescale(const void* x, int64_t M, int64_t C, void* y, float* scale, hipStream_t s);
+hipError_t launch_layer_norm_prescaled(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
+                                       const float* beta, float eps, void* y, float* scale, hipStream_t s);
+hipError_t launch_row_prescale(const void* x, int xdt, int64_t M, int64_t C, void* y, float* scale, hipStream_t s);
 hipError_t launch_act_quant(const void* x, int xdt, int64_t M, int64_t K, int bits, void* y, int ydt,
                             hipStream_t s);
 // weight quantizer (rpfq_quant.hip): reduction blocks per stage, and so the

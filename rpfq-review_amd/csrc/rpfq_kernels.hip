@@ -565,9 +565,9 @@ __device__ __forceinline__ void store8_ln(void* base, int64_t off, const float* 
 // bit-identical to GELU with float32 output followed by AQ.
 // Requires C % 8 == 0 and (AQ) C/2 % 8 == 0, so no 8-element chunk straddles
 // the two halves.
-// PS (bf16 x, fp16 y; after the LayerNorm or alone): the row rounded to bf16
-// (the LayerNorm's output as rpfq_layer_norm would store it, or x itself),
-// then multiplied by its power-of-two prescale
+// PS (bf16 / float32 x, fp16 y; after the LayerNorm or alone): the row in
+// x's dtype (bf16: the LayerNorm's output rounded as rpfq_layer_norm would
+// store it), then multiplied by its power-of-two prescale
 // (row_prescale of its largest magnitude, written to scale[row]) and stored
 // as fp16 -- the bits the DMA kernel's stage makes of the bf16 row with the
 // prescale rpfq_row_scales gives it, so a layer on the fp16 rows undoes the
@@ -724,7 +724,7 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const void* x, int64_t 
         for (int j = 0; j < NC; ++j) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                v[j][e] = bf16_to_f32(f32_to_bf16(v[j][e]));
+                if constexpr (XDT == RPFQ_BF16) v[j][e] = bf16_to_f32(f32_to_bf16(v[j][e]));
                 mx = fmaxf(mx, fabsf(v[j][e]));
             }
         }
@@ -993,7 +993,7 @@ static hipError_t ln_launch(const void* x, int64_t M, int C, const float* gamma,
         hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, false, true, true>), grid, dim3(256), 0, s, x, M, C,
                            gamma, beta, eps, bits, y, scale);
     else if (mode == 5 || mode == 6) {
-        if constexpr (XDT == RPFQ_BF16 && YDT == RPFQ_F16) {
+        if constexpr ((XDT == RPFQ_BF16 || XDT == RPFQ_F32) && YDT == RPFQ_F16) {
             if (mode == 5)
                 hipLaunchKernelGGL((layer_norm_kernel<XDT, YDT, TPR, NC, true, false, false, true>), grid, dim3(256),
                                    0, s, x, M, C, gamma, beta, eps, bits, y, scale);
@@ -1081,13 +1081,13 @@ hipError_t launch_gelu_act_quant(const void* x, int xdt, int64_t M, int64_t C, i
     return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 4, bits, y, ydt, s);
 }
 
-hipError_t launch_layer_norm_prescaled(const void* x, int64_t M, int64_t C, const float* gamma, const float* beta,
-                                       float eps, void* y, float* scale, hipStream_t s) {
-    return row_op(x, RPFQ_BF16, M, C, gamma, beta, eps, 5, 0, y, RPFQ_F16, s, scale);
+hipError_t launch_layer_norm_prescaled(const void* x, int xdt, int64_t M, int64_t C, const float* gamma,
+                                       const float* beta, float eps, void* y, float* scale, hipStream_t s) {
+    return row_op(x, xdt, M, C, gamma, beta, eps, 5, 0, y, RPFQ_F16, s, scale);
 }
 
-hipError_t launch_row_prescale(const void* x, int64_t M, int64_t C, void* y, float* scale, hipStream_t s) {
-    return row_op(x, RPFQ_BF16, M, C, nullptr, nullptr, 0.0f, 6, 0, y, RPFQ_F16, s, scale);
+hipError_t launch_row_prescale(const void* x, int xdt, int64_t M, int64_t C, void* y, float* scale, hipStream_t s) {
+    return row_op(x, xdt, M, C, nullptr, nullptr, 0.0f, 6, 0, y, RPFQ_F16, s, scale);
 }
 
 template <int CB>

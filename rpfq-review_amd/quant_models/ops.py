@@ -43,20 +43,23 @@ def row_scales(x2: torch.Tensor) -> torch.Tensor:
     return s
 
 
-# bf16 rows into a DMA-kernel launch go to the kernel as prescaled fp16 rows
-# (prescale_rows: one pass instead of the row-scale pass plus the kernel's
-# in-LDS conversion, same outputs bit for bit); RPFQ_PRESCALE_ROWS=0 keeps
-# the bf16 rows.
+# bf16 / float32 rows into a 16-bit-output launch the DMA kernel takes for
+# fp16 rows go there as prescaled fp16 rows (prescale_rows: for bf16 one pass
+# instead of the row-scale pass plus the kernel's in-LDS conversion, same
+# outputs bit for bit; float32 rows leave the register-staged kernel with
+# the same operands).  float32 outputs stay on the register-staged kernel,
+# whose float32 stores beat the DMA kernel's.  RPFQ_PRESCALE_ROWS=0 keeps
+# the rows as they are.
 PRESCALE_ROWS = __import__("os").environ.get("RPFQ_PRESCALE_ROWS", "1") != "0"
 
 
 def prescale_rows(x2: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(y, row_scale) for a [M, C] bf16 device tensor (rpfq_row_prescale):
-    row_scale = row_scales(x2) and y = x2 * row_scale rounded to fp16, the
-    DMA kernel's operand bits for those rows."""
+    """(y, row_scale) for a [M, C] bf16 / float32 device tensor
+    (rpfq_row_prescale): row_scale = row_scales(x2) and y = x2 * row_scale
+    rounded to fp16, the kernels' operand bits for those rows."""
     N.require_device(x2)
-    if x2.dtype != torch.bfloat16:
-        raise ValueError("prescale_rows takes bf16 rows")
+    if x2.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("prescale_rows takes bf16 or float32 rows")
     m, c = x2.shape
     y = torch.empty(m, c, dtype=torch.float16, device=x2.device)
     s = torch.empty(m, dtype=torch.float32, device=x2.device)
@@ -185,15 +188,16 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor 
 
 def layer_norm_prescaled(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
                          eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """(y, row_scale) for bf16 x (rpfq_layer_norm_prescaled): the rows of
-    layer_norm(x) as bf16, times their power-of-two prescale row_scale
-    (float32 [M], what row_scales() gives those bf16 rows), stored as fp16.
-    PackedWide.linear(y, ..., row_scale=row_scale) on a launch that takes
-    the DMA kernel equals linear(layer_norm(x)) on the bf16 rows bit for
-    bit, without the kernel's in-LDS bf16 conversion or a row-scale pass."""
+    """(y, row_scale) for bf16 / float32 x (rpfq_layer_norm_prescaled): the
+    rows of layer_norm(x) in x's dtype, times their power-of-two prescale
+    row_scale (float32 [M], what row_scales() gives those rows), stored as
+    fp16.  PackedWide.linear(y, ..., row_scale=row_scale) on a launch that
+    takes the DMA kernel equals linear(layer_norm(x)) on bf16 rows bit for
+    bit, without the kernel's in-LDS bf16 conversion or a row-scale pass,
+    and gives float32 rows the register-staged kernel's operands."""
     N.require_device(x, weight, bias)
-    if x.dtype != torch.bfloat16:
-        raise ValueError("layer_norm_prescaled takes bf16 rows")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("layer_norm_prescaled takes bf16 or float32 rows")
     c = x.shape[-1]
     x2 = _aligned_rows(x.reshape(-1, c))
     m = x2.shape[0]
@@ -310,11 +314,13 @@ class PackedWide:
         lib = N.load()
         # float32 / bf16 rows: the range guard's prescales (fp16 x is the
         # MFMA operand as it stands); supplied rows scales are used as given.
-        # bf16 rows the DMA kernel would take arrive there as prescaled fp16
-        # rows instead (same operand bits, no conversion in the kernel).
+        # Rows the DMA kernel would take as fp16 (16-bit outputs) arrive
+        # there as prescaled fp16 rows instead (bf16: the same operand bits,
+        # no conversion in the kernel; float32: the register-staged kernel's
+        # operands).
         if row_scale is None and RANGE_GUARD and x2.dtype != torch.float16:
             c = x2.shape[1]
-            if (PRESCALE_ROWS and x2.dtype == torch.bfloat16 and c % 8 == 0 and c <= 4096
+            if (PRESCALE_ROWS and out_dtype != torch.float32 and c % 8 == 0 and c <= 4096
                     and self.kernel_for(m, torch.float16, out_dtype, flags) == N.KERNEL_DMA):
                 x2, row_scale = prescale_rows(x2)
             else:

@@ -138,8 +138,8 @@ def test_residual_and_layer_norm_argument_errors():
 
 
 def test_layer_norm_prescaled_argument_errors():
-    """rpfq_layer_norm_prescaled and rpfq_row_prescale take bf16 rows and a
-    16-byte aligned scale array; rpfq_wide_linear_scaled takes prescaled fp16
+    """rpfq_layer_norm_prescaled and rpfq_row_prescale take bf16 / float32
+    rows and a 16-byte aligned scale array; rpfq_wide_linear_scaled takes prescaled fp16
     rows only on a launch the DMA kernel runs."""
     L, N = lib()
     p = ctypes.c_void_p(256)
@@ -152,7 +152,7 @@ def test_layer_norm_prescaled_argument_errors():
     assert L.rpfq_layer_norm_prescaled(p, 2, 4, 64, None, None, 1e-6, p, ctypes.c_void_p(260), None) == 3
     assert L.rpfq_row_prescale(None, 2, 4, 64, p, p, None) == 1
     assert L.rpfq_row_prescale(p, 2, 4, 64, p, None, None) == 1
-    assert L.rpfq_row_prescale(p, 0, 4, 64, p, p, None) == 5  # float32 x
+    assert L.rpfq_row_prescale(p, 1, 4, 64, p, p, None) == 5  # fp16 x
     assert L.rpfq_row_prescale(p, 2, 4, 8192, p, p, None) == 2  # C > 4096
     assert L.rpfq_row_prescale(p, 2, 4, 64, ctypes.c_void_p(264), p, None) == 3
     assert L.rpfq_row_prescale(p, 2, 4, 64, p, ctypes.c_void_p(260), None) == 3

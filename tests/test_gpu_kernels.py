@@ -1235,18 +1235,19 @@ def test_layer_norm(m, c, xdt, ydt):
     assert np.abs(y0 - ref0).max() <= 2e-5 * (np.abs(ref0).max() + 1)
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("gscale", [1.0, 1e6, 1e-9], ids=["g1", "g1e6", "g1e-9"])
 @pytest.mark.parametrize("m,c", [(300, 768), (2047, 768), (2048, 768), (129, 3072), (64, 96)])
-def test_layer_norm_prescaled(m, c, gscale):
+def test_layer_norm_prescaled(m, c, gscale, xdt):
     """rpfq_layer_norm_prescaled against the three steps it stands for:
-    rpfq_layer_norm to bf16, rpfq_row_scales of those rows, and the fp16
-    rounding of each bf16 row times its scale -- scales and fp16 bits equal,
+    rpfq_layer_norm in x's dtype, rpfq_row_scales of those rows, and the fp16
+    rounding of each row times its scale -- scales and fp16 bits equal,
     at both lane layouts of the row kernel (2,047 / 2,048 rows at C = 768),
     with affine parameters that put the rows beyond fp16's range (1e6) or
     below its normal range (1e-9), without them, and in place."""
     ops, _ = qm()
     r = rng(2100 + m + c)
-    x = torch.from_numpy((r.standard_normal((m, c)) * 3 + 1).astype(np.float32)).to(torch.bfloat16).to(DEV)
+    x = torch.from_numpy((r.standard_normal((m, c)) * 3 + 1).astype(np.float32)).to(xdt).to(DEV)
     g = tdev((r.standard_normal(c) * gscale).astype(np.float32))
     b = tdev((r.standard_normal(c) * gscale).astype(np.float32))
     for gg, bb in ((g, b), (None, None)):
@@ -1256,6 +1257,8 @@ def test_layer_norm_prescaled(m, c, gscale):
         assert torch.equal(sc, sc_ref)
         y_ref = (h.float() * sc_ref[:, None]).half()
         assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    if xdt != torch.bfloat16:
+        return
     # in place: the fp16 rows over the bf16 rows' storage
     N = qm()[1]
     x2 = x.clone()
@@ -1266,8 +1269,9 @@ def test_layer_norm_prescaled(m, c, gscale):
     assert torch.equal(x2.view(torch.int16), y2.view(torch.int16))
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
 @pytest.mark.parametrize("m,c", [(300, 768), (129, 3072), (64, 4096), (37, 96)])
-def test_row_prescale(m, c):
+def test_row_prescale(m, c, xdt):
     """rpfq_row_prescale: the scales equal rpfq_row_scales and the fp16 rows
     equal the bf16 rows times them, rounded (the DMA kernel's operand bits),
     for rows of 1e30 .. 1e-30, 7e4, zero, maxima near 2e38, an infinite
@@ -1277,16 +1281,17 @@ def test_row_prescale(m, c):
     mags = np.array([1.0, 1e30, 1e-30, 7e4, 0.0, 3e-6, 1e-12, 5e37])
     xs = r.standard_normal((m, c)) * mags[np.arange(m) % len(mags)][:, None]
     xs[min(2, m - 1), 1] = np.inf
-    x = torch.from_numpy(xs.astype(np.float32)).to(torch.bfloat16).to(DEV)
+    x = torch.from_numpy(xs.astype(np.float32)).to(xdt).to(DEV)
     y, sc = ops.prescale_rows(x)
     sc_ref = ops.row_scales(x)
     assert torch.equal(sc, sc_ref)
     y_ref = (x.float() * sc_ref[:, None]).half()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
-    x2 = x.clone()
-    N.check("rpfq_row_prescale", N.load().rpfq_row_prescale(x2.data_ptr(), N.dtype_code(x2.dtype), m, c,
-                                                          x2.data_ptr(), sc.data_ptr(), N.stream_of(x2)))
-    assert torch.equal(x2.view(torch.int16), y.view(torch.int16))
+    if xdt == torch.bfloat16:  # in place (same element size)
+        x2 = x.clone()
+        N.check("rpfq_row_prescale", N.load().rpfq_row_prescale(x2.data_ptr(), N.dtype_code(x2.dtype), m, c,
+                                                              x2.data_ptr(), sc.data_ptr(), N.stream_of(x2)))
+        assert torch.equal(x2.view(torch.int16), y.view(torch.int16))
 
 
 @pytest.mark.parametrize("case", [REAL_SHAPES[0], REAL_SHAPES[3], CASES[7]], ids=["qkv", "fc2", "rot"])
@@ -1294,7 +1299,9 @@ def test_bf16_rows_prescaled_pass(case, monkeypatch):
     """bf16 rows into a DMA-kernel launch go through prescale_rows: outputs
     equal the bf16-row path (row scales, in-kernel conversion) bit for bit,
     with bias and residual, rows beyond fp16's range and below its normal
-    range included."""
+    range included; float32 rows into fp16 outputs through it onto the DMA
+    kernel within float32 accumulation order and one fp16 rounding of the
+    register-staged kernel's result, float32 outputs not through it."""
     ops, N = qm()
     r = rng(2400 + case[0] + case[1])
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
@@ -1321,6 +1328,23 @@ def test_bf16_rows_prescaled_pass(case, monkeypatch):
     assert len(calls) == 2
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
     assert torch.equal(yr.view(torch.int16), yr_ref.view(torch.int16))
+    # float32 rows into fp16 outputs: the DMA kernel on the prescaled rows
+    # against the register-staged kernel on the float32 rows -- the same fp16
+    # operands, so within float32 accumulation order of sum |x| |A16| and one
+    # fp16 rounding of the output; float32 outputs keep the rows as they are
+    monkeypatch.setattr(ops, "PRESCALE_ROWS", True)
+    x32 = torch.from_numpy(xs).to(DEV)
+    assert pw.kernel_for(m, torch.float32, torch.float16) == N.KERNEL_TILED
+    y32 = pw.linear(x32, bias, out_dtype=torch.float16).float()
+    assert len(calls) == 3
+    pw.linear(x32, bias, out_dtype=torch.float32)
+    assert len(calls) == 3
+    monkeypatch.setattr(ops, "PRESCALE_ROWS", False)
+    y32_ref = pw.linear(x32, bias, out_dtype=torch.float16).float()
+    a16 = tdev(np.abs(O.wide_weight(oplanes, codebook, rotation, fp16=True)).astype(np.float32))
+    scale = x32.abs() @ a16.T + bias.abs()
+    near = (y32 - y32_ref).abs() <= 2.0 ** -10 * y32_ref.abs() + 2.0 ** -24 * 4 * c2 * scale
+    assert torch.all(near | (y32 == y32_ref))  # rows of 1e6: both overflow fp16 alike
 
 
 PRESCALED_SHAPES = [REAL_SHAPES[0], REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[5], CASES[7]]

@@ -1027,14 +1027,17 @@ def test_fused_layer_norm_wiring(name, dt):
     assert bool((y_f.argmax(1) == y_u.argmax(1))[confident].all())
 
 
-def test_prescaled_layer_norm_wiring():
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+def test_prescaled_layer_norm_wiring(dt):
     """bf16 activations at a batch whose qkv / fc1 launches take the DMA
     kernel: norm1 -> qkv and norm2 -> fc1 (+ GELU) run on prescaled fp16
     rows (ops.layer_norm_prescaled, two per block, counted); the logits
     within LOGIT_TOL["bf16"] * max|logit| + LOGIT_TOL["bf16"] / 10 of the
-    same model with the path off (the bf16 LayerNorm output into the
+    same model with the prescaled paths off (the LayerNorm output into the
     kernels' in-LDS conversion: qkv bit-identical, fc1 + GELU on another
-    kernel), identical top-1 on margin-confident samples."""
+    kernel), identical top-1 on margin-confident samples.  float32
+    activations (float32 outputs) never take the prescaled paths: no call,
+    logits identical."""
     import quant_models as qm
     from quant_models import _native as N
     from quant_models import ops
@@ -1045,35 +1048,40 @@ def test_prescaled_layer_norm_wiring():
     model = qm.create_model("rpfq_vit_tiny_patch16_224_q", img_size=224, quant_method_u="complex_phase_v2",
                             quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
     load_synthetic_codes(model, 31)
-    prepare_inference(model, DEV, torch.bfloat16)
+    act = torch.bfloat16 if dt == "bf16" else torch.float32
+    prepare_inference(model, DEV, act)
     batch = 128
     qkv = model.blocks[0].attn.qkv.packed(torch.device(DEV))
-    assert qkv.kernel_for(batch * 197, torch.float16, torch.bfloat16) == N.KERNEL_DMA
-    x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(32)).to(DEV, torch.bfloat16)
+    assert qkv.kernel_for(batch * 197, torch.float16, act) == N.KERNEL_DMA
+    x = torch.randn(batch, 3, 224, 224, generator=torch.Generator().manual_seed(32)).to(DEV, act)
     calls = []
     lnp = ops.layer_norm_prescaled
 
     def counting(*args, **kw):
         calls.append(1)
         return lnp(*args, **kw)
-    saved = qi.PRESCALED_LN
+    saved = qi.PRESCALED_LN, ops.PRESCALE_ROWS
     try:
         ops.layer_norm_prescaled = counting
         with torch.no_grad():
-            qi.PRESCALED_LN = True
+            qi.PRESCALED_LN, ops.PRESCALE_ROWS = True, True
             y_p = model(x)
             n = len(calls)
-            qi.PRESCALED_LN = False
+            qi.PRESCALED_LN, ops.PRESCALE_ROWS = False, False
             y_b = model(x)
     finally:
         ops.layer_norm_prescaled = lnp
-        qi.PRESCALED_LN = saved
+        qi.PRESCALED_LN, ops.PRESCALE_ROWS = saved
+    if dt == "fp32":
+        assert n == 0 and len(calls) == 0, calls
+        assert torch.equal(y_p, y_b)
+        return
     assert n == 2 * len(model.blocks) and len(calls) == n, calls
     y_p, y_b = y_p.float().cpu(), y_b.float().cpu()
     assert torch.isfinite(y_p).all()
     err = float((y_p - y_b).abs().max())
     tol = LOGIT_TOL["bf16"]
-    print(f"vit_tiny bf16 bs{batch}: prescaled rows vs bf16 rows max|dlogit| {err:.4g} "
+    print(f"vit_tiny {dt} bs{batch}: prescaled rows vs rows as they are max|dlogit| {err:.4g} "
           f"(max|logit| {float(y_b.abs().max()):.3g})")
     assert err <= tol * float(y_b.abs().max()) + tol / 10
     top = y_b.topk(2, dim=1).values
