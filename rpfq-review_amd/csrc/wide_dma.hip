@@ -492,8 +492,11 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     }
                 }
                 if (a.vec_store && n0 + 4 <= a.N) {
-                    __builtin_nontemporal_store((f32x4){vr[0], vr[1], vr[2], vr[3]}, reinterpret_cast<f32x4*>(yr));
-                    __builtin_nontemporal_store((f32x4){vi[0], vi[1], vi[2], vi[3]}, reinterpret_cast<f32x4*>(yi));
+                    // plain stores: each covers 16 B of a 128-B line the wave's
+                    // other stores complete, which L2 merges; non-temporal
+                    // partial lines went to memory one by one (qkv 523 -> 281 us)
+                    *reinterpret_cast<f32x4*>(yr) = (f32x4){vr[0], vr[1], vr[2], vr[3]};
+                    *reinterpret_cast<f32x4*>(yi) = (f32x4){vi[0], vi[1], vi[2], vi[3]};
                 } else {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {

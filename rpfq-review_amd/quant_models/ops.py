@@ -43,13 +43,11 @@ def row_scales(x2: torch.Tensor) -> torch.Tensor:
     return s
 
 
-# bf16 / float32 rows into a 16-bit-output launch the DMA kernel takes for
-# fp16 rows go there as prescaled fp16 rows (prescale_rows: for bf16 one pass
-# instead of the row-scale pass plus the kernel's in-LDS conversion, same
-# outputs bit for bit; float32 rows leave the register-staged kernel with
-# the same operands).  float32 outputs stay on the register-staged kernel,
-# whose float32 stores beat the DMA kernel's.  RPFQ_PRESCALE_ROWS=0 keeps
-# the rows as they are.
+# bf16 / float32 rows into a launch the DMA kernel takes for fp16 rows go
+# there as prescaled fp16 rows (prescale_rows: for bf16 one pass instead of
+# the row-scale pass plus the kernel's in-LDS conversion, same outputs bit
+# for bit; float32 rows leave the register-staged kernel with the same
+# operands); RPFQ_PRESCALE_ROWS=0 keeps the rows as they are.
 PRESCALE_ROWS = __import__("os").environ.get("RPFQ_PRESCALE_ROWS", "1") != "0"
 
 
@@ -314,13 +312,12 @@ class PackedWide:
         lib = N.load()
         # float32 / bf16 rows: the range guard's prescales (fp16 x is the
         # MFMA operand as it stands); supplied rows scales are used as given.
-        # Rows the DMA kernel would take as fp16 (16-bit outputs) arrive
-        # there as prescaled fp16 rows instead (bf16: the same operand bits,
-        # no conversion in the kernel; float32: the register-staged kernel's
-        # operands).
+        # Rows the DMA kernel would take as fp16 arrive there as prescaled
+        # fp16 rows instead (bf16: the same operand bits, no conversion in
+        # the kernel; float32: the register-staged kernel's operands).
         if row_scale is None and RANGE_GUARD and x2.dtype != torch.float16:
             c = x2.shape[1]
-            if (PRESCALE_ROWS and out_dtype != torch.float32 and c % 8 == 0 and c <= 4096
+            if (PRESCALE_ROWS and c % 8 == 0 and c <= 4096
                     and self.kernel_for(m, torch.float16, out_dtype, flags) == N.KERNEL_DMA):
                 x2, row_scale = prescale_rows(x2)
             else:

@@ -761,14 +761,13 @@ class QATLinearComplexPhase(nn.Linear):
         slower at one ViT-B/16 image (qkv 15.5 vs 5.2 + 9.5 us, fc1 19.3 vs
         5.2 + 12.0 us); the act quant alone pays in the prologue (proj 9.3 vs
         4.7 + 9.2 us), see _packed_forward / forward_residual.
-        bf16 rows the DMA kernel takes (large M) instead go through the
-        LayerNorm as prescaled fp16 operand rows (rpfq_layer_norm_prescaled):
-        bit-identical to the LayerNorm then the layer on the bf16 rows with
-        their range-guard prescales, without the kernel's in-LDS bf16
-        conversion or the prescale pass (ViT-B/16 qkv at 50,432 rows: 303 ->
-        209 us).  float32 models keep the register-staged kernel: its
-        float32-output stores beat the DMA kernel's (ViT-B/16 bs256 float32
-        7,846 against 7,107 images/s through the prescaled rows)."""
+        bf16 / float32 rows the DMA kernel takes (large M) instead go
+        through the LayerNorm as prescaled fp16 operand rows
+        (rpfq_layer_norm_prescaled): for bf16 bit-identical to the LayerNorm
+        then the layer on the bf16 rows with their range-guard prescales,
+        without the kernel's in-LDS bf16 conversion or the prescale pass
+        (ViT-B/16 qkv at 50,432 rows: 303 -> 209 us); float32 rows leave the
+        register-staged kernel with the same fp16 operands."""
         if not (x.is_cuda and not self.training and self.use_packed) or self.act_quantizer is not None \
                 or self._records_grad(x):
             return None
@@ -783,7 +782,7 @@ class QATLinearComplexPhase(nn.Linear):
         from . import ops
 
         c = x.shape[-1]
-        if (PRESCALED_LN and x.dtype == torch.bfloat16 and c % 8 == 0 and c <= 4096
+        if (PRESCALED_LN and x.dtype in (torch.bfloat16, torch.float32) and c % 8 == 0 and c <= 4096
                 and pw.kernel_for(m, torch.float16, x.dtype, N.FLAG_GELU if gelu else 0) == N.KERNEL_DMA):
             h, sc = ops.layer_norm_prescaled(x, ln_weight, ln_bias, eps)
             return pw.linear(h, bias, out_dtype=x.dtype, gelu=gelu, row_scale=sc)

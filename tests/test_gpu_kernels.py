@@ -1299,9 +1299,9 @@ def test_bf16_rows_prescaled_pass(case, monkeypatch):
     """bf16 rows into a DMA-kernel launch go through prescale_rows: outputs
     equal the bf16-row path (row scales, in-kernel conversion) bit for bit,
     with bias and residual, rows beyond fp16's range and below its normal
-    range included; float32 rows into fp16 outputs through it onto the DMA
-    kernel within float32 accumulation order and one fp16 rounding of the
-    register-staged kernel's result, float32 outputs not through it."""
+    range included; float32 rows through it onto the DMA kernel within
+    float32 accumulation order of the register-staged kernel's result (and
+    one fp16 rounding for fp16 outputs)."""
     ops, N = qm()
     r = rng(2400 + case[0] + case[1])
     pw, oplanes, a_ref, codebook, rotation = build_packed(r, case)
@@ -1328,23 +1328,24 @@ def test_bf16_rows_prescaled_pass(case, monkeypatch):
     assert len(calls) == 2
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
     assert torch.equal(yr.view(torch.int16), yr_ref.view(torch.int16))
-    # float32 rows into fp16 outputs: the DMA kernel on the prescaled rows
-    # against the register-staged kernel on the float32 rows -- the same fp16
-    # operands, so within float32 accumulation order of sum |x| |A16| and one
-    # fp16 rounding of the output; float32 outputs keep the rows as they are
+    # float32 rows: the DMA kernel on the prescaled rows against the
+    # register-staged kernel on the float32 rows -- the same fp16 operands, so
+    # within float32 accumulation order of sum |x| |A16| (float32 outputs),
+    # plus one fp16 rounding of the output (fp16 outputs)
     monkeypatch.setattr(ops, "PRESCALE_ROWS", True)
     x32 = torch.from_numpy(xs).to(DEV)
     assert pw.kernel_for(m, torch.float32, torch.float16) == N.KERNEL_TILED
-    y32 = pw.linear(x32, bias, out_dtype=torch.float16).float()
-    assert len(calls) == 3
-    pw.linear(x32, bias, out_dtype=torch.float32)
-    assert len(calls) == 3
+    y16 = pw.linear(x32, bias, out_dtype=torch.float16).float()
+    y32 = pw.linear(x32, bias, out_dtype=torch.float32)
+    assert len(calls) == 4
     monkeypatch.setattr(ops, "PRESCALE_ROWS", False)
-    y32_ref = pw.linear(x32, bias, out_dtype=torch.float16).float()
+    y16_ref = pw.linear(x32, bias, out_dtype=torch.float16).float()
+    y32_ref = pw.linear(x32, bias, out_dtype=torch.float32)
     a16 = tdev(np.abs(O.wide_weight(oplanes, codebook, rotation, fp16=True)).astype(np.float32))
-    scale = x32.abs() @ a16.T + bias.abs()
-    near = (y32 - y32_ref).abs() <= 2.0 ** -10 * y32_ref.abs() + 2.0 ** -24 * 4 * c2 * scale
-    assert torch.all(near | (y32 == y32_ref))  # rows of 1e6: both overflow fp16 alike
+    acc = 2.0 ** -24 * 4 * c2 * (x32.abs() @ a16.T + bias.abs())
+    assert torch.all((y32 - y32_ref).abs() <= acc)
+    near = (y16 - y16_ref).abs() <= 2.0 ** -10 * y16_ref.abs() + acc
+    assert torch.all(near | (y16 == y16_ref))  # rows of 1e6: both overflow fp16 alike
 
 
 PRESCALED_SHAPES = [REAL_SHAPES[0], REAL_SHAPES[2], REAL_SHAPES[3], REAL_SHAPES[5], CASES[7]]

@@ -1029,15 +1029,16 @@ def test_fused_layer_norm_wiring(name, dt):
 
 @pytest.mark.parametrize("dt", ["bf16", "fp32"])
 def test_prescaled_layer_norm_wiring(dt):
-    """bf16 activations at a batch whose qkv / fc1 launches take the DMA
-    kernel: norm1 -> qkv and norm2 -> fc1 (+ GELU) run on prescaled fp16
-    rows (ops.layer_norm_prescaled, two per block, counted); the logits
+    """bf16 / float32 activations at a batch whose qkv / fc1 launches take
+    the DMA kernel: norm1 -> qkv and norm2 -> fc1 (+ GELU) run on prescaled
+    fp16 rows (ops.layer_norm_prescaled, two per block, counted); the logits
     within LOGIT_TOL["bf16"] * max|logit| + LOGIT_TOL["bf16"] / 10 of the
-    same model with the prescaled paths off (the LayerNorm output into the
-    kernels' in-LDS conversion: qkv bit-identical, fc1 + GELU on another
-    kernel), identical top-1 on margin-confident samples.  float32
-    activations (float32 outputs) never take the prescaled paths: no call,
-    logits identical."""
+    same model with the prescaled paths off (bf16: the LayerNorm output into
+    the kernels' in-LDS conversion, qkv bit-identical, fc1 + GELU on another
+    kernel; float32: the register-staged kernel on the same fp16 operands,
+    each layer within float32 accumulation order (test_bf16_rows_prescaled_
+    pass), which 12 blocks of a random-code model amplify to ~7e-4 of
+    max|logit|: bar 2e-3), identical top-1 on margin-confident samples."""
     import quant_models as qm
     from quant_models import _native as N
     from quant_models import ops
@@ -1072,15 +1073,11 @@ def test_prescaled_layer_norm_wiring(dt):
     finally:
         ops.layer_norm_prescaled = lnp
         qi.PRESCALED_LN, ops.PRESCALE_ROWS = saved
-    if dt == "fp32":
-        assert n == 0 and len(calls) == 0, calls
-        assert torch.equal(y_p, y_b)
-        return
     assert n == 2 * len(model.blocks) and len(calls) == n, calls
     y_p, y_b = y_p.float().cpu(), y_b.float().cpu()
     assert torch.isfinite(y_p).all()
     err = float((y_p - y_b).abs().max())
-    tol = LOGIT_TOL["bf16"]
+    tol = LOGIT_TOL["bf16"] if dt == "bf16" else 2e-3
     print(f"vit_tiny {dt} bs{batch}: prescaled rows vs rows as they are max|dlogit| {err:.4g} "
           f"(max|logit| {float(y_b.abs().max()):.3g})")
     assert err <= tol * float(y_b.abs().max()) + tol / 10
