@@ -599,7 +599,12 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                                    add2_y(v.z, rres[j].z, f16), add2_y(v.w, rres[j].w, f16));
                 }
                 if constexpr (ACT != 0) v = gelu8_y(v, YDT == RPFQ_F16);
-                __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
+                // whole 128-byte lines stream past the cache; the per-wave half lines are
+                // left for L2 to merge (non-temporal partial lines measured slower)
+                if (wg)
+                    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
+                else
+                    *reinterpret_cast<u32x4*>(dst) = __builtin_bit_cast(u32x4, v);
             } else {
                 const uint16_t* hv = reinterpret_cast<const uint16_t*>(&v);
                 for (int t = 0; t < 8 && ncol + t < a.N; ++t) {
