@@ -106,11 +106,16 @@ __device__ __forceinline__ float2 derotate(float2 q, float c, float s) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// float32 -> bf16 by gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN
+// kept quiet with its sign and top payload bits, i.e. bit for bit
+//   u += 0x7fff + ((u >> 16) & 1), u >> 16   (NaN: (u >> 16) | 0x40)
+// for every float32 bit pattern (checked exhaustively on the device).
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// two bf16 in one instruction: lo in bits 0-15, hi in bits 16-31
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
@@ -192,7 +197,7 @@ __device__ __forceinline__ uint32_t add2_y(uint32_t v, uint32_t r, bool f16) {
     if (f16) return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, r) + __builtin_bit_cast(half2v, v));
     const float lo = bf16_to_f32(r & 0xffffu) + bf16_to_f32(v & 0xffffu);
     const float hi = bf16_to_f32(r >> 16) + bf16_to_f32(v >> 16);
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    return pack_bf2(lo, hi);
 }
 template <int YDT>
 __device__ __forceinline__ uint4 add_res8(uint4 v, const void* res, int64_t off) {
@@ -268,8 +273,7 @@ __device__ __forceinline__ uint32_t gelu2_y(uint32_t v, bool f16) {
         const half2v o = {(_Float16)gelu_fast((float)h.x), (_Float16)gelu_fast((float)h.y)};
         return __builtin_bit_cast(uint32_t, o);
     }
-    return (uint32_t)f32_to_bf16(gelu_fast(bf16_to_f32(v & 0xffffu))) |
-           ((uint32_t)f32_to_bf16(gelu_fast(bf16_to_f32(v >> 16))) << 16);
+    return pack_bf2(gelu_fast(bf16_to_f32(v & 0xffffu)), gelu_fast(bf16_to_f32(v >> 16)));
 }
 __device__ __forceinline__ uint4 gelu8_y(uint4 v, bool f16) {
     return make_uint4(gelu2_y(v.x, f16), gelu2_y(v.y, f16), gelu2_y(v.z, f16), gelu2_y(v.w, f16));

@@ -568,14 +568,10 @@ __global__ void __launch_bounds__(256, BM == 128 ? 2 : 1) wide_linear_dma_kernel
                     pi = make_uint2(cvt_pk(acc_im[i][4 * q] + bim[4 * q], acc_im[i][4 * q + 1] + bim[4 * q + 1]),
                                     cvt_pk(acc_im[i][4 * q + 2] + bim[4 * q + 2], acc_im[i][4 * q + 3] + bim[4 * q + 3]));
                 } else {
-                    pr = make_uint2(f32_to_bf16(acc_re[i][4 * q] + bre[4 * q]) |
-                                        ((uint32_t)f32_to_bf16(acc_re[i][4 * q + 1] + bre[4 * q + 1]) << 16),
-                                    f32_to_bf16(acc_re[i][4 * q + 2] + bre[4 * q + 2]) |
-                                        ((uint32_t)f32_to_bf16(acc_re[i][4 * q + 3] + bre[4 * q + 3]) << 16));
-                    pi = make_uint2(f32_to_bf16(acc_im[i][4 * q] + bim[4 * q]) |
-                                        ((uint32_t)f32_to_bf16(acc_im[i][4 * q + 1] + bim[4 * q + 1]) << 16),
-                                    f32_to_bf16(acc_im[i][4 * q + 2] + bim[4 * q + 2]) |
-                                        ((uint32_t)f32_to_bf16(acc_im[i][4 * q + 3] + bim[4 * q + 3]) << 16));
+                    pr = make_uint2(pack_bf2(acc_re[i][4 * q] + bre[4 * q], acc_re[i][4 * q + 1] + bre[4 * q + 1]),
+                                    pack_bf2(acc_re[i][4 * q + 2] + bre[4 * q + 2], acc_re[i][4 * q + 3] + bre[4 * q + 3]));
+                    pi = make_uint2(pack_bf2(acc_im[i][4 * q] + bim[4 * q], acc_im[i][4 * q + 1] + bim[4 * q + 1]),
+                                    pack_bf2(acc_im[i][4 * q + 2] + bim[4 * q + 2], acc_im[i][4 * q + 3] + bim[4 * q + 3]));
                 }
                 *reinterpret_cast<uint2*>(trow + (8 * q + 4 * g) * 2) = pr;
                 *reinterpret_cast<uint2*>(trow + 64 + (8 * q + 4 * g) * 2) = pi;

@@ -138,7 +138,7 @@ __device__ __forceinline__ half8 res_x16(uint4 v, float sc) {
 template <int YDT>
 __device__ __forceinline__ uint32_t res_pack2(float lo, float hi) {
     if constexpr (YDT == RPFQ_F16) return cvt_pk(lo, hi);
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    return pack_bf2(lo, hi);
 }
 
 // Subtiles in flight per wave (the register ring).  Deeper rings (4 at

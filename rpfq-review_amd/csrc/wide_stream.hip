@@ -1056,8 +1056,7 @@ __global__ void __launch_bounds__(64, 3) wide_linear_gemv_persist_kernel(WideArg
             if constexpr (YDT == RPFQ_F16) {
                 o = make_uint2(cvt_pk(v4[0], v4[1]), cvt_pk(v4[2], v4[3]));
             } else {
-                o = make_uint2((uint32_t)f32_to_bf16(v4[0]) | ((uint32_t)f32_to_bf16(v4[1]) << 16),
-                               (uint32_t)f32_to_bf16(v4[2]) | ((uint32_t)f32_to_bf16(v4[3]) << 16));
+                o = make_uint2(pack_bf2(v4[0], v4[1]), pack_bf2(v4[2], v4[3]));
             }
             if constexpr (RES) {
                 const uint2 rv = *reinterpret_cast<const uint2*>(res_s + 2 * GN * m + GN * l.p + j);
