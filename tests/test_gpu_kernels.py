@@ -1110,6 +1110,56 @@ def test_wide_linear_residual_bit_exact(m, flags, ydt):
         assert torch.equal(yf, res + y), (case, m, flags, ydt)
 
 
+def _bf16_rne_bits(v):
+    """float32 -> bf16 bits, round to nearest even (NaN: any NaN pattern)."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+@pytest.mark.parametrize("m,flags", [(3, 0), (197, 0), (33, 2), (300, 2), (300, 1)],
+                         ids=["stream3", "stream197", "reg33", "dma300", "reg128-300"])
+def test_bf16_store_rounding(m, flags):
+    """The stores' float32 -> bf16 conversion (the hardware's packed
+    conversion) is round-to-nearest-even bit for bit: with x = 0 each output
+    is 0 + bias exactly, so bias vectors of random float32 bit patterns plus
+    ties (low half 0x8000, even and odd), subnormals, the largest finite
+    value (rounds to inf), +-inf and NaN must come back as numpy's rounding of
+    them -- on each kernel path, at whole-line (N' = 1536) and element-tail
+    (N' = 50) stores; with a residual, res + bf16(bias) added in float32 and
+    rounded again."""
+    r = rng(1500 + m)
+    special = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000, 0x00008000, 0x00018000, 0x00000001,
+                        0x007FFFFF, 0x80000001, 0x807FFFFF, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x7F7E8000,
+                        0x7F800000, 0xFF800000, 0x7FC00001, 0xFFA12345, 0x3F80FFFF, 0x477FFFFF], np.uint32)
+    for case in (CASES[1], CASES[2]):
+        pw, *_ = build_packed(r, case)
+        n = 2 * case[0]
+        bits = r.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        bits[: len(special)] = special[:n]
+        bits[(bits & 0x7FFFFFFF) == 0] = 0x3F800000  # no +-0: 0 + -0 is +0
+        bias_np = bits.view(np.float32)
+        x = torch.zeros((m, 2 * case[1]), dtype=torch.float16, device=DEV)
+        y = pw.linear(x, tdev(bias_np), out_dtype=torch.bfloat16, flags=flags)
+        got = y.view(torch.int16).cpu().numpy().view(np.uint16)
+        want = _bf16_rne_bits(bias_np)
+        nan = np.isnan(bias_np)
+        got_nan = ((got & 0x7FFF) > 0x7F80)
+        assert np.array_equal(got_nan, np.broadcast_to(nan, got.shape)), (case, m, flags)
+        bad = (got != want) & ~nan
+        assert not bad.any(), (case, m, flags, hex(int(bits[np.nonzero(bad)[1][0]])))
+        # residual: res + bf16(bias) in float32, rounded again (finite biases)
+        fin = np.isfinite(bias_np)
+        res_np = (r.standard_normal((m, n)).astype(np.float32) * 4)
+        res = torch.from_numpy(res_np).to(torch.bfloat16).to(DEV)
+        yr = pw.linear(x, tdev(np.where(fin, bias_np, np.float32(1.0))), out_dtype=torch.bfloat16, flags=flags,
+                       residual=res)
+        rb = (res.view(torch.int16).cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        vb = (_bf16_rne_bits(np.where(fin, bias_np, np.float32(1.0))).astype(np.uint32) << 16).view(np.float32)
+        want_r = _bf16_rne_bits((rb + vb[None, :]).astype(np.float32))
+        got_r = yr.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got_r, want_r), (case, m, flags)
+
+
 @pytest.mark.parametrize("m,flags", [(3, 0), (197, 0), (33, 2), (300, 2), (300, 1)],
                          ids=["stream3", "stream197", "reg33", "dma300", "reg128-300"])
 @pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float32])
