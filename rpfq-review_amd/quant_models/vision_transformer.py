@@ -391,7 +391,18 @@ class VisionTransformer(nn.Module):
 
     def forward_features(self, x):
         x = self.patch_embed(x)
-        x = torch.cat((self._prefix_tokens(x), x), dim=1) + self.pos_embed.to(x.dtype)
+        pre, pos = self._prefix_tokens(x), self.pos_embed.to(x.dtype)
+        if torch.is_grad_enabled() and (x.requires_grad or pre.requires_grad or pos.requires_grad):
+            x = torch.cat((pre, x), dim=1) + pos
+        else:
+            # prefix and patch tokens written with their position embedding
+            # into one buffer: one pass instead of torch.cat and then the add
+            # (the same elementwise sums)
+            n = pre.shape[1]
+            out = x.new_empty((x.shape[0], n + x.shape[1], x.shape[2]))
+            torch.add(pre, pos[:, :n], out=out[:, :n])
+            torch.add(x, pos[:, n:], out=out[:, n:])
+            x = out
         x = self.norm_pre(self.pos_drop(x))
         x = self.blocks(x)
         return norm_fwd(self.norm, x)
