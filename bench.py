@@ -390,10 +390,13 @@ def stream_case(k_c: int, n_c: int, m: int, mode: str, gib: float, reps: int, se
     del layers
     torch.cuda.empty_cache()
     gbs = nbytes / (ms / 1e3) / 1e9
+    launches = 1 if mode == "stacked" else int(code_bytes // (k_c * n_layer))
+    # rotate: one small launch per real layer, so the figure is per-layer
+    # latency (us_per_launch), not a streaming rate
     return {"k_complex": k_c, "n_complex": n_layer, "m": m, "mode": mode, "kernel": kname,
-            "launches": (1 if mode == "stacked"
-            else int(code_bytes // (k_c * n_layer))), "code_gib": round(code_bytes / (1 << 30), 3),
-            "us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+            "launches": launches, "code_gib": round(code_bytes / (1 << 30), 3),
+            "us": round(ms * 1e3, 2), "us_per_launch": round(ms * 1e3 / launches, 2),
+            "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
 def stream_sweep(ms=(1, 4, 16), modes=("stacked", "rotate"), gib: float = 1.0, reps: int = 10, out=None,
