@@ -73,3 +73,29 @@ def test_timm_state_dict_keys():
     assert vit.pos_embed.shape == (1, 197, 768)
     deit = qm().create_model("rpfq_deit_tiny_patch16_224_q")
     assert deit.pos_embed.shape == (1, 198, 192) and "dist_token" in deit.state_dict()
+
+
+@pytest.mark.parametrize("name", ["rpfq_vit_tiny_patch16_224_q", "rpfq_deit_tiny_patch16_224_q"])
+def test_token_write_matches_cat(name):
+    """Outside autograd the prefix and patch tokens are written with their
+    position embedding into one buffer; recorded for autograd the forward
+    keeps torch.cat followed by the add. Both give the same bits (one class
+    token for ViT, class + distillation tokens for DeiT)."""
+    torch.manual_seed(0)
+    m = qm().create_model(name, pretrained=False, num_classes=10, img_size=32, quant_method_u="complex_phase_v2",
+                          quant_method_w="complex_phase_v2", enable_act_quant=False, enable_rotation=False)
+    m.eval()
+    with torch.no_grad():
+        m.pos_embed.normal_()
+        m.cls_token.normal_()
+        if getattr(m, "dist_token", None) is not None:
+            m.dist_token.normal_()
+    m.blocks, m.norm = torch.nn.Identity(), torch.nn.Identity()
+    x = torch.randn(3, 3, 32, 32)
+    with torch.no_grad():
+        fused = m.forward_features(x)
+    xg = x.clone().requires_grad_(True)
+    with torch.enable_grad():
+        cat = m.forward_features(xg)
+    assert cat.requires_grad and not fused.requires_grad
+    assert torch.equal(fused, cat.detach())
