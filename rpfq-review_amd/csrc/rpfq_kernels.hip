@@ -9,6 +9,9 @@
 //
 // The widely-linear GEMM kernels are in wide_dma.hip, wide_stream.hip and
 // wide_tiled.hip, their dispatch in wide_dispatch.hip.
+#include <cstdlib>
+#include <mutex>
+
 #include "rpfq_device.h"
 
 namespace rpfq {
@@ -1045,9 +1048,191 @@ static hipError_t row_block_go(const void* x, int64_t M, int C, int mode, int bi
     return hipGetLastError();
 }
 
+// GELU + act quant of fp16 rows (mode 4) with torch's float32 GELU taken from
+// a table: the GELU of an fp16 input depends on its 16 bits only, so gelu_f
+// of every fp16 x in (-16, 16) is computed once per device (gelu_tab_kernel,
+// the function layer_norm_kernel evaluates per element) and each element
+// reads its entry from the workgroup's LDS copy; inputs outside the table
+// (larger magnitudes, inf, NaN) evaluate gelu_f.  Everything after the GELU
+// is layer_norm_kernel's 64-lane act quant (exact per-half maxima, the
+// quotient table of the <= 16 levels by ds_bpermute), so the output equals
+// that kernel's bit for bit without its ~45 VALU of erff per element.
+// Table index: the fp16 bits for x in [+0, 16) (bits < 0x4C00), kGeluTabPos +
+// (bits & 0x7fff) for x in [-0, -16) (bits in [0x8000, 0xCC00)): at the
+// spread of ViT-B's fc1 outputs (sigma ~3) almost no row holds an input
+// outside, which would re-read the row for gelu_f.
+constexpr int kGeluTabPos = 0x4C00, kGeluTabNeg = 0x4C00;
+constexpr int kGeluTab = kGeluTabPos + kGeluTabNeg;  // 38,912 floats = 155,648 B of LDS (of 160 KB)
+static_assert(kGeluTab % 4 == 0, "the table is copied as float4");
+__device__ __align__(16) float g_gelu_tab[kGeluTab];
+
+__global__ void __launch_bounds__(256) gelu_tab_kernel() {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= kGeluTab) return;
+    const uint16_t h = (uint16_t)(i < kGeluTabPos ? i : 0x8000 + (i - kGeluTabPos));
+    g_gelu_tab[i] = gelu_f((float)__builtin_bit_cast(_Float16, h));
+}
+
+// One workgroup of 16 waves per CU (the table fills most of the LDS); each
+// wave walks rows, a row at a time over its 64 lanes (lane l: 8-element
+// chunks l, l + 64, ...; NC chunks at most).  y may equal x: a row is read
+// whole before it is stored, by one wave.
+template <int YDT, int NC>
+__global__ void __launch_bounds__(1024) gelu_aq_tab_kernel(const void* x, int64_t M, int C, int bits, void* y) {
+    extern __shared__ __align__(16) float tab[];
+    for (int i = 4 * (int)threadIdx.x; i < kGeluTab; i += 4 * 1024)
+        *reinterpret_cast<float4*>(tab + i) = *reinterpret_cast<const float4*>(g_gelu_tab + i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int nch = C >> 3, half_ch = nch >> 1;
+    const float qmax = (float)((1 << (bits - 1)) - 1);
+    const float qmin = -(float)(1 << (bits - 1));
+    for (int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); row < M; row += (int64_t)gridDim.x * 16) {
+        const int64_t base = row * C;
+        // the row's fp16 words (chunks past the row read as +0, whose entry is +0)
+        uint4 raw[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = lane + 64 * j;
+            raw[j] = c < nch ? *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + base + 8 * c)
+                             : make_uint4(0u, 0u, 0u, 0u);
+        }
+        // every element reads an entry (entry 0 where the table has none), so
+        // the reads issue back to back; the rare others evaluate gelu_f after
+        float v[NC][8];
+        bool outside = false;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t hb = (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu;
+                const uint32_t mag = hb & 0x7fffu;
+                const bool neg = hb >= 0x8000u;
+                const bool in = neg ? mag < (uint32_t)kGeluTabNeg : mag < (uint32_t)kGeluTabPos;
+                v[j][e] = tab[in ? (neg ? (uint32_t)kGeluTabPos + mag : mag) : 0u];
+                outside |= !in;
+            }
+        }
+        if (outside) {  // re-read (the row is stored only below, so x still holds it in place)
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int c = lane + 64 * j;
+                if (c >= nch) continue;
+                const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + base + 8 * c);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t hb = (e & 1) ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu;
+                    const uint32_t mag = hb & 0x7fffu;
+                    const bool in = hb >= 0x8000u ? mag < (uint32_t)kGeluTabNeg : mag < (uint32_t)kGeluTabPos;
+                    if (!in) v[j][e] = gelu_f((float)__builtin_bit_cast(_Float16, (uint16_t)hb));
+                }
+            }
+        }
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = lane + 64 * j;
+            if (c < nch) {
+                float mx = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[j][e]));
+                if (c < half_ch) m0 = fmaxf(m0, mx); else m1 = fmaxf(m1, mx);
+            }
+        }
+        m0 = group_max<64>(m0);
+        m1 = group_max<64>(m1);
+        // torch evaluates `float(qmax) / tensor` as reciprocal(tensor) * qmax
+        const float sc0 = (1.0f / fmaxf(m0, 1e-5f)) * qmax, sc1 = (1.0f / fmaxf(m1, 1e-5f)) * qmax;
+        // lane l < 32 divides level (l & 15) - 8 by the scale of half l >> 4
+        // once; each element fetches its quotient from that lane (every lane
+        // takes part; lanes past the row hold zeros and store nothing)
+        const float tv = (float)((lane & 15) - 8) / ((lane & 16) ? sc1 : sc0);
+        const int tvb = __float_as_int(tv);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const bool hi = lane + 64 * j >= half_ch;
+            const float sc = hi ? sc1 : sc0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float qv = rintf(v[j][e] * sc);
+                qv = fminf(fmaxf(qv, qmin), qmax);
+                const int src = (hi ? 16 : 0) + (int)qv + 8;
+                const float d = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, tvb));
+                v[j][e] = copysignf(d, qv);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = lane + 64 * j;
+            if (c < nch) store8_ln<YDT>(y, base + 8 * c, v[j]);
+        }
+    }
+}
+
+static std::atomic<uint64_t> g_gelu_tab_ready{0};
+static std::mutex g_gelu_tab_mu;
+
+// The table path is on unless RPFQ_GELU_TABLE=0.  The current device's table
+// is filled on the first call outside graph capture (on that call's stream,
+// synchronized once, so every later launch on any stream sees it); calls
+// under capture before that take the per-element kernel.
+static bool gelu_table_ready(hipStream_t s) {
+    static const bool enabled = [] {
+        const char* e = std::getenv("RPFQ_GELU_TABLE");
+        return !(e && e[0] == '0');
+    }();
+    if (!enabled) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    const uint64_t bit = (uint64_t)1 << dev;
+    if (g_gelu_tab_ready.load(std::memory_order_acquire) & bit) return true;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return false;
+    std::lock_guard<std::mutex> lock(g_gelu_tab_mu);
+    if (g_gelu_tab_ready.load(std::memory_order_acquire) & bit) return true;
+    hipLaunchKernelGGL(gelu_tab_kernel, dim3((kGeluTab + 255) / 256), dim3(256), 0, s);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return false;
+    g_gelu_tab_ready.fetch_or(bit, std::memory_order_release);
+    return true;
+}
+
+template <int YDT, int NC>
+static hipError_t gelu_aq_tab_launch(const void* x, int64_t M, int C, int bits, void* y, hipStream_t s) {
+    static std::atomic<uint64_t> attr_done{0};
+    constexpr int lds = kGeluTab * 4;
+    const hipError_t e =
+        set_lds_attr_once(reinterpret_cast<const void*>(&gelu_aq_tab_kernel<YDT, NC>), lds, attr_done);
+    if (e != hipSuccess) return e;
+    const int64_t groups = (M + 15) / 16;
+    const int grid = (int)(groups < device_cus() ? groups : device_cus());
+    hipLaunchKernelGGL((gelu_aq_tab_kernel<YDT, NC>), dim3(grid), dim3(1024), lds, s, x, M, C, bits, y);
+    return hipGetLastError();
+}
+
+template <int YDT>
+static hipError_t gelu_aq_tab_go(const void* x, int64_t M, int C, int bits, void* y, hipStream_t s) {
+    const int nch = C / 8;
+    if (nch <= 128) return gelu_aq_tab_launch<YDT, 2>(x, M, C, bits, y, s);
+    if (nch <= 256) return gelu_aq_tab_launch<YDT, 4>(x, M, C, bits, y, s);
+    return gelu_aq_tab_launch<YDT, 6>(x, M, C, bits, y, s);
+}
+
 template <int XDT>
 static hipError_t ln_y(const void* x, int64_t M, int C, const float* gamma, const float* beta, float eps, int mode,
                        int bits, void* y, int ydt, float* scale, hipStream_t s) {
+    if constexpr (XDT == RPFQ_F16) {
+        if (mode == 4 && M > kRowBlockMaxM && C % 16 == 0 && C / 8 <= 384 && bits >= 1 && bits <= 4 &&
+            reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+            gelu_table_ready(s)) {
+            switch (ydt) {
+                case RPFQ_F32: return gelu_aq_tab_go<RPFQ_F32>(x, M, C, bits, y, s);
+                case RPFQ_F16: return gelu_aq_tab_go<RPFQ_F16>(x, M, C, bits, y, s);
+                default: return gelu_aq_tab_go<RPFQ_BF16>(x, M, C, bits, y, s);
+            }
+        }
+    }
     if ((mode == 2 || mode == 4) && M <= kRowBlockMaxM && C % 16 == 0) {
         switch (ydt) {
             case RPFQ_F32: return row_block_go<XDT, RPFQ_F32>(x, M, C, mode, bits, y, s);

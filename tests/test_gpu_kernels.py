@@ -1740,6 +1740,46 @@ def test_gelu_act_quant_maximum_candidates(bits):
     assert torch.equal(fused, ref)
 
 
+@pytest.mark.parametrize("c", [768, 3072])
+@pytest.mark.parametrize("ydt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("bits", [2, 4])
+def test_gelu_act_quant_fp16_every_input(c, ydt, bits):
+    """fp16 rows past the workgroup-per-row limit read torch's float32 GELU
+    from a per-device table (every fp16 x in (-16, 16)) and evaluate it per
+    element beyond: every finite fp16 bit pattern, the table's edges and
+    neighbours (16, -16) and magnitudes to 65504, M = 1,100. Bit for bit
+    against the per-element kernel on the same rows (two 550-row launches,
+    a workgroup per row), against torch's GELU followed by the act quant,
+    and in place."""
+    import torch.nn.functional as F
+
+    ops, N = qm()
+    r = rng(1700 + c + bits)
+    m = 1100
+    vals = (r.standard_normal((m, c)) * 3).astype(np.float16)
+    flat = vals.reshape(-1)
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    allh = allh[np.isfinite(allh)]
+    flat[: len(allh)] = allh
+    edges = np.array([16.0, 15.99, 16.02, -16.0, -15.99, -16.02, 65504.0, -65504.0, 0.0, -0.0, 6e-8, -6e-8,
+                      8.0, -10.0, 1000.0, -1000.0], np.float16)
+    idx = r.choice(np.arange(len(allh), flat.size), size=len(edges) * 40, replace=False)
+    flat[idx] = np.tile(edges, 40)
+    x = torch.from_numpy(vals).to(DEV)
+    fused = ops.gelu_act_quant(x, bits, out_dtype=ydt)
+    per_elem = torch.cat([ops.gelu_act_quant(x[:550], bits, out_dtype=ydt),
+                          ops.gelu_act_quant(x[550:], bits, out_dtype=ydt)])
+    assert torch.equal(fused, per_elem)
+    assert torch.equal(fused, ops.act_quant(F.gelu(x.float()), bits, out_dtype=ydt))
+    if ydt == torch.float16:
+        y = x.clone()
+        N.check("rpfq_gelu_act_quant", N.load().rpfq_gelu_act_quant(
+            y.data_ptr(), N.dtype_code(torch.float16), m, c, bits, y.data_ptr(), N.dtype_code(ydt),
+            N.stream_of(y)))
+        torch.cuda.synchronize()
+        assert torch.equal(y, fused)
+
+
 @pytest.mark.parametrize("k", [8, 384, 1536])
 def test_act_quant_row_kernel_matches_oracle(k):
     """The register-resident act-quant kernel (K' % 8 == 0) is bit-exact with
